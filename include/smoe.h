@@ -1,0 +1,235 @@
+/*
+ * smoe.h — C ABI of libsmoe.so, the gfx950 (MI355X) Spider-MoE block.
+ *
+ * One loop of the recurrent block (spider_moe/model.py:240-317 of the
+ * reference, run num_loops times by model.py:445-448):
+ *   router top-k  ->  edge generator top-m  ->  destination-grouped edge
+ *   projection + message combine  ->  dispatch by expert  ->  grouped expert
+ *   FFN (f32 / bf16 / fp8-e4m3 / int4 weights)  ->  weighted combine +
+ *   residual + LayerNorm.
+ *
+ * Conventions follow the reference's native ABI (kernels/include/
+ * spider_kernels.h:26-149, spider_cuda.h:8-60):
+ *   - every entry point returns int: 0 ok, 1 invalid argument, 2 index out of
+ *     range, 3 capacity (workspace too small), -2 unsupported dtype/format,
+ *     4 HIP runtime error (the HIP error string is kept for smoe_last_error);
+ *   - the caller owns every buffer (inputs, outputs and the workspace, whose
+ *     size comes from the *_workspace_bytes queries); nothing allocates;
+ *   - the stream is an opaque hipStream_t passed as void* (spider_cuda.h:8);
+ *   - tensors are row-major and contiguous, indices int32;
+ *   - all device pointers; calls enqueue work on `stream` and return without
+ *     synchronizing.
+ * Calls that share a workspace must not overlap in time.
+ */
+#pragma once
+#include <stddef.h>
+#include <stdint.h>
+
+#if defined(_WIN32)
+#define SMOE_API __declspec(dllexport)
+#else
+#define SMOE_API __attribute__((visibility("default")))
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SMOE_ABI_VERSION 1
+
+/* status codes (spider_kernels.h convention; see scalar.cpp:9,45,58) */
+#define SMOE_OK 0
+#define SMOE_EINVAL 1
+#define SMOE_ERANGE 2
+#define SMOE_ECAPACITY 3
+#define SMOE_EUNSUPPORTED (-2)
+#define SMOE_EHIP 4
+
+/* element formats */
+#define SMOE_F32 0
+#define SMOE_BF16 1
+#define SMOE_FP8_E4M3 2 /* OCP e4m3fn codes + per-output-channel fp32 scale  */
+#define SMOE_INT4 3     /* 2 per byte, low nibble first, per-group scales     */
+#define SMOE_F16 4      /* scale dtype only                                   */
+
+/* expert activations */
+#define SMOE_ACT_GELU 0   /* Linear(+b) -> GELU(erf) -> Linear(+b)  (model.py:177-183) */
+#define SMOE_ACT_SWIGLU 1 /* W_down (silu(W_gate x) * (W_up x (+b_up))) (+b_down)     */
+
+/* Expert FFN weights, stacked over experts (the reference stacks them per
+ * call, model.py:305-308; here they are stacked once).
+ *   f32 / bf16: w_up [E,U,H], w_down [E,H,U] elements.
+ *   fp8:        codes with the same shapes; s_up f32 [E,U], s_down f32 [E,H]
+ *               (per output channel; quant.py:146-169 with a per-row scale).
+ *   int4:       w_up [E,U,H/2] bytes, s_up [E,U,H/g]; w_down [E,H,U/2],
+ *               s_down [E,H,U/g]; scales f32 or f16 (quant.py:89-143).
+ *   SwiGLU:     w_up holds the gate and up projections interleaved by
+ *               blocks of 32 rows — rows [64j, 64j+32) are gate rows
+ *               [32j, 32j+32) and rows [64j+32, 64j+64) are up rows
+ *               [32j, 32j+32) — so w_up is [E,2U,H] (and s_up [E,2U(,..)]).
+ *               w_gate must be NULL.
+ *   b_up [E,U] and b_down [E,H] are fp32 or NULL. */
+typedef struct smoe_experts {
+  int format;      /* SMOE_F32 / SMOE_BF16 / SMOE_FP8_E4M3 / SMOE_INT4 */
+  int act;         /* SMOE_ACT_GELU / SMOE_ACT_SWIGLU */
+  int E, H, U;
+  int group_size;  /* int4 only */
+  int scale_dtype; /* int4: SMOE_F32 or SMOE_F16; fp8: SMOE_F32 */
+  const void* w_up;
+  const void* w_gate; /* reserved, must be NULL */
+  const void* w_down;
+  const void* s_up;
+  const void* s_down;
+  const float* b_up;
+  const float* b_down;
+} smoe_experts;
+
+/* One Spider-MoE block (parameters of model.py:165-185).
+ * act_dtype (SMOE_F32 or SMOE_BF16) is the dtype of h, x0, the output and of
+ * router_w, edge_gen_w and edge_value_w.  loop_bias [R,E] and
+ * edge_loop_bias [R,E*E] are fp32; edge_loop_bias[r] = b_g + W_g[:,H:] .
+ * loop_embedding[r], filled by smoe_edge_loop_bias(). */
+typedef struct smoe_block {
+  int act_dtype;
+  int H, E, K, M, L, R; /* hidden, experts, top_k, edges_per_expert, loop_embed_size, num_loops */
+  const void* router_w;       /* [E,H]      router.weight          */
+  const float* loop_bias;     /* [R,E]      loop_bias              */
+  const void* edge_gen_w;     /* [E*E,H+L]  edge_generator.weight  */
+  const float* edge_loop_bias;/* [R,E*E]                           */
+  const void* edge_value_w;   /* [E,H,H]    edge_value.{e}.weight  */
+  smoe_experts experts;       /*            experts.{e}.{0,2}      */
+  const float* ln_w;          /* [H]        norm.weight            */
+  const float* ln_b;          /* [H]        norm.bias              */
+  float alpha;                /* residual_scale  (config.py:18)    */
+  float beta;                 /* re_inject_weight (config.py:19)   */
+  float eps;                  /* LayerNorm eps (1e-5)              */
+} smoe_block;
+
+/* Byte offsets of the named regions inside a block workspace (for tests and
+ * diagnostics: they hold the last loop's routing after a call). */
+typedef struct smoe_ws_layout {
+  size_t total;
+  size_t logits;    /* f32 [N,E]      router logits (+ loop bias)                 */
+  size_t top_idx;   /* i32 [N,K]      router top-k, descending probability        */
+  size_t top_w;     /* f32 [N,K]      renormalized top-k weights                  */
+  size_t tok_e;     /* i32 [N,K]      token's distinct experts, ascending, -1 pad  */
+  size_t tok_ew;    /* f32 [N,K]      merged weight of each                        */
+  size_t e_cnt;     /* i32 [E]        rows per expert (all distinct top-k pairs)  */
+  size_t e_acnt;    /* i32 [E]        rows with weight > 0 (the dispatch counts)  */
+  size_t e_off;     /* i32 [E+1]      row offsets                                 */
+  size_t e_rows;    /* i32 [N*K]      token of each row, (expert, token) order    */
+  size_t e_roww;    /* f32 [N*K]      weight of each row                          */
+  size_t e_tokrow;  /* i32 [N,K]      row of each tok_e entry                     */
+  size_t edge_logit;/* f32 [N*K,E]    edge logits of each source row              */
+  size_t edge_idx;  /* i32 [N*K,M]    top-m destinations of each source row       */
+  size_t edge_w;    /* f32 [N*K,M]    their softmax weights                       */
+  size_t tok_d;     /* i32 [N,S]      token's destinations, ascending, -1 pad     */
+  size_t tok_dc;    /* f32 [N,S]      destination coefficients                    */
+  size_t d_cnt;     /* i32 [E]        rows per destination                        */
+  size_t d_acnt;    /* i32 [E]        (same as d_cnt: zero coefficients are dropped) */
+  size_t d_off;     /* i32 [E+1]                                                 */
+  size_t d_rows;    /* i32 [N*S]                                                 */
+  size_t d_roww;    /* f32 [N*S]                                                 */
+  size_t d_tokrow;  /* i32 [N,S]                                                 */
+  size_t proj;      /* act  [N*S,H]   c * W_edge[d] h per destination row         */
+  size_t msg;       /* ffn  [N,H]     messages                                    */
+  size_t act;       /* ffn  [N*K,U]   expert hidden activations                   */
+  size_t y;         /* ffn  [N*K,H]   weighted expert outputs                     */
+  size_t h_tmp;     /* act  [N,H]     loop ping-pong buffer                       */
+  size_t scratch;   /* plan scratch                                               */
+  int S;            /* destinations per token: min(E, K*M)                        */
+  int ffn_dtype;    /* SMOE_F32 or SMOE_BF16                                      */
+} smoe_ws_layout;
+
+SMOE_API int smoe_abi_version(void);
+/* spider_backend_name / spider_backend_caps (spider_kernels.h:148-149) */
+SMOE_API const char* smoe_backend_name(void);
+SMOE_API uint32_t smoe_backend_caps(void); /* bit i set = format i supported */
+SMOE_API const char* smoe_last_error(void);
+
+/* Workspace for smoe_block_forward over N tokens, and its layout. */
+SMOE_API size_t smoe_block_workspace_bytes(const smoe_block* blk, int N);
+SMOE_API int smoe_block_workspace_layout(const smoe_block* blk, int N, smoe_ws_layout* out);
+
+/* edge_loop_bias[r, o] = b_g[o] + sum_l W_g[o, H+l] * loop_emb[r, l]
+ * (the loop-embedding half of edge_generator, model.py:261-263).
+ * W_g in act_dtype [E*E, H+L]; b_g f32 [E*E] or NULL; loop_emb f32 [R,L]. */
+SMOE_API int smoe_edge_loop_bias(const void* edge_gen_w, int act_dtype, const float* edge_gen_b,
+                                 const float* loop_emb, int E, int H, int L, int R,
+                                 float* out, void* stream);
+
+/* SpiderMoELayer.forward (model.py:240-317) for loops
+ * [loop_begin, loop_begin + num_loops), back to back on `stream`, no host
+ * synchronization; with num_loops > 1 it is SpiderWebLM._run_recurrent_full
+ * (model.py:445-448).  h_in, x0, h_out: [N,H] in act_dtype; h_out may alias
+ * h_in.  Replaces the reference's fused step spider_moe_loop_step_f32
+ * (spider_kernels.h:113-121) and the declared-only
+ * spider_cuda_moe_loop_step_f32 (spider_cuda.h:35-44). */
+SMOE_API int smoe_block_forward(const smoe_block* blk, const void* h_in, const void* x0,
+                                void* h_out, int N, int loop_begin, int num_loops,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
+/* Router stage alone (model.py:255-258; spider_router_f32,
+ * spider_kernels.h:26-28, with the logits GEMM of model.py:255 fused in):
+ * x [N,H] act_dtype, router_w [E,H] act_dtype, loop_bias_row f32 [E] or NULL
+ * -> logits f32 [N,E] (may be NULL), top_w f32 [N,K], top_idx i32 [N,K]. */
+SMOE_API size_t smoe_router_workspace_bytes(int N, int E);
+SMOE_API int smoe_router_topk(const void* x, int act_dtype, int N, int H, const void* router_w,
+                              const float* loop_bias_row, int E, int K, float* logits,
+                              float* top_w, int32_t* top_idx, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
+/* Dispatch plan (spider_infer/forge/ep/dispatch.py:56-115 build_dispatch_plan,
+ * sparse_experts.py:51-56): idx/w [N,K] -> per expert ascending, the tokens
+ * whose merged weight is > 0, ascending.  counts [E], offsets [E+1],
+ * rows [N*K] (token per row; entries past offsets[E] are unspecified),
+ * row_w [N*K], tok_row [N,K] (row of each distinct positive (token, expert),
+ * in ascending expert order, -1 padded).  Expert ids outside [0, E) match
+ * no expert and are dropped, as the reference's per-expert masks drop them. */
+SMOE_API size_t smoe_dispatch_workspace_bytes(int N, int K, int E);
+SMOE_API int smoe_dispatch_plan(const int32_t* idx, const float* w, int N, int K, int E,
+                                int32_t* counts, int32_t* offsets, int32_t* rows, float* row_w,
+                                int32_t* tok_row, void* workspace, size_t workspace_bytes,
+                                void* stream);
+
+/* sparse_expert_delta (sparse_experts.py:11-68; dispatch_expert_ffn
+ * forge/ep/dispatch.py:145-185; spider_expert_grouped_gemm_f32
+ * spider_kernels.h:89-92): msg [N,H] in ffn dtype (f32 for f32 experts,
+ * bf16 otherwise), idx i32 / w f32 [N,K] -> delta [N,H] in out_dtype
+ * (SMOE_F32 or SMOE_BF16). */
+SMOE_API size_t smoe_expert_delta_workspace_bytes(const smoe_experts* ex, int N, int K);
+SMOE_API int smoe_expert_delta(const smoe_experts* ex, const void* msg, const int32_t* idx,
+                               const float* w, int N, int K, void* delta, int out_dtype,
+                               void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- diagnostics (no counterpart in the reference; used by bench.py) ----
+ * Stage ids of smoe_block_forward, in launch order within a loop. */
+#define SMOE_STAGE_ROUTER_GEMM 0
+#define SMOE_STAGE_ROUTE_TOPK 1
+#define SMOE_STAGE_EXPERT_PLAN 2
+#define SMOE_STAGE_EDGE_LOGITS 3
+#define SMOE_STAGE_EDGE_TOPM 4
+#define SMOE_STAGE_DEST_PLAN 5
+#define SMOE_STAGE_EDGE_GEMM 6
+#define SMOE_STAGE_MSG_COMBINE 7
+#define SMOE_STAGE_UP_GEMM 8
+#define SMOE_STAGE_DOWN_GEMM 9
+#define SMOE_STAGE_EPILOGUE 10
+#define SMOE_NUM_STAGES 11
+/* When `events` is not NULL, every later smoe_block_forward records
+ * events[2*i] before and events[2*i+1] after the i-th launch of a stage in
+ * `stage_mask` (bit s = stage s), for i < capacity, on the call's stream.
+ * Process-wide and not thread-safe; pass NULL to stop.  smoe_profile_count
+ * returns how many pairs were recorded and resets the counter; stage_of[i]
+ * (may be NULL) receives the stage of pair i. */
+SMOE_API int smoe_profile_stages(uint32_t stage_mask, void** events, int capacity);
+SMOE_API int smoe_profile_count(int32_t* stage_of, int capacity);
+/* hipEvent helpers for callers without a HIP binding. */
+SMOE_API int smoe_events_create(int n, void** events);
+SMOE_API int smoe_events_destroy(int n, void** events);
+/* ms[i] = elapsed time between events[2*i] and events[2*i+1] (synchronizes). */
+SMOE_API int smoe_events_elapsed(int pairs, void** events, float* ms);
+
+#ifdef __cplusplus
+}
+#endif

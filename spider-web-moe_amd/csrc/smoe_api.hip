@@ -1,0 +1,561 @@
+// C ABI of libsmoe.so (declared in include/smoe.h).
+//
+// smoe_block_forward enqueues, per loop, on the caller's stream:
+//   1  logits GEMM        h . W_r^T + loop_bias[r]            (model.py:255)
+//   2  route_topk         softmax / top-k / renorm            (model.py:256-258)
+//   3  plan (experts)     stable (expert, token) order        (dispatch.py:56-115)
+//   4  edge-logit GEMM    per source expert: W_g[s] h + bias  (model.py:261-264)
+//   5  edge_topm          top-m, softmax, dest. coefficients  (model.py:265-288)
+//   6  plan (dests)       stable (destination, token) order
+//   7  edge GEMM          c * W_edge[d] h per (token, d)      (model.py:271-272)
+//   8  msg combine        sum over the token's destinations   (model.py:288)
+//   9  up GEMM            act(W_up msg + b_up)                (sparse_experts.py:60-61)
+//   10 down GEMM          w * (W_down act + b_down)           (sparse_experts.py:62-63)
+//   11 epilogue           LN(h + a*sum_e y + b*x0)            (model.py:317)
+// No step reads routing back to the host; grids are sized for the worst case.
+#include <string>
+#include <type_traits>
+
+#include "smoe_common.hpp"
+#include "smoe_internal.hpp"
+
+using namespace smoe;
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int rc, const char* what) {
+  g_err = what;
+  return rc;
+}
+
+int hip_rc(int rc, const char* what) {
+  if (rc == SMOE_EHIP) {
+    g_err = std::string(what) + ": " + hipGetErrorString(hipGetLastError());
+  } else if (rc != SMOE_OK) {
+    g_err = std::string(what) + ": rc " + std::to_string(rc);
+  }
+  return rc;
+}
+
+// ---- stage profiling (diagnostics) ----
+uint32_t g_prof_mask = 0;
+hipEvent_t* g_prof_ev = nullptr;
+int g_prof_cap = 0;
+int g_prof_n = 0;
+int32_t g_prof_stage[1 << 16];
+
+struct StageScope {
+  int i = -1;
+  hipStream_t s;
+  StageScope(int stage, hipStream_t st) : s(st) {
+    if (g_prof_ev && (g_prof_mask >> stage & 1u) && g_prof_n < g_prof_cap && g_prof_n < (1 << 16)) {
+      i = g_prof_n++;
+      g_prof_stage[i] = stage;
+      (void)hipEventRecord(g_prof_ev[2 * i], s);
+    }
+  }
+  ~StageScope() {
+    if (i >= 0) (void)hipEventRecord(g_prof_ev[2 * i + 1], s);
+  }
+};
+
+#define SMOE_TRY(expr, what)            \
+  do {                                  \
+    const int _rc = (expr);             \
+    if (_rc != SMOE_OK) return hip_rc(_rc, what); \
+  } while (0)
+
+// SMOE_TRY inside a profiling scope of stage `id`
+#define STAGE(id, expr, what)           \
+  do {                                  \
+    StageScope _ps((id), s);            \
+    SMOE_TRY(expr, what);               \
+  } while (0)
+
+size_t esize(int dtype) { return dtype == SMOE_F32 ? 4 : 2; }
+
+size_t align_up(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+struct Bump {
+  size_t off = 0;
+  size_t take(size_t bytes) {
+    const size_t o = off;
+    off = align_up(off + bytes);
+    return o;
+  }
+};
+
+int ffn_dtype_of(const smoe_experts& ex) { return ex.format == SMOE_F32 ? SMOE_F32 : SMOE_BF16; }
+
+int check_experts(const smoe_experts& ex, int H) {
+  if (ex.E < 1 || ex.E > 64 || ex.H != H || ex.U <= 0) return fail(SMOE_EINVAL, "expert shape");
+  if (!ex.w_up || !ex.w_down) return fail(SMOE_EINVAL, "expert weights missing");
+  if (ex.w_gate) return fail(SMOE_EINVAL, "w_gate must be NULL (gate interleaved into w_up)");
+  if (ex.act != SMOE_ACT_GELU && ex.act != SMOE_ACT_SWIGLU) return fail(SMOE_EINVAL, "act");
+  switch (ex.format) {
+    case SMOE_F32:
+      if (ex.act == SMOE_ACT_SWIGLU) return fail(SMOE_EUNSUPPORTED, "SwiGLU with fp32 experts");
+      if (H % 16 || ex.U % 16) return fail(SMOE_EINVAL, "fp32 experts need H, U % 16 == 0");
+      break;
+    case SMOE_BF16:
+      break;
+    case SMOE_FP8_E4M3:
+      if (!ex.s_up || !ex.s_down) return fail(SMOE_EINVAL, "fp8 scales missing");
+      break;
+    case SMOE_INT4:
+      if (!ex.s_up || !ex.s_down) return fail(SMOE_EINVAL, "int4 scales missing");
+      if (ex.group_size <= 0 || ex.group_size % 8 || H % ex.group_size || ex.U % ex.group_size)
+        return fail(SMOE_EINVAL, "int4 group size must divide H and U and be a multiple of 8");
+      if (ex.scale_dtype != SMOE_F32 && ex.scale_dtype != SMOE_F16)
+        return fail(SMOE_EUNSUPPORTED, "int4 scale dtype");
+      break;
+    default:
+      return fail(SMOE_EUNSUPPORTED, "expert format");
+  }
+  if (ex.format != SMOE_F32) {
+    if (H % 32 || ex.U % 32) return fail(SMOE_EINVAL, "MFMA experts need H, U % 32 == 0");
+    if (ex.act == SMOE_ACT_SWIGLU && ex.U % 64)
+      return fail(SMOE_EINVAL, "SwiGLU needs U % 64 == 0");
+  }
+  return SMOE_OK;
+}
+
+int check_block(const smoe_block* b) {
+  if (!b) return fail(SMOE_EINVAL, "null block");
+  if (b->act_dtype != SMOE_F32 && b->act_dtype != SMOE_BF16)
+    return fail(SMOE_EUNSUPPORTED, "act_dtype");
+  if (b->H <= 0 || b->H % 8 || b->H > 4096) return fail(SMOE_EINVAL, "H");
+  if (b->act_dtype == SMOE_BF16 && b->H % 32) return fail(SMOE_EINVAL, "bf16 needs H % 32 == 0");
+  if (b->act_dtype == SMOE_F32 && b->H % 16) return fail(SMOE_EINVAL, "fp32 needs H % 16 == 0");
+  if (b->E < 1 || b->E > 64) return fail(SMOE_EINVAL, "E must be in [1, 64]");
+  if (b->K < 1 || b->K > b->E || b->K > 16) return fail(SMOE_EINVAL, "top_k");
+  if (b->M < 1 || b->M > b->E || b->M > 16) return fail(SMOE_EINVAL, "edges_per_expert");
+  if (b->L < 0 || b->R < 1) return fail(SMOE_EINVAL, "loops");
+  if (!b->router_w || !b->loop_bias || !b->edge_gen_w || !b->edge_loop_bias || !b->edge_value_w)
+    return fail(SMOE_EINVAL, "block weights missing");
+  if (b->experts.E != b->E) return fail(SMOE_EINVAL, "experts.E != E");
+  if (b->experts.format == SMOE_F32 && b->act_dtype != SMOE_F32)
+    return fail(SMOE_EUNSUPPORTED, "fp32 experts need fp32 activations");
+  return check_experts(b->experts, b->H);
+}
+
+void make_layout(const smoe_block* b, int N, smoe_ws_layout* l) {
+  const size_t n = N > 0 ? static_cast<size_t>(N) : 1;
+  const int E = b->E, K = b->K, M = b->M, H = b->H;
+  const int S = E < K * M ? E : K * M;
+  const int fdt = ffn_dtype_of(b->experts);
+  const int U = b->experts.U;
+  Bump z;
+  l->logits = z.take(n * E * 4);
+  l->top_idx = z.take(n * K * 4);
+  l->top_w = z.take(n * K * 4);
+  l->tok_e = z.take(n * K * 4);
+  l->tok_ew = z.take(n * K * 4);
+  l->e_cnt = z.take(E * 4);
+  l->e_acnt = z.take(E * 4);
+  l->e_off = z.take((E + 1) * 4);
+  l->e_rows = z.take(n * K * 4);
+  l->e_roww = z.take(n * K * 4);
+  l->e_tokrow = z.take(n * K * 4);
+  l->edge_logit = z.take(n * K * E * 4);
+  l->edge_idx = z.take(n * K * M * 4);
+  l->edge_w = z.take(n * K * M * 4);
+  l->tok_d = z.take(n * S * 4);
+  l->tok_dc = z.take(n * S * 4);
+  l->d_cnt = z.take(E * 4);
+  l->d_acnt = z.take(E * 4);
+  l->d_off = z.take((E + 1) * 4);
+  l->d_rows = z.take(n * S * 4);
+  l->d_roww = z.take(n * S * 4);
+  l->d_tokrow = z.take(n * S * 4);
+  l->proj = z.take(n * S * H * esize(b->act_dtype));
+  l->msg = z.take(n * H * esize(fdt));
+  l->act = z.take(n * K * U * esize(fdt));
+  l->y = z.take(n * K * H * esize(fdt));
+  l->h_tmp = z.take(n * H * esize(b->act_dtype));
+  l->scratch = z.take(plan_scratch_bytes(N, E));
+  l->total = z.off;
+  l->S = S;
+  l->ffn_dtype = fdt;
+}
+
+template <typename T>
+T* at(void* ws, size_t off) {
+  return reinterpret_cast<T*>(reinterpret_cast<char*>(ws) + off);
+}
+
+// Expert up + down GEMMs over a plan.
+int run_experts(const smoe_experts& ex, const void* msg, const int32_t* off, const int32_t* rows,
+                const float* roww, int max_rows, void* act, void* y, hipStream_t s) {
+  const int H = ex.H, U = ex.U, E = ex.E;
+  const int fdt = ffn_dtype_of(ex);
+  const int nup = ex.act == SMOE_ACT_SWIGLU ? 2 * U : U;
+  GemmArgs up;
+  up.fmt = ex.format;
+  up.epi = ex.act == SMOE_ACT_SWIGLU ? EPI_SWIGLU : EPI_GELU;
+  up.A = msg;
+  up.lda = H;
+  up.a_rows = rows;
+  up.W = ex.w_up;
+  up.w_gstride = static_cast<int64_t>(nup) * H;
+  up.ldw = H;
+  up.S = ex.s_up;
+  up.s_f16 = ex.scale_dtype == SMOE_F16;
+  up.group_size = ex.group_size;
+  up.s_gstride = ex.format == SMOE_INT4 ? static_cast<int64_t>(nup) * (H / ex.group_size) : nup;
+  up.K = H;
+  up.N_out = nup;
+  up.grp_off = off;
+  up.G = E;
+  up.max_rows = max_rows;
+  up.out = act;
+  up.ldo = U;
+  up.out_dtype = fdt;
+  up.bias = ex.b_up;
+  up.bias_gstride = U;
+  STAGE(SMOE_STAGE_UP_GEMM, launch_grouped_gemm(up, s), "expert up GEMM");
+
+  GemmArgs dn;
+  dn.fmt = ex.format;
+  dn.epi = EPI_DOWN;
+  dn.A = act;
+  dn.lda = U;
+  dn.a_rows = nullptr;  // act rows are already in plan order
+  dn.W = ex.w_down;
+  dn.w_gstride = static_cast<int64_t>(H) * U;
+  dn.ldw = U;
+  dn.S = ex.s_down;
+  dn.s_f16 = ex.scale_dtype == SMOE_F16;
+  dn.group_size = ex.group_size;
+  dn.s_gstride = ex.format == SMOE_INT4 ? static_cast<int64_t>(H) * (U / ex.group_size) : H;
+  dn.K = U;
+  dn.N_out = H;
+  dn.grp_off = off;
+  dn.G = E;
+  dn.max_rows = max_rows;
+  dn.out = y;
+  dn.ldo = H;
+  dn.out_dtype = fdt;
+  dn.bias = ex.b_down;
+  dn.bias_gstride = H;
+  dn.row_scale = roww;
+  STAGE(SMOE_STAGE_DOWN_GEMM, launch_grouped_gemm(dn, s), "expert down GEMM");
+  return SMOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+SMOE_API int smoe_abi_version(void) { return SMOE_ABI_VERSION; }
+SMOE_API const char* smoe_backend_name(void) { return "hip-gfx950"; }
+SMOE_API uint32_t smoe_backend_caps(void) {
+  return (1u << SMOE_F32) | (1u << SMOE_BF16) | (1u << SMOE_FP8_E4M3) | (1u << SMOE_INT4);
+}
+SMOE_API const char* smoe_last_error(void) { return g_err.c_str(); }
+
+SMOE_API size_t smoe_block_workspace_bytes(const smoe_block* blk, int N) {
+  if (check_block(blk) != SMOE_OK || N < 0) return 0;
+  smoe_ws_layout l;
+  make_layout(blk, N, &l);
+  return l.total;
+}
+
+SMOE_API int smoe_block_workspace_layout(const smoe_block* blk, int N, smoe_ws_layout* out) {
+  const int rc = check_block(blk);
+  if (rc != SMOE_OK) return rc;
+  if (!out || N < 0) return fail(SMOE_EINVAL, "layout args");
+  make_layout(blk, N, out);
+  return SMOE_OK;
+}
+
+SMOE_API int smoe_edge_loop_bias(const void* edge_gen_w, int act_dtype, const float* edge_gen_b,
+                                 const float* loop_emb, int E, int H, int L, int R, float* out,
+                                 void* stream) {
+  if (!edge_gen_w || !out || (L > 0 && !loop_emb) || E < 1 || H < 1 || L < 0 || R < 1)
+    return fail(SMOE_EINVAL, "edge_loop_bias args");
+  if (act_dtype != SMOE_F32 && act_dtype != SMOE_BF16) return fail(SMOE_EUNSUPPORTED, "dtype");
+  SMOE_TRY(launch_edge_loop_bias(edge_gen_w, act_dtype, edge_gen_b, loop_emb, E, H, L, R, out,
+                                 static_cast<hipStream_t>(stream)),
+           "edge_loop_bias");
+  return SMOE_OK;
+}
+
+SMOE_API int smoe_block_forward(const smoe_block* b, const void* h_in, const void* x0,
+                                void* h_out, int N, int loop_begin, int num_loops, void* ws,
+                                size_t ws_bytes, void* stream) {
+  int rc = check_block(b);
+  if (rc != SMOE_OK) return rc;
+  if (N < 0 || loop_begin < 0 || num_loops < 0 || loop_begin + num_loops > b->R)
+    return fail(SMOE_EINVAL, "N / loop range");
+  if (N == 0 || num_loops == 0) return SMOE_OK;
+  if (!h_in || !x0 || !h_out || !ws) return fail(SMOE_EINVAL, "null buffer");
+  smoe_ws_layout l;
+  make_layout(b, N, &l);
+  if (ws_bytes < l.total) return fail(SMOE_ECAPACITY, "workspace too small");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int H = b->H, E = b->E, K = b->K, M = b->M, L = b->L, S = l.S;
+  const int adt = b->act_dtype, fdt = l.ffn_dtype;
+  const int gfmt = adt == SMOE_F32 ? SMOE_F32 : SMOE_BF16;  // router / edge weights
+
+  const void* cur = h_in;
+  for (int i = 0; i < num_loops; ++i) {
+    const int r = loop_begin + i;
+    void* dst = ((num_loops - 1 - i) % 2 == 0) ? h_out : at<void>(ws, l.h_tmp);
+
+    // 1 router logits (+ loop bias)
+    GemmArgs rg;
+    rg.fmt = gfmt;
+    rg.epi = EPI_F32_BIAS;
+    rg.A = cur;
+    rg.lda = H;
+    rg.W = b->router_w;
+    rg.ldw = H;
+    rg.K = H;
+    rg.N_out = E;
+    rg.G = 0;
+    rg.single_rows = N;
+    rg.out = at<float>(ws, l.logits);
+    rg.ldo = E;
+    rg.bias = b->loop_bias + static_cast<int64_t>(r) * E;
+    rg.bias_gstride = 0;
+    STAGE(SMOE_STAGE_ROUTER_GEMM, launch_grouped_gemm(rg, s), "router GEMM");
+    // 2 top-k
+    STAGE(SMOE_STAGE_ROUTE_TOPK, launch_route_topk(at<float>(ws, l.logits), N, E, K, at<int32_t>(ws, l.top_idx),
+                               at<float>(ws, l.top_w), at<int32_t>(ws, l.tok_e),
+                               at<float>(ws, l.tok_ew), s),
+             "route_topk");
+    // 3 expert / source plan (keeps every selected source; the FFN combine
+    //   skips weights <= 0)
+    STAGE(SMOE_STAGE_EXPERT_PLAN, launch_plan(at<int32_t>(ws, l.tok_e), at<float>(ws, l.tok_ew), N, K, E, 0,
+                         at<int32_t>(ws, l.e_cnt), at<int32_t>(ws, l.e_acnt),
+                         at<int32_t>(ws, l.e_off), at<int32_t>(ws, l.e_rows),
+                         at<float>(ws, l.e_roww), at<int32_t>(ws, l.e_tokrow),
+                         at<void>(ws, l.scratch), s),
+             "expert plan");
+    // 4 edge logits of each (token, selected source) row
+    GemmArgs eg;
+    eg.fmt = gfmt;
+    eg.epi = EPI_F32_BIAS;
+    eg.A = cur;
+    eg.lda = H;
+    eg.a_rows = at<int32_t>(ws, l.e_rows);
+    eg.W = b->edge_gen_w;
+    eg.w_gstride = static_cast<int64_t>(E) * (H + L);
+    eg.ldw = H + L;
+    eg.K = H;
+    eg.N_out = E;
+    eg.grp_off = at<int32_t>(ws, l.e_off);
+    eg.G = E;
+    eg.max_rows = N * K;
+    eg.out = at<float>(ws, l.edge_logit);
+    eg.ldo = E;
+    eg.bias = b->edge_loop_bias + static_cast<int64_t>(r) * E * E;
+    eg.bias_gstride = E;
+    STAGE(SMOE_STAGE_EDGE_LOGITS, launch_grouped_gemm(eg, s), "edge-logit GEMM");
+    // 5 top-m + destination coefficients
+    STAGE(SMOE_STAGE_EDGE_TOPM, launch_edge_topm(at<float>(ws, l.edge_logit), at<int32_t>(ws, l.tok_e),
+                              at<int32_t>(ws, l.e_tokrow), N, E, K, M, S,
+                              at<int32_t>(ws, l.edge_idx), at<float>(ws, l.edge_w),
+                              at<int32_t>(ws, l.tok_d), at<float>(ws, l.tok_dc), s),
+             "edge_topm");
+    // 6 destination plan
+    STAGE(SMOE_STAGE_DEST_PLAN, launch_plan(at<int32_t>(ws, l.tok_d), at<float>(ws, l.tok_dc), N, S, E, 1,
+                         at<int32_t>(ws, l.d_cnt), at<int32_t>(ws, l.d_acnt),
+                         at<int32_t>(ws, l.d_off), at<int32_t>(ws, l.d_rows),
+                         at<float>(ws, l.d_roww), at<int32_t>(ws, l.d_tokrow),
+                         at<void>(ws, l.scratch), s),
+             "destination plan");
+    // 7 edge projections c * W_edge[d] h
+    GemmArgs pg;
+    pg.fmt = gfmt;
+    pg.epi = EPI_ROWSCALE;
+    pg.A = cur;
+    pg.lda = H;
+    pg.a_rows = at<int32_t>(ws, l.d_rows);
+    pg.W = b->edge_value_w;
+    pg.w_gstride = static_cast<int64_t>(H) * H;
+    pg.ldw = H;
+    pg.K = H;
+    pg.N_out = H;
+    pg.grp_off = at<int32_t>(ws, l.d_off);
+    pg.G = E;
+    pg.max_rows = N * S;
+    pg.out = at<void>(ws, l.proj);
+    pg.ldo = H;
+    pg.out_dtype = adt;
+    pg.row_scale = at<float>(ws, l.d_roww);
+    STAGE(SMOE_STAGE_EDGE_GEMM, launch_grouped_gemm(pg, s), "edge GEMM");
+    // 8 messages
+    STAGE(SMOE_STAGE_MSG_COMBINE, launch_msg_combine(at<void>(ws, l.proj), adt, at<int32_t>(ws, l.tok_d),
+                                at<int32_t>(ws, l.d_tokrow), N, S, H, at<void>(ws, l.msg), fdt, s),
+             "msg combine");
+    // 9, 10 experts
+    rc = run_experts(b->experts, at<void>(ws, l.msg), at<int32_t>(ws, l.e_off),
+                     at<int32_t>(ws, l.e_rows), at<float>(ws, l.e_roww), N * K,
+                     at<void>(ws, l.act), at<void>(ws, l.y), s);
+    if (rc != SMOE_OK) return rc;
+    // 11 combine + residual + LayerNorm
+    STAGE(SMOE_STAGE_EPILOGUE, launch_epilogue(cur, x0, adt, at<void>(ws, l.y), fdt, at<int32_t>(ws, l.tok_e),
+                             at<float>(ws, l.tok_ew), at<int32_t>(ws, l.e_tokrow), N, K, H,
+                             b->alpha, b->beta, b->ln_w, b->ln_b, b->eps, dst, s),
+             "epilogue");
+    cur = dst;
+  }
+  return SMOE_OK;
+}
+
+SMOE_API int smoe_profile_stages(uint32_t stage_mask, void** events, int capacity) {
+  if (events && capacity < 0) return fail(SMOE_EINVAL, "capacity");
+  g_prof_mask = stage_mask;
+  g_prof_ev = reinterpret_cast<hipEvent_t*>(events);
+  g_prof_cap = events ? capacity : 0;
+  g_prof_n = 0;
+  return SMOE_OK;
+}
+
+SMOE_API int smoe_profile_count(int32_t* stage_of, int capacity) {
+  const int n = g_prof_n;
+  if (stage_of)
+    for (int i = 0; i < n && i < capacity; ++i) stage_of[i] = g_prof_stage[i];
+  g_prof_n = 0;
+  return n;
+}
+
+SMOE_API int smoe_events_create(int n, void** events) {
+  if (n < 0 || (n && !events)) return fail(SMOE_EINVAL, "events");
+  for (int i = 0; i < n; ++i) {
+    hipEvent_t e;
+    if (hipEventCreate(&e) != hipSuccess) return fail(SMOE_EHIP, "hipEventCreate");
+    events[i] = e;
+  }
+  return SMOE_OK;
+}
+
+SMOE_API int smoe_events_destroy(int n, void** events) {
+  for (int i = 0; i < n; ++i)
+    if (events[i]) (void)hipEventDestroy(static_cast<hipEvent_t>(events[i]));
+  return SMOE_OK;
+}
+
+SMOE_API int smoe_events_elapsed(int pairs, void** events, float* ms) {
+  if (pairs < 0 || (pairs && (!events || !ms))) return fail(SMOE_EINVAL, "events");
+  for (int i = 0; i < pairs; ++i) {
+    hipEvent_t b = static_cast<hipEvent_t>(events[2 * i]);
+    hipEvent_t e = static_cast<hipEvent_t>(events[2 * i + 1]);
+    if (hipEventSynchronize(e) != hipSuccess) return fail(SMOE_EHIP, "hipEventSynchronize");
+    if (hipEventElapsedTime(&ms[i], b, e) != hipSuccess) return fail(SMOE_EHIP, "hipEventElapsedTime");
+  }
+  return SMOE_OK;
+}
+
+SMOE_API size_t smoe_router_workspace_bytes(int N, int E) {
+  const size_t n = N > 0 ? N : 1;
+  return align_up(n * E * 4) + 2 * align_up(n * 16 * 4);
+}
+
+SMOE_API int smoe_router_topk(const void* x, int act_dtype, int N, int H, const void* router_w,
+                              const float* loop_bias_row, int E, int K, float* logits,
+                              float* top_w, int32_t* top_idx, void* ws, size_t ws_bytes,
+                              void* stream) {
+  if (act_dtype != SMOE_F32 && act_dtype != SMOE_BF16) return fail(SMOE_EUNSUPPORTED, "dtype");
+  if (N < 0 || H <= 0 || E < 1 || E > 64 || K < 1 || K > E || K > 16)
+    return fail(SMOE_EINVAL, "router shape");
+  if (N == 0) return SMOE_OK;
+  if (!x || !router_w || !top_w || !top_idx || !ws) return fail(SMOE_EINVAL, "null buffer");
+  if (ws_bytes < smoe_router_workspace_bytes(N, E)) return fail(SMOE_ECAPACITY, "workspace");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Bump z;
+  float* lg = logits ? logits : at<float>(ws, z.take(static_cast<size_t>(N) * E * 4));
+  if (logits) z.take(static_cast<size_t>(N) * E * 4);
+  int32_t* te = at<int32_t>(ws, z.take(static_cast<size_t>(N) * 16 * 4));
+  float* tw = at<float>(ws, z.take(static_cast<size_t>(N) * 16 * 4));
+  GemmArgs rg;
+  rg.fmt = act_dtype == SMOE_F32 ? SMOE_F32 : SMOE_BF16;
+  rg.epi = EPI_F32_BIAS;
+  rg.A = x;
+  rg.lda = H;
+  rg.W = router_w;
+  rg.ldw = H;
+  rg.K = H;
+  rg.N_out = E;
+  rg.single_rows = N;
+  rg.out = lg;
+  rg.ldo = E;
+  rg.bias = loop_bias_row;
+  SMOE_TRY(launch_grouped_gemm(rg, s), "router GEMM");
+  SMOE_TRY(launch_route_topk(lg, N, E, K, top_idx, top_w, te, tw, s), "route_topk");
+  return SMOE_OK;
+}
+
+SMOE_API size_t smoe_dispatch_workspace_bytes(int N, int K, int E) {
+  const size_t n = N > 0 ? N : 1;
+  return 2 * align_up(n * K * 4) + align_up(E * 4) + align_up(plan_scratch_bytes(N, E));
+}
+
+SMOE_API int smoe_dispatch_plan(const int32_t* idx, const float* w, int N, int K, int E,
+                                int32_t* counts, int32_t* offsets, int32_t* rows, float* row_w,
+                                int32_t* tok_row, void* ws, size_t ws_bytes, void* stream) {
+  if (N < 0 || K < 1 || E < 1 || E > 256) return fail(SMOE_EINVAL, "plan shape");
+  if (!counts || !offsets) return fail(SMOE_EINVAL, "null buffer");
+  if (N > 0 && (!idx || !w || !rows || !row_w || !tok_row || !ws))
+    return fail(SMOE_EINVAL, "null buffer");
+  if (ws_bytes < smoe_dispatch_workspace_bytes(N, K, E)) return fail(SMOE_ECAPACITY, "workspace");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  Bump z;
+  int32_t* tg = at<int32_t>(ws, z.take(static_cast<size_t>(N) * K * 4));
+  float* tw = at<float>(ws, z.take(static_cast<size_t>(N) * K * 4));
+  int32_t* acnt = at<int32_t>(ws, z.take(E * 4));
+  void* scratch = at<void>(ws, z.take(plan_scratch_bytes(N, E)));
+  SMOE_TRY(launch_merge_slots(idx, w, N, K, E, 1, tg, tw, s), "merge slots");
+  SMOE_TRY(launch_plan(tg, tw, N, K, E, 1, counts, acnt, offsets, rows, row_w, tok_row, scratch, s),
+           "plan");
+  return SMOE_OK;
+}
+
+SMOE_API size_t smoe_expert_delta_workspace_bytes(const smoe_experts* ex, int N, int K) {
+  if (!ex || check_experts(*ex, ex->H) != SMOE_OK) return 0;
+  const size_t n = N > 0 ? N : 1;
+  const size_t es = esize(ffn_dtype_of(*ex));
+  return smoe_dispatch_workspace_bytes(N, K, ex->E) + align_up((ex->E + 1) * 4) +
+         align_up(ex->E * 4) + 3 * align_up(n * K * 4) + align_up(n * K * ex->U * es) +
+         align_up(n * K * ex->H * es);
+}
+
+SMOE_API int smoe_expert_delta(const smoe_experts* ex, const void* msg, const int32_t* idx,
+                               const float* w, int N, int K, void* delta, int out_dtype,
+                               void* ws, size_t ws_bytes, void* stream) {
+  if (!ex) return fail(SMOE_EINVAL, "null experts");
+  int rc = check_experts(*ex, ex->H);
+  if (rc != SMOE_OK) return rc;
+  if (N < 0 || K < 1) return fail(SMOE_EINVAL, "shape");
+  if (out_dtype != SMOE_F32 && out_dtype != SMOE_BF16) return fail(SMOE_EUNSUPPORTED, "out dtype");
+  if (N == 0) return SMOE_OK;
+  if (!msg || !idx || !w || !delta || !ws) return fail(SMOE_EINVAL, "null buffer");
+  if (ws_bytes < smoe_expert_delta_workspace_bytes(ex, N, K))
+    return fail(SMOE_ECAPACITY, "workspace");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int E = ex->E;
+  const size_t es = esize(ffn_dtype_of(*ex));
+  Bump z;
+  void* pws = at<void>(ws, z.take(smoe_dispatch_workspace_bytes(N, K, E)));
+  int32_t* off = at<int32_t>(ws, z.take((E + 1) * 4));
+  int32_t* cnt = at<int32_t>(ws, z.take(E * 4));
+  int32_t* rows = at<int32_t>(ws, z.take(static_cast<size_t>(N) * K * 4));
+  float* roww = at<float>(ws, z.take(static_cast<size_t>(N) * K * 4));
+  int32_t* tokrow = at<int32_t>(ws, z.take(static_cast<size_t>(N) * K * 4));
+  void* act = at<void>(ws, z.take(static_cast<size_t>(N) * K * ex->U * es));
+  void* y = at<void>(ws, z.take(static_cast<size_t>(N) * K * ex->H * es));
+  rc = smoe_dispatch_plan(idx, w, N, K, E, cnt, off, rows, roww, tokrow, pws,
+                          smoe_dispatch_workspace_bytes(N, K, E), stream);
+  if (rc != SMOE_OK) return rc;
+  rc = run_experts(*ex, msg, off, rows, roww, N * K, act, y, s);
+  if (rc != SMOE_OK) return rc;
+  SMOE_TRY(launch_delta_combine(y, ffn_dtype_of(*ex), tokrow, N, K, ex->H, delta, out_dtype, s),
+           "delta combine");
+  return SMOE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,385 @@
+// Grouped GEMMs of the Spider-MoE block on gfx950.
+//
+//   C[row, n] = sum_k A[a_row(row), k] * W_g[n, k]      (row in group g)
+//
+// Rows are the entries of a dispatch plan (tokens sorted by expert or by
+// edge destination; group g owns rows [grp_off[g], grp_off[g+1])).  A rows
+// are gathered through a_rows, W_g is group g's [N_out, K] nn.Linear weight
+// (K contiguous), so both MFMA operands load as 16-byte K-runs.
+//
+// bf16 / fp8 / int4 weights: bf16 MFMA (v_mfma_f32_16x16x32_bf16), fp32
+// accumulate.  fp8-e4m3 codes are widened to bf16 exactly on the way into
+// LDS and their per-output-channel scale is applied in the epilogue; int4
+// nibbles are dequantized (q * group scale, fp32, rounded once to bf16) on
+// the way into LDS.  fp32 weights (fp32 models) use a VALU fp32 tile kernel.
+//
+// Tiles: one workgroup computes BM plan rows x BN output channels; the grid
+// is sized for the worst case (sum of ceil(rows_g / BM) <= ceil(R / BM) + G)
+// and workgroups past the real tile count exit at once, so no host ever
+// reads the routing.  Operands stream through double-buffered LDS with a
+// register prefetch of the next K slice.
+#include "smoe_common.hpp"
+#include "smoe_internal.hpp"
+
+namespace smoe {
+
+// Block-uniform tile lookup: the tile-th BM-row tile in group order.
+__device__ __forceinline__ bool find_tile(const GemmArgs& p, int BM, int tile, int& g, int& m0,
+                                          int& mrows) {
+  if (p.G == 0) {
+    const int t = (p.single_rows + BM - 1) / BM;
+    if (tile >= t) return false;
+    g = 0;
+    m0 = tile * BM;
+    mrows = min(BM, p.single_rows - m0);
+    return true;
+  }
+  int acc = 0;
+  int lo = p.grp_off[0];
+  for (int i = 0; i < p.G; ++i) {
+    const int hi = p.grp_off[i + 1];
+    const int t = (hi - lo + BM - 1) / BM;
+    if (tile < acc + t) {
+      g = i;
+      m0 = lo + (tile - acc) * BM;
+      mrows = min(BM, hi - m0);
+      return true;
+    }
+    acc += t;
+    lo = hi;
+  }
+  return false;
+}
+
+__device__ __forceinline__ void store_out(void* out, int dtype, int64_t idx, float v) {
+  if (dtype == SMOE_F32)
+    reinterpret_cast<float*>(out)[idx] = v;
+  else
+    reinterpret_cast<uint16_t*>(out)[idx] = f2bf(v);
+}
+
+__device__ __forceinline__ float col_scale(const GemmArgs& p, int fmt, int g, int n) {
+  if (fmt == SMOE_FP8_E4M3) return reinterpret_cast<const float*>(p.S)[g * p.s_gstride + n];
+  return 1.0f;
+}
+
+__device__ __forceinline__ float bias_at(const GemmArgs& p, int g, int n) {
+  return p.bias ? p.bias[g * p.bias_gstride + n] : 0.0f;
+}
+
+// Single-element epilogue (all but SwiGLU).
+template <int EPI>
+__device__ __forceinline__ void epi_one(const GemmArgs& p, int fmt, int g, int row, int n,
+                                        float acc) {
+  const int64_t o = static_cast<int64_t>(row) * p.ldo + n;
+  if constexpr (EPI == EPI_F32_BIAS) {
+    reinterpret_cast<float*>(p.out)[o] = acc * col_scale(p, fmt, g, n) + bias_at(p, g, n);
+  } else if constexpr (EPI == EPI_ROWSCALE) {
+    store_out(p.out, p.out_dtype, o, acc * p.row_scale[row]);
+  } else if constexpr (EPI == EPI_GELU) {
+    store_out(p.out, p.out_dtype, o, gelu_erf(acc * col_scale(p, fmt, g, n) + bias_at(p, g, n)));
+  } else if constexpr (EPI == EPI_DOWN) {
+    store_out(p.out, p.out_dtype, o,
+              (acc * col_scale(p, fmt, g, n) + bias_at(p, g, n)) * p.row_scale[row]);
+  }
+}
+
+// SwiGLU pair: interleaved column c (gate, c % 64 < 32) and c + 32 (up).
+__device__ __forceinline__ void epi_swiglu(const GemmArgs& p, int fmt, int g, int row, int c,
+                                           float gate, float up) {
+  const int u = (c >> 6) * 32 + (c & 31);
+  const float gs = gate * col_scale(p, fmt, g, c);
+  const float us = up * col_scale(p, fmt, g, c + 32) + bias_at(p, g, u);
+  store_out(p.out, p.out_dtype, static_cast<int64_t>(row) * p.ldo + u, silu(gs) * us);
+}
+
+// ------------------------------------------------------------------ MFMA ----
+template <int FMT>
+__device__ __forceinline__ u32x4 load_w8(const GemmArgs& p, const void* wrow, int k, int g, int n) {
+  if constexpr (FMT == SMOE_BF16) {
+    return *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(wrow) + k);
+  } else if constexpr (FMT == SMOE_FP8_E4M3) {
+    const u32x2 v = *reinterpret_cast<const u32x2*>(reinterpret_cast<const uint8_t*>(wrow) + k);
+    const u32x2 lo = fp8x4_to_bf16x4(v.x);
+    const u32x2 hi = fp8x4_to_bf16x4(v.y);
+    return u32x4{lo.x, lo.y, hi.x, hi.y};
+  } else {  // INT4
+    const uint32_t v = *reinterpret_cast<const uint32_t*>(reinterpret_cast<const uint8_t*>(wrow) + (k >> 1));
+    const int ng = p.K / p.group_size;
+    const float s = load_scale(p.S, g * p.s_gstride + static_cast<int64_t>(n) * ng + k / p.group_size,
+                               p.s_f16);
+    return int4x8_to_bf16x8(v, s);
+  }
+}
+
+template <int FMT>
+__device__ __forceinline__ const void* w_row_ptr(const GemmArgs& p, int g, int n) {
+  const int64_t e = g * p.w_gstride + static_cast<int64_t>(n) * p.ldw;
+  if constexpr (FMT == SMOE_BF16) return reinterpret_cast<const uint16_t*>(p.W) + e;
+  else if constexpr (FMT == SMOE_FP8_E4M3) return reinterpret_cast<const uint8_t*>(p.W) + e;
+  else return reinterpret_cast<const uint8_t*>(p.W) + (e >> 1);
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int FMT, int EPI>
+__global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(const GemmArgs p) {
+  constexpr int NT = WM * WN * 64;
+  constexpr int TM = BM / WM, TN = BN / WN;
+  constexpr int FM = TM / 16, FN = TN / 16;
+  constexpr int LDK = BK + 8;  // +16 B per row against bank conflicts
+  constexpr int CPR = BK / 8;  // 8-element chunks per row
+  constexpr int A_CH = (BM * CPR + NT - 1) / NT;
+  constexpr int B_CH = (BN * CPR + NT - 1) / NT;
+  static_assert(TM % 16 == 0 && TN % 16 == 0 && BK % 32 == 0, "tile shape");
+  static_assert(EPI != EPI_SWIGLU || TN % 64 == 0, "SwiGLU pairs 32-column blocks");
+
+  __shared__ __attribute__((aligned(16))) uint16_t sA[2][BM * LDK];
+  __shared__ __attribute__((aligned(16))) uint16_t sB[2][BN * LDK];
+
+  int g, m0, mrows;
+  if (!find_tile(p, BM, blockIdx.x, g, m0, mrows)) return;
+  const int n0 = blockIdx.y * BN;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+
+  const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A);
+  const uint16_t* arow[A_CH];
+  int a_lds[A_CH];
+#pragma unroll
+  for (int i = 0; i < A_CH; ++i) {
+    const int c = tid + i * NT;
+    const int r = c / CPR, kc = (c % CPR) * 8;
+    a_lds[i] = (c < BM * CPR) ? r * LDK + kc : -1;
+    arow[i] = nullptr;
+    if (c < BM * CPR && r < mrows) {
+      const int ar = p.a_rows ? p.a_rows[m0 + r] : (m0 + r);
+      arow[i] = A + static_cast<int64_t>(ar) * p.lda + kc;
+    }
+  }
+  const void* wrow[B_CH];
+  int b_lds[B_CH], b_kc[B_CH], b_n[B_CH];
+#pragma unroll
+  for (int i = 0; i < B_CH; ++i) {
+    const int c = tid + i * NT;
+    const int r = c / CPR, kc = (c % CPR) * 8;
+    b_lds[i] = (c < BN * CPR) ? r * LDK + kc : -1;
+    b_kc[i] = kc;
+    b_n[i] = n0 + r;
+    // rows past N_out (a partial last N tile) load zeros and are not stored
+    wrow[i] = (c < BN * CPR && n0 + r < p.N_out) ? w_row_ptr<FMT>(p, g, n0 + r) : nullptr;
+  }
+
+  f32x4 acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  u32x4 ra[A_CH], rb[B_CH];
+  auto gload = [&](int kt) {
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i)
+      ra[i] = arow[i] ? *reinterpret_cast<const u32x4*>(arow[i] + k0) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int i = 0; i < B_CH; ++i)
+      rb[i] = wrow[i] ? load_w8<FMT>(p, wrow[i], k0 + b_kc[i], g, b_n[i]) : u32x4{0u, 0u, 0u, 0u};
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i)
+      if (a_lds[i] >= 0) *reinterpret_cast<u32x4*>(&sA[buf][a_lds[i]]) = ra[i];
+#pragma unroll
+    for (int i = 0; i < B_CH; ++i)
+      if (b_lds[i] >= 0) *reinterpret_cast<u32x4*>(&sB[buf][b_lds[i]]) = rb[i];
+  };
+
+  const int KT = p.K / BK;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < KT; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < KT) gload(kt + 1);
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      bf16x8 af[FM], bfr[FN];
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        af[i] = *reinterpret_cast<const bf16x8*>(
+            &sA[buf][(wm * TM + i * 16 + (lane & 15)) * LDK + ks * 32 + (lane >> 4) * 8]);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        bfr[j] = *reinterpret_cast<const bf16x8*>(
+            &sB[buf][(wn * TN + j * 16 + (lane & 15)) * LDK + ks * 32 + (lane >> 4) * 8]);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < KT) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // C layout of 16x16 MFMA: lane holds rows 4*(lane/16)+r, column lane%16.
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int lr = wm * TM + i * 16 + (lane >> 4) * 4 + r;
+      if (lr >= mrows) continue;
+      const int row = m0 + lr;
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int c = n0 + wn * TN + j * 16 + (lane & 15);
+        if (c >= p.N_out) continue;
+        if constexpr (EPI == EPI_SWIGLU) {
+          if ((j & 3) < 2) epi_swiglu(p, FMT, g, row, c, acc[i][j][r], acc[i][j + 2][r]);
+        } else {
+          epi_one<EPI>(p, FMT, g, row, c, acc[i][j][r]);
+        }
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------------------- fp32 ----
+template <int BM, int BN, int EPI>
+__global__ __launch_bounds__(256) void k_gemm_f32(const GemmArgs p) {
+  constexpr int BK = 16;
+  constexpr int TM = BM / 16, TN = BN / 16;
+  __shared__ float sA[BK][BM + 4];
+  __shared__ float sB[BK][BN + 4];
+  int g, m0, mrows;
+  if (!find_tile(p, BM, blockIdx.x, g, m0, mrows)) return;
+  const int n0 = blockIdx.y * BN;
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+  const float* A = reinterpret_cast<const float*>(p.A);
+  const float* W = reinterpret_cast<const float*>(p.W) + g * p.w_gstride;
+  float acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = 0.f;
+  for (int k0 = 0; k0 < p.K; k0 += BK) {
+    for (int e = tid; e < BM * BK; e += 256) {
+      const int r = e / BK, kk = e % BK;
+      float v = 0.f;
+      if (r < mrows) {
+        const int ar = p.a_rows ? p.a_rows[m0 + r] : (m0 + r);
+        v = A[static_cast<int64_t>(ar) * p.lda + k0 + kk];
+      }
+      sA[kk][r] = v;
+    }
+    for (int e = tid; e < BN * BK; e += 256) {
+      const int r = e / BK, kk = e % BK;
+      sB[kk][r] = (n0 + r < p.N_out) ? W[static_cast<int64_t>(n0 + r) * p.ldw + k0 + kk] : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < BK; ++kk) {
+      float a[TM], b[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) a[i] = sA[kk][ty + 16 * i];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) b[j] = sB[kk][tx + 16 * j];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int lr = ty + 16 * i;
+    if (lr >= mrows) continue;
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+      if (n0 + tx + 16 * j < p.N_out) epi_one<EPI>(p, SMOE_F32, g, m0 + lr, n0 + tx + 16 * j, acc[i][j]);
+  }
+}
+
+// --------------------------------------------------------------- launch ----
+namespace {
+
+int max_tiles(const GemmArgs& a, int BM) {
+  if (a.G == 0) return (a.single_rows + BM - 1) / BM;
+  return (a.max_rows + BM - 1) / BM + a.G;
+}
+
+template <int BM, int BN, int BK, int WM, int WN, int FMT>
+int launch_mfma_fmt(const GemmArgs& a, hipStream_t s) {
+  const dim3 grid(max_tiles(a, BM), (a.N_out + BN - 1) / BN);
+  const dim3 block(WM * WN * 64);
+  if (grid.x == 0) return SMOE_OK;
+  switch (a.epi) {
+    case EPI_F32_BIAS: hipLaunchKernelGGL((k_gemm_mfma<BM, BN, BK, WM, WN, FMT, EPI_F32_BIAS>), grid, block, 0, s, a); break;
+    case EPI_ROWSCALE: hipLaunchKernelGGL((k_gemm_mfma<BM, BN, BK, WM, WN, FMT, EPI_ROWSCALE>), grid, block, 0, s, a); break;
+    case EPI_GELU: hipLaunchKernelGGL((k_gemm_mfma<BM, BN, BK, WM, WN, FMT, EPI_GELU>), grid, block, 0, s, a); break;
+    case EPI_DOWN: hipLaunchKernelGGL((k_gemm_mfma<BM, BN, BK, WM, WN, FMT, EPI_DOWN>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU:
+      if constexpr ((BN / WN) % 64 == 0) {
+        hipLaunchKernelGGL((k_gemm_mfma<BM, BN, BK, WM, WN, FMT, EPI_SWIGLU>), grid, block, 0, s, a);
+        break;
+      }
+      return SMOE_EINVAL;
+    default: return SMOE_EINVAL;
+  }
+  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
+template <int BM, int BN, int BK, int WM, int WN>
+int launch_mfma(const GemmArgs& a, hipStream_t s) {
+  switch (a.fmt) {
+    case SMOE_BF16: return launch_mfma_fmt<BM, BN, BK, WM, WN, SMOE_BF16>(a, s);
+    case SMOE_FP8_E4M3: return launch_mfma_fmt<BM, BN, BK, WM, WN, SMOE_FP8_E4M3>(a, s);
+    case SMOE_INT4: return launch_mfma_fmt<BM, BN, BK, WM, WN, SMOE_INT4>(a, s);
+    default: return SMOE_EUNSUPPORTED;
+  }
+}
+
+template <int BM, int BN>
+int launch_f32_bn(const GemmArgs& a, hipStream_t s) {
+  const dim3 grid(max_tiles(a, BM), (a.N_out + BN - 1) / BN);
+  if (grid.x == 0) return SMOE_OK;
+  switch (a.epi) {
+    case EPI_F32_BIAS: hipLaunchKernelGGL((k_gemm_f32<BM, BN, EPI_F32_BIAS>), grid, dim3(256), 0, s, a); break;
+    case EPI_ROWSCALE: hipLaunchKernelGGL((k_gemm_f32<BM, BN, EPI_ROWSCALE>), grid, dim3(256), 0, s, a); break;
+    case EPI_GELU: hipLaunchKernelGGL((k_gemm_f32<BM, BN, EPI_GELU>), grid, dim3(256), 0, s, a); break;
+    case EPI_DOWN: hipLaunchKernelGGL((k_gemm_f32<BM, BN, EPI_DOWN>), grid, dim3(256), 0, s, a); break;
+    default: return SMOE_EUNSUPPORTED;  // SwiGLU on fp32 experts is not provided
+  }
+  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
+}  // namespace
+
+int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
+  if (a.N_out <= 0 || a.K <= 0) return SMOE_EINVAL;
+  // BN: the whole N range when it is small (router / edge logits: N_out = E),
+  // otherwise 128 (64 for fp32); a partial last N tile is masked.
+  if (a.fmt == SMOE_F32) {
+    if (a.K % 16 || a.epi == EPI_SWIGLU) return a.epi == EPI_SWIGLU ? SMOE_EUNSUPPORTED : SMOE_EINVAL;
+    if (a.N_out <= 16) return launch_f32_bn<64, 16>(a, s);
+    if (a.N_out <= 32) return launch_f32_bn<64, 32>(a, s);
+    return launch_f32_bn<64, 64>(a, s);
+  }
+  if (a.fmt == SMOE_INT4 && (a.group_size <= 0 || a.group_size % 8 || a.K % a.group_size))
+    return SMOE_EINVAL;
+  const int bk = (a.K % 64 == 0) ? 64 : (a.K % 32 == 0 ? 32 : 0);
+  if (!bk) return SMOE_EINVAL;
+  if (a.epi == EPI_SWIGLU && a.N_out % 128) return SMOE_EINVAL;
+  const bool b64 = bk == 64;
+  if (a.N_out <= 16)
+    return b64 ? launch_mfma<128, 16, 64, 4, 1>(a, s) : launch_mfma<128, 16, 32, 4, 1>(a, s);
+  if (a.N_out <= 32)
+    return b64 ? launch_mfma<128, 32, 64, 4, 1>(a, s) : launch_mfma<128, 32, 32, 4, 1>(a, s);
+  if (a.N_out <= 64)
+    return b64 ? launch_mfma<128, 64, 64, 4, 1>(a, s) : launch_mfma<128, 64, 32, 4, 1>(a, s);
+  return b64 ? launch_mfma<128, 128, 64, 2, 2>(a, s) : launch_mfma<128, 128, 32, 2, 2>(a, s);
+}
+
+}  // namespace smoe

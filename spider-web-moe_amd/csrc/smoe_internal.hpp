@@ -1,0 +1,73 @@
+// Host-side launcher interfaces shared by the .hip translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "smoe.h"
+
+namespace smoe {
+
+// Epilogues of the grouped GEMM  C[row, n] = sum_k A[a_row(row), k] * W_g[n, k]
+enum Epi : int {
+  EPI_F32_BIAS = 0,  // out f32 = acc*cs + col_bias[g*bias_gstride + n]           (logits)
+  EPI_ROWSCALE = 1,  // out     = acc * row_scale[row]                            (edge projection)
+  EPI_GELU = 2,      // out     = gelu_erf(acc*cs + bias[g*bias_gstride + n])      (expert up)
+  EPI_SWIGLU = 3,    // out[u]  = silu(gate) * (up + bias[g*bias_gstride + u])     (expert gate/up)
+  EPI_DOWN = 4,      // out     = (acc*cs + bias[g*bias_gstride + n]) * row_scale  (expert down)
+};
+
+struct GemmArgs {
+  int fmt = SMOE_BF16;     // weight format; A is f32 for SMOE_F32, bf16 otherwise
+  int epi = EPI_F32_BIAS;
+  const void* A = nullptr;
+  int lda = 0;                   // elements
+  const int32_t* a_rows = nullptr;  // plan row -> A row; nullptr = identity
+  const void* W = nullptr;
+  int64_t w_gstride = 0;         // elements between groups
+  int ldw = 0;                   // elements between rows of W
+  const void* S = nullptr;       // fp8: f32 [G, N_out]; int4: [G, N_out, K/gs]
+  int64_t s_gstride = 0;
+  int s_f16 = 0;
+  int group_size = 0;            // int4
+  int K = 0, N_out = 0;
+  const int32_t* grp_off = nullptr;  // [G+1]; G == 0 -> one group of single_rows rows
+  int G = 0;
+  int single_rows = 0;
+  int max_rows = 0;              // worst-case total rows (grid sizing)
+  void* out = nullptr;
+  int ldo = 0;
+  int out_dtype = SMOE_F32;      // SMOE_F32 / SMOE_BF16
+  const float* bias = nullptr;
+  int64_t bias_gstride = 0;
+  const float* row_scale = nullptr;
+};
+
+int launch_grouped_gemm(const GemmArgs& a, hipStream_t s);
+
+// ---- routing ----
+int launch_route_topk(const float* logits, int N, int E, int K, int32_t* top_idx, float* top_w,
+                      int32_t* tok_e, float* tok_ew, hipStream_t s);
+int launch_merge_slots(const int32_t* idx, const float* w, int N, int K, int E, int drop_nonpos,
+                       int32_t* tok_g, float* tok_w, hipStream_t s);
+int launch_edge_topm(const float* edge_logit, const int32_t* tok_e, const int32_t* e_tokrow,
+                     int N, int E, int K, int M, int S, int32_t* edge_idx, float* edge_w,
+                     int32_t* tok_d, float* tok_dc, hipStream_t s);
+size_t plan_scratch_bytes(int N, int G);
+int launch_plan(const int32_t* tok_g, const float* tok_w, int N, int S, int G, int drop_nonpos,
+                int32_t* cnt, int32_t* acnt, int32_t* off, int32_t* rows, float* roww,
+                int32_t* tokrow, void* scratch, hipStream_t s);
+int launch_edge_loop_bias(const void* wg, int act_dtype, const float* bg, const float* emb, int E,
+                          int H, int L, int R, float* out, hipStream_t s);
+
+// ---- combine ----
+int launch_msg_combine(const void* proj, int proj_dtype, const int32_t* tok_d,
+                       const int32_t* d_tokrow, int N, int S, int H, void* msg, int msg_dtype,
+                       hipStream_t s);
+int launch_epilogue(const void* h, const void* x0, int act_dtype, const void* y, int y_dtype,
+                    const int32_t* tok_e, const float* tok_ew, const int32_t* e_tokrow, int N,
+                    int K, int H, float alpha, float beta, const float* ln_w, const float* ln_b,
+                    float eps, void* out, hipStream_t s);
+int launch_delta_combine(const void* y, int y_dtype, const int32_t* tok_row, int N, int K, int H,
+                         void* out, int out_dtype, hipStream_t s);
+
+}  // namespace smoe

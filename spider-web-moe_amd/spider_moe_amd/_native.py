@@ -1,0 +1,173 @@
+"""ctypes binding of libsmoe.so (the gfx950 HIP kernels behind include/smoe.h).
+
+torch is imported before the library is opened: PyTorch-ROCm ships its own
+HIP runtime with soname libamdhip64.so.7, and libsmoe.so then binds to that
+already-loaded runtime, so device pointers and streams are shared.  There is
+no fallback: when the library is missing every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must precede loading libsmoe.so, see above)
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libsmoe.so")
+
+# formats / activations / status codes (include/smoe.h)
+F32, BF16, FP8_E4M3, INT4, F16 = 0, 1, 2, 3, 4
+ACT_GELU, ACT_SWIGLU = 0, 1
+STATUS = {0: "ok", 1: "invalid argument", 2: "index out of range", 3: "capacity",
+          -2: "unsupported dtype/format", 4: "HIP runtime error"}
+
+_c_int, _c_float, _vp, _sz = ctypes.c_int, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
+
+
+class SmoeExperts(ctypes.Structure):
+    _fields_ = [("format", _c_int), ("act", _c_int), ("E", _c_int), ("H", _c_int), ("U", _c_int),
+                ("group_size", _c_int), ("scale_dtype", _c_int),
+                ("w_up", _vp), ("w_gate", _vp), ("w_down", _vp), ("s_up", _vp), ("s_down", _vp),
+                ("b_up", _vp), ("b_down", _vp)]
+
+
+class SmoeBlock(ctypes.Structure):
+    _fields_ = [("act_dtype", _c_int), ("H", _c_int), ("E", _c_int), ("K", _c_int),
+                ("M", _c_int), ("L", _c_int), ("R", _c_int),
+                ("router_w", _vp), ("loop_bias", _vp), ("edge_gen_w", _vp),
+                ("edge_loop_bias", _vp), ("edge_value_w", _vp), ("experts", SmoeExperts),
+                ("ln_w", _vp), ("ln_b", _vp), ("alpha", _c_float), ("beta", _c_float),
+                ("eps", _c_float)]
+
+
+_LAYOUT_FIELDS = ["total", "logits", "top_idx", "top_w", "tok_e", "tok_ew", "e_cnt", "e_acnt",
+                  "e_off", "e_rows", "e_roww", "e_tokrow", "edge_logit", "edge_idx", "edge_w",
+                  "tok_d", "tok_dc", "d_cnt", "d_acnt", "d_off", "d_rows", "d_roww", "d_tokrow",
+                  "proj", "msg", "act", "y", "h_tmp", "scratch"]
+
+
+class SmoeWsLayout(ctypes.Structure):
+    _fields_ = [(n, _sz) for n in _LAYOUT_FIELDS] + [("S", _c_int), ("ffn_dtype", _c_int)]
+
+
+# every entry point of include/smoe.h: name -> (restype, argtypes)
+SIGNATURES = {
+    "smoe_abi_version": (_c_int, []),
+    "smoe_backend_name": (ctypes.c_char_p, []),
+    "smoe_backend_caps": (ctypes.c_uint32, []),
+    "smoe_last_error": (ctypes.c_char_p, []),
+    "smoe_block_workspace_bytes": (_sz, [ctypes.POINTER(SmoeBlock), _c_int]),
+    "smoe_block_workspace_layout": (_c_int, [ctypes.POINTER(SmoeBlock), _c_int,
+                                             ctypes.POINTER(SmoeWsLayout)]),
+    "smoe_edge_loop_bias": (_c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp,
+                                     _vp]),
+    "smoe_block_forward": (_c_int, [ctypes.POINTER(SmoeBlock), _vp, _vp, _vp, _c_int, _c_int,
+                                    _c_int, _vp, _sz, _vp]),
+    "smoe_router_workspace_bytes": (_sz, [_c_int, _c_int]),
+    "smoe_router_topk": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int, _c_int, _vp,
+                                  _vp, _vp, _vp, _sz, _vp]),
+    "smoe_dispatch_workspace_bytes": (_sz, [_c_int, _c_int, _c_int]),
+    "smoe_dispatch_plan": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _vp, _vp, _vp, _vp, _vp,
+                                    _vp, _sz, _vp]),
+    "smoe_expert_delta_workspace_bytes": (_sz, [ctypes.POINTER(SmoeExperts), _c_int, _c_int]),
+    "smoe_expert_delta": (_c_int, [ctypes.POINTER(SmoeExperts), _vp, _vp, _vp, _c_int, _c_int,
+                                   _vp, _c_int, _vp, _sz, _vp]),
+    "smoe_profile_stages": (_c_int, [ctypes.c_uint32, ctypes.POINTER(_vp), _c_int]),
+    "smoe_profile_count": (_c_int, [ctypes.POINTER(ctypes.c_int32), _c_int]),
+    "smoe_events_create": (_c_int, [_c_int, ctypes.POINTER(_vp)]),
+    "smoe_events_destroy": (_c_int, [_c_int, ctypes.POINTER(_vp)]),
+    "smoe_events_elapsed": (_c_int, [_c_int, ctypes.POINTER(_vp), ctypes.POINTER(ctypes.c_float)]),
+}
+
+STAGES = ["router_gemm", "route_topk", "expert_plan", "edge_logits", "edge_topm", "dest_plan",
+          "edge_gemm", "msg_combine", "up_gemm", "down_gemm", "epilogue"]
+
+_LIB = None
+
+
+def lib():
+    """The loaded library; raises when it was not built."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python spider-web-moe_amd/build.py` "
+                "(spider_moe_amd has no CPU fallback)")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        if handle.smoe_abi_version() != 1:
+            raise RuntimeError("libsmoe.so ABI version mismatch")
+        _LIB = handle
+    return _LIB
+
+
+class StageTimer:
+    """HIP events around every launch of the selected stages of
+    smoe_block_forward (smoe_profile_stages); durations in ms per stage."""
+
+    def __init__(self, stages=None, capacity: int = 8192):
+        self.cap = capacity
+        self.ev = (_vp * (2 * capacity))()
+        check(lib().smoe_events_create(2 * capacity, self.ev), "smoe_events_create")
+        ids = range(len(STAGES)) if stages is None else [STAGES.index(s) for s in stages]
+        self.mask = sum(1 << i for i in ids)
+
+    def start(self):
+        check(lib().smoe_profile_stages(self.mask, self.ev, self.cap), "smoe_profile_stages")
+
+    def stop(self) -> dict:
+        torch.cuda.synchronize()
+        stage_of = (ctypes.c_int32 * self.cap)()
+        n = lib().smoe_profile_count(stage_of, self.cap)
+        check(lib().smoe_profile_stages(0, None, 0), "smoe_profile_stages")
+        ms = (ctypes.c_float * max(n, 1))()
+        check(lib().smoe_events_elapsed(n, self.ev, ms), "smoe_events_elapsed")
+        out: dict = {}
+        for i in range(n):
+            out.setdefault(STAGES[stage_of[i]], []).append(ms[i])
+        return out
+
+    def close(self):
+        lib().smoe_events_destroy(2 * self.cap, self.ev)
+
+
+def check(rc: int, fn: str) -> None:
+    """Raise RuntimeError("<fn> failed: rc") like the reference's ctypes
+    wrappers (kernels/python/spider_native.py:224-225)."""
+    if rc != 0:
+        msg = lib().smoe_last_error().decode(errors="replace")
+        raise RuntimeError(f"{fn} failed: rc={rc} ({STATUS.get(rc, '?')}): {msg}")
+
+
+def ptr(t) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_gpu(*tensors) -> torch.device:
+    """All tensors on one ROCm GPU, else raise (no CPU fallback)."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise RuntimeError("spider_moe_amd runs on a ROCm GPU only; got a tensor on "
+                               f"{t.device} (move the module and inputs to the GPU)")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise RuntimeError("all tensors must be on the same GPU")
+    return dev
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float32:
+        return F32
+    if dt == torch.bfloat16:
+        return BF16
+    raise RuntimeError(f"unsupported activation dtype {dt} (float32 or bfloat16)")
