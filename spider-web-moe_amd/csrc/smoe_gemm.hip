@@ -245,6 +245,194 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(const GemmArgs p) {
   }
 }
 
+// ------------------------------------------------------- MFMA, big tile ----
+// 256 x 256 x 64 block tile, 4 waves in a 2 x 2 grid, 128 x 128 per wave
+// (8 x 8 MFMA 16x16x32 tiles, 256 fp32 accumulators per lane).  Operands are
+// fed transposed — a = weight rows (output channels), b = plan rows — so a
+// lane's accumulator holds 4 consecutive output channels of one row and
+// stores them as one vector; SwiGLU's gate and up channels (32 apart) land
+// in the same lane.  LDS rows are 128 B (64 bf16) with the 16-byte chunks
+// XOR-swizzled by (row >> 1) & 7, so the 16 lanes of a ds_read_b128 phase
+// hit 16 distinct bank groups without padding.  Operands are staged global ->
+// VGPR -> LDS with one K slice of register prefetch and two LDS buffers.
+//
+// Tile order: the tile grid (real count, from the plan) is split into 8
+// contiguous ranges, one per XCD (workgroup ids are dealt to XCDs round
+// robin), and each range is walked in super-rows of GM m-tiles x all n-tiles
+// so the super-row's A tiles stay in that XCD's L2 while weight tiles stream.
+__device__ __forceinline__ int swz(int row, int chunk) {  // byte offset in a 128 B-row tile
+  return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4);
+}
+
+template <int BM>
+__device__ __forceinline__ int count_m_tiles(const GemmArgs& p) {
+  if (p.G == 0) return (p.single_rows + BM - 1) / BM;
+  int t = 0;
+  for (int i = 0; i < p.G; ++i) t += (p.grp_off[i + 1] - p.grp_off[i] + BM - 1) / BM;
+  return t;
+}
+
+template <int BM, int BN, int GM>
+__device__ __forceinline__ bool big_tile(const GemmArgs& p, int& g, int& m0, int& mrows, int& n0) {
+  const int tn_count = (p.N_out + BN - 1) / BN;
+  const int tm_count = count_m_tiles<BM>(p);
+  const int T = tm_count * tn_count;
+  const int bid = blockIdx.x;
+  if (bid >= T) return false;
+  const int x = bid & 7, local = bid >> 3;
+  const int base = T >> 3, rem = T & 7;
+  const int logical = x * base + min(x, rem) + local;
+  const int grp = logical / (GM * tn_count);
+  const int first_m = grp * GM;
+  const int gsize = min(GM, tm_count - first_m);
+  const int in = logical - grp * GM * tn_count;
+  const int tm = first_m + in % gsize;
+  n0 = (in / gsize) * BN;
+  return find_tile(p, BM, tm, g, m0, mrows);
+}
+
+template <int EPI>
+__device__ __forceinline__ void store4(const GemmArgs& p, int fmt, int g, int row, int n, f32x4 v) {
+  // 4 consecutive channels n..n+3 of one row
+  const int64_t o = static_cast<int64_t>(row) * p.ldo + n;
+  float r[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float a = v[i] * col_scale(p, fmt, g, n + i);
+    if constexpr (EPI == EPI_F32_BIAS) r[i] = a + bias_at(p, g, n + i);
+    else if constexpr (EPI == EPI_ROWSCALE) r[i] = v[i] * p.row_scale[row];
+    else if constexpr (EPI == EPI_GELU) r[i] = gelu_erf(a + bias_at(p, g, n + i));
+    else r[i] = (a + bias_at(p, g, n + i)) * p.row_scale[row];  // EPI_DOWN
+  }
+  if (EPI == EPI_F32_BIAS || p.out_dtype == SMOE_F32) {
+    *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + o) = f32x4{r[0], r[1], r[2], r[3]};
+  } else {
+    *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + o) =
+        u32x2{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3])};
+  }
+}
+
+template <int BM, int BN, int GM, int EPI>
+__global__ __launch_bounds__(256) void k_gemm_big(const GemmArgs p) {
+  constexpr int BK = 64;
+  constexpr int TM = BM / 2, TN = BN / 2;     // wave tile (rows x channels)
+  constexpr int FM = TM / 16, FN = TN / 16;
+  constexpr int A_CH = BM * 8 / 256;          // 16 B chunks per thread per stage
+  constexpr int B_CH = BN * 8 / 256;
+  static_assert(EPI != EPI_SWIGLU || TN % 64 == 0, "SwiGLU pairs 32-channel blocks");
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * (BM + BN) * 128];
+  uint8_t* const sA0 = smem;
+  uint8_t* const sB0 = smem + 2 * BM * 128;
+
+  int g, m0, mrows, n0;
+  if (!big_tile<BM, BN, GM>(p, g, m0, mrows, n0)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // global sources and LDS destinations of this thread's chunks
+  const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A);
+  const uint16_t* W = reinterpret_cast<const uint16_t*>(p.W) + g * p.w_gstride;
+  const uint16_t* asrc[A_CH];
+  const uint16_t* bsrc[B_CH];
+  int adst[A_CH], bdst[B_CH];
+#pragma unroll
+  for (int i = 0; i < A_CH; ++i) {
+    const int c = tid + i * 256, r = c >> 3, ch = c & 7;
+    // rows past the group end read a valid row; their outputs are never stored
+    const int rr = r < mrows ? r : 0;
+    const int ar = p.a_rows ? p.a_rows[m0 + rr] : (m0 + rr);
+    asrc[i] = A + static_cast<int64_t>(ar) * p.lda + ch * 8;
+    adst[i] = swz(r, ch);
+  }
+#pragma unroll
+  for (int i = 0; i < B_CH; ++i) {
+    const int c = tid + i * 256, r = c >> 3, ch = c & 7;
+    const int n = n0 + r < p.N_out ? n0 + r : n0;
+    bsrc[i] = W + static_cast<int64_t>(n) * p.ldw + ch * 8;
+    bdst[i] = swz(r, ch);
+  }
+
+  f32x4 acc[FN][FM];
+#pragma unroll
+  for (int j = 0; j < FN; ++j)
+#pragma unroll
+    for (int i = 0; i < FM; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  u32x4 ra[A_CH], rb[B_CH];
+  auto gload = [&](int kt) {
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) ra[i] = *reinterpret_cast<const u32x4*>(asrc[i] + k0);
+#pragma unroll
+    for (int i = 0; i < B_CH; ++i) rb[i] = *reinterpret_cast<const u32x4*>(bsrc[i] + k0);
+  };
+  auto sstore = [&](int buf) {
+    uint8_t* sa = sA0 + buf * BM * 128;
+    uint8_t* sb = sB0 + buf * BN * 128;
+#pragma unroll
+    for (int i = 0; i < A_CH; ++i) *reinterpret_cast<u32x4*>(sa + adst[i]) = ra[i];
+#pragma unroll
+    for (int i = 0; i < B_CH; ++i) *reinterpret_cast<u32x4*>(sb + bdst[i]) = rb[i];
+  };
+
+  // fragment read offsets: row = base + 16 x + (lane & 15), chunk = 4 ks + lane / 16
+  const int fr = lane & 15, fc = lane >> 4;
+  const int KT = p.K / BK;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  for (int kt = 0; kt < KT; ++kt) {
+    const int buf = kt & 1;
+    if (kt + 1 < KT) gload(kt + 1);
+    const uint8_t* sa = sA0 + buf * BM * 128;
+    const uint8_t* sb = sB0 + buf * BN * 128;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      bf16x8 wf[FN], af[FM];
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        wf[j] = *reinterpret_cast<const bf16x8*>(sb + swz(wn * TN + j * 16 + fr, ks * 4 + fc));
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        af[i] = *reinterpret_cast<const bf16x8*>(sa + swz(wm * TM + i * 16 + fr, ks * 4 + fc));
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+          acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[j][i], 0, 0, 0);
+    }
+    if (kt + 1 < KT) sstore(buf ^ 1);
+    __syncthreads();
+  }
+
+  // lane holds channels n0 + wn*TN + 16 j + 4 (lane/16) + {0..3} of row wm*TM + 16 i + lane%16
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int lr = wm * TM + i * 16 + fr;
+    if (lr >= mrows) continue;
+    const int row = m0 + lr;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int c = n0 + wn * TN + j * 16 + fc * 4;
+      if (c >= p.N_out) continue;
+      if constexpr (EPI == EPI_SWIGLU) {
+        if ((j & 3) < 2) {
+          const int u = (c >> 6) * 32 + (c & 31);
+          float r[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            r[q] = silu(acc[j][i][q]) * (acc[j + 2][i][q] + bias_at(p, g, u + q));
+          *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) +
+                                    static_cast<int64_t>(row) * p.ldo + u) =
+              u32x2{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3])};
+        }
+      } else {
+        store4<EPI>(p, SMOE_BF16, g, row, c, acc[j][i]);
+      }
+    }
+  }
+}
+
 // ----------------------------------------------------------------- fp32 ----
 template <int BM, int BN, int EPI>
 __global__ __launch_bounds__(256) void k_gemm_f32(const GemmArgs p) {
@@ -341,6 +529,22 @@ int launch_mfma(const GemmArgs& a, hipStream_t s) {
   }
 }
 
+template <int BM, int BN, int GM>
+int launch_big(const GemmArgs& a, hipStream_t s) {
+  const int tiles = max_tiles(a, BM) * ((a.N_out + BN - 1) / BN);
+  if (tiles == 0) return SMOE_OK;
+  const dim3 grid(tiles), block(256);
+  switch (a.epi) {
+    case EPI_F32_BIAS: hipLaunchKernelGGL((k_gemm_big<BM, BN, GM, EPI_F32_BIAS>), grid, block, 0, s, a); break;
+    case EPI_ROWSCALE: hipLaunchKernelGGL((k_gemm_big<BM, BN, GM, EPI_ROWSCALE>), grid, block, 0, s, a); break;
+    case EPI_GELU: hipLaunchKernelGGL((k_gemm_big<BM, BN, GM, EPI_GELU>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU: hipLaunchKernelGGL((k_gemm_big<BM, BN, GM, EPI_SWIGLU>), grid, block, 0, s, a); break;
+    case EPI_DOWN: hipLaunchKernelGGL((k_gemm_big<BM, BN, GM, EPI_DOWN>), grid, block, 0, s, a); break;
+    default: return SMOE_EINVAL;
+  }
+  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
 template <int BM, int BN>
 int launch_f32_bn(const GemmArgs& a, hipStream_t s) {
   const dim3 grid(max_tiles(a, BM), (a.N_out + BN - 1) / BN);
@@ -372,6 +576,10 @@ int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
   const int bk = (a.K % 64 == 0) ? 64 : (a.K % 32 == 0 ? 32 : 0);
   if (!bk) return SMOE_EINVAL;
   if (a.epi == EPI_SWIGLU && a.N_out % 128) return SMOE_EINVAL;
+  // large bf16 problems: 256 x 256 tiles (N_out and K multiples of the tile)
+  if (a.fmt == SMOE_BF16 && bk == 64 && a.N_out % 256 == 0 && a.ldw % 8 == 0 && a.lda % 8 == 0 &&
+      (a.G == 0 ? a.single_rows : a.max_rows / (a.G > 0 ? a.G : 1)) >= 256)
+    return launch_big<256, 256, 4>(a, s);
   const bool b64 = bk == 64;
   if (a.N_out <= 16)
     return b64 ? launch_mfma<128, 16, 64, 4, 1>(a, s) : launch_mfma<128, 16, 32, 4, 1>(a, s);

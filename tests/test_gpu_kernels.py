@@ -255,3 +255,40 @@ def test_invalid_arguments_are_rejected():
     rc = n8.lib().smoe_router_topk(None, n8.BF16, 4, 64, None, None, 4, 5, None, None, None, None,
                                    0, None)
     assert rc == 1
+
+
+@pytest.mark.parametrize("act", ["gelu", "swiglu"])
+def test_large_bf16_experts_ragged_groups(act):
+    """Shapes that take the 256 x 256 tile path (N_out % 256 == 0, >= 256 rows
+    per expert on average) with skewed routing: empty experts, single-row
+    experts and experts spanning several tiles."""
+    from spider_moe_amd.quant import interleave_gate_up
+    n8 = nat()
+    say("large bf16 experts", act)
+    n, h, u, e, k = 2304, 512, 768, 8, 2
+    g = torch.Generator().manual_seed(21)
+    # skew: experts 0,1 take most tokens, 5 gets one token, 6 and 7 none
+    p = torch.tensor([0.45, 0.3, 0.12, 0.08, 0.05, 0.0, 0.0, 0.0])
+    idx = torch.multinomial(p.expand(n, e), k, replacement=False, generator=g)
+    idx[7, 1] = 5
+    w = torch.rand(n, k, generator=g)
+    msg = torch.randn(n, h, generator=g).to(torch.bfloat16)
+    nup = 2 * u if act == "swiglu" else u
+    wu = (torch.randn(e, nup, h, generator=g) * 0.04).to(torch.bfloat16)
+    wd = (torch.randn(e, h, u, generator=g) * 0.04).to(torch.bfloat16)
+    bu = torch.randn(e, u, generator=g) * 0.1 if act == "gelu" else None
+    bd = torch.randn(e, h, generator=g) * 0.1 if act == "gelu" else None
+    if act == "swiglu":
+        ref = _oracle_delta(msg.float(), idx, w, wu.float()[:, u:], None, wd.float(), None,
+                            w_gate=wu.float()[:, :u])
+        wu_dev = interleave_gate_up(wu[:, :u], wu[:, u:]).to(dev)
+    else:
+        ref = _oracle_delta(msg.float(), idx, w, wu.float(), bu, wd.float(), bd)
+        wu_dev = wu.to(dev)
+    wd_dev = wd.contiguous().to(dev)
+    bu_d = bu.to(dev) if bu is not None else None
+    bd_d = bd.to(dev) if bd is not None else None
+    ex = _experts_struct(n8, n8.BF16, n8.ACT_SWIGLU if act == "swiglu" else n8.ACT_GELU, e, h, u,
+                         wu_dev, wd_dev, b_up=bu_d, b_down=bd_d)
+    got = _run_delta(n8, ex, msg.to(dev), idx.to(torch.int32).to(dev), w.to(dev))
+    torch.testing.assert_close(got, ref, rtol=1e-2, atol=1e-2)
