@@ -94,9 +94,25 @@ __device__ __forceinline__ void wave_argmax(float& v, int& i) {
   }
 }
 
-__device__ __forceinline__ float gelu_erf(float x) {  // nn.GELU() default
-  return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
+// erf by Abramowitz & Stegun, Handbook of Mathematical Functions, eq. 7.1.26:
+// erf(a) = 1 - (a1 t + a2 t^2 + a3 t^3 + a4 t^4 + a5 t^5) exp(-a^2),
+// t = 1 / (1 + p a), a >= 0, |error| <= 1.5e-7 (far below the bf16 rounding of
+// the values it feeds).
+__device__ __forceinline__ float erf_as(float x) {
+  const float a = fabsf(x);
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, a, 1.0f));
+  float y = fmaf(1.061405429f, t, -1.453152027f);
+  y = fmaf(y, t, 1.421413741f);
+  y = fmaf(y, t, -0.284496736f);
+  y = fmaf(y, t, 0.254829592f);
+  y = 1.0f - y * t * __expf(-a * a);
+  return copysignf(y, x);
 }
-__device__ __forceinline__ float silu(float x) { return x / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float gelu_erf(float x) {  // nn.GELU() default (exact-erf GELU)
+  return 0.5f * x * (1.0f + erf_as(x * 0.70710678118654752f));
+}
+__device__ __forceinline__ float silu(float x) {
+  return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));
+}
 
 }  // namespace smoe

@@ -433,6 +433,196 @@ __global__ __launch_bounds__(256) void k_gemm_big(const GemmArgs p) {
   }
 }
 
+// ------------------------------------------------- MFMA, LDS-DMA ring ----
+// 256 x BN block tile (BN = 256 or 128), 4 waves in a 2 x 2 grid, wave tile
+// 128 x BN/2.  K advances 32 per stage; operands go global -> LDS directly
+// with global_load_lds_dwordx4 (no VGPR staging) into an NS-stage LDS ring,
+// loads for stage s+NS-1 are issued while stage s computes, and each
+// iteration waits only for the loads of the stage it needs next (explicit
+// vmcnt — the in-order VMEM counter — then one s_barrier).  The fragments of
+// stage s+1 are read into a second register set while stage s's MFMAs run.
+//
+// LDS rows are 64 B (32 bf16 = 4 chunks of 16 B), chunk c of row r stored at
+// chunk c ^ ((r >> 1) & 3).  Measured on gfx950, fragment reads (16 rows x one
+// chunk per ds_read_b128) run at ~226 B/clk/CU with this swizzle against
+// ~118 with c ^ ((r >> 2) & 3) or no swizzle.  A DMA instruction writes 1 KB
+// lane-linearly (16 rows x 64 B): lane i covers row i/4, physical chunk i%4,
+// and loads the logical chunk that the swizzle places there.
+__device__ __forceinline__ int swz32(int row, int chunk) {
+  return row * 64 + ((chunk ^ ((row >> 1) & 3)) << 4);
+}
+
+// s_waitcnt vmcnt(n) (gfx9 encoding; expcnt / lgkmcnt left at "no wait")
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (0xF << 8));
+}
+
+typedef __attribute__((address_space(3))) void* lds_vptr;
+typedef __attribute__((address_space(1))) void* gbl_vptr;
+
+template <int BN, int NS, int GM, int EPI>
+__global__ __launch_bounds__(256) void k_gemm_ring(const GemmArgs p) {
+  constexpr int BM = 256;
+  constexpr int TM = BM / 2, TN = BN / 2;
+  constexpr int FM = TM / 16, FN = TN / 16;
+  constexpr int A_BYTES = BM * 64, B_BYTES = BN * 64, STAGE = A_BYTES + B_BYTES;
+  constexpr int A_LD = BM / 16 / 4, B_LD = BN / 16 / 4;  // DMA instructions per wave per stage
+  constexpr int LD = A_LD + B_LD;
+  static_assert(EPI != EPI_SWIGLU || TN % 64 == 0, "SwiGLU pairs 32-channel blocks");
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE];
+
+  int g, m0, mrows, n0;
+  if (!big_tile<BM, BN, GM>(p, g, m0, mrows, n0)) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // DMA sources: instruction j of this wave covers rows 16 (4 j + wave) ..
+  const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A);
+  const uint16_t* W = reinterpret_cast<const uint16_t*>(p.W) + g * p.w_gstride;
+  const uint16_t* asrc[A_LD];
+  const uint16_t* bsrc[B_LD];
+  {
+    const int pr = lane >> 2, pc = lane & 3;
+#pragma unroll
+    for (int j = 0; j < A_LD; ++j) {
+      const int r = (4 * j + wave) * 16 + pr;
+      const int rr = r < mrows ? r : 0;  // rows past the group end: valid data, never stored
+      const int ar = p.a_rows ? p.a_rows[m0 + rr] : (m0 + rr);
+      asrc[j] = A + static_cast<int64_t>(ar) * p.lda + ((pc ^ ((r >> 1) & 3)) << 3);
+    }
+#pragma unroll
+    for (int j = 0; j < B_LD; ++j) {
+      const int r = (4 * j + wave) * 16 + pr;
+      const int n = n0 + r < p.N_out ? n0 + r : n0;
+      bsrc[j] = W + static_cast<int64_t>(n) * p.ldw + ((pc ^ ((r >> 1) & 3)) << 3);
+    }
+  }
+  auto issue = [&](int stage) {  // DMA of K slice `stage` into ring slot stage % NS
+    uint8_t* base = ring + (stage % NS) * STAGE;
+    const int k0 = stage * 32;
+#pragma unroll
+    for (int j = 0; j < A_LD; ++j)
+      __builtin_amdgcn_global_load_lds((gbl_vptr)(asrc[j] + k0),
+                                       (lds_vptr)(base + (4 * j + wave) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int j = 0; j < B_LD; ++j)
+      __builtin_amdgcn_global_load_lds((gbl_vptr)(bsrc[j] + k0),
+                                       (lds_vptr)(base + A_BYTES + (4 * j + wave) * 1024), 16, 0, 0);
+  };
+
+  const int fr = lane & 15, fc = lane >> 4;
+  // two fragment sets, addressed statically (the stage loop is unrolled by 2)
+  bf16x8 wf0[FN], af0[FM], wf1[FN], af1[FM];
+  auto read_frags = [&](int stage, bf16x8 (&wf)[FN], bf16x8 (&af)[FM]) {
+    const uint8_t* sa = ring + (stage % NS) * STAGE;
+    const uint8_t* sb = sa + A_BYTES;
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      wf[j] = *reinterpret_cast<const bf16x8*>(sb + swz32(wn * TN + j * 16 + fr, fc));
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      af[i] = *reinterpret_cast<const bf16x8*>(sa + swz32(wm * TM + i * 16 + fr, fc));
+  };
+
+  f32x4 acc[FN][FM];
+#pragma unroll
+  for (int j = 0; j < FN; ++j)
+#pragma unroll
+    for (int i = 0; i < FM; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int KT = p.K / 32;
+  // one stage: make stage s+1 resident and read its fragments into the
+  // other set, then the MFMAs of stage s
+  auto step = [&](int s, bf16x8 (&wc)[FN], bf16x8 (&ac)[FM], bf16x8 (&wn_)[FN],
+                  bf16x8 (&an)[FM]) {
+    if (s + 1 < KT) {
+      // stage s+1 landed (stages s+2 .. s+NS-2 may still be in flight)
+      if (s + NS - 2 < KT) wait_vmcnt<(NS - 3) * LD>();
+      else wait_vmcnt<0>();
+      __builtin_amdgcn_s_barrier();
+      if (s + NS - 1 < KT) issue(s + NS - 1);  // into the slot stage s-1 used
+      read_frags(s + 1, wn_, an);
+    }
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wc[j], ac[i], acc[j][i], 0, 0, 0);
+  };
+
+  // prologue: stages 0 .. NS-2 in flight, stage 0 landed everywhere
+#pragma unroll
+  for (int st = 0; st < NS - 1; ++st)
+    if (st < KT) issue(st);
+  if (KT >= NS - 1) wait_vmcnt<(NS - 2) * LD>();
+  else wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();
+  read_frags(0, wf0, af0);
+  // KT is even (K % 64 == 0, checked by the launcher): no conditional step,
+  // so the accumulators stay in AGPRs across the loop
+  for (int s = 0; s < KT; s += 2) {
+    step(s, wf0, af0, wf1, af1);
+    step(s + 1, wf1, af1, wf0, af0);
+  }
+
+  // ---- epilogue: math in registers, bf16 tile staged in the (idle) LDS
+  // ring, then coalesced 16-byte row stores.  Staging layout: row r, 16-byte
+  // chunk c at chunk c ^ (r & 15) (rows of OW bf16, no padding; r & 7 for
+  // 8-chunk rows).
+  constexpr int OW = (EPI == EPI_SWIGLU) ? BN / 2 : BN;  // output columns of the tile
+  static_assert(BM * OW * 2 <= NS * STAGE, "output staging fits in the ring");
+  constexpr int SWM = (OW / 8 >= 16 ? 16 : OW / 8) - 1;  // chunk swizzle mask
+  __syncthreads();  // every wave is done with the ring (no DMA is outstanding here)
+  uint16_t* stg = reinterpret_cast<uint16_t*>(ring);
+  auto stg_at = [&](int r, int col) {  // col: multiple of 4
+    return stg + r * OW + ((((col >> 3) ^ (r & SWM)) << 3) | (col & 7));
+  };
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int lr = wm * TM + i * 16 + fr;
+    const bool live = lr < mrows;
+    const int row = m0 + (live ? lr : 0);
+    float rs = 0.f;
+    if constexpr (EPI == EPI_ROWSCALE || EPI == EPI_DOWN) rs = live ? p.row_scale[row] : 0.f;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int cl = wn * TN + j * 16 + fc * 4;  // channel within the tile
+      const int c = n0 + cl;
+      float r[4];
+      if constexpr (EPI == EPI_SWIGLU) {
+        if ((j & 3) >= 2) continue;
+        const int ul = (cl >> 6) * 32 + (cl & 31);
+        const int u = (n0 >> 1) + ul;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) r[q] = silu(acc[j][i][q]) * (acc[j + 2][i][q] + bias_at(p, g, u + q));
+        *reinterpret_cast<u32x2*>(stg_at(lr, ul)) = u32x2{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3])};
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float a = acc[j][i][q];
+          if constexpr (EPI == EPI_ROWSCALE) r[q] = a * rs;
+          else if constexpr (EPI == EPI_GELU) r[q] = gelu_erf(a + bias_at(p, g, c + q));
+          else if constexpr (EPI == EPI_DOWN) r[q] = (a + bias_at(p, g, c + q)) * rs;
+          else r[q] = a + bias_at(p, g, c + q);
+        }
+        *reinterpret_cast<u32x2*>(stg_at(lr, cl)) = u32x2{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3])};
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int CPR_OUT = OW / 8;  // 16-byte chunks per output row
+  const int ncol0 = (EPI == EPI_SWIGLU) ? (n0 >> 1) : n0;
+  uint16_t* out = reinterpret_cast<uint16_t*>(p.out);
+  for (int q = tid; q < BM * CPR_OUT; q += 256) {
+    const int r = q / CPR_OUT, cc = (q % CPR_OUT) * 8;
+    if (r < mrows)
+      *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(m0 + r) * p.ldo + ncol0 + cc) =
+          *reinterpret_cast<const u32x4*>(stg_at(r, cc));
+  }
+}
+
 // ----------------------------------------------------------------- fp32 ----
 template <int BM, int BN, int EPI>
 __global__ __launch_bounds__(256) void k_gemm_f32(const GemmArgs p) {
@@ -545,6 +735,22 @@ int launch_big(const GemmArgs& a, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 
+template <int BN, int NS, int GM>
+int launch_ring(const GemmArgs& a, hipStream_t s) {
+  const int tiles = max_tiles(a, 256) * ((a.N_out + BN - 1) / BN);
+  if (tiles == 0) return SMOE_OK;
+  const dim3 grid(tiles), block(256);
+  switch (a.epi) {
+    case EPI_F32_BIAS: hipLaunchKernelGGL((k_gemm_ring<BN, NS, GM, EPI_F32_BIAS>), grid, block, 0, s, a); break;
+    case EPI_ROWSCALE: hipLaunchKernelGGL((k_gemm_ring<BN, NS, GM, EPI_ROWSCALE>), grid, block, 0, s, a); break;
+    case EPI_GELU: hipLaunchKernelGGL((k_gemm_ring<BN, NS, GM, EPI_GELU>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU: hipLaunchKernelGGL((k_gemm_ring<BN, NS, GM, EPI_SWIGLU>), grid, block, 0, s, a); break;
+    case EPI_DOWN: hipLaunchKernelGGL((k_gemm_ring<BN, NS, GM, EPI_DOWN>), grid, block, 0, s, a); break;
+    default: return SMOE_EINVAL;
+  }
+  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
 template <int BM, int BN>
 int launch_f32_bn(const GemmArgs& a, hipStream_t s) {
   const dim3 grid(max_tiles(a, BM), (a.N_out + BN - 1) / BN);
@@ -563,6 +769,10 @@ int launch_f32_bn(const GemmArgs& a, hipStream_t s) {
 
 int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
   if (a.N_out <= 0 || a.K <= 0) return SMOE_EINVAL;
+  // pointers every launched workgroup dereferences
+  if (!a.A || !a.W || !a.out || (a.G > 0 && !a.grp_off)) return SMOE_EINVAL;
+  if ((a.epi == EPI_ROWSCALE || a.epi == EPI_DOWN) && !a.row_scale) return SMOE_EINVAL;
+  if ((a.fmt == SMOE_FP8_E4M3 || a.fmt == SMOE_INT4) && !a.S) return SMOE_EINVAL;
   // BN: the whole N range when it is small (router / edge logits: N_out = E),
   // otherwise 128 (64 for fp32); a partial last N tile is masked.
   if (a.fmt == SMOE_F32) {
@@ -577,9 +787,12 @@ int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
   if (!bk) return SMOE_EINVAL;
   if (a.epi == EPI_SWIGLU && a.N_out % 128) return SMOE_EINVAL;
   // large bf16 problems: 256 x 256 tiles (N_out and K multiples of the tile)
-  if (a.fmt == SMOE_BF16 && bk == 64 && a.N_out % 256 == 0 && a.ldw % 8 == 0 && a.lda % 8 == 0 &&
-      (a.G == 0 ? a.single_rows : a.max_rows / (a.G > 0 ? a.G : 1)) >= 256)
-    return launch_big<256, 256, 4>(a, s);
+  if (a.fmt == SMOE_BF16 && a.out_dtype == SMOE_BF16 && a.epi != EPI_F32_BIAS && a.K % 64 == 0 &&
+      a.ldw % 8 == 0 && a.lda % 8 == 0 && a.ldo % 8 == 0 &&
+      (a.G == 0 ? a.single_rows : a.max_rows / (a.G > 0 ? a.G : 1)) >= 256) {
+    if (a.N_out % 256 == 0) return launch_ring<256, 4, 4>(a, s);
+    if (a.N_out % 128 == 0) return launch_ring<128, 6, 4>(a, s);
+  }
   const bool b64 = bk == 64;
   if (a.N_out <= 16)
     return b64 ? launch_mfma<128, 16, 64, 4, 1>(a, s) : launch_mfma<128, 16, 32, 4, 1>(a, s);
