@@ -186,7 +186,10 @@ def message_grouped(h, w: BlockWeights, coef: torch.Tensor) -> torch.Tensor:
 
 
 # ------------------------------------------------------------ experts ----
-def _expert_ffn(x, w: BlockWeights, e: int, act: str = "auto"):
+def _expert_ffn(x, w: BlockWeights, e: int, act: str = "auto", hidden_bf16: bool = False):
+    """hidden_bf16 rounds the FFN hidden activation to bf16 before the down
+    projection, the storage the device path gives it (the reference keeps it
+    in the weights' dtype, fp32 here)."""
     act = w.act if act == "auto" else act
     if act == "swiglu":
         gate = x @ w.w_gate[e].t()
@@ -199,13 +202,15 @@ def _expert_ffn(x, w: BlockWeights, e: int, act: str = "auto"):
         if w.b_up is not None:
             up = up + w.b_up[e]
         hid = F.gelu(up) if act == "gelu" else F.gelu(up, approximate="tanh")
+    if hidden_bf16:
+        hid = round_bf16(hid)
     out = hid @ w.w_down[e].t()
     if w.b_down is not None:
         out = out + w.b_down[e]
     return out
 
 
-def expert_delta(msg, top_i, top_w, w: BlockWeights, act: str = "auto"):
+def expert_delta(msg, top_i, top_w, w: BlockWeights, act: str = "auto", hidden_bf16: bool = False):
     """sparse_experts.py:45-65: for each expert, merged token weight over the
     k slots, drop weight <= 0, FFN on the active tokens, weighted add."""
     n, hid = msg.shape
@@ -218,7 +223,7 @@ def expert_delta(msg, top_i, top_w, w: BlockWeights, act: str = "auto"):
         active = tw > 0
         if not bool(active.any()):
             continue
-        out = _expert_ffn(msg[active], w, eid, act)
+        out = _expert_ffn(msg[active], w, eid, act, hidden_bf16)
         delta[active] = delta[active] + out * tw[active].unsqueeze(-1)
     return delta
 

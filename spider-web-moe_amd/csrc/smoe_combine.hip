@@ -48,6 +48,8 @@ __device__ __forceinline__ void store8(void* base, int dtype, int64_t off, const
 }
 
 // CPL = 8-element chunks per lane (H <= 512 * CPL)
+// Lane j (< S) fetches the token's j-th (destination, row) entry; the rows
+// are then broadcast and all their loads issued before any is consumed.
 template <int CPL>
 __global__ __launch_bounds__(256) void k_msg_combine(const void* __restrict__ proj, int pdt,
                                                      const int32_t* __restrict__ tok_d,
@@ -57,15 +59,16 @@ __global__ __launch_bounds__(256) void k_msg_combine(const void* __restrict__ pr
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= N) return;
+  const int64_t e = static_cast<int64_t>(t) * S + lane;
+  const int my_row = (lane < S && tok_d[e] >= 0) ? d_tokrow[e] : -1;
+  const int n = __popcll(__ballot(my_row >= 0));  // entries are packed first (ascending destination)
   float acc[CPL][8];
 #pragma unroll
   for (int c = 0; c < CPL; ++c)
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[c][i] = 0.f;
-  for (int j = 0; j < S; ++j) {
-    const int64_t e = static_cast<int64_t>(t) * S + j;
-    if (tok_d[e] < 0) break;
-    const int64_t row = d_tokrow[e];
+  for (int j = 0; j < n; ++j) {
+    const int64_t row = __shfl(my_row, j);
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
       const int col = (lane + 64 * c) * 8;
@@ -94,16 +97,27 @@ __global__ __launch_bounds__(256) void k_epilogue(
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= N) return;
-  float d[CPL][8];
+  // lane j (< K): the token's j-th expert row if its weight is > 0 (rows
+  // with weight <= 0 are dropped from the FFN, sparse_experts.py:56)
+  const int64_t e = static_cast<int64_t>(t) * K + lane;
+  int my_row = -1;
+  if (lane < K && tok_e[e] >= 0 && tok_ew[e] > 0.f) my_row = e_tokrow[e];
+  uint64_t live = __ballot(my_row >= 0);
+  float hv[CPL][8], xv[CPL][8], d[CPL][8];
 #pragma unroll
-  for (int c = 0; c < CPL; ++c)
+  for (int c = 0; c < CPL; ++c) {
+    const int col = (lane + 64 * c) * 8;
 #pragma unroll
     for (int i = 0; i < 8; ++i) d[c][i] = 0.f;
-  for (int j = 0; j < K; ++j) {
-    const int64_t e = static_cast<int64_t>(t) * K + j;
-    if (tok_e[e] < 0) break;
-    if (!(tok_ew[e] > 0.f)) continue;  // dropped from the FFN (sparse_experts.py:56)
-    const int64_t row = e_tokrow[e];
+    if (col < H) {
+      load8(h, adt, static_cast<int64_t>(t) * H + col, hv[c]);
+      load8(x0, adt, static_cast<int64_t>(t) * H + col, xv[c]);
+    }
+  }
+  while (live) {  // ascending expert order (tok_e is ascending)
+    const int j = __ffsll(static_cast<unsigned long long>(live)) - 1;
+    live &= live - 1;
+    const int64_t row = __shfl(my_row, j);
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
       const int col = (lane + 64 * c) * 8;
@@ -119,16 +133,12 @@ __global__ __launch_bounds__(256) void k_epilogue(
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
     const int col = (lane + 64 * c) * 8;
-    if (col < H) {
-      float hv[8], xv[8];
-      load8(h, adt, static_cast<int64_t>(t) * H + col, hv);
-      load8(x0, adt, static_cast<int64_t>(t) * H + col, xv);
+    if (col < H)
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        d[c][i] = (hv[i] + alpha * d[c][i]) + beta * xv[i];
+        d[c][i] = (hv[c][i] + alpha * d[c][i]) + beta * xv[c][i];
         s += d[c][i];
       }
-    }
   }
   const float mean = wave_sum(s) / static_cast<float>(H);
   float q = 0.f;

@@ -245,25 +245,12 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(const GemmArgs p) {
   }
 }
 
-// ------------------------------------------------------- MFMA, big tile ----
-// 256 x 256 x 64 block tile, 4 waves in a 2 x 2 grid, 128 x 128 per wave
-// (8 x 8 MFMA 16x16x32 tiles, 256 fp32 accumulators per lane).  Operands are
-// fed transposed — a = weight rows (output channels), b = plan rows — so a
-// lane's accumulator holds 4 consecutive output channels of one row and
-// stores them as one vector; SwiGLU's gate and up channels (32 apart) land
-// in the same lane.  LDS rows are 128 B (64 bf16) with the 16-byte chunks
-// XOR-swizzled by (row >> 1) & 7, so the 16 lanes of a ds_read_b128 phase
-// hit 16 distinct bank groups without padding.  Operands are staged global ->
-// VGPR -> LDS with one K slice of register prefetch and two LDS buffers.
-//
-// Tile order: the tile grid (real count, from the plan) is split into 8
-// contiguous ranges, one per XCD (workgroup ids are dealt to XCDs round
-// robin), and each range is walked in super-rows of GM m-tiles x all n-tiles
-// so the super-row's A tiles stay in that XCD's L2 while weight tiles stream.
-__device__ __forceinline__ int swz(int row, int chunk) {  // byte offset in a 128 B-row tile
-  return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4);
-}
-
+// ------------------------------------------------ tile order, 4-wide out ----
+// Tile order of the large-tile kernels: the tile grid (real count, from the
+// plan) is split into 8 contiguous ranges, one per XCD (workgroup ids are
+// dealt to XCDs round robin), and each range is walked in super-rows of GM
+// m-tiles x all n-tiles so the super-row's A tiles stay in that XCD's L2
+// while weight tiles stream.
 template <int BM>
 __device__ __forceinline__ int count_m_tiles(const GemmArgs& p) {
   if (p.G == 0) return (p.single_rows + BM - 1) / BM;
@@ -309,127 +296,6 @@ __device__ __forceinline__ void store4(const GemmArgs& p, int fmt, int g, int ro
   } else {
     *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + o) =
         u32x2{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3])};
-  }
-}
-
-template <int BM, int BN, int GM, int EPI>
-__global__ __launch_bounds__(256) void k_gemm_big(const GemmArgs p) {
-  constexpr int BK = 64;
-  constexpr int TM = BM / 2, TN = BN / 2;     // wave tile (rows x channels)
-  constexpr int FM = TM / 16, FN = TN / 16;
-  constexpr int A_CH = BM * 8 / 256;          // 16 B chunks per thread per stage
-  constexpr int B_CH = BN * 8 / 256;
-  static_assert(EPI != EPI_SWIGLU || TN % 64 == 0, "SwiGLU pairs 32-channel blocks");
-  __shared__ __attribute__((aligned(1024))) uint8_t smem[2 * (BM + BN) * 128];
-  uint8_t* const sA0 = smem;
-  uint8_t* const sB0 = smem + 2 * BM * 128;
-
-  int g, m0, mrows, n0;
-  if (!big_tile<BM, BN, GM>(p, g, m0, mrows, n0)) return;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-
-  // global sources and LDS destinations of this thread's chunks
-  const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A);
-  const uint16_t* W = reinterpret_cast<const uint16_t*>(p.W) + g * p.w_gstride;
-  const uint16_t* asrc[A_CH];
-  const uint16_t* bsrc[B_CH];
-  int adst[A_CH], bdst[B_CH];
-#pragma unroll
-  for (int i = 0; i < A_CH; ++i) {
-    const int c = tid + i * 256, r = c >> 3, ch = c & 7;
-    // rows past the group end read a valid row; their outputs are never stored
-    const int rr = r < mrows ? r : 0;
-    const int ar = p.a_rows ? p.a_rows[m0 + rr] : (m0 + rr);
-    asrc[i] = A + static_cast<int64_t>(ar) * p.lda + ch * 8;
-    adst[i] = swz(r, ch);
-  }
-#pragma unroll
-  for (int i = 0; i < B_CH; ++i) {
-    const int c = tid + i * 256, r = c >> 3, ch = c & 7;
-    const int n = n0 + r < p.N_out ? n0 + r : n0;
-    bsrc[i] = W + static_cast<int64_t>(n) * p.ldw + ch * 8;
-    bdst[i] = swz(r, ch);
-  }
-
-  f32x4 acc[FN][FM];
-#pragma unroll
-  for (int j = 0; j < FN; ++j)
-#pragma unroll
-    for (int i = 0; i < FM; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  u32x4 ra[A_CH], rb[B_CH];
-  auto gload = [&](int kt) {
-    const int k0 = kt * BK;
-#pragma unroll
-    for (int i = 0; i < A_CH; ++i) ra[i] = *reinterpret_cast<const u32x4*>(asrc[i] + k0);
-#pragma unroll
-    for (int i = 0; i < B_CH; ++i) rb[i] = *reinterpret_cast<const u32x4*>(bsrc[i] + k0);
-  };
-  auto sstore = [&](int buf) {
-    uint8_t* sa = sA0 + buf * BM * 128;
-    uint8_t* sb = sB0 + buf * BN * 128;
-#pragma unroll
-    for (int i = 0; i < A_CH; ++i) *reinterpret_cast<u32x4*>(sa + adst[i]) = ra[i];
-#pragma unroll
-    for (int i = 0; i < B_CH; ++i) *reinterpret_cast<u32x4*>(sb + bdst[i]) = rb[i];
-  };
-
-  // fragment read offsets: row = base + 16 x + (lane & 15), chunk = 4 ks + lane / 16
-  const int fr = lane & 15, fc = lane >> 4;
-  const int KT = p.K / BK;
-  gload(0);
-  sstore(0);
-  __syncthreads();
-  for (int kt = 0; kt < KT; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < KT) gload(kt + 1);
-    const uint8_t* sa = sA0 + buf * BM * 128;
-    const uint8_t* sb = sB0 + buf * BN * 128;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      bf16x8 wf[FN], af[FM];
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        wf[j] = *reinterpret_cast<const bf16x8*>(sb + swz(wn * TN + j * 16 + fr, ks * 4 + fc));
-#pragma unroll
-      for (int i = 0; i < FM; ++i)
-        af[i] = *reinterpret_cast<const bf16x8*>(sa + swz(wm * TM + i * 16 + fr, ks * 4 + fc));
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-          acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[j][i], 0, 0, 0);
-    }
-    if (kt + 1 < KT) sstore(buf ^ 1);
-    __syncthreads();
-  }
-
-  // lane holds channels n0 + wn*TN + 16 j + 4 (lane/16) + {0..3} of row wm*TM + 16 i + lane%16
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int lr = wm * TM + i * 16 + fr;
-    if (lr >= mrows) continue;
-    const int row = m0 + lr;
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int c = n0 + wn * TN + j * 16 + fc * 4;
-      if (c >= p.N_out) continue;
-      if constexpr (EPI == EPI_SWIGLU) {
-        if ((j & 3) < 2) {
-          const int u = (c >> 6) * 32 + (c & 31);
-          float r[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            r[q] = silu(acc[j][i][q]) * (acc[j + 2][i][q] + bias_at(p, g, u + q));
-          *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) +
-                                    static_cast<int64_t>(row) * p.ldo + u) =
-              u32x2{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3])};
-        }
-      } else {
-        store4<EPI>(p, SMOE_BF16, g, row, c, acc[j][i]);
-      }
-    }
   }
 }
 
@@ -623,6 +489,205 @@ __global__ __launch_bounds__(256) void k_gemm_ring(const GemmArgs p) {
   }
 }
 
+// --------------------------------------------------------------- skinny ----
+// Few rows per group (decode): the weights are nearly all of the traffic, so
+// a workgroup streams one strip of 16*TN weight rows (output channels) of one
+// group from HBM straight into registers and its NW waves split K.  In each
+// 64-wide K step a lane loads the 16 consecutive k at k0 + 16*(lane/16) of
+// its weight row (fp8 16 B, bf16 32 B, int4 8 B) and of its activation row;
+// the step's two MFMAs take the low and the high 8 of them (the order of k
+// inside a step is free as long as both operands follow it).  The loads of U
+// steps are issued before the first MFMA of the batch.  The waves' partial
+// sums meet in LDS and are added in wave order, so results are bit-identical
+// run to run; the epilogue writes 4 consecutive channels per lane.
+// Rows go in passes of 16*RT (a single-group GEMM spreads its passes over
+// grid.z; a grouped one loops over them).
+template <int FMT>
+struct WRaw {
+  u32x4 a, b;
+  float s;
+};
+
+template <int FMT>
+__device__ __forceinline__ WRaw<FMT> skinny_wload(const GemmArgs& p, const uint8_t* wrow, int k,
+                                                  int g, int n) {
+  WRaw<FMT> r;
+  if constexpr (FMT == SMOE_BF16) {
+    const u32x4* q = reinterpret_cast<const u32x4*>(wrow + 2 * static_cast<int64_t>(k));
+    r.a = q[0];
+    r.b = q[1];
+    r.s = 1.f;
+  } else if constexpr (FMT == SMOE_FP8_E4M3) {
+    r.a = *reinterpret_cast<const u32x4*>(wrow + k);
+    r.b = r.a;
+    r.s = 1.f;
+  } else {  // INT4: 16 nibbles, inside one scale group (group_size % 16 == 0)
+    const u32x2 v = *reinterpret_cast<const u32x2*>(wrow + (k >> 1));
+    r.a = u32x4{v.x, v.y, 0u, 0u};
+    r.b = r.a;
+    r.s = load_scale(p.S,
+                     g * p.s_gstride + static_cast<int64_t>(n) * (p.K / p.group_size) +
+                         k / p.group_size,
+                     p.s_f16);
+  }
+  return r;
+}
+
+// The raw 16 k of a lane -> the bf16 A operands of the step's two MFMAs.
+template <int FMT>
+__device__ __forceinline__ void skinny_wconv(const WRaw<FMT>& r, bf16x8& lo, bf16x8& hi) {
+  u32x4 l, h;
+  if constexpr (FMT == SMOE_BF16) {
+    l = r.a;
+    h = r.b;
+  } else if constexpr (FMT == SMOE_FP8_E4M3) {
+    const u32x2 a0 = fp8x4_to_bf16x4(r.a.x), a1 = fp8x4_to_bf16x4(r.a.y);
+    const u32x2 b0 = fp8x4_to_bf16x4(r.a.z), b1 = fp8x4_to_bf16x4(r.a.w);
+    l = u32x4{a0.x, a0.y, a1.x, a1.y};
+    h = u32x4{b0.x, b0.y, b1.x, b1.y};
+  } else {
+    l = int4x8_to_bf16x8(r.a.x, r.s);
+    h = int4x8_to_bf16x8(r.a.y, r.s);
+  }
+  lo = __builtin_bit_cast(bf16x8, l);
+  hi = __builtin_bit_cast(bf16x8, h);
+}
+
+template <int FMT, int EPI, int TN, int RT, int NW, int U>
+__global__ __launch_bounds__(NW * 64) void k_gemm_skinny(const GemmArgs p) {
+  constexpr int BN = 16 * TN;
+  constexpr int ESZ2 = FMT == SMOE_BF16 ? 4 : (FMT == SMOE_FP8_E4M3 ? 2 : 1);  // 2 x bytes/elt
+  static_assert(EPI != EPI_SWIGLU || TN == 4, "SwiGLU pairs channel c with c + 32");
+  static_assert(NW >= TN, "one wave per channel tile in the epilogue");
+  __shared__ f32x4 red[NW][TN * RT][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q = lane >> 4, l16 = lane & 15;
+  const int g = blockIdx.y;
+  const int n0 = blockIdx.x * BN;
+  int r_lo, r_hi;
+  if (p.G == 0) {
+    r_lo = 0;
+    r_hi = p.single_rows;
+  } else {
+    r_lo = p.grp_off[g];
+    r_hi = p.grp_off[g + 1];
+  }
+  if (r_hi <= r_lo) return;  // workgroup-uniform, before any barrier
+  const uint8_t* wrow[TN];
+  int wn[TN];
+#pragma unroll
+  for (int t = 0; t < TN; ++t) {
+    const int n = min(n0 + 16 * t + l16, p.N_out - 1);  // rows past N_out: loaded, never stored
+    wn[t] = n;
+    wrow[t] = reinterpret_cast<const uint8_t*>(p.W) +
+              (g * p.w_gstride + static_cast<int64_t>(n) * p.ldw) * ESZ2 / 2;
+  }
+  const int KS = p.K / 64;
+  const int s_begin = wave * KS / NW, s_end = (wave + 1) * KS / NW;
+  const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A);
+  const int pass0 = p.G == 0 ? static_cast<int>(blockIdx.z) : 0;
+  const int pstep = p.G == 0 ? static_cast<int>(gridDim.z) : 1;
+  for (int m0 = r_lo + pass0 * 16 * RT; m0 < r_hi; m0 += pstep * 16 * RT) {
+    const uint16_t* arow[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      int r = m0 + 16 * rt + l16;
+      r = r < r_hi ? r : r_lo;  // rows past the group: a valid row, never stored
+      const int ar = p.a_rows ? p.a_rows[r] : r;
+      arow[rt] = A + static_cast<int64_t>(ar) * p.lda + 16 * q;
+    }
+    f32x4 acc[TN][RT];
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) acc[t][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = s_begin; s0 < s_end; s0 += U) {
+      WRaw<FMT> wr[U][TN];
+      u32x4 av[U][RT][2];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {  // steps past s_end reload the last one (not used)
+        const int st = min(s0 + u, s_end - 1);
+        const int k = st * 64 + 16 * q;
+#pragma unroll
+        for (int t = 0; t < TN; ++t) wr[u][t] = skinny_wload<FMT>(p, wrow[t], k, g, wn[t]);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          const u32x4* ap = reinterpret_cast<const u32x4*>(arow[rt] + st * 64);
+          av[u][rt][0] = ap[0];
+          av[u][rt][1] = ap[1];
+        }
+      }
+      // steps past s_end multiply zeros (both operands, so 0 * 0): no branch
+      // for the compiler to sink the batch's loads into
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const bool live = s0 + u < s_end;
+        const u32x4 z = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int t = 0; t < TN; ++t) {
+          bf16x8 lo, hi;
+          skinny_wconv<FMT>(wr[u][t], lo, hi);
+          if (u > 0) {  // step s0 is always live
+            lo = live ? lo : __builtin_bit_cast(bf16x8, z);
+            hi = live ? hi : __builtin_bit_cast(bf16x8, z);
+          }
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) {
+            const u32x4 b0 = (u == 0 || live) ? av[u][rt][0] : z;
+            const u32x4 b1 = (u == 0 || live) ? av[u][rt][1] : z;
+            acc[t][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                lo, __builtin_bit_cast(bf16x8, b0), acc[t][rt], 0, 0, 0);
+            acc[t][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                hi, __builtin_bit_cast(bf16x8, b1), acc[t][rt], 0, 0, 0);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) red[wave][t * RT + rt][lane] = acc[t][rt];
+    __syncthreads();
+    // lane: channels n0 + 16 t + 4 q + (0..3) of row m0 + 16 rt + l16
+    constexpr int ET = EPI == EPI_SWIGLU ? TN / 2 : TN;
+    if (wave < ET) {
+      const int t = wave;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        const int row = m0 + 16 * rt + l16;
+        f32x4 v = red[0][t * RT + rt][lane];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) v += red[w][t * RT + rt][lane];
+        const int c = n0 + 16 * t + 4 * q;
+        if (row >= r_hi || c >= p.N_out) continue;
+        if constexpr (EPI == EPI_SWIGLU) {
+          f32x4 up = red[0][(t + TN / 2) * RT + rt][lane];
+#pragma unroll
+          for (int w = 1; w < NW; ++w) up += red[w][(t + TN / 2) * RT + rt][lane];
+          const int u0 = (c >> 6) * 32 + (c & 31);
+          float o[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float gs = v[i] * col_scale(p, FMT, g, c + i);
+            const float us = up[i] * col_scale(p, FMT, g, c + 32 + i) + bias_at(p, g, u0 + i);
+            o[i] = silu(gs) * us;
+          }
+          const int64_t off = static_cast<int64_t>(row) * p.ldo + u0;
+          if (p.out_dtype == SMOE_F32)
+            *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + off) =
+                f32x4{o[0], o[1], o[2], o[3]};
+          else
+            *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + off) =
+                u32x2{pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3])};
+        } else {
+          store4<EPI>(p, FMT, g, row, c, v);
+        }
+      }
+    }
+    __syncthreads();  // red is rewritten by the next pass
+  }
+}
+
 // ----------------------------------------------------------------- fp32 ----
 template <int BM, int BN, int EPI>
 __global__ __launch_bounds__(256) void k_gemm_f32(const GemmArgs p) {
@@ -719,22 +784,6 @@ int launch_mfma(const GemmArgs& a, hipStream_t s) {
   }
 }
 
-template <int BM, int BN, int GM>
-int launch_big(const GemmArgs& a, hipStream_t s) {
-  const int tiles = max_tiles(a, BM) * ((a.N_out + BN - 1) / BN);
-  if (tiles == 0) return SMOE_OK;
-  const dim3 grid(tiles), block(256);
-  switch (a.epi) {
-    case EPI_F32_BIAS: hipLaunchKernelGGL((k_gemm_big<BM, BN, GM, EPI_F32_BIAS>), grid, block, 0, s, a); break;
-    case EPI_ROWSCALE: hipLaunchKernelGGL((k_gemm_big<BM, BN, GM, EPI_ROWSCALE>), grid, block, 0, s, a); break;
-    case EPI_GELU: hipLaunchKernelGGL((k_gemm_big<BM, BN, GM, EPI_GELU>), grid, block, 0, s, a); break;
-    case EPI_SWIGLU: hipLaunchKernelGGL((k_gemm_big<BM, BN, GM, EPI_SWIGLU>), grid, block, 0, s, a); break;
-    case EPI_DOWN: hipLaunchKernelGGL((k_gemm_big<BM, BN, GM, EPI_DOWN>), grid, block, 0, s, a); break;
-    default: return SMOE_EINVAL;
-  }
-  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
-}
-
 template <int BN, int NS, int GM>
 int launch_ring(const GemmArgs& a, hipStream_t s) {
   const int tiles = max_tiles(a, 256) * ((a.N_out + BN - 1) / BN);
@@ -767,6 +816,51 @@ int launch_f32_bn(const GemmArgs& a, hipStream_t s) {
 
 }  // namespace
 
+// Passes of 16 * RT rows; a single-group GEMM puts one pass per grid.z.
+template <int FMT, int TN, int RT, int NW, int U>
+int launch_skinny_fmt(const GemmArgs& a, hipStream_t s) {
+  const int passes = a.G == 0 ? (a.single_rows + 16 * RT - 1) / (16 * RT) : 1;
+  if (passes == 0) return SMOE_OK;
+  const dim3 grid((a.N_out + 16 * TN - 1) / (16 * TN), a.G == 0 ? 1 : a.G, passes);
+  const dim3 block(NW * 64);
+  switch (a.epi) {
+    case EPI_F32_BIAS: hipLaunchKernelGGL((k_gemm_skinny<FMT, EPI_F32_BIAS, TN, RT, NW, U>), grid, block, 0, s, a); break;
+    case EPI_ROWSCALE: hipLaunchKernelGGL((k_gemm_skinny<FMT, EPI_ROWSCALE, TN, RT, NW, U>), grid, block, 0, s, a); break;
+    case EPI_GELU: hipLaunchKernelGGL((k_gemm_skinny<FMT, EPI_GELU, TN, RT, NW, U>), grid, block, 0, s, a); break;
+    case EPI_DOWN: hipLaunchKernelGGL((k_gemm_skinny<FMT, EPI_DOWN, TN, RT, NW, U>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU:
+      if constexpr (TN == 4) {
+        hipLaunchKernelGGL((k_gemm_skinny<FMT, EPI_SWIGLU, TN, RT, NW, U>), grid, block, 0, s, a);
+        break;
+      }
+      return SMOE_EINVAL;
+    default: return SMOE_EINVAL;
+  }
+  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
+template <int TN, int RT>
+int launch_skinny(const GemmArgs& a, hipStream_t s) {
+  switch (a.fmt) {
+    case SMOE_BF16: return launch_skinny_fmt<SMOE_BF16, TN, RT, 4, 2>(a, s);
+    case SMOE_FP8_E4M3: return launch_skinny_fmt<SMOE_FP8_E4M3, TN, RT, 4, 4>(a, s);
+    case SMOE_INT4: return launch_skinny_fmt<SMOE_INT4, TN, RT, 4, 4>(a, s);
+    default: return SMOE_EUNSUPPORTED;
+  }
+}
+
+// Whether the skinny kernel takes the GEMM: few rows per group, and every
+// 16-byte (int4: 8-byte) load it issues aligned.
+bool skinny_fits(const GemmArgs& a) {
+  const int rows_per_group = a.G == 0 ? a.single_rows : a.max_rows / a.G;
+  if (rows_per_group > (a.G == 0 ? 64 : 32)) return false;
+  if (a.K % 64 || a.N_out % 4 || a.ldo % 4 || a.lda % 8) return false;
+  const int walign = a.fmt == SMOE_BF16 ? 8 : 16;  // elements per aligned load
+  if (a.ldw % walign || a.w_gstride % walign) return false;
+  if (a.fmt == SMOE_INT4 && a.group_size % 16) return false;
+  return true;
+}
+
 int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
   if (a.N_out <= 0 || a.K <= 0) return SMOE_EINVAL;
   // pointers every launched workgroup dereferences
@@ -786,6 +880,14 @@ int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
   const int bk = (a.K % 64 == 0) ? 64 : (a.K % 32 == 0 ? 32 : 0);
   if (!bk) return SMOE_EINVAL;
   if (a.epi == EPI_SWIGLU && a.N_out % 128) return SMOE_EINVAL;
+  // decode: a few rows per group, weight streaming
+  if (skinny_fits(a)) {
+    const int rpg = a.G == 0 ? a.single_rows : a.max_rows / a.G;
+    if (a.N_out <= 16) return rpg <= 16 ? launch_skinny<1, 1>(a, s) : launch_skinny<1, 2>(a, s);
+    if (a.N_out <= 32 && a.epi != EPI_SWIGLU)
+      return rpg <= 16 ? launch_skinny<2, 1>(a, s) : launch_skinny<2, 2>(a, s);
+    return rpg <= 8 ? launch_skinny<4, 1>(a, s) : launch_skinny<4, 2>(a, s);
+  }
   // large bf16 problems: 256 x 256 tiles (N_out and K multiples of the tile)
   if (a.fmt == SMOE_BF16 && a.out_dtype == SMOE_BF16 && a.epi != EPI_F32_BIAS && a.K % 64 == 0 &&
       a.ldw % 8 == 0 && a.lda % 8 == 0 && a.ldo % 8 == 0 &&
@@ -794,12 +896,14 @@ int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
     if (a.N_out % 128 == 0) return launch_ring<128, 6, 4>(a, s);
   }
   const bool b64 = bk == 64;
+  // narrow outputs (router / edge logits, N_out = E): 64-row tiles, one
+  // 16-row MFMA strip per wave, so the grid has enough workgroups
   if (a.N_out <= 16)
-    return b64 ? launch_mfma<128, 16, 64, 4, 1>(a, s) : launch_mfma<128, 16, 32, 4, 1>(a, s);
+    return b64 ? launch_mfma<64, 16, 64, 4, 1>(a, s) : launch_mfma<64, 16, 32, 4, 1>(a, s);
   if (a.N_out <= 32)
-    return b64 ? launch_mfma<128, 32, 64, 4, 1>(a, s) : launch_mfma<128, 32, 32, 4, 1>(a, s);
+    return b64 ? launch_mfma<64, 32, 64, 4, 1>(a, s) : launch_mfma<64, 32, 32, 4, 1>(a, s);
   if (a.N_out <= 64)
-    return b64 ? launch_mfma<128, 64, 64, 4, 1>(a, s) : launch_mfma<128, 64, 32, 4, 1>(a, s);
+    return b64 ? launch_mfma<64, 64, 64, 4, 1>(a, s) : launch_mfma<64, 64, 32, 4, 1>(a, s);
   return b64 ? launch_mfma<128, 128, 64, 2, 2>(a, s) : launch_mfma<128, 128, 32, 2, 2>(a, s);
 }
 

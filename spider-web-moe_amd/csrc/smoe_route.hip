@@ -196,232 +196,311 @@ int launch_edge_topm(const float* edge_logit, const int32_t* tok_e, const int32_
 }
 
 // -------------------------------------------------------------- plan ----
-// Entries: tok_g [N,S] groups ascending per token (-1 pad), tok_w [N,S].
-// An entry is kept when 0 <= g < G and (!drop_nonpos || w > 0).
-constexpr int kPlanThreads = 256;
+// Entries: tok_g [N,S] and tok_w [N,S], S <= 256.  A token's valid entries
+// are the prefix of strictly ascending groups in [0, G); from the first
+// entry that is not greater than the previous one or not in [0, G) on, the
+// row is padding (the producers write the token's groups ascending followed
+// by -1 pads).  A valid entry is kept when !drop_nonpos || w > 0.
+//
+// Tokens are cut into chunks of 64 (one wave, one token per lane) and groups
+// into windows of at most 64.
+//   rank:    one wave per (chunk, window): each lane turns its token's
+//            entries into bit masks over the window (present / kept /
+//            positive weight); one ballot per group gives the chunk's count
+//            (kept in the lane of that group) and each kept entry's rank
+//            among the chunk's earlier tokens
+//   scan:    one wave per group: exclusive scan of the chunk counts
+//   scatter: group offsets by a workgroup scan of the group totals, then
+//            row = off[g] + chunk prefix + rank -> rows / row_w / tok_row
+// Token order inside a group is preserved (stable) and no atomics are used,
+// so the plan is bit-exact run to run.
 constexpr int kPlanMaxG = 256;
+constexpr int kPlanMaxS = 256;
 
-__device__ __forceinline__ bool keep_entry(int g, float w, int G, int drop) {
-  return g >= 0 && g < G && (!drop || w > 0.f);
-}
-
-// Rank the kept entries of tokens [t0, t0+256) within the block and scatter
-// them to rows base[g] + rank.  base[] (LDS) advances by the chunk's counts.
-__device__ void plan_scatter_chunk(const int32_t* __restrict__ tok_g,
-                                   const float* __restrict__ tok_w, int N, int S, int G, int drop,
-                                   int t0, int* base, int (*wcnt)[kPlanMaxG],
-                                   int32_t* __restrict__ rows, float* __restrict__ roww,
-                                   int32_t* __restrict__ tokrow) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int t = t0 + tid;
+// One wave ranks tokens [t0, t0 + 64) for groups [g0, g0 + win) (win <= 64):
+// cnt[g * cs] / acnt[g * cs] get the chunk's kept / positive-weight counts,
+// tokrow the rank of each kept entry among the chunk's earlier tokens and -1
+// for every other entry (the g0 == 0 wave writes the padding entries).
+// acnt is only counted when drop == 0 (otherwise it equals cnt).
+template <typename P>
+__device__ __forceinline__ void rank_chunk(const int32_t* __restrict__ tok_g,
+                                           const float* __restrict__ tok_w, int N, int S, int G,
+                                           int drop, int t0, int g0, int win, P cnt, P acnt,
+                                           int cs, int32_t* __restrict__ tokrow) {
+  const int lane = threadIdx.x & 63;
+  const int t = t0 + lane;
   const bool valid = t < N;
-  const int32_t* tg = tok_g + static_cast<int64_t>(t) * S;
-  const float* tw = tok_w + static_cast<int64_t>(t) * S;
-  // phase A: within-wave rank of each kept entry, stored in tokrow
-  int j = 0;  // entries are sorted by group, so matches arrive in slot order
-  int gj = valid && S > 0 ? tg[0] : -1;
-  for (int g = 0; g < G; ++g) {
-    while (valid && j < S && gj >= 0 && gj < g) {  // skip out-of-order / dropped
-      tokrow[static_cast<int64_t>(t) * S + j] = -1;
-      ++j;
-      gj = j < S ? tg[j] : -1;
-    }
-    const bool has = valid && j < S && gj == g && keep_entry(g, tw[j], G, drop);
-    const uint64_t m = __ballot(has);
-    if (lane == 0) wcnt[wave][g] = __popcll(m);
-    if (valid && j < S && gj == g) {
-      tokrow[static_cast<int64_t>(t) * S + j] = has ? __popcll(m & ((1ull << lane) - 1)) : -1;
-      ++j;
-      gj = j < S ? tg[j] : -1;
-    }
-  }
-  for (; valid && j < S; ++j) tokrow[static_cast<int64_t>(t) * S + j] = -1;
-  __syncthreads();
-  // phase B: per-group wave prefixes -> wcnt[w][g] becomes the wave's row base
-  for (int g = tid; g < G; g += kPlanThreads) {
-    int run = base[g];
-    for (int w = 0; w < kPlanThreads / 64; ++w) {
-      const int c = wcnt[w][g];
-      wcnt[w][g] = run;
-      run += c;
-    }
-    base[g] = run;
-  }
-  __syncthreads();
-  // phase C: final rows
+  const int nb = G - g0 < win ? G - g0 : win;
+  const int64_t e0 = static_cast<int64_t>(t) * S;
+  uint64_t gm = 0, km = 0, am = 0;
+  int below = 0;  // valid entries with a group < g0
   if (valid) {
-    for (int jj = 0; jj < S; ++jj) {
-      const int g = tg[jj];
-      const int64_t o = static_cast<int64_t>(t) * S + jj;
-      const int r = tokrow[o];
-      if (r < 0 || g < 0 || g >= G) continue;
-      const int row = wcnt[wave][g] + r;
-      tokrow[o] = row;
+    int prev = -1;
+    bool open = true;
+    for (int j0 = 0; j0 < S; j0 += 8) {
+      int gv[8];
+      float wv[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {  // unconditional (clamped) loads: issued together
+        const int jj = j0 + u < S ? j0 + u : S - 1;
+        gv[u] = tok_g[e0 + jj];
+        wv[u] = tok_w[e0 + jj];
+      }
+#pragma unroll
+      for (int u = 0; u < 8; ++u) gv[u] = j0 + u < S ? gv[u] : -1;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {  // branch-free, so no load is sunk behind a branch
+        const int g = gv[u];
+        open = open && g > prev && g < G;  // g > prev >= -1, so g >= 0
+        prev = open ? g : prev;
+        below += (open && g < g0) ? 1 : 0;
+        const int b = g - g0;
+        const uint64_t bit = (open && b >= 0 && b < nb) ? (1ull << (b & 63)) : 0ull;
+        const bool pos = wv[u] > 0.f;
+        gm |= bit;
+        km |= (!drop || pos) ? bit : 0ull;
+        am |= pos ? bit : 0ull;
+        if (!open && g0 == 0 && j0 + u < S) tokrow[e0 + j0 + u] = -1;
+      }
+    }
+  }
+  int mycnt = 0, myacnt = 0;
+  for (int b = 0; b < nb; ++b) {
+    const uint64_t bit = 1ull << b;
+    const uint64_t m = __ballot((km & bit) != 0);
+    mycnt = lane == b ? static_cast<int>(__popcll(m)) : mycnt;
+    if (!drop) {
+      const uint64_t ma = __ballot((am & bit) != 0);
+      myacnt = lane == b ? static_cast<int>(__popcll(ma)) : myacnt;
+    }
+    if (gm & bit) {
+      const int j = below + static_cast<int>(__popcll(gm & (bit - 1)));
+      const int r = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
+                                              __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
+      tokrow[e0 + j] = (km & bit) ? r : -1;
+    }
+  }
+  if (lane < nb) {
+    cnt[(g0 + lane) * cs] = mycnt;
+    acnt[(g0 + lane) * cs] = drop ? mycnt : myacnt;
+  }
+}
+
+// Scatter of one token: row = goff[g] + base[g * bs] + rank (group offset,
+// the chunk's prefix inside the group, the rank inside the chunk).
+template <typename P>
+__device__ __forceinline__ void scatter_token(const int32_t* __restrict__ tok_g,
+                                              const float* __restrict__ tok_w, int t, int S,
+                                              int G, P base, int bs, const int* goff,
+                                              int32_t* __restrict__ rows,
+                                              float* __restrict__ roww,
+                                              int32_t* __restrict__ tokrow) {
+  const int64_t e0 = static_cast<int64_t>(t) * S;
+  for (int j0 = 0; j0 < S; j0 += 8) {
+    int gv[8], rv[8], bv[8], ov[8];
+    float wv[8];
+    // every load unconditional (clamped indices), so each batch is one
+    // round trip to memory
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int jj = j0 + u < S ? j0 + u : S - 1;
+      gv[u] = tok_g[e0 + jj];
+      rv[u] = tokrow[e0 + jj];
+      wv[u] = tok_w[e0 + jj];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int gc = (gv[u] >= 0 && gv[u] < G) ? gv[u] : 0;
+      bv[u] = base[gc * bs];
+      ov[u] = goff[gc];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      if (j0 + u >= S || rv[u] < 0 || gv[u] < 0 || gv[u] >= G) continue;
+      const int row = ov[u] + bv[u] + rv[u];
+      tokrow[e0 + j0 + u] = row;
       rows[row] = t;
-      roww[row] = tw[jj];
+      roww[row] = wv[u];
     }
+  }
+}
+
+// Exclusive scan of tot[0..G) into goff[0..G].  Every thread of the
+// workgroup calls it (it holds barriers); the first 256 do the work.
+__device__ __forceinline__ void block_group_offsets(const int32_t* tot, int G, int* goff,
+                                                    int* wsum) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool act = tid < 256;
+  const int v = (act && tid < G) ? tot[tid] : 0;
+  int incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int u = __shfl_up(incl, o);
+    if (lane >= o) incl += u;
+  }
+  if (act && lane == 63) wsum[wave] = incl;
+  __syncthreads();
+  if (act) {
+    int before = 0;
+    for (int w = 0; w < wave; ++w) before += wsum[w];
+    if (tid < G) goff[tid] = before + incl - v;
+    if (tid == 0) goff[G] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
   }
   __syncthreads();
 }
 
-// Single-workgroup plan (small N): count, scan and scatter in one launch.
-__global__ __launch_bounds__(kPlanThreads) void k_plan_fused(
-    const int32_t* __restrict__ tok_g, const float* __restrict__ tok_w, int N, int S, int G,
-    int drop, int32_t* __restrict__ cnt, int32_t* __restrict__ acnt, int32_t* __restrict__ off,
-    int32_t* __restrict__ rows, float* __restrict__ roww, int32_t* __restrict__ tokrow) {
-  __shared__ int hist[kPlanMaxG], ahist[kPlanMaxG], base[kPlanMaxG];
-  __shared__ int wcnt[kPlanThreads / 64][kPlanMaxG];
-  const int tid = threadIdx.x;
-  for (int g = tid; g < G; g += kPlanThreads) hist[g] = ahist[g] = 0;
-  __syncthreads();
-  for (int t = tid; t < N; t += kPlanThreads)
-    for (int j = 0; j < S; ++j) {
-      const int g = tok_g[static_cast<int64_t>(t) * S + j];
-      const float w = tok_w[static_cast<int64_t>(t) * S + j];
-      if (keep_entry(g, w, G, drop)) {
-        atomicAdd(&hist[g], 1);
-        if (w > 0.f) atomicAdd(&ahist[g], 1);
-      }
-    }
-  __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int g = 0; g < G; ++g) {
-      base[g] = run;
-      off[g] = run;
-      cnt[g] = hist[g];
-      acnt[g] = ahist[g];
-      run += hist[g];
-    }
-    off[G] = run;
-  }
-  __syncthreads();
-  for (int t0 = 0; t0 < N; t0 += kPlanThreads)
-    plan_scatter_chunk(tok_g, tok_w, N, S, G, drop, t0, base, wcnt, rows, roww, tokrow);
+// ccnt / cacnt are [G, C] (group-major).  Wave w of the grid ranks chunk
+// w / W for the window w % W (W = ceil(G / 64)).
+__global__ __launch_bounds__(256) void k_plan_rank(const int32_t* __restrict__ tok_g,
+                                                   const float* __restrict__ tok_w, int N, int S,
+                                                   int G, int drop, int C, int W,
+                                                   int32_t* __restrict__ ccnt,
+                                                   int32_t* __restrict__ cacnt,
+                                                   int32_t* __restrict__ tokrow) {
+  const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (item >= C * W) return;
+  const int chunk = item / W, g0 = (item % W) * 64;
+  rank_chunk(tok_g, tok_w, N, S, G, drop, chunk * 64, g0, 64, ccnt + chunk, cacnt + chunk, C,
+             tokrow);
 }
 
-__global__ __launch_bounds__(kPlanThreads) void k_plan_count(const int32_t* __restrict__ tok_g,
-                                                             const float* __restrict__ tok_w,
-                                                             int N, int S, int G, int drop,
-                                                             int chunk, int32_t* __restrict__ bc,
-                                                             int32_t* __restrict__ bac) {
-  __shared__ int hist[kPlanMaxG], ahist[kPlanMaxG];
-  const int tid = threadIdx.x;
-  for (int g = tid; g < G; g += kPlanThreads) hist[g] = ahist[g] = 0;
-  __syncthreads();
-  const int t_end = min(N, (blockIdx.x + 1) * chunk);
-  for (int t = blockIdx.x * chunk + tid; t < t_end; t += kPlanThreads)
-    for (int j = 0; j < S; ++j) {
-      const int g = tok_g[static_cast<int64_t>(t) * S + j];
-      const float w = tok_w[static_cast<int64_t>(t) * S + j];
-      if (keep_entry(g, w, G, drop)) {
-        atomicAdd(&hist[g], 1);
-        if (w > 0.f) atomicAdd(&ahist[g], 1);
-      }
+// One wave per group: chunk counts -> exclusive chunk prefixes (in place),
+// group totals -> cnt, positive-weight totals -> acnt.
+__global__ __launch_bounds__(64) void k_plan_scan(int C, int32_t* __restrict__ ccnt,
+                                                  const int32_t* __restrict__ cacnt,
+                                                  int32_t* __restrict__ cnt,
+                                                  int32_t* __restrict__ acnt) {
+  const int g = blockIdx.x, lane = threadIdx.x;
+  int32_t* row = ccnt + static_cast<int64_t>(g) * C;
+  const int32_t* arow = cacnt + static_cast<int64_t>(g) * C;
+  int run = 0;  // sum of all earlier passes
+  int a = 0;
+  for (int c0 = 0; c0 < C; c0 += 256) {
+    int v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int c = c0 + lane * 4 + k;
+      v[k] = c < C ? row[c] : 0;
+      a += c < C ? arow[c] : 0;
     }
-  __syncthreads();
-  for (int g = tid; g < G; g += kPlanThreads) {
-    bc[static_cast<int64_t>(blockIdx.x) * G + g] = hist[g];
-    bac[static_cast<int64_t>(blockIdx.x) * G + g] = ahist[g];
+    const int s = v[0] + v[1] + v[2] + v[3];
+    int incl = s;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(incl, o);
+      if (lane >= o) incl += u;
+    }
+    int p = run + incl - s;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int c = c0 + lane * 4 + k;
+      if (c < C) row[c] = p;
+      p += v[k];
+    }
+    run += __shfl(incl, 63);
   }
-}
-
-// One workgroup: totals per group, exclusive scan over groups, and each
-// block's base row per group (bc is overwritten with the bases).
-__global__ __launch_bounds__(kPlanThreads) void k_plan_scan(int nblk, int G,
-                                                            int32_t* __restrict__ bc,
-                                                            const int32_t* __restrict__ bac,
-                                                            int32_t* __restrict__ cnt,
-                                                            int32_t* __restrict__ acnt,
-                                                            int32_t* __restrict__ off) {
-  __shared__ int tot[kPlanMaxG], goff[kPlanMaxG + 1];
-  const int tid = threadIdx.x;
-  for (int g = tid; g < G; g += kPlanThreads) {
-    int s = 0, a = 0;
-    for (int b = 0; b < nblk; ++b) {
-      s += bc[static_cast<int64_t>(b) * G + g];
-      a += bac[static_cast<int64_t>(b) * G + g];
-    }
-    tot[g] = s;
-    cnt[g] = s;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o);
+  if (lane == 0) {
+    cnt[g] = run;
     acnt[g] = a;
   }
-  __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int g = 0; g < G; ++g) {
-      goff[g] = run;
-      run += tot[g];
-    }
-    goff[G] = run;
-  }
-  __syncthreads();
-  for (int g = tid; g <= G; g += kPlanThreads) off[g] = goff[g];
-  for (int g = tid; g < G; g += kPlanThreads) {
-    int run = goff[g];
-    for (int b = 0; b < nblk; ++b) {
-      const int64_t i = static_cast<int64_t>(b) * G + g;
-      const int c = bc[i];
-      bc[i] = run;
-      run += c;
-    }
-  }
 }
 
-__global__ __launch_bounds__(kPlanThreads) void k_plan_scatter(
-    const int32_t* __restrict__ tok_g, const float* __restrict__ tok_w, int N, int S, int G,
-    int drop, int chunk, const int32_t* __restrict__ bbase, int32_t* __restrict__ rows,
-    float* __restrict__ roww, int32_t* __restrict__ tokrow) {
-  __shared__ int base[kPlanMaxG];
-  __shared__ int wcnt[kPlanThreads / 64][kPlanMaxG];
-  const int tid = threadIdx.x;
-  for (int g = tid; g < G; g += kPlanThreads)
-    base[g] = bbase[static_cast<int64_t>(blockIdx.x) * G + g];
-  __syncthreads();
-  const int t_beg = blockIdx.x * chunk;
-  const int t_end = min(N, t_beg + chunk);
-  for (int t0 = t_beg; t0 < t_end; t0 += kPlanThreads)
-    plan_scatter_chunk(tok_g, tok_w, t_end, S, G, drop, t0, base, wcnt, rows, roww, tokrow);
+__global__ __launch_bounds__(256) void k_plan_scatter(const int32_t* __restrict__ tok_g,
+                                                      const float* __restrict__ tok_w, int N,
+                                                      int S, int G, int C,
+                                                      const int32_t* __restrict__ cbase,
+                                                      const int32_t* __restrict__ cnt,
+                                                      int32_t* __restrict__ off,
+                                                      int32_t* __restrict__ rows,
+                                                      float* __restrict__ roww,
+                                                      int32_t* __restrict__ tokrow) {
+  __shared__ int goff[kPlanMaxG + 1], wsum[4];
+  block_group_offsets(cnt, G, goff, wsum);
+  if (blockIdx.x == 0)
+    for (int g = threadIdx.x; g <= G; g += 256) off[g] = goff[g];
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t >= N) return;
+  scatter_token(tok_g, tok_w, t, S, G, cbase + (t >> 6), C, goff, rows, roww, tokrow);
 }
 
-namespace {
-constexpr int kFusedMaxN = 4096;
-constexpr int kMaxBlocks = 256;
-int plan_blocks(int N, int* chunk) {
-  int nblk = (N + kPlanThreads - 1) / kPlanThreads;
-  if (nblk > kMaxBlocks) nblk = kMaxBlocks;
-  int c = (N + nblk - 1) / nblk;
-  c = (c + kPlanThreads - 1) / kPlanThreads * kPlanThreads;
-  *chunk = c;
-  return (N + c - 1) / c;
+// Small N: the three phases in one workgroup of 1024 threads, the [G, C]
+// chunk counts in LDS (C <= 64: one chunk per lane in the scan).  Groups are
+// cut into windows of `win` so that the rank work spreads over the waves.
+constexpr int kSmallMaxCells = 8192;
+__global__ __launch_bounds__(1024) void k_plan_small(const int32_t* __restrict__ tok_g,
+                                                     const float* __restrict__ tok_w, int N,
+                                                     int S, int G, int drop, int win,
+                                                     int32_t* __restrict__ cnt,
+                                                     int32_t* __restrict__ acnt,
+                                                     int32_t* __restrict__ off,
+                                                     int32_t* __restrict__ rows,
+                                                     float* __restrict__ roww,
+                                                     int32_t* __restrict__ tokrow) {
+  __shared__ int cc[kSmallMaxCells], ca[kSmallMaxCells];
+  __shared__ int tot[kPlanMaxG], goff[kPlanMaxG + 1], wsum[4];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int C = (N + 63) / 64;
+  const int W = (G + win - 1) / win;
+  for (int item = wave; item < C * W; item += 16) {
+    const int c = item / W;
+    rank_chunk(tok_g, tok_w, N, S, G, drop, c * 64, (item % W) * win, win, cc + c, ca + c, C,
+               tokrow);
+  }
+  __syncthreads();
+  for (int g = wave; g < G; g += 16) {
+    const int v = lane < C ? cc[g * C + lane] : 0;
+    int a = lane < C ? ca[g * C + lane] : 0;
+    int incl = v;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int u = __shfl_up(incl, o);
+      if (lane >= o) incl += u;
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o);
+    if (lane < C) cc[g * C + lane] = incl - v;
+    if (lane == 63) {
+      tot[g] = incl;
+      cnt[g] = incl;
+      acnt[g] = a;
+    }
+  }
+  __syncthreads();
+  block_group_offsets(tot, G, goff, wsum);
+  for (int g = threadIdx.x; g <= G; g += 1024) off[g] = goff[g];
+  for (int t = threadIdx.x; t < N; t += 1024)
+    scatter_token(tok_g, tok_w, t, S, G, cc + (t >> 6), C, goff, rows, roww, tokrow);
 }
-}  // namespace
 
 size_t plan_scratch_bytes(int N, int G) {
-  int chunk;
-  const int nblk = plan_blocks(N > 0 ? N : 1, &chunk);
-  return static_cast<size_t>(2) * nblk * G * sizeof(int32_t);
+  const size_t C = (static_cast<size_t>(N > 0 ? N : 1) + 63) / 64;
+  return 2 * C * static_cast<size_t>(G) * sizeof(int32_t);
 }
 
 int launch_plan(const int32_t* tok_g, const float* tok_w, int N, int S, int G, int drop,
                 int32_t* cnt, int32_t* acnt, int32_t* off, int32_t* rows, float* roww,
                 int32_t* tokrow, void* scratch, hipStream_t s) {
-  if (G < 1 || G > kPlanMaxG || S < 1) return SMOE_EINVAL;
-  if (N <= kFusedMaxN) {
-    hipLaunchKernelGGL(k_plan_fused, dim3(1), dim3(kPlanThreads), 0, s, tok_g, tok_w, N, S, G,
-                       drop, cnt, acnt, off, rows, roww, tokrow);
+  if (G < 1 || G > kPlanMaxG || S < 1 || S > kPlanMaxS || N < 0) return SMOE_EINVAL;
+  const int C = (N + 63) / 64;
+  // One workgroup while its rank work (C x G ballots) stays small; the
+  // three-kernel form spreads larger plans over the chip.
+  if (C * G <= 512) {
+    int win = 64;  // narrower windows until the 16 waves have work
+    while (win > 8 && C * ((G + win - 1) / win) < 16) win >>= 1;
+    hipLaunchKernelGGL(k_plan_small, dim3(1), dim3(1024), 0, s, tok_g, tok_w, N, S, G, drop, win,
+                       cnt, acnt, off, rows, roww, tokrow);
     return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
   }
-  int chunk;
-  const int nblk = plan_blocks(N, &chunk);
-  int32_t* bc = reinterpret_cast<int32_t*>(scratch);
-  int32_t* bac = bc + static_cast<int64_t>(nblk) * G;
-  hipLaunchKernelGGL(k_plan_count, dim3(nblk), dim3(kPlanThreads), 0, s, tok_g, tok_w, N, S, G,
-                     drop, chunk, bc, bac);
-  hipLaunchKernelGGL(k_plan_scan, dim3(1), dim3(kPlanThreads), 0, s, nblk, G, bc, bac, cnt, acnt,
-                     off);
-  hipLaunchKernelGGL(k_plan_scatter, dim3(nblk), dim3(kPlanThreads), 0, s, tok_g, tok_w, N, S, G,
-                     drop, chunk, bc, rows, roww, tokrow);
+  const int W = (G + 63) / 64;
+  int32_t* ccnt = reinterpret_cast<int32_t*>(scratch);
+  int32_t* cacnt = ccnt + static_cast<int64_t>(C) * G;
+  hipLaunchKernelGGL(k_plan_rank, dim3((C * W + 3) / 4), dim3(256), 0, s, tok_g, tok_w, N, S, G,
+                     drop, C, W, ccnt, cacnt, tokrow);
+  hipLaunchKernelGGL(k_plan_scan, dim3(G), dim3(64), 0, s, C, ccnt, cacnt, cnt, acnt);
+  hipLaunchKernelGGL(k_plan_scatter, dim3((N + 255) / 256), dim3(256), 0, s, tok_g, tok_w, N, S,
+                     G, C, ccnt, cnt, off, rows, roww, tokrow);
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 

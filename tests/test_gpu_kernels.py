@@ -30,10 +30,11 @@ def nat():
 # ------------------------------------------------------------- router ----
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("e,k", [(4, 2), (16, 2), (32, 4), (64, 2), (64, 8)])
-def test_router_topk_matches_oracle(dtype, e, k):
+@pytest.mark.parametrize("n", [1000, 40])  # 40 tokens: the decode (weight-streaming) GEMM
+def test_router_topk_matches_oracle(dtype, e, k, n):
     n8 = nat()
-    n, h = 1000, 256
-    say("router", dtype, e, k)
+    h = 256
+    say("router", dtype, e, k, n)
     g = torch.Generator().manual_seed(e * 10 + k)
     x = torch.randn(n, h, generator=g).to(dtype)
     w = (torch.randn(e, h, generator=g) * 0.1).to(dtype)
@@ -64,7 +65,8 @@ def test_router_topk_matches_oracle(dtype, e, k):
 
 # ------------------------------------------------------- dispatch plan ----
 @pytest.mark.parametrize("n,k,e", [(0, 2, 4), (1, 1, 1), (100, 2, 4), (777, 3, 16),
-                                   (5000, 2, 16), (20000, 4, 32), (3000, 8, 64)])
+                                   (5000, 2, 16), (20000, 4, 32), (3000, 8, 64),
+                                   (4000, 12, 64), (70000, 20, 200), (300, 40, 256)])
 def test_dispatch_plan_bit_exact(n, k, e):
     from spider_moe_amd.dispatch import plan_tensors
     say("plan", n, k, e)
@@ -116,13 +118,13 @@ def _delta_case(n, h, u, e, k, seed, scale=0.05):
     return msg, idx, w, wu, bu, wd, bd
 
 
-def _oracle_delta(msg, idx, w, wu, bu, wd, bd, w_gate=None):
+def _oracle_delta(msg, idx, w, wu, bu, wd, bd, w_gate=None, hidden_bf16=False):
     e, _, h = wu.shape
     ow = B.BlockWeights(router_w=torch.zeros(e, h), loop_bias=torch.zeros(1, e), loop_emb=torch.zeros(1, 1),
                         edge_gen_w=torch.zeros(e * e, h + 1), edge_gen_b=torch.zeros(e * e),
                         edge_value_w=torch.zeros(e, 1, 1), w_up=wu, w_down=wd, b_up=bu, b_down=bd,
                         w_gate=w_gate)
-    return B.expert_delta(msg, idx, w, ow)
+    return B.expert_delta(msg, idx, w, ow, hidden_bf16=hidden_bf16)
 
 
 def test_sparse_expert_delta_golden_f32():
@@ -244,6 +246,71 @@ def test_int4_experts_match_oracle(group, sdt):
     ref_fp = _oracle_delta(msg.float(), idx, w, wu, bu, wd, bd)
     env = (ref - ref_fp).abs().max()
     assert (got - ref).abs().max() < max(float(env), 1e-3)
+
+
+@pytest.mark.parametrize("fmt,act", [("bf16", "gelu"), ("bf16", "swiglu"), ("fp8", "gelu"),
+                                     ("fp8", "swiglu"), ("int4-g32-f32", "gelu"),
+                                     ("int4-g128-f16", "gelu")])
+def test_decode_experts_match_oracle(fmt, act):
+    """Decode shapes (a few rows per expert) take the weight-streaming GEMM:
+    K split over the waves with a ragged tail (up K = 384: 6 steps of 64,
+    down K = 640: 10), an expert with more rows than one pass holds, an
+    empty expert, a one-row expert."""
+    from spider_moe_amd.quant import interleave_gate_up, interleave_gate_up_rows, quantize_int4
+    n8 = nat()
+    say("decode experts", fmt, act)
+    n, h, u, e, k = 60, 384, 640, 8, 2
+    g = torch.Generator().manual_seed(31)
+    idx = torch.stack([torch.randperm(e - 2, generator=g)[:k] + 1 for _ in range(n)])
+    idx[:, 0] = 0                # expert 0: every token (60 rows > 32 per pass)
+    idx[5, 1] = e - 1            # expert e-1: one row;  expert e-2: none
+    w = torch.rand(n, k, generator=g)
+    msg = torch.randn(n, h, generator=g).to(torch.bfloat16)
+    nup = 2 * u if act == "swiglu" else u
+    wu = torch.randn(e, nup, h, generator=g) * 0.05
+    wd = torch.randn(e, h, u, generator=g) * 0.05
+    bu = torch.randn(e, u, generator=g) * 0.1
+    bd = torch.randn(e, h, generator=g) * 0.1
+    kw = {}
+    if fmt == "bf16":
+        wu, wd = wu.to(torch.bfloat16), wd.to(torch.bfloat16)
+        wu_f, wd_f = wu.float(), wd.float()
+        code, dev_up, dev_dn = n8.BF16, wu, wd
+    elif fmt == "fp8":
+        cu, su = Q.fp8_quantize_per_channel(wu.numpy())
+        cd, sd = Q.fp8_quantize_per_channel(wd.numpy())
+        wu_f = torch.from_numpy(Q.fp8_dequantize_per_channel(cu, su))
+        wd_f = torch.from_numpy(Q.fp8_dequantize_per_channel(cd, sd))
+        code, dev_up, dev_dn = n8.FP8_E4M3, torch.from_numpy(cu), torch.from_numpy(cd)
+        su_t = torch.from_numpy(su).float()
+        kw = dict(s_up=su_t, s_down=torch.from_numpy(sd).float(), scale_dtype=n8.F32)
+    else:
+        group = 32 if "g32" in fmt else 128
+        sdt = torch.float32 if "f32" in fmt else torch.float16
+        qu, qd = quantize_int4(wu, group, sdt), quantize_int4(wd, group, sdt)
+        wu_f = torch.from_numpy(Q.int4_dequantize(qu.packed.numpy(), qu.scales.float().numpy(), group))
+        wd_f = torch.from_numpy(Q.int4_dequantize(qd.packed.numpy(), qd.scales.float().numpy(), group))
+        # the device widens q * s to bf16 once (fp32 product, RNE)
+        wu_f, wd_f = B.round_bf16(wu_f), B.round_bf16(wd_f)
+        code, dev_up, dev_dn = n8.INT4, qu.packed, qd.packed
+        kw = dict(s_up=qu.scales, s_down=qd.scales, group=group,
+                  scale_dtype=n8.F16 if sdt == torch.float16 else n8.F32)
+    # the device keeps the FFN hidden activation in bf16: model that rounding
+    if act == "swiglu":
+        ref = _oracle_delta(msg.float(), idx, w, wu_f[:, u:], bu, wd_f, bd, w_gate=wu_f[:, :u],
+                            hidden_bf16=True)
+        dev_up = interleave_gate_up(dev_up[:, :u], dev_up[:, u:])
+        if "s_up" in kw:
+            kw["s_up"] = interleave_gate_up_rows(kw["s_up"][:, :u], kw["s_up"][:, u:])
+    else:
+        ref = _oracle_delta(msg.float(), idx, w, wu_f, bu, wd_f, bd, hidden_bf16=True)
+    kw = {a: (v.contiguous().to(dev) if torch.is_tensor(v) else v) for a, v in kw.items()}
+    up_d, dn_d = dev_up.contiguous().to(dev), dev_dn.contiguous().to(dev)
+    bu_d, bd_d = bu.to(dev), bd.to(dev)
+    ex = _experts_struct(n8, code, n8.ACT_SWIGLU if act == "swiglu" else n8.ACT_GELU, e, h, u,
+                         up_d, dn_d, b_up=bu_d, b_down=bd_d, **kw)
+    got = _run_delta(n8, ex, msg.to(dev), idx.to(torch.int32).to(dev), w.to(dev))
+    torch.testing.assert_close(got, ref, rtol=1e-2, atol=1e-2)
 
 
 def test_invalid_arguments_are_rejected():
