@@ -10,9 +10,12 @@ U 2816 SwiGLU, 6 loops, 16384 tokens.  The other workloads are reported under
 
 Roofline: the dominant kernel of each workload (the expert up / gate GEMM) is
 timed with HIP events around its launches (on the stream the kernels run on)
-in a second pass of the same K steps; achieved = algorithmic flops (prefill,
-MFMA-bound) or algorithmic bytes (decode, HBM-bound) per launch / its average
-duration.  Algorithmic work follows the per-token / per-loop accounting of
+inside the timed region; achieved = algorithmic flops (prefill, MFMA-bound)
+or algorithmic bytes (decode, HBM-bound) per launch / its average duration.
+A second pass of the same K steps times every stage (stage_ms_per_step).
+`traffic` is the HBM bytes per launch of that kernel measured with rocprofv3
+--pmc FETCH_SIZE and WRITE_SIZE (scaled by the same counters' reading of a
+plain copy, `--copy-calibration`), read from profiles/hbm_traffic.md.  Algorithmic work follows the per-token / per-loop accounting of
 the block: F_t = 2HE + 2(H+L)Ek + 2H^2|D_t| + c H U |S_t| (c = 4 GELU, 6
 SwiGLU), with |D_t| / |S_t| counted from the run's own routing.
 """
@@ -38,6 +41,29 @@ DESC = {
     "c4": "int4 experts g128 fp16 scales: H2048 E64 k2 m4 U1408 GELU R4 N2176 (128 decode + 2048 prefill)",
 }
 BOUND = {"c1": "mfma", "c2": "hbm", "c3": "mfma", "c4": "hbm"}
+# the up / gate GEMM kernel the launcher picks for each workload's shapes
+# (rows per expert, N_out, format); rocprof summaries under profiles/ name it too
+UP_KERNEL = {
+    "c1": "k_gemm_ring<256,4,4> (bf16 SwiGLU, LDS-DMA ring)",
+    "c2": "k_gemm_skinny<fp8,SwiGLU,4,1> (weight streaming)",
+    "c3": "k_gemm_ring<128,6,4> (bf16 GELU, LDS-DMA ring)",
+    "c4": "k_gemm_mfma<128,128,64,2,2> (int4 GELU)",
+}
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.md")
+
+
+def measured_traffic(name):
+    """HBM bytes per launch of the workload's up GEMM from the committed pmc
+    summary: lines `traffic <workload> <bytes>` (None when not measured)."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                parts = line.strip().strip("`").split()
+                if len(parts) == 3 and parts[0] == "traffic" and parts[1] == name:
+                    return float(parts[2])
+    except OSError:
+        pass
+    return None
 
 
 def log(*a):
@@ -125,7 +151,11 @@ def run_workload(name, steps, warmup):
         torch.cuda.synchronize()
         log(name, "timing", steps, "steps")
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        # timed region: HIP events around the up GEMM launches only (on the
+        # block's stream), so the dominant kernel is timed in the same steps
+        up_timer = nat.StageTimer(stages=["up_gemm"], capacity=steps * r + 16)
         torch.cuda.synchronize()
+        up_timer.start()
         t0 = time.perf_counter()
         e0.record()
         for _ in range(steps):
@@ -134,7 +164,9 @@ def run_workload(name, steps, warmup):
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         ms = e0.elapsed_time(e1) / steps
-        # second pass: HIP events around every stage launch
+        up = up_timer.stop().get("up_gemm", [])
+        up_timer.close()
+        # second pass: HIP events around every stage launch (breakdown)
         timer = nat.StageTimer(capacity=steps * r * len(nat.STAGES) + 16)
         timer.start()
         for _ in range(steps):
@@ -143,7 +175,6 @@ def run_workload(name, steps, warmup):
         timer.close()
     acc = accounting(layer, h, x0)
     flops, bytes_ = block_work(layer, n, acc)
-    up = stages.get("up_gemm", [])
     up_ms = sum(up) / max(len(up), 1)
     hidden, u = layer.hidden_size, layer.expert_ffn_size
     upc = 4 if layer.expert_activation == "swiglu" else 2
@@ -153,8 +184,8 @@ def run_workload(name, steps, warmup):
     if bound == "mfma":
         ach = up_flops / (up_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": None,
-                "kernel": "expert up/gate grouped GEMM (k_gemm_mfma)",
+                "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic(name),
+                "kernel": UP_KERNEL[name],
                 "work_per_launch": f"{up_flops:.4g} flop", "avg_launch_ms": round(up_ms, 4)}
         blk = flops / (ms * 1e-3) / 1e12
         block_roof = {"bound": "mfma", "achieved": round(blk, 1), "unit": "TFLOP/s",
@@ -162,8 +193,8 @@ def run_workload(name, steps, warmup):
     else:
         ach = up_bytes / (up_ms * 1e-3) / 1e9
         roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": None,
-                "kernel": "expert up/gate grouped GEMM (k_gemm_mfma)",
+                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": measured_traffic(name),
+                "kernel": UP_KERNEL[name],
                 "work_per_launch": f"{up_bytes:.4g} B", "avg_launch_ms": round(up_ms, 4)}
         blk = bytes_ / (ms * 1e-3) / 1e9
         block_roof = {"bound": "hbm", "achieved": round(blk, 1), "unit": "GB/s",
@@ -184,7 +215,7 @@ def run_workload(name, steps, warmup):
     return res
 
 
-def cpu_baseline(name="c1", sample_tokens=1024, budget_s=20.0):
+def cpu_baseline(name="c1", sample_tokens=8192, budget_s=30.0):
     """The oracle's faithful restatement (dense edge projection, per-expert
     masks, fp32 math on the bf16-valued weights) on the host cores."""
     import torch
@@ -220,6 +251,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workloads", default="c1,c2,c3,c4")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
+                    help="only run a plain device copy of BYTES (to scale rocprof FETCH/WRITE_SIZE)")
     a = ap.parse_args()
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build's hot path runs on a single MI355X "
@@ -229,6 +262,14 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         sys.exit(1)
+    if a.copy_calibration:
+        src = torch.ones(a.copy_calibration, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes": a.copy_calibration, "copies": 3}), flush=True)
+        return
     names = [x for x in a.workloads.split(",") if x]
     results = {nm: run_workload(nm, a.steps, a.warmup) for nm in names}
     head = results.get("c1") or results[names[0]]
