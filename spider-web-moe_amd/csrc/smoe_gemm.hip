@@ -329,7 +329,10 @@ typedef __attribute__((address_space(3))) void* lds_vptr;
 typedef __attribute__((address_space(1))) void* gbl_vptr;
 
 template <int BN, int NS, int GM, int EPI>
-__global__ __launch_bounds__(256) void k_gemm_ring(const GemmArgs p) {
+// A ring of 3 stages (72 KB of LDS at BN = 128) lets two workgroups share a
+// CU (registers are held to 256 per lane by the launch bound), so one's
+// epilogue math and DMA waits overlap the other's MFMAs.
+__global__ __launch_bounds__(256, NS <= 3 ? 2 : 1) void k_gemm_ring(const GemmArgs p) {
   constexpr int BM = 256;
   constexpr int TM = BM / 2, TN = BN / 2;
   constexpr int FM = TM / 16, FN = TN / 16;
@@ -888,12 +891,11 @@ int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
       return rpg <= 16 ? launch_skinny<2, 1>(a, s) : launch_skinny<2, 2>(a, s);
     return rpg <= 8 ? launch_skinny<4, 1>(a, s) : launch_skinny<4, 2>(a, s);
   }
-  // large bf16 problems: 256 x 256 tiles (N_out and K multiples of the tile)
+  // large bf16 problems: 256 x 128 tiles, two workgroups per CU (N_out % 128, K % 64)
   if (a.fmt == SMOE_BF16 && a.out_dtype == SMOE_BF16 && a.epi != EPI_F32_BIAS && a.K % 64 == 0 &&
       a.ldw % 8 == 0 && a.lda % 8 == 0 && a.ldo % 8 == 0 &&
       (a.G == 0 ? a.single_rows : a.max_rows / (a.G > 0 ? a.G : 1)) >= 256) {
-    if (a.N_out % 256 == 0) return launch_ring<256, 4, 4>(a, s);
-    if (a.N_out % 128 == 0) return launch_ring<128, 6, 4>(a, s);
+    if (a.N_out % 128 == 0) return launch_ring<128, 3, 4>(a, s);
   }
   const bool b64 = bk == 64;
   // narrow outputs (router / edge logits, N_out = E): 64-row tiles, one

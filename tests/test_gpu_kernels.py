@@ -326,8 +326,8 @@ def test_invalid_arguments_are_rejected():
 
 @pytest.mark.parametrize("act", ["gelu", "swiglu"])
 def test_large_bf16_experts_ragged_groups(act):
-    """Shapes that take the 256 x 256 tile path (N_out % 256 == 0, >= 256 rows
-    per expert on average) with skewed routing: empty experts, single-row
+    """Shapes that take the large-tile LDS-DMA ring path (N_out % 128 == 0,
+    >= 256 rows per expert on average) with skewed routing: empty experts, single-row
     experts and experts spanning several tiles."""
     from spider_moe_amd.quant import interleave_gate_up
     n8 = nat()
