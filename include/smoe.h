@@ -185,7 +185,8 @@ SMOE_API int smoe_router_topk(const void* x, int act_dtype, int N, int H, const 
  * rows [N*K] (token per row; entries past offsets[E] are unspecified),
  * row_w [N*K], tok_row [N,K] (row of each distinct positive (token, expert),
  * in ascending expert order, -1 padded).  Expert ids outside [0, E) match
- * no expert and are dropped, as the reference's per-expert masks drop them. */
+ * no expert and are dropped, as the reference's per-expert masks drop them.
+ * 1 <= K <= 256, 1 <= E <= 256. */
 SMOE_API size_t smoe_dispatch_workspace_bytes(int N, int K, int E);
 SMOE_API int smoe_dispatch_plan(const int32_t* idx, const float* w, int N, int K, int E,
                                 int32_t* counts, int32_t* offsets, int32_t* rows, float* row_w,
@@ -196,7 +197,7 @@ SMOE_API int smoe_dispatch_plan(const int32_t* idx, const float* w, int N, int K
  * forge/ep/dispatch.py:145-185; spider_expert_grouped_gemm_f32
  * spider_kernels.h:89-92): msg [N,H] in ffn dtype (f32 for f32 experts,
  * bf16 otherwise), idx i32 / w f32 [N,K] -> delta [N,H] in out_dtype
- * (SMOE_F32 or SMOE_BF16). */
+ * (SMOE_F32 or SMOE_BF16).  1 <= K <= 64. */
 SMOE_API size_t smoe_expert_delta_workspace_bytes(const smoe_experts* ex, int N, int K);
 SMOE_API int smoe_expert_delta(const smoe_experts* ex, const void* msg, const int32_t* idx,
                                const float* w, int N, int K, void* delta, int out_dtype,

@@ -498,7 +498,7 @@ SMOE_API size_t smoe_dispatch_workspace_bytes(int N, int K, int E) {
 SMOE_API int smoe_dispatch_plan(const int32_t* idx, const float* w, int N, int K, int E,
                                 int32_t* counts, int32_t* offsets, int32_t* rows, float* row_w,
                                 int32_t* tok_row, void* ws, size_t ws_bytes, void* stream) {
-  if (N < 0 || K < 1 || E < 1 || E > 256) return fail(SMOE_EINVAL, "plan shape");
+  if (N < 0 || K < 1 || K > 256 || E < 1 || E > 256) return fail(SMOE_EINVAL, "plan shape");
   if (!counts || !offsets) return fail(SMOE_EINVAL, "null buffer");
   if (N > 0 && (!idx || !w || !rows || !row_w || !tok_row || !ws))
     return fail(SMOE_EINVAL, "null buffer");
@@ -530,7 +530,7 @@ SMOE_API int smoe_expert_delta(const smoe_experts* ex, const void* msg, const in
   if (!ex) return fail(SMOE_EINVAL, "null experts");
   int rc = check_experts(*ex, ex->H);
   if (rc != SMOE_OK) return rc;
-  if (N < 0 || K < 1) return fail(SMOE_EINVAL, "shape");
+  if (N < 0 || K < 1 || K > 64) return fail(SMOE_EINVAL, "shape (1 <= top_k <= 64)");
   if (out_dtype != SMOE_F32 && out_dtype != SMOE_BF16) return fail(SMOE_EUNSUPPORTED, "out dtype");
   if (N == 0) return SMOE_OK;
   if (!msg || !idx || !w || !delta || !ws) return fail(SMOE_EINVAL, "null buffer");

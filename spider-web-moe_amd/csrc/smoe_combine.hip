@@ -15,8 +15,12 @@
 
 namespace smoe {
 
-__device__ __forceinline__ void load8(const void* base, int dtype, int64_t off, float* v) {
-  if (dtype == SMOE_F32) {
+// 8 consecutive elements of a bf16 or f32 array <-> 8 floats, as 16-byte
+// vectors.  The dtype is a template argument: a run-time dtype branch would
+// make each load wait before the branches join.
+template <int DT>
+__device__ __forceinline__ void load8(const void* base, int64_t off, float* v) {
+  if constexpr (DT == SMOE_F32) {
     const f32x4 a = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(base) + off);
     const f32x4 b = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(base) + off + 4);
 #pragma unroll
@@ -34,8 +38,9 @@ __device__ __forceinline__ void load8(const void* base, int dtype, int64_t off, 
   }
 }
 
-__device__ __forceinline__ void store8(void* base, int dtype, int64_t off, const float* v) {
-  if (dtype == SMOE_F32) {
+template <int DT>
+__device__ __forceinline__ void store8(void* base, int64_t off, const float* v) {
+  if constexpr (DT == SMOE_F32) {
     float* p = reinterpret_cast<float*>(base) + off;
     *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
     *reinterpret_cast<f32x4*>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
@@ -47,88 +52,119 @@ __device__ __forceinline__ void store8(void* base, int dtype, int64_t off, const
   }
 }
 
+// Keeps a loaded value live here, so the compiler issues the loads of a
+// batch together instead of sinking each into the branch that consumes it.
+__device__ __forceinline__ void pin(float x) { asm volatile("" : : "v"(x)); }
+
+// acc += the rows named by the set bits of `live` (lane j of my_row holds a
+// row index when bit j is set), in ascending bit order.  Loads of a batch of
+// rows are issued together; a batch slot past the last row loads row 0 and
+// is not added.
+template <int CPL, int DT>
+__device__ __forceinline__ void gather_add(const void* __restrict__ base, int H,
+                                           int my_row, uint64_t live, float (&acc)[CPL][8]) {
+  constexpr int B = CPL >= 8 ? 1 : 8 / CPL;  // rows per batch (<= 8 x 16 B loads per lane)
+  const int lane = threadIdx.x & 63;
+  while (live) {
+    float v[B][CPL][8];
+    bool use[B];
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      use[b] = live != 0;
+      const int src = use[b] ? __ffsll(static_cast<unsigned long long>(live)) - 1 : 0;
+      live &= live - 1;
+      const int r = __shfl(my_row, src);
+      const int64_t row = use[b] ? r : 0;
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {  // columns past H load column 0 (not stored)
+        const int col = (lane + 64 * c) * 8;
+        load8<DT>(base, row * H + (col < H ? col : 0), v[b][c]);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+#pragma unroll
+      for (int c = 0; c < CPL; ++c)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pin(v[b][c][i]);
+#pragma unroll
+    for (int b = 0; b < B; ++b)
+#pragma unroll
+      for (int c = 0; c < CPL; ++c)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[c][i] += use[b] ? v[b][c][i] : 0.f;
+  }
+}
+
 // CPL = 8-element chunks per lane (H <= 512 * CPL)
-// Lane j (< S) fetches the token's j-th (destination, row) entry; the rows
-// are then broadcast and all their loads issued before any is consumed.
-template <int CPL>
-__global__ __launch_bounds__(256) void k_msg_combine(const void* __restrict__ proj, int pdt,
+// Lane j (< S) holds the token's j-th (destination, row) entry.
+template <int CPL, int PDT, int MDT>
+__global__ __launch_bounds__(256) void k_msg_combine(const void* __restrict__ proj,
                                                      const int32_t* __restrict__ tok_d,
                                                      const int32_t* __restrict__ d_tokrow, int N,
-                                                     int S, int H, void* __restrict__ msg,
-                                                     int mdt) {
+                                                     int S, int H, void* __restrict__ msg) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= N) return;
-  const int64_t e = static_cast<int64_t>(t) * S + lane;
-  const int my_row = (lane < S && tok_d[e] >= 0) ? d_tokrow[e] : -1;
-  const int n = __popcll(__ballot(my_row >= 0));  // entries are packed first (ascending destination)
+  // unconditional loads (lanes past S read entry S-1 and drop it): no
+  // branch for the compiler to wait at
+  const int64_t e = static_cast<int64_t>(t) * S + (lane < S ? lane : S - 1);
+  const int d = tok_d[e];
+  const int r = d_tokrow[e];
+  const int my_row = (lane < S && d >= 0) ? r : -1;  // ascending destination (tok_d is sorted)
   float acc[CPL][8];
 #pragma unroll
   for (int c = 0; c < CPL; ++c)
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[c][i] = 0.f;
-  for (int j = 0; j < n; ++j) {
-    const int64_t row = __shfl(my_row, j);
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      const int col = (lane + 64 * c) * 8;
-      if (col < H) {
-        float v[8];
-        load8(proj, pdt, row * H + col, v);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[c][i] += v[i];
-      }
-    }
-  }
+  gather_add<CPL, PDT>(proj, H, my_row, __ballot(my_row >= 0), acc);
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
     const int col = (lane + 64 * c) * 8;
-    if (col < H) store8(msg, mdt, static_cast<int64_t>(t) * H + col, acc[c]);
+    if (col < H) store8<MDT>(msg, static_cast<int64_t>(t) * H + col, acc[c]);
   }
 }
 
-template <int CPL>
+template <int CPL, int ADT, int YDT>
 __global__ __launch_bounds__(256) void k_epilogue(
-    const void* __restrict__ h, const void* __restrict__ x0, int adt, const void* __restrict__ y,
-    int ydt, const int32_t* __restrict__ tok_e, const float* __restrict__ tok_ew,
+    const void* __restrict__ h, const void* __restrict__ x0, const void* __restrict__ y,
+    const int32_t* __restrict__ tok_e, const float* __restrict__ tok_ew,
     const int32_t* __restrict__ e_tokrow, int N, int K, int H, float alpha, float beta,
     const float* __restrict__ ln_w, const float* __restrict__ ln_b, float eps,
     void* __restrict__ out) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= N) return;
-  // lane j (< K): the token's j-th expert row if its weight is > 0 (rows
-  // with weight <= 0 are dropped from the FFN, sparse_experts.py:56)
-  const int64_t e = static_cast<int64_t>(t) * K + lane;
-  int my_row = -1;
-  if (lane < K && tok_e[e] >= 0 && tok_ew[e] > 0.f) my_row = e_tokrow[e];
-  uint64_t live = __ballot(my_row >= 0);
-  float hv[CPL][8], xv[CPL][8], d[CPL][8];
+  // the token's own rows and the LayerNorm parameters do not depend on the
+  // routing: their loads go out first, with the routing metadata
+  float hv[CPL][8], xv[CPL][8], d[CPL][8], gw[CPL][8], gb[CPL][8];
 #pragma unroll
-  for (int c = 0; c < CPL; ++c) {
+  for (int c = 0; c < CPL; ++c) {  // columns past H load column 0 (not stored)
     const int col = (lane + 64 * c) * 8;
+    const int cc = col < H ? col : 0;
+    const int64_t o = static_cast<int64_t>(t) * H + cc;
 #pragma unroll
     for (int i = 0; i < 8; ++i) d[c][i] = 0.f;
-    if (col < H) {
-      load8(h, adt, static_cast<int64_t>(t) * H + col, hv[c]);
-      load8(x0, adt, static_cast<int64_t>(t) * H + col, xv[c]);
-    }
-  }
-  while (live) {  // ascending expert order (tok_e is ascending)
-    const int j = __ffsll(static_cast<unsigned long long>(live)) - 1;
-    live &= live - 1;
-    const int64_t row = __shfl(my_row, j);
+    load8<ADT>(h, o, hv[c]);
+    load8<ADT>(x0, o, xv[c]);
+    if (ln_w) load8<SMOE_F32>(ln_w, cc, gw[c]);
+    else
 #pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      const int col = (lane + 64 * c) * 8;
-      if (col < H) {
-        float v[8];
-        load8(y, ydt, row * H + col, v);
+      for (int i = 0; i < 8; ++i) gw[c][i] = 1.f;
+    if (ln_b) load8<SMOE_F32>(ln_b, cc, gb[c]);
+    else
 #pragma unroll
-        for (int i = 0; i < 8; ++i) d[c][i] += v[i];
-      }
-    }
+      for (int i = 0; i < 8; ++i) gb[c][i] = 0.f;
   }
+  // lane j (< K): the token's j-th expert row if its weight is > 0 (rows
+  // with weight <= 0 are dropped from the FFN, sparse_experts.py:56); lanes
+  // past K read entry K-1 and drop it
+  const int64_t e = static_cast<int64_t>(t) * K + (lane < K ? lane : K - 1);
+  const int te = tok_e[e];
+  const float tw = tok_ew[e];
+  const int tr = e_tokrow[e];
+  const int my_row = (lane < K && te >= 0 && tw > 0.f) ? tr : -1;
+  gather_add<CPL, YDT>(y, H, my_row, __ballot(my_row >= 0), d);  // ascending expert order
   float s = 0.f;
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
@@ -159,18 +195,16 @@ __global__ __launch_bounds__(256) void k_epilogue(
     if (col < H) {
       float o[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i)
-        o[i] = (d[c][i] - mean) * rstd * (ln_w ? ln_w[col + i] : 1.f) + (ln_b ? ln_b[col + i] : 0.f);
-      store8(out, adt, static_cast<int64_t>(t) * H + col, o);
+      for (int i = 0; i < 8; ++i) o[i] = (d[c][i] - mean) * rstd * gw[c][i] + gb[c][i];
+      store8<ADT>(out, static_cast<int64_t>(t) * H + col, o);
     }
   }
 }
 
-template <int CPL>
-__global__ __launch_bounds__(256) void k_delta_combine(const void* __restrict__ y, int ydt,
+template <int CPL, int YDT, int ODT>
+__global__ __launch_bounds__(256) void k_delta_combine(const void* __restrict__ y,
                                                        const int32_t* __restrict__ tok_row, int N,
-                                                       int K, int H, void* __restrict__ out,
-                                                       int odt) {
+                                                       int K, int H, void* __restrict__ out) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= N) return;
@@ -179,24 +213,13 @@ __global__ __launch_bounds__(256) void k_delta_combine(const void* __restrict__ 
   for (int c = 0; c < CPL; ++c)
 #pragma unroll
     for (int i = 0; i < 8; ++i) d[c][i] = 0.f;
-  for (int j = 0; j < K; ++j) {
-    const int row = tok_row[static_cast<int64_t>(t) * K + j];
-    if (row < 0) continue;
-#pragma unroll
-    for (int c = 0; c < CPL; ++c) {
-      const int col = (lane + 64 * c) * 8;
-      if (col < H) {
-        float v[8];
-        load8(y, ydt, static_cast<int64_t>(row) * H + col, v);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) d[c][i] += v[i];
-      }
-    }
-  }
+  const int r = tok_row[static_cast<int64_t>(t) * K + (lane < K ? lane : K - 1)];
+  const int my_row = lane < K ? r : -1;
+  gather_add<CPL, YDT>(y, H, my_row, __ballot(my_row >= 0), d);  // slot (= ascending expert) order
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
     const int col = (lane + 64 * c) * 8;
-    if (col < H) store8(out, odt, static_cast<int64_t>(t) * H + col, d[c]);
+    if (col < H) store8<ODT>(out, static_cast<int64_t>(t) * H + col, d[c]);
   }
 }
 
@@ -210,16 +233,28 @@ int by_cpl(int H, F&& f) {
   if (H <= 4096) return f(std::integral_constant<int, 8>{});
   return SMOE_EINVAL;
 }
+// dtype code (SMOE_F32 / SMOE_BF16) -> compile-time constant
+template <typename F>
+int by_dt(int dt, F&& f) {
+  if (dt == SMOE_F32) return f(std::integral_constant<int, SMOE_F32>{});
+  if (dt == SMOE_BF16) return f(std::integral_constant<int, SMOE_BF16>{});
+  return SMOE_EUNSUPPORTED;
+}
 int last_rc() { return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP; }
 }  // namespace
 
 int launch_msg_combine(const void* proj, int pdt, const int32_t* tok_d, const int32_t* d_tokrow,
                        int N, int S, int H, void* msg, int mdt, hipStream_t s) {
+  if (S < 1 || S > 64) return SMOE_EINVAL;  // one lane per entry
   if (N <= 0) return SMOE_OK;
   return by_cpl(H, [&](auto cpl) {
-    hipLaunchKernelGGL((k_msg_combine<decltype(cpl)::value>), dim3((N + 3) / 4), dim3(256), 0, s,
-                       proj, pdt, tok_d, d_tokrow, N, S, H, msg, mdt);
-    return last_rc();
+    return by_dt(pdt, [&](auto pd) {
+      return by_dt(mdt, [&](auto md) {
+        hipLaunchKernelGGL((k_msg_combine<decltype(cpl)::value, decltype(pd)::value, decltype(md)::value>),
+                           dim3((N + 3) / 4), dim3(256), 0, s, proj, tok_d, d_tokrow, N, S, H, msg);
+        return last_rc();
+      });
+    });
   });
 }
 
@@ -227,22 +262,32 @@ int launch_epilogue(const void* h, const void* x0, int adt, const void* y, int y
                     const int32_t* tok_e, const float* tok_ew, const int32_t* e_tokrow, int N,
                     int K, int H, float alpha, float beta, const float* ln_w, const float* ln_b,
                     float eps, void* out, hipStream_t s) {
+  if (K < 1 || K > 64) return SMOE_EINVAL;  // one lane per entry
   if (N <= 0) return SMOE_OK;
   return by_cpl(H, [&](auto cpl) {
-    hipLaunchKernelGGL((k_epilogue<decltype(cpl)::value>), dim3((N + 3) / 4), dim3(256), 0, s, h,
-                       x0, adt, y, ydt, tok_e, tok_ew, e_tokrow, N, K, H, alpha, beta, ln_w, ln_b,
-                       eps, out);
-    return last_rc();
+    return by_dt(adt, [&](auto ad) {
+      return by_dt(ydt, [&](auto yd) {
+        hipLaunchKernelGGL((k_epilogue<decltype(cpl)::value, decltype(ad)::value, decltype(yd)::value>),
+                           dim3((N + 3) / 4), dim3(256), 0, s, h, x0, y, tok_e, tok_ew, e_tokrow, N,
+                           K, H, alpha, beta, ln_w, ln_b, eps, out);
+        return last_rc();
+      });
+    });
   });
 }
 
 int launch_delta_combine(const void* y, int ydt, const int32_t* tok_row, int N, int K, int H,
                          void* out, int odt, hipStream_t s) {
+  if (K < 1 || K > 64) return SMOE_EINVAL;  // one lane per entry
   if (N <= 0) return SMOE_OK;
   return by_cpl(H, [&](auto cpl) {
-    hipLaunchKernelGGL((k_delta_combine<decltype(cpl)::value>), dim3((N + 3) / 4), dim3(256), 0,
-                       s, y, ydt, tok_row, N, K, H, out, odt);
-    return last_rc();
+    return by_dt(ydt, [&](auto yd) {
+      return by_dt(odt, [&](auto od) {
+        hipLaunchKernelGGL((k_delta_combine<decltype(cpl)::value, decltype(yd)::value, decltype(od)::value>),
+                           dim3((N + 3) / 4), dim3(256), 0, s, y, tok_row, N, K, H, out);
+        return last_rc();
+      });
+    });
   });
 }
 

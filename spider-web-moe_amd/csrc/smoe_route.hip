@@ -129,6 +129,11 @@ int launch_merge_slots(const int32_t* idx, const float* w, int N, int K, int E, 
 }
 
 // ------------------------------------------------------------- edges ----
+// One wave per token, lane d = destination.  The token's KB source slots
+// (KB >= K, a compile-time bucket) are fetched one lane per slot, then all
+// their logit rows at once (slots past K or empty read row 0 and are
+// dropped), so the kernel waits on memory twice.
+template <int KB>
 __global__ __launch_bounds__(256) void k_edge_topm(const float* __restrict__ edge_logit,
                                                    const int32_t* __restrict__ tok_e,
                                                    const int32_t* __restrict__ e_tokrow, int N,
@@ -141,19 +146,32 @@ __global__ __launch_bounds__(256) void k_edge_topm(const float* __restrict__ edg
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= N) return;
   const bool in = lane < E;
+  const int64_t e = static_cast<int64_t>(t) * K + (lane < K ? lane : K - 1);
+  const int src_l = tok_e[e];
+  const int row_l = e_tokrow[e];
+  int row[KB];
+  bool live[KB];
+  float v[KB];
+#pragma unroll
+  for (int j = 0; j < KB; ++j) {
+    const int sj = __shfl(src_l, j);
+    const int rj = __shfl(row_l, j);
+    live[j] = j < K && sj >= 0;  // sources are packed first (ascending expert)
+    row[j] = live[j] ? rj : 0;
+    v[j] = edge_logit[static_cast<int64_t>(row[j]) * E + (in ? lane : 0)];
+  }
   float c = 0.f;
-  for (int j = 0; j < K; ++j) {
-    const int src = tok_e[static_cast<int64_t>(t) * K + j];
-    if (src < 0) break;
-    const int row = e_tokrow[static_cast<int64_t>(t) * K + j];
-    const float v = in ? edge_logit[static_cast<int64_t>(row) * E + lane] : -INFINITY;
+#pragma unroll
+  for (int j = 0; j < KB; ++j) {
+    if (!live[j]) continue;  // uniform
+    const float vj = in ? v[j] : -INFINITY;
     bool sel = false;
     float vmax = 0.f, den = 0.f, rec_v = 0.f;
     int rec_i = 0;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {  // M <= 16
       if (i < M) {
-        float cv = (in && !sel) ? v : -INFINITY;
+        float cv = (in && !sel) ? vj : -INFINITY;
         int ci = (in && !sel) ? lane : kBig;
         wave_argmax(cv, ci);
         if (lane == ci) sel = true;
@@ -165,10 +183,10 @@ __global__ __launch_bounds__(256) void k_edge_topm(const float* __restrict__ edg
         den += expf(cv - vmax);  // softmax over the m values, slot order
       }
     }
-    if (sel) c += expf(v - vmax) / den;
+    if (sel) c += expf(vj - vmax) / den;
     if (lane < M) {
-      edge_idx[static_cast<int64_t>(row) * M + lane] = rec_i;
-      edge_w[static_cast<int64_t>(row) * M + lane] = expf(rec_v - vmax) / den;
+      edge_idx[static_cast<int64_t>(row[j]) * M + lane] = rec_i;
+      edge_w[static_cast<int64_t>(row[j]) * M + lane] = expf(rec_v - vmax) / den;
     }
   }
   const bool nz = in && c != 0.f;
@@ -188,10 +206,19 @@ __global__ __launch_bounds__(256) void k_edge_topm(const float* __restrict__ edg
 int launch_edge_topm(const float* edge_logit, const int32_t* tok_e, const int32_t* e_tokrow,
                      int N, int E, int K, int M, int S, int32_t* edge_idx, float* edge_w,
                      int32_t* tok_d, float* tok_dc, hipStream_t s) {
-  if (E < 1 || E > 64 || M < 1 || M > E || M > 16 || S < 1 || S > 64) return SMOE_EINVAL;
+  if (E < 1 || E > 64 || M < 1 || M > E || M > 16 || S < 1 || S > 64 || K < 1 || K > 16)
+    return SMOE_EINVAL;
   if (N <= 0) return SMOE_OK;
-  hipLaunchKernelGGL(k_edge_topm, dim3((N + 3) / 4), dim3(256), 0, s, edge_logit, tok_e, e_tokrow,
-                     N, E, K, M, S, edge_idx, edge_w, tok_d, tok_dc);
+  const dim3 grid((N + 3) / 4), block(256);
+#define SMOE_EDGE_TOPM(KB)                                                                     \
+  hipLaunchKernelGGL(k_edge_topm<KB>, grid, block, 0, s, edge_logit, tok_e, e_tokrow, N, E, K, M, \
+                     S, edge_idx, edge_w, tok_d, tok_dc)
+  if (K <= 1) SMOE_EDGE_TOPM(1);
+  else if (K <= 2) SMOE_EDGE_TOPM(2);
+  else if (K <= 4) SMOE_EDGE_TOPM(4);
+  else if (K <= 8) SMOE_EDGE_TOPM(8);
+  else SMOE_EDGE_TOPM(16);
+#undef SMOE_EDGE_TOPM
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 
