@@ -299,6 +299,69 @@ __device__ __forceinline__ void store4(const GemmArgs& p, int fmt, int g, int ro
   }
 }
 
+// Epilogue of a 256-row LDS-staged tile: math in registers, the bf16 tile
+// staged in the (idle) LDS ring, then coalesced 16-byte row stores.  Staging
+// layout: row r, 16-byte chunk c at chunk c ^ (r & 15) (rows of OW bf16, no
+// padding; r & 7 for 8-chunk rows).  The caller has synchronised the
+// workgroup after its last read of the ring.
+template <int BM, int BN, int TM, int TN, int NT, int EPI>
+__device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const f32x4 (&acc)[TN / 16][TM / 16],
+                                              int g, int m0, int mrows, int n0, int wm, int wn,
+                                              uint8_t* ring) {
+  constexpr int FM = TM / 16, FN = TN / 16;
+  constexpr int OW = (EPI == EPI_SWIGLU) ? BN / 2 : BN;  // output columns of the tile
+  constexpr int SWM = (OW / 8 >= 16 ? 16 : OW / 8) - 1;  // chunk swizzle mask
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int fr = lane & 15, fc = lane >> 4;
+  uint16_t* stg = reinterpret_cast<uint16_t*>(ring);
+  auto stg_at = [&](int r, int col) {  // col: multiple of 4
+    return stg + r * OW + ((((col >> 3) ^ (r & SWM)) << 3) | (col & 7));
+  };
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int lr = wm * TM + i * 16 + fr;
+    const bool live = lr < mrows;
+    const int row = m0 + (live ? lr : 0);
+    float rs = 0.f;
+    if constexpr (EPI == EPI_ROWSCALE || EPI == EPI_DOWN) rs = live ? p.row_scale[row] : 0.f;
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int cl = wn * TN + j * 16 + fc * 4;  // channel within the tile
+      const int c = n0 + cl;
+      float r[4];
+      if constexpr (EPI == EPI_SWIGLU) {
+        if ((j & 3) >= 2) continue;
+        const int ul = (cl >> 6) * 32 + (cl & 31);
+        const int u = (n0 >> 1) + ul;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) r[q] = silu(acc[j][i][q]) * (acc[j + 2][i][q] + bias_at(p, g, u + q));
+        *reinterpret_cast<u32x2*>(stg_at(lr, ul)) = u32x2{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3])};
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float a = acc[j][i][q];
+          if constexpr (EPI == EPI_ROWSCALE) r[q] = a * rs;
+          else if constexpr (EPI == EPI_GELU) r[q] = gelu_erf(a + bias_at(p, g, c + q));
+          else if constexpr (EPI == EPI_DOWN) r[q] = (a + bias_at(p, g, c + q)) * rs;
+          else r[q] = a + bias_at(p, g, c + q);
+        }
+        *reinterpret_cast<u32x2*>(stg_at(lr, cl)) = u32x2{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3])};
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int CPR_OUT = OW / 8;  // 16-byte chunks per output row
+  const int ncol0 = (EPI == EPI_SWIGLU) ? (n0 >> 1) : n0;
+  const int ncols = (EPI == EPI_SWIGLU) ? (p.N_out >> 1) : p.N_out;  // a last tile may be partial
+  uint16_t* out = reinterpret_cast<uint16_t*>(p.out);
+  for (int q = tid; q < BM * CPR_OUT; q += NT) {
+    const int r = q / CPR_OUT, cc = (q % CPR_OUT) * 8;
+    if (r < mrows && ncol0 + cc < ncols)
+      *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(m0 + r) * p.ldo + ncol0 + cc) =
+          *reinterpret_cast<const u32x4*>(stg_at(r, cc));
+  }
+}
+
 // ------------------------------------------------- MFMA, LDS-DMA ring ----
 // 256 x BN block tile (BN = 256 or 128), 4 waves in a 2 x 2 grid, wave tile
 // 128 x BN/2.  K advances 32 per stage; operands go global -> LDS directly
@@ -324,6 +387,8 @@ __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (0xF << 8));
 }
+// s_waitcnt lgkmcnt(0) (vmcnt / expcnt left at "no wait")
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
 
 typedef __attribute__((address_space(3))) void* lds_vptr;
 typedef __attribute__((address_space(1))) void* gbl_vptr;
@@ -340,6 +405,8 @@ __global__ __launch_bounds__(256, NS <= 3 ? 2 : 1) void k_gemm_ring(const GemmAr
   constexpr int A_LD = BM / 16 / 4, B_LD = BN / 16 / 4;  // DMA instructions per wave per stage
   constexpr int LD = A_LD + B_LD;
   static_assert(EPI != EPI_SWIGLU || TN % 64 == 0, "SwiGLU pairs 32-channel blocks");
+  static_assert(BM * ((EPI == EPI_SWIGLU) ? BN / 2 : BN) * 2 <= NS * STAGE,
+                "output staging fits in the ring");
   __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE];
 
   int g, m0, mrows, n0;
@@ -403,15 +470,18 @@ __global__ __launch_bounds__(256, NS <= 3 ? 2 : 1) void k_gemm_ring(const GemmAr
 
   const int KT = p.K / 32;
   // one stage: make stage s+1 resident and read its fragments into the
-  // other set, then the MFMAs of stage s
+  // other set, then the MFMAs of stage s.  Stage s's fragments are in
+  // registers by the barrier (lgkmcnt(0)), so its slot takes stage s+NS:
+  // NS slots keep NS-1 stages in flight while the registers hold the NS-th.
   auto step = [&](int s, bf16x8 (&wc)[FN], bf16x8 (&ac)[FM], bf16x8 (&wn_)[FN],
                   bf16x8 (&an)[FM]) {
     if (s + 1 < KT) {
-      // stage s+1 landed (stages s+2 .. s+NS-2 may still be in flight)
-      if (s + NS - 2 < KT) wait_vmcnt<(NS - 3) * LD>();
+      // stage s+1 landed (stages s+2 .. s+NS-1 may still be in flight)
+      if (s + NS - 1 < KT) wait_vmcnt<(NS - 2) * LD>();
       else wait_vmcnt<0>();
+      wait_lgkm0();
       __builtin_amdgcn_s_barrier();
-      if (s + NS - 1 < KT) issue(s + NS - 1);  // into the slot stage s-1 used
+      if (s + NS < KT) issue(s + NS);  // into the slot stage s used
       read_frags(s + 1, wn_, an);
     }
 #pragma unroll
@@ -421,11 +491,11 @@ __global__ __launch_bounds__(256, NS <= 3 ? 2 : 1) void k_gemm_ring(const GemmAr
         acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wc[j], ac[i], acc[j][i], 0, 0, 0);
   };
 
-  // prologue: stages 0 .. NS-2 in flight, stage 0 landed everywhere
+  // prologue: stages 0 .. NS-1 in flight, stage 0 landed everywhere
 #pragma unroll
-  for (int st = 0; st < NS - 1; ++st)
+  for (int st = 0; st < NS; ++st)
     if (st < KT) issue(st);
-  if (KT >= NS - 1) wait_vmcnt<(NS - 2) * LD>();
+  if (KT >= NS) wait_vmcnt<(NS - 1) * LD>();
   else wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();
   read_frags(0, wf0, af0);
@@ -436,60 +506,126 @@ __global__ __launch_bounds__(256, NS <= 3 ? 2 : 1) void k_gemm_ring(const GemmAr
     step(s + 1, wf1, af1, wf0, af0);
   }
 
-  // ---- epilogue: math in registers, bf16 tile staged in the (idle) LDS
-  // ring, then coalesced 16-byte row stores.  Staging layout: row r, 16-byte
-  // chunk c at chunk c ^ (r & 15) (rows of OW bf16, no padding; r & 7 for
-  // 8-chunk rows).
-  constexpr int OW = (EPI == EPI_SWIGLU) ? BN / 2 : BN;  // output columns of the tile
-  static_assert(BM * OW * 2 <= NS * STAGE, "output staging fits in the ring");
-  constexpr int SWM = (OW / 8 >= 16 ? 16 : OW / 8) - 1;  // chunk swizzle mask
   __syncthreads();  // every wave is done with the ring (no DMA is outstanding here)
-  uint16_t* stg = reinterpret_cast<uint16_t*>(ring);
-  auto stg_at = [&](int r, int col) {  // col: multiple of 4
-    return stg + r * OW + ((((col >> 3) ^ (r & SWM)) << 3) | (col & 7));
-  };
+  tile_epilogue<BM, BN, TM, TN, 256, EPI>(p, acc, g, m0, mrows, n0, wm, wn, ring);
+}
+
+// --------------------------------------------- MFMA, ping-pong 8 waves ----
+// 256 x 256 block tile, 8 waves: wave w and w + 4 share SIMD w % 4, wave tile
+// 128 x 64 (rows 128 (w >> 2), channels 64 (w & 3)).  The two wave groups
+// (w < 4, w >= 4) run half a K step apart and alternate between a memory
+// phase (DMA issue for a later stage, fragment reads of the next stage) and
+// an MFMA phase, so on every SIMD one wave feeds the matrix core while its
+// partner moves data.  Two workgroup barriers per K step keep them in
+// lock-step:
+//
+//   group 0:  MEM(0) | MFMA(0) | MEM(1)  | MFMA(1) | ...           | MFMA(KT-1)
+//   group 1:  ------ | MEM(0)  | MFMA(0) | MEM(1)  | ... | MFMA(KT-1)
+//
+// MEM(k) issues stage k+NS-1 into the slot of stage k-1 (read by both groups'
+// MEM(k-1), which end with lgkmcnt(0) before their barriers), reads stage k's
+// fragments, then waits for its own part of stage k+1 (vmcnt) so the next
+// barrier certifies stage k+1 for both groups.  LDS layout and DMA scheme as
+// in the ring kernel (32-bf16 rows, chunk c of row r at c ^ ((r >> 1) & 3)).
+template <int NS, int GM, int EPI>
+__global__ __launch_bounds__(512) void k_gemm_pp(const GemmArgs p) {
+  constexpr int BM = 256, BN = 256, TM = 128, TN = 64;
+  constexpr int FM = TM / 16, FN = TN / 16;
+  constexpr int A_BYTES = BM * 64, B_BYTES = BN * 64, STAGE = A_BYTES + B_BYTES;
+  constexpr int A_LD = BM / 16 / 8, B_LD = BN / 16 / 8;  // DMA instructions per wave per stage
+  constexpr int LD = A_LD + B_LD;
+  static_assert(NS >= 2, "ring depth");
+  static_assert(BM * ((EPI == EPI_SWIGLU) ? BN / 2 : BN) * 2 <= NS * STAGE,
+                "output staging fits in the ring");
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE];
+
+  int g, m0, mrows, n0;
+  if (!big_tile<BM, BN, GM>(p, g, m0, mrows, n0)) return;  // workgroup-uniform
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int grp = wave >> 2;
+  const int wm = grp, wn = wave & 3;
+
+  // DMA sources: instruction j of wave w covers rows 16 (8 j + w) ..
+  const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A);
+  const uint16_t* W = reinterpret_cast<const uint16_t*>(p.W) + g * p.w_gstride;
+  const uint16_t* asrc[A_LD];
+  const uint16_t* bsrc[B_LD];
+  {
+    const int pr = lane >> 2, pc = lane & 3;
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int lr = wm * TM + i * 16 + fr;
-    const bool live = lr < mrows;
-    const int row = m0 + (live ? lr : 0);
-    float rs = 0.f;
-    if constexpr (EPI == EPI_ROWSCALE || EPI == EPI_DOWN) rs = live ? p.row_scale[row] : 0.f;
+    for (int j = 0; j < A_LD; ++j) {
+      const int r = (8 * j + wave) * 16 + pr;
+      const int rr = r < mrows ? r : 0;  // rows past the group end: valid data, never stored
+      const int ar = p.a_rows ? p.a_rows[m0 + rr] : (m0 + rr);
+      asrc[j] = A + static_cast<int64_t>(ar) * p.lda + ((pc ^ ((r >> 1) & 3)) << 3);
+    }
 #pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      const int cl = wn * TN + j * 16 + fc * 4;  // channel within the tile
-      const int c = n0 + cl;
-      float r[4];
-      if constexpr (EPI == EPI_SWIGLU) {
-        if ((j & 3) >= 2) continue;
-        const int ul = (cl >> 6) * 32 + (cl & 31);
-        const int u = (n0 >> 1) + ul;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) r[q] = silu(acc[j][i][q]) * (acc[j + 2][i][q] + bias_at(p, g, u + q));
-        *reinterpret_cast<u32x2*>(stg_at(lr, ul)) = u32x2{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3])};
-      } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float a = acc[j][i][q];
-          if constexpr (EPI == EPI_ROWSCALE) r[q] = a * rs;
-          else if constexpr (EPI == EPI_GELU) r[q] = gelu_erf(a + bias_at(p, g, c + q));
-          else if constexpr (EPI == EPI_DOWN) r[q] = (a + bias_at(p, g, c + q)) * rs;
-          else r[q] = a + bias_at(p, g, c + q);
-        }
-        *reinterpret_cast<u32x2*>(stg_at(lr, cl)) = u32x2{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3])};
-      }
+    for (int j = 0; j < B_LD; ++j) {
+      const int r = (8 * j + wave) * 16 + pr;
+      const int n = n0 + r < p.N_out ? n0 + r : n0;
+      bsrc[j] = W + static_cast<int64_t>(n) * p.ldw + ((pc ^ ((r >> 1) & 3)) << 3);
     }
   }
-  __syncthreads();
-  constexpr int CPR_OUT = OW / 8;  // 16-byte chunks per output row
-  const int ncol0 = (EPI == EPI_SWIGLU) ? (n0 >> 1) : n0;
-  uint16_t* out = reinterpret_cast<uint16_t*>(p.out);
-  for (int q = tid; q < BM * CPR_OUT; q += 256) {
-    const int r = q / CPR_OUT, cc = (q % CPR_OUT) * 8;
-    if (r < mrows)
-      *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(m0 + r) * p.ldo + ncol0 + cc) =
-          *reinterpret_cast<const u32x4*>(stg_at(r, cc));
+  auto issue = [&](int stage) {  // DMA of K slice `stage` into ring slot stage % NS
+    uint8_t* base = ring + (stage % NS) * STAGE;
+    const int k0 = stage * 32;
+#pragma unroll
+    for (int j = 0; j < A_LD; ++j)
+      __builtin_amdgcn_global_load_lds((gbl_vptr)(asrc[j] + k0),
+                                       (lds_vptr)(base + (8 * j + wave) * 1024), 16, 0, 0);
+#pragma unroll
+    for (int j = 0; j < B_LD; ++j)
+      __builtin_amdgcn_global_load_lds((gbl_vptr)(bsrc[j] + k0),
+                                       (lds_vptr)(base + A_BYTES + (8 * j + wave) * 1024), 16, 0, 0);
+  };
+  const int fr = lane & 15, fc = lane >> 4;
+  bf16x8 wf[FN], af[FM];
+  auto read_frags = [&](int stage) {
+    const uint8_t* sa = ring + (stage % NS) * STAGE;
+    const uint8_t* sb = sa + A_BYTES;
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      wf[j] = *reinterpret_cast<const bf16x8*>(sb + swz32(wn * TN + j * 16 + fr, fc));
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+      af[i] = *reinterpret_cast<const bf16x8*>(sa + swz32(wm * TM + i * 16 + fr, fc));
+  };
+
+  f32x4 acc[FN][FM];
+#pragma unroll
+  for (int j = 0; j < FN; ++j)
+#pragma unroll
+    for (int i = 0; i < FM; ++i) acc[j][i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int KT = p.K / 32;
+  // prologue: stages 0 .. NS-2 in flight, stage 0 landed everywhere
+#pragma unroll
+  for (int st = 0; st < NS - 1; ++st)
+    if (st < KT) issue(st);
+  if (KT >= NS - 1) wait_vmcnt<(NS - 2) * LD>();
+  else wait_vmcnt<0>();
+  __builtin_amdgcn_s_barrier();
+  if (grp == 1) __builtin_amdgcn_s_barrier();  // group 1 starts half a step behind
+  for (int k = 0; k < KT; ++k) {
+    // MEM(k)
+    if (k + NS - 1 < KT) issue(k + NS - 1);
+    read_frags(k);
+    if (k + 1 < KT) {  // own part of stage k+1 landed (stages k+2 .. k+NS-1 may fly)
+      if (k + NS - 1 < KT) wait_vmcnt<(NS - 2) * LD>();
+      else wait_vmcnt<0>();
+    }
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+    // MFMA(k)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[j][i], 0, 0, 0);
+    if (grp == 0 || k + 1 < KT) __builtin_amdgcn_s_barrier();
   }
+  __syncthreads();  // every wave is done with the ring (no DMA is outstanding here)
+  tile_epilogue<BM, BN, TM, TN, 512, EPI>(p, acc, g, m0, mrows, n0, wm, wn, ring);
 }
 
 // --------------------------------------------------------------- skinny ----
@@ -803,6 +939,21 @@ int launch_ring(const GemmArgs& a, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 
+template <int NS, int GM>
+int launch_pp(const GemmArgs& a, hipStream_t s) {
+  const int tiles = max_tiles(a, 256) * ((a.N_out + 255) / 256);
+  if (tiles == 0) return SMOE_OK;
+  const dim3 grid(tiles), block(512);
+  switch (a.epi) {
+    case EPI_ROWSCALE: hipLaunchKernelGGL((k_gemm_pp<NS, GM, EPI_ROWSCALE>), grid, block, 0, s, a); break;
+    case EPI_GELU: hipLaunchKernelGGL((k_gemm_pp<NS, GM, EPI_GELU>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU: hipLaunchKernelGGL((k_gemm_pp<NS, GM, EPI_SWIGLU>), grid, block, 0, s, a); break;
+    case EPI_DOWN: hipLaunchKernelGGL((k_gemm_pp<NS, GM, EPI_DOWN>), grid, block, 0, s, a); break;
+    default: return SMOE_EINVAL;
+  }
+  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
 template <int BM, int BN>
 int launch_f32_bn(const GemmArgs& a, hipStream_t s) {
   const dim3 grid(max_tiles(a, BM), (a.N_out + BN - 1) / BN);
@@ -891,10 +1042,14 @@ int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
       return rpg <= 16 ? launch_skinny<2, 1>(a, s) : launch_skinny<2, 2>(a, s);
     return rpg <= 8 ? launch_skinny<4, 1>(a, s) : launch_skinny<4, 2>(a, s);
   }
-  // large bf16 problems: 256 x 128 tiles, two workgroups per CU (N_out % 128, K % 64)
+  // large bf16 problems (K % 64): 256 x 256 tiles, 8 waves in two ping-pong
+  // groups when N_out % 256 == 0; otherwise 256 x 128 ring tiles, two
+  // workgroups per CU (a half-empty 256-wide last tile costs more than the
+  // ring's weaker main loop)
   if (a.fmt == SMOE_BF16 && a.out_dtype == SMOE_BF16 && a.epi != EPI_F32_BIAS && a.K % 64 == 0 &&
       a.ldw % 8 == 0 && a.lda % 8 == 0 && a.ldo % 8 == 0 &&
       (a.G == 0 ? a.single_rows : a.max_rows / (a.G > 0 ? a.G : 1)) >= 256) {
+    if (a.N_out % 256 == 0) return launch_pp<4, 4>(a, s);
     if (a.N_out % 128 == 0) return launch_ring<128, 3, 4>(a, s);
   }
   const bool b64 = bk == 64;
