@@ -641,11 +641,12 @@ __global__ __launch_bounds__(512) void k_gemm_pp(const GemmArgs p) {
 // run to run; the epilogue writes 4 consecutive channels per lane.
 // Rows go in passes of 16*RT (a single-group GEMM spreads its passes over
 // grid.z; a grouped one loops over them).
-template <int FMT>
-struct WRaw {
-  u32x4 a, b;
-  float s;
-};
+// A lane's raw 16 consecutive k of one weight row, in its storage format
+// (only what the format needs stays in registers).
+template <int FMT> struct WRaw;
+template <> struct WRaw<SMOE_BF16> { u32x4 a, b; };
+template <> struct WRaw<SMOE_FP8_E4M3> { u32x4 a; };
+template <> struct WRaw<SMOE_INT4> { u32x2 a; float s; };  // 16 nibbles + their group scale
 
 template <int FMT>
 __device__ __forceinline__ WRaw<FMT> skinny_wload(const GemmArgs& p, const uint8_t* wrow, int k,
@@ -655,15 +656,10 @@ __device__ __forceinline__ WRaw<FMT> skinny_wload(const GemmArgs& p, const uint8
     const u32x4* q = reinterpret_cast<const u32x4*>(wrow + 2 * static_cast<int64_t>(k));
     r.a = q[0];
     r.b = q[1];
-    r.s = 1.f;
   } else if constexpr (FMT == SMOE_FP8_E4M3) {
     r.a = *reinterpret_cast<const u32x4*>(wrow + k);
-    r.b = r.a;
-    r.s = 1.f;
-  } else {  // INT4: 16 nibbles, inside one scale group (group_size % 16 == 0)
-    const u32x2 v = *reinterpret_cast<const u32x2*>(wrow + (k >> 1));
-    r.a = u32x4{v.x, v.y, 0u, 0u};
-    r.b = r.a;
+  } else {  // INT4: inside one scale group (group_size % 16 == 0)
+    r.a = *reinterpret_cast<const u32x2*>(wrow + (k >> 1));
     r.s = load_scale(p.S,
                      g * p.s_gstride + static_cast<int64_t>(n) * (p.K / p.group_size) +
                          k / p.group_size,
@@ -824,6 +820,172 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(const GemmArgs p) {
       }
     }
     __syncthreads();  // red is rewritten by the next pass
+  }
+}
+
+// ------------------------------------------------------- weight stream ----
+// Medium rows per group (a few dozen to ~128: mixed decode + prefill steps,
+// quantized experts).  The weights dominate the traffic and each weight is
+// used by every row of its group, so a workgroup owns one group and a strip
+// of 256 output channels (wave w: channels 64 w .. 64 w + 63, four 16-channel
+// MFMA tiles) and all of the group's rows in passes of RT*16.  Per 64-wide K
+// chunk:
+//   weights:     each lane loads the 16 consecutive k at k0 + 16*(lane/16)
+//                of its four channels straight into registers (fp8 16 B,
+//                int4 8 B + its group scale, bf16 32 B), D chunks ahead;
+//   activations: the pass's rows x 64 k (bf16) go global -> registers -> a
+//                double-buffered LDS chunk (128 B rows, 16-byte chunk c of
+//                row r at c ^ (r & 7)), one chunk ahead, one barrier per
+//                chunk (lgkmcnt only, so the weight prefetch stays in flight);
+//   MFMAs:       the step's two MFMAs take the low and the high 8 k of a
+//                lane's 16 (the same permutation for both operands).
+// Results go from registers to memory, 4 consecutive channels per lane.
+template <int FMT, int EPI, int RT, int D>
+__global__ __launch_bounds__(256, 2) void k_gemm_stream(const GemmArgs p) {
+  constexpr int TN = 4;                         // 16-channel tiles per wave
+  constexpr int ROWS = RT * 16;                 // rows per pass
+  constexpr int CHUNK = ROWS * 128;             // bytes of one activation chunk
+  constexpr int AL = ROWS * 8 / 256;            // 16-byte activation loads per lane per chunk
+  constexpr int ESZ2 = FMT == SMOE_BF16 ? 4 : (FMT == SMOE_FP8_E4M3 ? 2 : 1);  // 2 x bytes/elt
+  static_assert(AL >= 1 && ROWS * 8 % 256 == 0, "activation chunk split");
+  static_assert(EPI != EPI_SWIGLU || TN == 4, "SwiGLU pairs channel c with c + 32");
+  __shared__ __attribute__((aligned(1024))) uint8_t abuf[2 * CHUNK];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int q = lane >> 4, l16 = lane & 15;
+  const int g = blockIdx.y;
+  const int n0 = blockIdx.x * 256 + wave * 64;  // this wave's first channel
+  int r_lo, r_hi;
+  if (p.G == 0) {
+    r_lo = 0;
+    r_hi = p.single_rows;
+  } else {
+    r_lo = p.grp_off[g];
+    r_hi = p.grp_off[g + 1];
+  }
+  if (r_hi <= r_lo) return;  // workgroup-uniform, before any barrier
+  const uint8_t* wrow[TN];
+  int wn[TN];
+#pragma unroll
+  for (int t = 0; t < TN; ++t) {
+    const int n = min(n0 + 16 * t + l16, p.N_out - 1);  // channels past N_out: loaded, never stored
+    wn[t] = n;
+    wrow[t] = reinterpret_cast<const uint8_t*>(p.W) +
+              (g * p.w_gstride + static_cast<int64_t>(n) * p.ldw) * ESZ2 / 2;
+  }
+  const int KC = p.K / 64;
+  const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A);
+  for (int m0 = r_lo; m0 < r_hi; m0 += ROWS) {  // passes (uniform)
+    // activation loads: load a of this lane covers row (tid + 256 a) / 8,
+    // logical 16-byte chunk (tid % 8) of the row's 64 k
+    const uint16_t* asrc[AL];
+    int adst[AL];
+#pragma unroll
+    for (int a = 0; a < AL; ++a) {
+      const int e = tid + 256 * a;
+      const int r = e >> 3, c = e & 7;
+      int pr = m0 + r;
+      pr = pr < r_hi ? pr : r_lo;  // rows past the group: a valid row, never stored
+      const int ar = p.a_rows ? p.a_rows[pr] : pr;
+      asrc[a] = A + static_cast<int64_t>(ar) * p.lda + c * 8;
+      adst[a] = r * 128 + ((c ^ (r & 7)) << 4);
+    }
+    u32x4 areg[AL];
+    auto aload = [&](int kc) {
+#pragma unroll
+      for (int a = 0; a < AL; ++a) areg[a] = *reinterpret_cast<const u32x4*>(asrc[a] + kc * 64);
+    };
+    auto astore = [&](int kc) {
+      uint8_t* base = abuf + (kc & 1) * CHUNK;
+#pragma unroll
+      for (int a = 0; a < AL; ++a) *reinterpret_cast<u32x4*>(base + adst[a]) = areg[a];
+    };
+    WRaw<FMT> wr[D][TN];
+    auto wload = [&](int kc, WRaw<FMT> (&dst)[TN]) {
+      const int k = kc * 64 + 16 * q;
+#pragma unroll
+      for (int t = 0; t < TN; ++t) dst[t] = skinny_wload<FMT>(p, wrow[t], k, g, wn[t]);
+    };
+    f32x4 acc[TN][RT];
+#pragma unroll
+    for (int t = 0; t < TN; ++t)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) acc[t][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // prologue: weights of chunks 0 .. D-2, activations of chunk 0 in LDS,
+    // of chunk 1 in registers
+#pragma unroll
+    for (int u = 0; u < D - 1; ++u)
+      if (u < KC) wload(u, wr[u]);
+    aload(0);
+    astore(0);
+    if (KC > 1) aload(1);
+    wait_lgkm0();
+    __builtin_amdgcn_s_barrier();
+    for (int c0 = 0; c0 < KC; c0 += D) {
+#pragma unroll
+      for (int u = 0; u < D; ++u) {
+        const int c = c0 + u;
+        if (c < KC) {  // uniform
+          if (c > 0) {
+            // chunk c was stored by every wave, chunk c-1 is no longer read
+            wait_lgkm0();
+            __builtin_amdgcn_s_barrier();
+          }
+          if (c + 1 < KC) astore(c + 1);  // into the buffer chunk c-1 used
+          if (c + 2 < KC) aload(c + 2);
+          if (c + D - 1 < KC) wload(c + D - 1, wr[(u + D - 1) % D]);
+          const uint8_t* sb = abuf + (c & 1) * CHUNK;
+#pragma unroll
+          for (int rt = 0; rt < RT; ++rt) {
+            const int r = rt * 16 + l16;
+            const bf16x8 blo = *reinterpret_cast<const bf16x8*>(sb + r * 128 + (((2 * q) ^ (r & 7)) << 4));
+            const bf16x8 bhi = *reinterpret_cast<const bf16x8*>(sb + r * 128 + (((2 * q + 1) ^ (r & 7)) << 4));
+#pragma unroll
+            for (int t = 0; t < TN; ++t) {
+              bf16x8 lo, hi;
+              skinny_wconv<FMT>(wr[u][t], lo, hi);
+              acc[t][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, blo, acc[t][rt], 0, 0, 0);
+              acc[t][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, bhi, acc[t][rt], 0, 0, 0);
+            }
+          }
+        }
+      }
+    }
+    // lane: channels n0 + 16 t + 4 q + (0..3) of row m0 + 16 rt + l16
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int row = m0 + rt * 16 + l16;
+      if (row >= r_hi) continue;
+#pragma unroll
+      for (int t = 0; t < TN; ++t) {
+        const int c = n0 + 16 * t + 4 * q;
+        if (c >= p.N_out) continue;
+        if constexpr (EPI == EPI_SWIGLU) {
+          if (t >= 2) continue;
+          const f32x4 v = acc[t][rt], up = acc[t + 2][rt];
+          const int u0 = (c >> 6) * 32 + (c & 31);
+          float o[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float gs = v[i] * col_scale(p, FMT, g, c + i);
+            const float us = up[i] * col_scale(p, FMT, g, c + 32 + i) + bias_at(p, g, u0 + i);
+            o[i] = silu(gs) * us;
+          }
+          const int64_t off = static_cast<int64_t>(row) * p.ldo + u0;
+          if (p.out_dtype == SMOE_F32)
+            *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + off) = f32x4{o[0], o[1], o[2], o[3]};
+          else
+            *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + off) =
+                u32x2{pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3])};
+        } else {
+          store4<EPI>(p, FMT, g, row, c, acc[t][rt]);
+        }
+      }
+    }
+    if (m0 + ROWS < r_hi) {  // another pass: every wave is done with the buffers
+      wait_lgkm0();
+      __builtin_amdgcn_s_barrier();
+    }
   }
 }
 
@@ -1003,6 +1165,39 @@ int launch_skinny(const GemmArgs& a, hipStream_t s) {
   }
 }
 
+template <int FMT, int RT, int D>
+int launch_stream_fmt(const GemmArgs& a, hipStream_t s) {
+  const dim3 grid((a.N_out + 255) / 256, a.G == 0 ? 1 : a.G), block(256);
+  switch (a.epi) {
+    case EPI_F32_BIAS: hipLaunchKernelGGL((k_gemm_stream<FMT, EPI_F32_BIAS, RT, D>), grid, block, 0, s, a); break;
+    case EPI_ROWSCALE: hipLaunchKernelGGL((k_gemm_stream<FMT, EPI_ROWSCALE, RT, D>), grid, block, 0, s, a); break;
+    case EPI_GELU: hipLaunchKernelGGL((k_gemm_stream<FMT, EPI_GELU, RT, D>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU: hipLaunchKernelGGL((k_gemm_stream<FMT, EPI_SWIGLU, RT, D>), grid, block, 0, s, a); break;
+    case EPI_DOWN: hipLaunchKernelGGL((k_gemm_stream<FMT, EPI_DOWN, RT, D>), grid, block, 0, s, a); break;
+    default: return SMOE_EINVAL;
+  }
+  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
+int launch_stream(const GemmArgs& a, hipStream_t s) {
+  switch (a.fmt) {
+    case SMOE_BF16: return launch_stream_fmt<SMOE_BF16, 6, 2>(a, s);
+    case SMOE_FP8_E4M3: return launch_stream_fmt<SMOE_FP8_E4M3, 6, 2>(a, s);
+    case SMOE_INT4: return launch_stream_fmt<SMOE_INT4, 6, 2>(a, s);
+    default: return SMOE_EUNSUPPORTED;
+  }
+}
+
+// Whether the weight-streaming kernels can take the GEMM: every 16-byte
+// (int4: 8-byte) load they issue aligned, K in 64-wide steps.
+bool stream_aligned(const GemmArgs& a) {
+  if (a.K % 64 || a.N_out % 4 || a.ldo % 4 || a.lda % 8) return false;
+  const int walign = a.fmt == SMOE_BF16 ? 8 : 16;  // elements per aligned load
+  if (a.ldw % walign || a.w_gstride % walign) return false;
+  if (a.fmt == SMOE_INT4 && a.group_size % 16) return false;
+  return a.fmt == SMOE_BF16 || a.fmt == SMOE_FP8_E4M3 || a.fmt == SMOE_INT4;
+}
+
 // Whether the skinny kernel takes the GEMM: few rows per group, and every
 // 16-byte (int4: 8-byte) load it issues aligned.
 bool skinny_fits(const GemmArgs& a) {
@@ -1041,6 +1236,12 @@ int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
     if (a.N_out <= 32 && a.epi != EPI_SWIGLU)
       return rpg <= 16 ? launch_skinny<2, 1>(a, s) : launch_skinny<2, 2>(a, s);
     return rpg <= 8 ? launch_skinny<4, 1>(a, s) : launch_skinny<4, 2>(a, s);
+  }
+  // a few dozen to 128 rows per group (mixed decode + prefill): weights
+  // streamed into registers, activations through LDS
+  {
+    const int rpg = a.G == 0 ? a.single_rows : a.max_rows / a.G;
+    if (a.G > 0 && rpg <= 128 && a.N_out >= 128 && stream_aligned(a)) return launch_stream(a, s);
   }
   // large bf16 problems (K % 64): 256 x 256 tiles, 8 waves in two ping-pong
   // groups when N_out % 256 == 0; otherwise 256 x 128 ring tiles, two
