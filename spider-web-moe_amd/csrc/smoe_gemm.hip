@@ -825,35 +825,57 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(const GemmArgs p) {
 
 // ------------------------------------------------------- weight stream ----
 // Medium rows per group (a few dozen to ~128: mixed decode + prefill steps,
-// quantized experts).  The weights dominate the traffic and each weight is
-// used by every row of its group, so a workgroup owns one group and a strip
-// of 256 output channels (wave w: channels 64 w .. 64 w + 63, four 16-channel
-// MFMA tiles) and all of the group's rows in passes of RT*16.  Per 64-wide K
-// chunk:
-//   weights:     each lane loads the 16 consecutive k at k0 + 16*(lane/16)
-//                of its four channels straight into registers (fp8 16 B,
-//                int4 8 B + its group scale, bf16 32 B), D chunks ahead;
-//   activations: the pass's rows x 64 k (bf16) go global -> registers -> a
-//                double-buffered LDS chunk (128 B rows, 16-byte chunk c of
-//                row r at c ^ (r & 7)), one chunk ahead, one barrier per
-//                chunk (lgkmcnt only, so the weight prefetch stays in flight);
-//   MFMAs:       the step's two MFMAs take the low and the high 8 k of a
-//                lane's 16 (the same permutation for both operands).
-// Results go from registers to memory, 4 consecutive channels per lane.
-template <int FMT, int EPI, int RT, int D>
-__global__ __launch_bounds__(256, 2) void k_gemm_stream(const GemmArgs p) {
-  constexpr int TN = 4;                         // 16-channel tiles per wave
-  constexpr int ROWS = RT * 16;                 // rows per pass
-  constexpr int CHUNK = ROWS * 128;             // bytes of one activation chunk
-  constexpr int AL = ROWS * 8 / 256;            // 16-byte activation loads per lane per chunk
+// quantized experts).  The weights dominate the traffic and every weight is
+// used by all rows of its group, so a workgroup owns one group, a strip of
+// 256 output channels (wave w: channels 64 w .. 64 w + 63, four 16-channel
+// MFMA tiles) and the group's rows in passes of RT*16.  Both operands stream
+// global -> LDS by DMA (global_load_lds_dwordx4) through an NS-stage ring of
+// 64-wide K chunks, so the main loop's only vector-memory operations are the
+// DMAs and the explicit vmcnt waits stay exact:
+//   weights:     256 channel rows x 64 k in storage format (int4 32 B, fp8
+//                64 B, bf16 128 B per row); a lane reads the 16 k at
+//                16*(lane/16) of its channel and widens them to bf16 (int4:
+//                with the group scale from an LDS table of the strip)
+//   activations: RT*16 rows x 64 k bf16 (128 B rows)
+//   MFMAs:       the step's two MFMAs take the low and the high 8 of the 16 k
+//                (the same permutation for both operands).
+// Every LDS row's 16-byte chunk c is stored at c ^ ((r / R) % C), C chunks
+// per row, R rows per 256 bytes: the 16 rows a ds_read phase touches then
+// cover all 64 banks once.  One barrier per chunk; chunk k+NS-1 is in flight
+// while chunk k computes.  Results go from registers to memory, 4
+// consecutive channels per lane.
+template <int FMT>
+constexpr int stream_wb() {  // bytes of one channel's 64-k slice
+  return FMT == SMOE_BF16 ? 128 : (FMT == SMOE_FP8_E4M3 ? 64 : 32);
+}
+constexpr int kStreamScaleMax = 4096;  // int4 scale-table entries per strip
+
+// physical 16-byte chunk of logical chunk c in row r (rows of 16*CPR bytes)
+template <int CPR>
+__device__ __forceinline__ int sw_chunk(int r, int c) {
+  return c ^ ((r / (16 / CPR)) & (CPR - 1));
+}
+
+template <int FMT, int EPI, int RT, int NS, int WGS>
+__global__ __launch_bounds__(256, WGS) void k_gemm_stream(const GemmArgs p) {
+  constexpr int TN = 4;
+  constexpr int WB = stream_wb<FMT>();
+  constexpr int CPR = WB / 16;  // 16-byte chunks per weight row
+  constexpr int ROWS = RT * 16;
+  constexpr int W_BYTES = 256 * WB, A_BYTES = ROWS * 128, STAGE = W_BYTES + A_BYTES;
+  constexpr int W_LD = W_BYTES / 4096, A_LD = A_BYTES / 4096;  // DMA instructions per wave per stage
+  constexpr int LD = W_LD + A_LD;
   constexpr int ESZ2 = FMT == SMOE_BF16 ? 4 : (FMT == SMOE_FP8_E4M3 ? 2 : 1);  // 2 x bytes/elt
-  static_assert(AL >= 1 && ROWS * 8 % 256 == 0, "activation chunk split");
+  static_assert(W_BYTES % 4096 == 0 && A_BYTES % 4096 == 0, "whole DMA instructions per wave");
+  static_assert(NS >= 3, "ring depth");
   static_assert(EPI != EPI_SWIGLU || TN == 4, "SwiGLU pairs channel c with c + 32");
-  __shared__ __attribute__((aligned(1024))) uint8_t abuf[2 * CHUNK];
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE];
+  __shared__ float sc[FMT == SMOE_INT4 ? kStreamScaleMax : 1];
+
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int q = lane >> 4, l16 = lane & 15;
   const int g = blockIdx.y;
-  const int n0 = blockIdx.x * 256 + wave * 64;  // this wave's first channel
+  const int nb = blockIdx.x * 256;
   int r_lo, r_hi;
   if (p.G == 0) {
     r_lo = 0;
@@ -863,47 +885,53 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream(const GemmArgs p) {
     r_hi = p.grp_off[g + 1];
   }
   if (r_hi <= r_lo) return;  // workgroup-uniform, before any barrier
-  const uint8_t* wrow[TN];
-  int wn[TN];
-#pragma unroll
-  for (int t = 0; t < TN; ++t) {
-    const int n = min(n0 + 16 * t + l16, p.N_out - 1);  // channels past N_out: loaded, never stored
-    wn[t] = n;
-    wrow[t] = reinterpret_cast<const uint8_t*>(p.W) +
-              (g * p.w_gstride + static_cast<int64_t>(n) * p.ldw) * ESZ2 / 2;
-  }
   const int KC = p.K / 64;
+  const int ng = FMT == SMOE_INT4 ? p.K / p.group_size : 1;
+  const int gshift = FMT == SMOE_INT4 ? __builtin_ctz(p.group_size) : 0;  // power of two (launcher)
+  if constexpr (FMT == SMOE_INT4) {  // the strip's group scales, channel-major
+    for (int i = tid; i < 256 * ng; i += 256) {
+      const int ch = i / ng, kg = i - ch * ng;
+      const int n = min(nb + ch, p.N_out - 1);
+      sc[i] = load_scale(p.S, g * p.s_gstride + static_cast<int64_t>(n) * ng + kg, p.s_f16);
+    }
+  }
+  // weight DMA: instruction j of wave w fills bytes [(4 j + w) KB, +1 KB) of
+  // the stage's weight region; lane l writes byte b = that + 16 l, i.e. row
+  // b / WB, physical chunk (b % WB) / 16 (which holds the logical chunk the
+  // swizzle maps there)
+  const uint8_t* wsrc[W_LD];
+#pragma unroll
+  for (int j = 0; j < W_LD; ++j) {
+    const int b = (4 * j + wave) * 1024 + 16 * lane;
+    const int row = b / WB, pc = (b % WB) >> 4;
+    const int lc = sw_chunk<CPR>(row, pc);  // the map is an involution
+    const int n = min(nb + row, p.N_out - 1);  // channels past N_out: loaded, never stored
+    wsrc[j] = reinterpret_cast<const uint8_t*>(p.W) +
+              (g * p.w_gstride + static_cast<int64_t>(n) * p.ldw) * ESZ2 / 2 + lc * 16;
+  }
   const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A);
   for (int m0 = r_lo; m0 < r_hi; m0 += ROWS) {  // passes (uniform)
-    // activation loads: load a of this lane covers row (tid + 256 a) / 8,
-    // logical 16-byte chunk (tid % 8) of the row's 64 k
-    const uint16_t* asrc[AL];
-    int adst[AL];
+    // activation DMA: instruction j of wave w covers rows 8 (4 j + w) .. +8,
+    // lane l: row + l / 8, physical chunk l % 8
+    const uint16_t* asrc[A_LD];
 #pragma unroll
-    for (int a = 0; a < AL; ++a) {
-      const int e = tid + 256 * a;
-      const int r = e >> 3, c = e & 7;
-      int pr = m0 + r;
-      pr = pr < r_hi ? pr : r_lo;  // rows past the group: a valid row, never stored
+    for (int j = 0; j < A_LD; ++j) {
+      const int r = 8 * (4 * j + wave) + (lane >> 3);
+      const int pr = m0 + r < r_hi ? m0 + r : r_lo;  // rows past the group: valid, never stored
       const int ar = p.a_rows ? p.a_rows[pr] : pr;
-      asrc[a] = A + static_cast<int64_t>(ar) * p.lda + c * 8;
-      adst[a] = r * 128 + ((c ^ (r & 7)) << 4);
+      asrc[j] = A + static_cast<int64_t>(ar) * p.lda + (sw_chunk<8>(r, lane & 7) << 3);
     }
-    u32x4 areg[AL];
-    auto aload = [&](int kc) {
+    auto issue = [&](int kc) {  // DMA of chunk kc into ring slot kc % NS
+      uint8_t* base = ring + (kc % NS) * STAGE;
 #pragma unroll
-      for (int a = 0; a < AL; ++a) areg[a] = *reinterpret_cast<const u32x4*>(asrc[a] + kc * 64);
-    };
-    auto astore = [&](int kc) {
-      uint8_t* base = abuf + (kc & 1) * CHUNK;
+      for (int j = 0; j < W_LD; ++j)
+        __builtin_amdgcn_global_load_lds((gbl_vptr)(wsrc[j] + static_cast<int64_t>(kc) * WB),
+                                         (lds_vptr)(base + (4 * j + wave) * 1024), 16, 0, 0);
 #pragma unroll
-      for (int a = 0; a < AL; ++a) *reinterpret_cast<u32x4*>(base + adst[a]) = areg[a];
-    };
-    WRaw<FMT> wr[D][TN];
-    auto wload = [&](int kc, WRaw<FMT> (&dst)[TN]) {
-      const int k = kc * 64 + 16 * q;
-#pragma unroll
-      for (int t = 0; t < TN; ++t) dst[t] = skinny_wload<FMT>(p, wrow[t], k, g, wn[t]);
+      for (int j = 0; j < A_LD; ++j)
+        __builtin_amdgcn_global_load_lds((gbl_vptr)(asrc[j] + kc * 64),
+                                         (lds_vptr)(base + W_BYTES + (4 * j + wave) * 1024), 16,
+                                         0, 0);
     };
     f32x4 acc[TN][RT];
 #pragma unroll
@@ -911,54 +939,64 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream(const GemmArgs p) {
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) acc[t][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // prologue: weights of chunks 0 .. D-2, activations of chunk 0 in LDS,
-    // of chunk 1 in registers
+    // prologue: chunks 0 .. NS-2 in flight, chunk 0 landed everywhere
 #pragma unroll
-    for (int u = 0; u < D - 1; ++u)
-      if (u < KC) wload(u, wr[u]);
-    aload(0);
-    astore(0);
-    if (KC > 1) aload(1);
-    wait_lgkm0();
+    for (int st = 0; st < NS - 1; ++st)
+      if (st < KC) issue(st);
+    if (KC >= NS - 1) wait_vmcnt<(NS - 2) * LD>();
+    else wait_vmcnt<0>();
+    wait_lgkm0();  // the scale table (int4) is written
     __builtin_amdgcn_s_barrier();
-    for (int c0 = 0; c0 < KC; c0 += D) {
+    for (int kc = 0; kc < KC; ++kc) {
+      if (kc > 0) {
+        // own part of chunk kc landed (kc+1 .. kc+NS-2 may fly); chunk kc-1
+        // is no longer read by anyone after the barrier
+        if (kc + NS - 2 < KC) wait_vmcnt<(NS - 2) * LD>();
+        else wait_vmcnt<0>();
+        wait_lgkm0();
+        __builtin_amdgcn_s_barrier();
+      }
+      if (kc + NS - 1 < KC) issue(kc + NS - 1);  // into the slot chunk kc-1 used
+      const uint8_t* sw = ring + (kc % NS) * STAGE;
+      const uint8_t* sa = sw + W_BYTES;
+      const int kg = (kc * 64 + 16 * q) >> gshift;  // int4 scale group of this lane's 16 k
+      bf16x8 wlo[TN], whi[TN];
 #pragma unroll
-      for (int u = 0; u < D; ++u) {
-        const int c = c0 + u;
-        if (c < KC) {  // uniform
-          if (c > 0) {
-            // chunk c was stored by every wave, chunk c-1 is no longer read
-            wait_lgkm0();
-            __builtin_amdgcn_s_barrier();
-          }
-          if (c + 1 < KC) astore(c + 1);  // into the buffer chunk c-1 used
-          if (c + 2 < KC) aload(c + 2);
-          if (c + D - 1 < KC) wload(c + D - 1, wr[(u + D - 1) % D]);
-          const uint8_t* sb = abuf + (c & 1) * CHUNK;
+      for (int t = 0; t < TN; ++t) {
+        const int row = wave * 64 + t * 16 + l16;
+        WRaw<FMT> r;
+        if constexpr (FMT == SMOE_BF16) {
+          r.a = *reinterpret_cast<const u32x4*>(sw + row * WB + (sw_chunk<CPR>(row, 2 * q) << 4));
+          r.b = *reinterpret_cast<const u32x4*>(sw + row * WB + (sw_chunk<CPR>(row, 2 * q + 1) << 4));
+        } else if constexpr (FMT == SMOE_FP8_E4M3) {
+          r.a = *reinterpret_cast<const u32x4*>(sw + row * WB + (sw_chunk<CPR>(row, q) << 4));
+        } else {
+          r.a = *reinterpret_cast<const u32x2*>(sw + row * WB + (sw_chunk<CPR>(row, q >> 1) << 4) +
+                                                ((q & 1) << 3));
+          r.s = sc[row * ng + kg];
+        }
+        skinny_wconv<FMT>(r, wlo[t], whi[t]);
+      }
 #pragma unroll
-          for (int rt = 0; rt < RT; ++rt) {
-            const int r = rt * 16 + l16;
-            const bf16x8 blo = *reinterpret_cast<const bf16x8*>(sb + r * 128 + (((2 * q) ^ (r & 7)) << 4));
-            const bf16x8 bhi = *reinterpret_cast<const bf16x8*>(sb + r * 128 + (((2 * q + 1) ^ (r & 7)) << 4));
+      for (int rt = 0; rt < RT; ++rt) {
+        const int r = rt * 16 + l16;
+        const bf16x8 blo = *reinterpret_cast<const bf16x8*>(sa + r * 128 + (sw_chunk<8>(r, 2 * q) << 4));
+        const bf16x8 bhi = *reinterpret_cast<const bf16x8*>(sa + r * 128 + (sw_chunk<8>(r, 2 * q + 1) << 4));
 #pragma unroll
-            for (int t = 0; t < TN; ++t) {
-              bf16x8 lo, hi;
-              skinny_wconv<FMT>(wr[u][t], lo, hi);
-              acc[t][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(lo, blo, acc[t][rt], 0, 0, 0);
-              acc[t][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(hi, bhi, acc[t][rt], 0, 0, 0);
-            }
-          }
+        for (int t = 0; t < TN; ++t) {
+          acc[t][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wlo[t], blo, acc[t][rt], 0, 0, 0);
+          acc[t][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(whi[t], bhi, acc[t][rt], 0, 0, 0);
         }
       }
     }
-    // lane: channels n0 + 16 t + 4 q + (0..3) of row m0 + 16 rt + l16
+    // lane: channels nb + 64 wave + 16 t + 4 q + (0..3) of row m0 + 16 rt + l16
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       const int row = m0 + rt * 16 + l16;
       if (row >= r_hi) continue;
 #pragma unroll
       for (int t = 0; t < TN; ++t) {
-        const int c = n0 + 16 * t + 4 * q;
+        const int c = nb + wave * 64 + 16 * t + 4 * q;
         if (c >= p.N_out) continue;
         if constexpr (EPI == EPI_SWIGLU) {
           if (t >= 2) continue;
@@ -982,7 +1020,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream(const GemmArgs p) {
         }
       }
     }
-    if (m0 + ROWS < r_hi) {  // another pass: every wave is done with the buffers
+    if (m0 + ROWS < r_hi) {  // another pass: every wave is done with the ring
       wait_lgkm0();
       __builtin_amdgcn_s_barrier();
     }
@@ -1165,25 +1203,31 @@ int launch_skinny(const GemmArgs& a, hipStream_t s) {
   }
 }
 
-template <int FMT, int RT, int D>
+template <int FMT, int RT, int NS, int WGS>
 int launch_stream_fmt(const GemmArgs& a, hipStream_t s) {
   const dim3 grid((a.N_out + 255) / 256, a.G == 0 ? 1 : a.G), block(256);
   switch (a.epi) {
-    case EPI_F32_BIAS: hipLaunchKernelGGL((k_gemm_stream<FMT, EPI_F32_BIAS, RT, D>), grid, block, 0, s, a); break;
-    case EPI_ROWSCALE: hipLaunchKernelGGL((k_gemm_stream<FMT, EPI_ROWSCALE, RT, D>), grid, block, 0, s, a); break;
-    case EPI_GELU: hipLaunchKernelGGL((k_gemm_stream<FMT, EPI_GELU, RT, D>), grid, block, 0, s, a); break;
-    case EPI_SWIGLU: hipLaunchKernelGGL((k_gemm_stream<FMT, EPI_SWIGLU, RT, D>), grid, block, 0, s, a); break;
-    case EPI_DOWN: hipLaunchKernelGGL((k_gemm_stream<FMT, EPI_DOWN, RT, D>), grid, block, 0, s, a); break;
+    case EPI_F32_BIAS: hipLaunchKernelGGL((k_gemm_stream<FMT, EPI_F32_BIAS, RT, NS, WGS>), grid, block, 0, s, a); break;
+    case EPI_ROWSCALE: hipLaunchKernelGGL((k_gemm_stream<FMT, EPI_ROWSCALE, RT, NS, WGS>), grid, block, 0, s, a); break;
+    case EPI_GELU: hipLaunchKernelGGL((k_gemm_stream<FMT, EPI_GELU, RT, NS, WGS>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU: hipLaunchKernelGGL((k_gemm_stream<FMT, EPI_SWIGLU, RT, NS, WGS>), grid, block, 0, s, a); break;
+    case EPI_DOWN: hipLaunchKernelGGL((k_gemm_stream<FMT, EPI_DOWN, RT, NS, WGS>), grid, block, 0, s, a); break;
     default: return SMOE_EINVAL;
   }
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 
+// Two workgroups per CU (one's dequant and waits overlap the other's MFMAs):
+// LDS per workgroup int4 3 x 20 KB + 16 KB scales, fp8 3 x 24 KB (64-row
+// passes), bf16 3 x 40 KB (one workgroup per CU).
 int launch_stream(const GemmArgs& a, hipStream_t s) {
   switch (a.fmt) {
-    case SMOE_BF16: return launch_stream_fmt<SMOE_BF16, 6, 2>(a, s);
-    case SMOE_FP8_E4M3: return launch_stream_fmt<SMOE_FP8_E4M3, 6, 2>(a, s);
-    case SMOE_INT4: return launch_stream_fmt<SMOE_INT4, 6, 2>(a, s);
+    case SMOE_BF16: return launch_stream_fmt<SMOE_BF16, 4, 3, 1>(a, s);
+    case SMOE_FP8_E4M3: return launch_stream_fmt<SMOE_FP8_E4M3, 4, 3, 2>(a, s);
+    case SMOE_INT4:
+      if (256 * (a.K / a.group_size) > kStreamScaleMax || (a.group_size & (a.group_size - 1)))
+        return SMOE_EUNSUPPORTED;
+      return launch_stream_fmt<SMOE_INT4, 6, 3, 2>(a, s);
     default: return SMOE_EUNSUPPORTED;
   }
 }
@@ -1241,7 +1285,10 @@ int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
   // streamed into registers, activations through LDS
   {
     const int rpg = a.G == 0 ? a.single_rows : a.max_rows / a.G;
-    if (a.G > 0 && rpg <= 128 && a.N_out >= 128 && stream_aligned(a)) return launch_stream(a, s);
+    if (a.G > 0 && rpg <= 128 && a.N_out >= 128 && stream_aligned(a) &&
+        (a.fmt != SMOE_INT4 || (256 * (a.K / a.group_size) <= kStreamScaleMax &&
+                                (a.group_size & (a.group_size - 1)) == 0)))
+      return launch_stream(a, s);
   }
   // large bf16 problems (K % 64): 256 x 256 tiles, 8 waves in two ping-pong
   // groups when N_out % 256 == 0; otherwise 256 x 128 ring tiles, two
