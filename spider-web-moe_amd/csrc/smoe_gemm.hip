@@ -527,14 +527,18 @@ __global__ __launch_bounds__(256, NS <= 3 ? 2 : 1) void k_gemm_ring(const GemmAr
 // fragments, then waits for its own part of stage k+1 (vmcnt) so the next
 // barrier certifies stage k+1 for both groups.  LDS layout and DMA scheme as
 // in the ring kernel (32-bf16 rows, chunk c of row r at c ^ ((r >> 1) & 3)).
-template <int NS, int GM, int EPI>
-__global__ __launch_bounds__(512) void k_gemm_pp(const GemmArgs p) {
-  constexpr int BM = 256, BN = 256, TM = 128, TN = 64;
+// BM = 256 (wave tile 128 x 64) for many rows per group; BM = 128 (wave tile
+// 64 x 64, two workgroups per CU) when groups hold a few hundred rows and a
+// 256-row tile would be mostly padding.
+template <int NS, int GM, int EPI, int BM>
+__global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmArgs p) {
+  constexpr int BN = 256, TM = BM / 2, TN = 64;
   constexpr int FM = TM / 16, FN = TN / 16;
   constexpr int A_BYTES = BM * 64, B_BYTES = BN * 64, STAGE = A_BYTES + B_BYTES;
   constexpr int A_LD = BM / 16 / 8, B_LD = BN / 16 / 8;  // DMA instructions per wave per stage
   constexpr int LD = A_LD + B_LD;
   static_assert(NS >= 2, "ring depth");
+  static_assert(BM == 128 || BM == 256, "block rows");
   static_assert(BM * ((EPI == EPI_SWIGLU) ? BN / 2 : BN) * 2 <= NS * STAGE,
                 "output staging fits in the ring");
   __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE];
@@ -1139,16 +1143,16 @@ int launch_ring(const GemmArgs& a, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 
-template <int NS, int GM>
+template <int NS, int GM, int BM>
 int launch_pp(const GemmArgs& a, hipStream_t s) {
-  const int tiles = max_tiles(a, 256) * ((a.N_out + 255) / 256);
+  const int tiles = max_tiles(a, BM) * ((a.N_out + 255) / 256);
   if (tiles == 0) return SMOE_OK;
   const dim3 grid(tiles), block(512);
   switch (a.epi) {
-    case EPI_ROWSCALE: hipLaunchKernelGGL((k_gemm_pp<NS, GM, EPI_ROWSCALE>), grid, block, 0, s, a); break;
-    case EPI_GELU: hipLaunchKernelGGL((k_gemm_pp<NS, GM, EPI_GELU>), grid, block, 0, s, a); break;
-    case EPI_SWIGLU: hipLaunchKernelGGL((k_gemm_pp<NS, GM, EPI_SWIGLU>), grid, block, 0, s, a); break;
-    case EPI_DOWN: hipLaunchKernelGGL((k_gemm_pp<NS, GM, EPI_DOWN>), grid, block, 0, s, a); break;
+    case EPI_ROWSCALE: hipLaunchKernelGGL((k_gemm_pp<NS, GM, EPI_ROWSCALE, BM>), grid, block, 0, s, a); break;
+    case EPI_GELU: hipLaunchKernelGGL((k_gemm_pp<NS, GM, EPI_GELU, BM>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU: hipLaunchKernelGGL((k_gemm_pp<NS, GM, EPI_SWIGLU, BM>), grid, block, 0, s, a); break;
+    case EPI_DOWN: hipLaunchKernelGGL((k_gemm_pp<NS, GM, EPI_DOWN, BM>), grid, block, 0, s, a); break;
     default: return SMOE_EINVAL;
   }
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
@@ -1297,7 +1301,9 @@ int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
   if (a.fmt == SMOE_BF16 && a.out_dtype == SMOE_BF16 && a.epi != EPI_F32_BIAS && a.K % 64 == 0 &&
       a.ldw % 8 == 0 && a.lda % 8 == 0 && a.ldo % 8 == 0 &&
       (a.G == 0 ? a.single_rows : a.max_rows / (a.G > 0 ? a.G : 1)) >= 256) {
-    if (a.N_out % 256 == 0) return launch_pp<4, 4>(a, s);
+    const int rpg = a.G == 0 ? a.single_rows : a.max_rows / a.G;
+    if (a.N_out % 256 == 0)
+      return rpg < 512 ? launch_pp<3, 4, 128>(a, s) : launch_pp<4, 4, 256>(a, s);
     if (a.N_out % 128 == 0) return launch_ring<128, 3, 4>(a, s);
   }
   const bool b64 = bk == 64;

@@ -324,17 +324,19 @@ def test_invalid_arguments_are_rejected():
     assert rc == 1
 
 
-@pytest.mark.parametrize("act,u", [("gelu", 768), ("swiglu", 768), ("gelu", 640), ("swiglu", 704)])
-def test_large_bf16_experts_ragged_groups(act, u):
+@pytest.mark.parametrize("act,u,n", [("gelu", 768, 2304), ("swiglu", 768, 2304), ("gelu", 640, 2304),
+                                     ("swiglu", 704, 2304), ("gelu", 768, 1536)])
+def test_large_bf16_experts_ragged_groups(act, u, n):
     """Shapes that take the large-tile LDS-DMA paths (>= 256 rows per expert
     on average) with skewed routing: empty experts, single-row experts and
     experts spanning several tiles.  Up N_out 768 / 1536 and down N_out 512
-    (multiples of 256) take the 8-wave ping-pong kernel; up N_out 640 / 1408
-    (odd multiples of 128) the 256 x 128 ring kernel."""
+    (multiples of 256) take the 8-wave ping-pong kernel (256-row tiles; with
+    n = 1536, 384 rows per expert on average, its 128-row tiles); up N_out
+    640 / 1408 (odd multiples of 128) the 256 x 128 ring kernel."""
     from spider_moe_amd.quant import interleave_gate_up
     n8 = nat()
-    say("large bf16 experts", act, u)
-    n, h, e, k = 2304, 512, 8, 2
+    say("large bf16 experts", act, u, n)
+    h, e, k = 512, 8, 2
     g = torch.Generator().manual_seed(21)
     # skew: experts 0,1 take most tokens, 5 gets one token, 6 and 7 none
     p = torch.tensor([0.45, 0.3, 0.12, 0.08, 0.05, 0.0, 0.0, 0.0])
