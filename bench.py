@@ -47,7 +47,7 @@ UP_KERNEL = {
     "c1": "k_gemm_pp<4,4> (bf16 SwiGLU, 8-wave ping-pong, LDS-DMA ring)",
     "c2": "k_gemm_skinny<fp8,SwiGLU,4,1> (weight streaming)",
     "c3": "k_gemm_ring<128,3,4> (bf16 GELU, LDS-DMA ring, 2 workgroups/CU)",
-    "c4": "k_gemm_stream<int4,GELU,6,2> (weight streaming, activations via LDS)",
+    "c4": "k_gemm_stream<int4,GELU,6,3,2> (weight streaming, both operands by LDS-DMA ring, 2 workgroups/CU)",
 }
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.md")
 
