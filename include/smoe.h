@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define SMOE_ABI_VERSION 1
+#define SMOE_ABI_VERSION 2
 
 /* status codes (spider_kernels.h convention; see scalar.cpp:9,45,58) */
 #define SMOE_OK 0
@@ -137,6 +137,8 @@ typedef struct smoe_ws_layout {
   size_t y;         /* ffn  [N*K,H]   weighted expert outputs                     */
   size_t h_tmp;     /* act  [N,H]     loop ping-pong buffer                       */
   size_t scratch;   /* plan scratch                                               */
+  size_t front;     /* f32 [N,E+E*E]  router logits | edge logits of every source,  */
+                    /*                bf16 steps of N <= 64 (else 0 bytes)          */
   int S;            /* destinations per token: min(E, K*M)                        */
   int ffn_dtype;    /* SMOE_F32 or SMOE_BF16                                      */
 } smoe_ws_layout;
@@ -216,7 +218,10 @@ SMOE_API int smoe_expert_delta(const smoe_experts* ex, const void* msg, const in
 #define SMOE_STAGE_UP_GEMM 8
 #define SMOE_STAGE_DOWN_GEMM 9
 #define SMOE_STAGE_EPILOGUE 10
-#define SMOE_NUM_STAGES 11
+/* bf16 steps of N <= 64 run stages 0-5 as these two launches */
+#define SMOE_STAGE_FRONT_GEMM 11  /* router + all edge-generator logits, one GEMM */
+#define SMOE_STAGE_FRONT_ROUTE 12 /* top-k, expert plan, top-m, destination plan */
+#define SMOE_NUM_STAGES 13
 /* When `events` is not NULL, every later smoe_block_forward records
  * events[2*i] before and events[2*i+1] after the i-th launch of a stage in
  * `stage_mask` (bit s = stage s), for i < capacity, on the call's stream.

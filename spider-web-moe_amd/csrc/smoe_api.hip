@@ -141,6 +141,16 @@ int check_block(const smoe_block* b) {
   return check_experts(b->experts, b->H);
 }
 
+// Small bf16 steps take the fused front: one GEMM for the router logits and
+// the edge logits of every source (the E x E edge generator rows, so no
+// source grouping is needed), then one workgroup for top-k, both plans and
+// top-m.  Shapes follow the skinny GEMM's alignment rules.
+bool front_ok(const smoe_block* b, int N) {
+  const int E = b->E, S = (E < b->K * b->M) ? E : b->K * b->M;
+  return b->act_dtype == SMOE_BF16 && N >= 1 && N <= kFrontMaxN && E <= 64 && b->K <= 16 &&
+         b->M <= 16 && S <= 64 && b->H % 64 == 0 && (E + E * E) % 4 == 0 && E % 4 == 0 && (b->H + b->L) % 8 == 0;
+}
+
 void make_layout(const smoe_block* b, int N, smoe_ws_layout* l) {
   const size_t n = N > 0 ? static_cast<size_t>(N) : 1;
   const int E = b->E, K = b->K, M = b->M, H = b->H;
@@ -176,6 +186,7 @@ void make_layout(const smoe_block* b, int N, smoe_ws_layout* l) {
   l->y = z.take(n * K * H * esize(fdt));
   l->h_tmp = z.take(n * H * esize(b->act_dtype));
   l->scratch = z.take(plan_scratch_bytes(N, E));
+  l->front = z.take(front_ok(b, N) ? n * (E + E * E) * 4 : 0);
   l->total = z.off;
   l->S = S;
   l->ffn_dtype = fdt;
@@ -300,10 +311,48 @@ SMOE_API int smoe_block_forward(const smoe_block* b, const void* h_in, const voi
   const int adt = b->act_dtype, fdt = l.ffn_dtype;
   const int gfmt = adt == SMOE_F32 ? SMOE_F32 : SMOE_BF16;  // router / edge weights
 
+  const bool front = front_ok(b, N);
   const void* cur = h_in;
   for (int i = 0; i < num_loops; ++i) {
     const int r = loop_begin + i;
     void* dst = ((num_loops - 1 - i) % 2 == 0) ? h_out : at<void>(ws, l.h_tmp);
+    if (front) {
+      // 1-6 fused: [router | all edge generator rows] logits, then routing
+      const int ldf = E + E * E;
+      GemmArgs fg;
+      fg.fmt = SMOE_BF16;
+      fg.epi = EPI_F32_BIAS;
+      fg.A = cur;
+      fg.lda = H;
+      fg.W = b->router_w;
+      fg.ldw = H;
+      fg.K = H;
+      fg.N_out = ldf;
+      fg.G = 0;
+      fg.single_rows = N;
+      fg.out = at<float>(ws, l.front);
+      fg.ldo = ldf;
+      fg.bias = b->loop_bias + static_cast<int64_t>(r) * E;
+      fg.W2 = b->edge_gen_w;
+      fg.ldw2 = H + L;
+      fg.n_split = E;
+      fg.bias2 = b->edge_loop_bias + static_cast<int64_t>(r) * E * E;
+      STAGE(SMOE_STAGE_FRONT_GEMM, launch_front_gemm(fg, s), "front GEMM");
+      STAGE(SMOE_STAGE_FRONT_ROUTE,
+            launch_front_route(at<float>(ws, l.front), ldf, N, E, K, M, S, at<float>(ws, l.logits),
+                               at<int32_t>(ws, l.top_idx), at<float>(ws, l.top_w),
+                               at<int32_t>(ws, l.tok_e), at<float>(ws, l.tok_ew),
+                               at<int32_t>(ws, l.e_cnt), at<int32_t>(ws, l.e_acnt),
+                               at<int32_t>(ws, l.e_off), at<int32_t>(ws, l.e_rows),
+                               at<float>(ws, l.e_roww), at<int32_t>(ws, l.e_tokrow),
+                               at<float>(ws, l.edge_logit), at<int32_t>(ws, l.edge_idx),
+                               at<float>(ws, l.edge_w), at<int32_t>(ws, l.tok_d),
+                               at<float>(ws, l.tok_dc), at<int32_t>(ws, l.d_cnt),
+                               at<int32_t>(ws, l.d_acnt), at<int32_t>(ws, l.d_off),
+                               at<int32_t>(ws, l.d_rows), at<float>(ws, l.d_roww),
+                               at<int32_t>(ws, l.d_tokrow), s),
+            "front routing");
+    } else {
 
     // 1 router logits (+ loop bias)
     GemmArgs rg;
@@ -368,6 +417,7 @@ SMOE_API int smoe_block_forward(const smoe_block* b, const void* h_in, const voi
                          at<float>(ws, l.d_roww), at<int32_t>(ws, l.d_tokrow),
                          at<void>(ws, l.scratch), s),
              "destination plan");
+    }
     // 7 edge projections c * W_edge[d] h
     GemmArgs pg;
     pg.fmt = gfmt;

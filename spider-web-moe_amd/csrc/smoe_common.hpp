@@ -74,24 +74,101 @@ __device__ __forceinline__ float load_scale(const void* p, int64_t i, int is_f16
 }
 
 // ----------------------------------------------------------- reductions ----
+// Wave reductions: within each 16-lane row by DPP (quad_perm xor 1, xor 2,
+// row_half_mirror, row_mirror: after them every lane holds its row's
+// result), then the four rows' results read from lanes 0, 16, 32, 48 and
+// combined uniformly.  A DPP step costs a few cycles where a ds_bpermute
+// shuffle waits on LDS.  Every lane of the wave must be active.
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int x) {
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float x) {
+  return __int_as_float(dpp_i<CTRL>(__float_as_int(x)));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within 8
+constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within 16
+__device__ __forceinline__ float lane_f(float v, int l) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  v += dpp_f<kDppXor1>(v);
+  v += dpp_f<kDppXor2>(v);
+  v += dpp_f<kDppHalfMirror>(v);
+  v += dpp_f<kDppMirror>(v);
+  return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
+  v = fmaxf(v, dpp_f<kDppXor1>(v));
+  v = fmaxf(v, dpp_f<kDppXor2>(v));
+  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_f<kDppMirror>(v));
+  return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 // (value, index) arg-max over the wave; ties -> lowest index.  NaN never wins.
+// Branch-free (bitwise, no short circuit): a branch here becomes exec-mask
+// bookkeeping whose scalar ops wait on each vector compare.
+__device__ __forceinline__ void argmax_take(float& v, int& i, float ov, int oi) {
+  const bool take = (ov > v) | ((ov == v) & (oi < i));
+  v = take ? ov : v;
+  i = take ? oi : i;
+}
+template <int CTRL>
+__device__ __forceinline__ void argmax_dpp(float& v, int& i) {
+  argmax_take(v, i, dpp_f<CTRL>(v), dpp_i<CTRL>(i));
+}
+// Reductions over aligned segments of SEG lanes (SEG = 16, 32 or 64): the
+// 16-lane row by the DPP steps above, then xor 16 / xor 32 shuffles; every
+// lane gets its segment's result.  Ties of the arg-max go to the lowest
+// index; the order of the sum is fixed (deterministic).
+template <int SEG>
+__device__ __forceinline__ float seg_max(float v) {
+  static_assert(SEG == 16 || SEG == 32 || SEG == 64, "segment");
+  v = fmaxf(v, dpp_f<kDppXor1>(v));
+  v = fmaxf(v, dpp_f<kDppXor2>(v));
+  v = fmaxf(v, dpp_f<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_f<kDppMirror>(v));
+  if constexpr (SEG >= 32) v = fmaxf(v, __shfl_xor(v, 16));
+  if constexpr (SEG >= 64) v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+template <int SEG>
+__device__ __forceinline__ float seg_sum(float v) {
+  static_assert(SEG == 16 || SEG == 32 || SEG == 64, "segment");
+  v += dpp_f<kDppXor1>(v);
+  v += dpp_f<kDppXor2>(v);
+  v += dpp_f<kDppHalfMirror>(v);
+  v += dpp_f<kDppMirror>(v);
+  if constexpr (SEG >= 32) v += __shfl_xor(v, 16);
+  if constexpr (SEG >= 64) v += __shfl_xor(v, 32);
+  return v;
+}
+template <int SEG>
+__device__ __forceinline__ void seg_argmax(float& v, int& i) {
+  static_assert(SEG == 16 || SEG == 32 || SEG == 64, "segment");
+  argmax_dpp<kDppXor1>(v, i);
+  argmax_dpp<kDppXor2>(v, i);
+  argmax_dpp<kDppHalfMirror>(v, i);
+  argmax_dpp<kDppMirror>(v, i);
+  if constexpr (SEG >= 32) argmax_take(v, i, __shfl_xor(v, 16), __shfl_xor(i, 16));
+  if constexpr (SEG >= 64) argmax_take(v, i, __shfl_xor(v, 32), __shfl_xor(i, 32));
+}
+
 __device__ __forceinline__ void wave_argmax(float& v, int& i) {
+  argmax_dpp<kDppXor1>(v, i);
+  argmax_dpp<kDppXor2>(v, i);
+  argmax_dpp<kDppHalfMirror>(v, i);
+  argmax_dpp<kDppMirror>(v, i);
+  float bv = lane_f(v, 0);
+  int bi = __builtin_amdgcn_readlane(i, 0);
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float ov = __shfl_xor(v, o);
-    const int oi = __shfl_xor(i, o);
-    if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
-  }
+  for (int r = 16; r < 64; r += 16) argmax_take(bv, bi, lane_f(v, r), __builtin_amdgcn_readlane(i, r));
+  v = bv;
+  i = bi;
 }
 
 // erf by Abramowitz & Stegun, Handbook of Mathematical Functions, eq. 7.1.26:

@@ -286,7 +286,9 @@ __device__ __forceinline__ void store4(const GemmArgs& p, int fmt, int g, int ro
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const float a = v[i] * col_scale(p, fmt, g, n + i);
-    if constexpr (EPI == EPI_F32_BIAS) r[i] = a + bias_at(p, g, n + i);
+    if constexpr (EPI == EPI_F32_BIAS)
+      r[i] = a + ((p.W2 && n >= p.n_split) ? (p.bias2 ? p.bias2[n - p.n_split + i] : 0.f)
+                                            : bias_at(p, g, n + i));
     else if constexpr (EPI == EPI_ROWSCALE) r[i] = v[i] * p.row_scale[row];
     else if constexpr (EPI == EPI_GELU) r[i] = gelu_erf(a + bias_at(p, g, n + i));
     else r[i] = (a + bias_at(p, g, n + i)) * p.row_scale[row];  // EPI_DOWN
@@ -721,8 +723,11 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(const GemmArgs p) {
   for (int t = 0; t < TN; ++t) {
     const int n = min(n0 + 16 * t + l16, p.N_out - 1);  // rows past N_out: loaded, never stored
     wn[t] = n;
-    wrow[t] = reinterpret_cast<const uint8_t*>(p.W) +
-              (g * p.w_gstride + static_cast<int64_t>(n) * p.ldw) * ESZ2 / 2;
+    wrow[t] = (p.W2 && n >= p.n_split)
+                  ? reinterpret_cast<const uint8_t*>(p.W2) +
+                        static_cast<int64_t>(n - p.n_split) * p.ldw2 * ESZ2 / 2
+                  : reinterpret_cast<const uint8_t*>(p.W) +
+                        (g * p.w_gstride + static_cast<int64_t>(n) * p.ldw) * ESZ2 / 2;
   }
   const int KS = p.K / 64;
   const int s_begin = wave * KS / NW, s_end = (wave + 1) * KS / NW;
@@ -1261,8 +1266,21 @@ bool skinny_fits(const GemmArgs& a) {
   return true;
 }
 
+int launch_front_gemm(const GemmArgs& a, hipStream_t s) {
+  if (a.fmt != SMOE_BF16 || a.epi != EPI_F32_BIAS || a.G != 0 || a.single_rows < 1 ||
+      a.single_rows > kFrontMaxN || !a.A || !a.W || !a.out || a.N_out <= 0)
+    return SMOE_EINVAL;
+  if (a.W2 && (a.n_split < 0 || a.n_split > a.N_out || a.n_split % 4 || a.ldw2 % 8))
+    return SMOE_EINVAL;
+  if (a.K % 64 || a.N_out % 4 || a.ldo % 4 || a.lda % 8 || a.ldw % 8) return SMOE_EINVAL;
+  // 16 channels per workgroup: the few hundred output channels spread over
+  // enough workgroups to stream the weights at a useful rate
+  return a.single_rows <= 16 ? launch_skinny<1, 1>(a, s) : launch_skinny<1, 2>(a, s);
+}
+
 int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
   if (a.N_out <= 0 || a.K <= 0) return SMOE_EINVAL;
+  if (a.W2) return SMOE_EINVAL;  // two weight segments: launch_front_gemm
   // pointers every launched workgroup dereferences
   if (!a.A || !a.W || !a.out || (a.G > 0 && !a.grp_off)) return SMOE_EINVAL;
   if ((a.epi == EPI_ROWSCALE || a.epi == EPI_DOWN) && !a.row_scale) return SMOE_EINVAL;

@@ -40,9 +40,19 @@ struct GemmArgs {
   const float* bias = nullptr;
   int64_t bias_gstride = 0;
   const float* row_scale = nullptr;
+  // optional second weight segment (launch_front_gemm only): output channels
+  // n >= n_split take row n - n_split of W2 (ldw2 elements apart) and bias2
+  const void* W2 = nullptr;
+  int ldw2 = 0;
+  int n_split = 0;
+  const float* bias2 = nullptr;
 };
 
 int launch_grouped_gemm(const GemmArgs& a, hipStream_t s);
+// One bf16 GEMM over a few rows (G == 0, single_rows <= 64) with f32 logits
+// out (EPI_F32_BIAS) from two weight segments: the router and all edge
+// generator rows of a small decode step in one pass.
+int launch_front_gemm(const GemmArgs& a, hipStream_t s);
 
 // ---- routing ----
 int launch_route_topk(const float* logits, int N, int E, int K, int32_t* top_idx, float* top_w,
@@ -56,6 +66,19 @@ size_t plan_scratch_bytes(int N, int G);
 int launch_plan(const int32_t* tok_g, const float* tok_w, int N, int S, int G, int drop_nonpos,
                 int32_t* cnt, int32_t* acnt, int32_t* off, int32_t* rows, float* roww,
                 int32_t* tokrow, void* scratch, hipStream_t s);
+// Small N: router top-k, expert plan, edge top-m over the dense per-source
+// edge logits and the destination plan in one workgroup.  front: f32
+// [N, ldf] with router logits in columns [0, E) and the edge logits of
+// source s in columns E + s E .. E + s E + E - 1.  Writes every output the
+// separate stages write (logits and edge_logit too).
+int launch_front_route(const float* front, int ldf, int N, int E, int K, int M, int S,
+                       float* logits, int32_t* top_idx, float* top_w, int32_t* tok_e,
+                       float* tok_ew, int32_t* e_cnt, int32_t* e_acnt, int32_t* e_off,
+                       int32_t* e_rows, float* e_roww, int32_t* e_tokrow, float* edge_logit,
+                       int32_t* edge_idx, float* edge_w, int32_t* tok_d, float* tok_dc,
+                       int32_t* d_cnt, int32_t* d_acnt, int32_t* d_off, int32_t* d_rows,
+                       float* d_roww, int32_t* d_tokrow, hipStream_t s);
+constexpr int kFrontMaxN = 64;
 int launch_edge_loop_bias(const void* wg, int act_dtype, const float* bg, const float* emb, int E,
                           int H, int L, int R, float* out, hipStream_t s);
 

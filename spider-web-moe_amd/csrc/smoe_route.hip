@@ -2,9 +2,10 @@
 // per-token destination coefficients, and the stable dispatch plan.
 //
 // Router (model.py:255-258): logits (fp32, loop bias added by the logits
-// GEMM) -> softmax -> top-k -> renorm by max(sum, 1e-9).  One wave per token,
-// lane e holds expert e (E <= 64); selection is on the logits (softmax is
-// monotonic), ties to the lowest index.
+// GEMM) -> softmax -> top-k -> renorm by max(sum, 1e-9).  One segment of
+// SEG = 16 / 32 / 64 lanes per token (the smallest that holds E <= 64; a wave
+// holds 64 / SEG tokens), lane e of the segment holds expert e; selection is
+// on the logits (softmax is monotonic), ties to the lowest index.
 //
 // Edges (model.py:261-288): for each of the token's router-selected sources
 // s, top-m over the raw edge logits g[s, :] and an fp32 softmax over the m
@@ -24,59 +25,91 @@ namespace smoe {
 constexpr int kBig = 1 << 20;
 
 // ------------------------------------------------------------ router ----
+// Segment of token t (lane e of the segment: expert e, logit v, -inf past
+// E); tokens with !ok compute but store nothing.  tok_e2 / tok_ew2 (may be
+// null) receive a second copy of tok_e / tok_ew (indexed t * K + slot).
+// The K loop stays rolled: unrolled copies overflow the instruction cache of
+// the single-workgroup front, which runs each instruction a few times only.
+// p of the selected expert is recomputed from its logit (the same ops on the
+// same value as p itself).
+template <int SEG>
+__device__ __forceinline__ void topk_seg(float v, int t, bool ok, int E, int K,
+                                         int32_t* __restrict__ top_idx, float* __restrict__ top_w,
+                                         int32_t* __restrict__ tok_e, float* __restrict__ tok_ew,
+                                         int32_t* tok_e2, float* tok_ew2) {
+  const int lane = threadIdx.x & 63;
+  const int e = lane & (SEG - 1), sbase = lane - e;
+  const bool in = e < E;
+  v = in ? v : -INFINITY;
+  const float mx = seg_max<SEG>(v);
+  const float ex = in ? expf(v - mx) : 0.f;
+  const float sum = seg_sum<SEG>(ex);
+  const float p = ex / sum;
+  bool sel = false;
+  float psum = 0.f, slot_p = 0.f;
+  int slot_i = 0;
+#pragma unroll 1
+  for (int j = 0; j < K; ++j) {
+    float cv = (in && !sel) ? v : -INFINITY;
+    int ci = (in && !sel) ? e : kBig;
+    seg_argmax<SEG>(cv, ci);
+    const float pj = expf(cv - mx) / sum;
+    sel = sel || e == ci;
+    slot_p = e == j ? pj : slot_p;
+    slot_i = e == j ? ci : slot_i;
+    psum += pj;  // slot order, as torch sums the k values
+  }
+  const float denom = fmaxf(psum, 1e-9f);
+  if (ok && e < K) {
+    top_idx[static_cast<int64_t>(t) * K + e] = slot_i;
+    top_w[static_cast<int64_t>(t) * K + e] = slot_p / denom;
+  }
+  // distinct experts of the token in ascending order (lane order)
+  const uint64_t segm = SEG == 64 ? ~0ull : ((1ull << SEG) - 1);
+  const uint64_t m = (__ballot(sel) >> sbase) & segm;
+  if (ok && sel) {
+    const int rank = __popcll(m & ((1ull << e) - 1));
+    tok_e[static_cast<int64_t>(t) * K + rank] = e;
+    tok_ew[static_cast<int64_t>(t) * K + rank] = p / denom;
+    if (tok_e2) {
+      tok_e2[t * K + rank] = e;
+      tok_ew2[t * K + rank] = p / denom;
+    }
+  }
+}
+
+template <int SEG>
 __global__ __launch_bounds__(256) void k_route_topk(const float* __restrict__ logits, int N, int E,
                                                     int K, int32_t* __restrict__ top_idx,
                                                     float* __restrict__ top_w,
                                                     int32_t* __restrict__ tok_e,
                                                     float* __restrict__ tok_ew) {
+  constexpr int TPW = 64 / SEG;
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= N) return;
-  const bool in = lane < E;
-  const float v = in ? logits[static_cast<int64_t>(t) * E + lane] : -INFINITY;
-  const float mx = wave_max(v);
-  const float ex = in ? expf(v - mx) : 0.f;
-  const float sum = wave_sum(ex);
-  const float p = ex / sum;
-  bool sel = false;
-  float psum = 0.f;
-  float slot_p = 0.f;
-  int slot_i = 0;
-#pragma unroll
-  for (int j = 0; j < 16; ++j) {  // K <= 16
-    if (j < K) {
-      float cv = (in && !sel) ? v : -INFINITY;
-      int ci = (in && !sel) ? lane : kBig;
-      wave_argmax(cv, ci);
-      const float pj = __shfl(p, ci & 63);
-      if (lane == ci) sel = true;
-      if (lane == j) {
-        slot_p = pj;
-        slot_i = ci;
-      }
-      psum += pj;  // slot order, as torch sums the k values
-    }
-  }
-  const float denom = fmaxf(psum, 1e-9f);
-  if (lane < K) {
-    top_idx[static_cast<int64_t>(t) * K + lane] = slot_i;
-    top_w[static_cast<int64_t>(t) * K + lane] = slot_p / denom;
-  }
-  // distinct experts of the token in ascending order (lane order)
-  const uint64_t m = __ballot(sel);
-  if (sel) {
-    const int rank = __popcll(m & ((1ull << lane) - 1));
-    tok_e[static_cast<int64_t>(t) * K + rank] = lane;
-    tok_ew[static_cast<int64_t>(t) * K + rank] = p / denom;
-  }
+  const int t0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * TPW;
+  if (t0 >= N) return;  // wave-uniform
+  const int e = lane & (SEG - 1);
+  const int t = t0 + lane / SEG;
+  const bool ok = t < N;
+  const float v = logits[static_cast<int64_t>(ok ? t : N - 1) * E + (e < E ? e : E - 1)];
+  topk_seg<SEG>(v, t, ok, E, K, top_idx, top_w, tok_e, tok_ew, nullptr, nullptr);
 }
+
+// segment width for E entries per token (E <= 64)
+inline int seg_of(int E) { return E <= 16 ? 16 : (E <= 32 ? 32 : 64); }
 
 int launch_route_topk(const float* logits, int N, int E, int K, int32_t* top_idx, float* top_w,
                       int32_t* tok_e, float* tok_ew, hipStream_t s) {
   if (E < 1 || E > 64 || K < 1 || K > E || K > 16) return SMOE_EINVAL;
   if (N <= 0) return SMOE_OK;
-  hipLaunchKernelGGL(k_route_topk, dim3((N + 3) / 4), dim3(256), 0, s, logits, N, E, K, top_idx,
-                     top_w, tok_e, tok_ew);
+  const int seg = seg_of(E), per_block = 4 * (64 / seg);
+  const dim3 grid((N + per_block - 1) / per_block), block(256);
+  if (seg == 16)
+    hipLaunchKernelGGL(k_route_topk<16>, grid, block, 0, s, logits, N, E, K, top_idx, top_w, tok_e, tok_ew);
+  else if (seg == 32)
+    hipLaunchKernelGGL(k_route_topk<32>, grid, block, 0, s, logits, N, E, K, top_idx, top_w, tok_e, tok_ew);
+  else
+    hipLaunchKernelGGL(k_route_topk<64>, grid, block, 0, s, logits, N, E, K, top_idx, top_w, tok_e, tok_ew);
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 
@@ -129,11 +162,78 @@ int launch_merge_slots(const int32_t* idx, const float* w, int N, int K, int E, 
 }
 
 // ------------------------------------------------------------- edges ----
-// One wave per token, lane d = destination.  The token's KB source slots
-// (KB >= K, a compile-time bucket) are fetched one lane per slot, then all
-// their logit rows at once (slots past K or empty read row 0 and are
-// dropped), so the kernel waits on memory twice.
-template <int KB>
+// Segment of token t, lane d of the segment = destination d.  Source slot j
+// of the token has logit v[j] (lane d: the logit of edge s_j -> d), plan
+// row row[j] and is live when j < K and the slot holds a source (dead slots
+// compute on garbage and store nothing; tokens with !ok store nothing).
+// Writes top-m and softmax weights per source row (edge_idx / edge_w at the
+// plan row) and the token's destination coefficients (tok_d / tok_dc, and a
+// second copy in tok_d2 / tok_dc2 when not null, indexed t * S + slot).
+template <int SEG, int KB>
+__device__ __forceinline__ void topm_seg(const float (&v)[KB], const int (&row)[KB],
+                                         const bool (&live)[KB], int t, bool ok, int E, int M,
+                                         int S, int32_t* __restrict__ edge_idx,
+                                         float* __restrict__ edge_w, int32_t* __restrict__ tok_d,
+                                         float* __restrict__ tok_dc, int32_t* tok_d2,
+                                         float* tok_dc2) {
+  const int lane = threadIdx.x & 63;
+  const int d = lane & (SEG - 1), sbase = lane - d;
+  const bool in = d < E;
+  float c = 0.f;
+#pragma unroll
+  for (int j = 0; j < KB; ++j) {
+    if (!__ballot(live[j])) continue;  // uniform (sources are packed first)
+    const float vj = (in && live[j]) ? v[j] : -INFINITY;
+    bool sel = false;
+    float vmax = 0.f, den = 0.f, rec_v = 0.f;
+    int rec_i = 0;
+#pragma unroll 1
+    for (int i = 0; i < M; ++i) {  // rolled, as the top-k loop
+      float cv = (in && !sel) ? vj : -INFINITY;
+      int ci = (in && !sel) ? d : kBig;
+      seg_argmax<SEG>(cv, ci);
+      sel = sel || d == ci;
+      vmax = i == 0 ? cv : vmax;
+      rec_v = d == i ? cv : rec_v;
+      rec_i = d == i ? ci : rec_i;
+      den += expf(cv - vmax);  // softmax over the m values, slot order
+    }
+    if (live[j]) {
+      if (sel) c += expf(vj - vmax) / den;
+      if (ok && d < M) {
+        edge_idx[static_cast<int64_t>(row[j]) * M + d] = rec_i;
+        edge_w[static_cast<int64_t>(row[j]) * M + d] = expf(rec_v - vmax) / den;
+      }
+    }
+  }
+  const bool nz = in && c != 0.f;
+  const uint64_t segm = SEG == 64 ? ~0ull : ((1ull << SEG) - 1);
+  const uint64_t m = (__ballot(nz) >> sbase) & segm;
+  const int cnt = __popcll(m);
+  if (ok && nz) {
+    const int rank = __popcll(m & ((1ull << d) - 1));
+    tok_d[static_cast<int64_t>(t) * S + rank] = d;
+    tok_dc[static_cast<int64_t>(t) * S + rank] = c;
+    if (tok_d2) {
+      tok_d2[t * S + rank] = d;
+      tok_dc2[t * S + rank] = c;
+    }
+  }
+  if (ok && d >= cnt && d < S) {
+    tok_d[static_cast<int64_t>(t) * S + d] = -1;
+    tok_dc[static_cast<int64_t>(t) * S + d] = 0.f;
+    if (tok_d2) {
+      tok_d2[t * S + d] = -1;
+      tok_dc2[t * S + d] = 0.f;
+    }
+  }
+}
+
+// The segment's KB source slots (KB >= K, a compile-time bucket): their
+// sources and plan rows (every lane reads the same entries, one load each),
+// then all their logit rows at once (rows in expert-plan order; slots past K
+// or empty read row 0 and are dropped), so the wave waits on memory twice.
+template <int SEG, int KB>
 __global__ __launch_bounds__(256) void k_edge_topm(const float* __restrict__ edge_logit,
                                                    const int32_t* __restrict__ tok_e,
                                                    const int32_t* __restrict__ e_tokrow, int N,
@@ -142,65 +242,31 @@ __global__ __launch_bounds__(256) void k_edge_topm(const float* __restrict__ edg
                                                    float* __restrict__ edge_w,
                                                    int32_t* __restrict__ tok_d,
                                                    float* __restrict__ tok_dc) {
+  constexpr int TPW = 64 / SEG;
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= N) return;
-  const bool in = lane < E;
-  const int64_t e = static_cast<int64_t>(t) * K + (lane < K ? lane : K - 1);
-  const int src_l = tok_e[e];
-  const int row_l = e_tokrow[e];
+  const int t0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * TPW;
+  if (t0 >= N) return;  // wave-uniform
+  const int d = lane & (SEG - 1);
+  const int t = t0 + lane / SEG;
+  const bool ok = t < N;
+  const int64_t tb = static_cast<int64_t>(ok ? t : N - 1) * K;
+  int src[KB], rw[KB];
+#pragma unroll
+  for (int j = 0; j < KB; ++j) {
+    const int jj = j < K ? j : K - 1;
+    src[j] = tok_e[tb + jj];
+    rw[j] = e_tokrow[tb + jj];
+  }
   int row[KB];
   bool live[KB];
   float v[KB];
 #pragma unroll
   for (int j = 0; j < KB; ++j) {
-    const int sj = __shfl(src_l, j);
-    const int rj = __shfl(row_l, j);
-    live[j] = j < K && sj >= 0;  // sources are packed first (ascending expert)
-    row[j] = live[j] ? rj : 0;
-    v[j] = edge_logit[static_cast<int64_t>(row[j]) * E + (in ? lane : 0)];
+    live[j] = ok && j < K && src[j] >= 0;  // sources are packed first (ascending expert)
+    row[j] = live[j] ? rw[j] : 0;
+    v[j] = edge_logit[static_cast<int64_t>(row[j]) * E + (d < E ? d : E - 1)];
   }
-  float c = 0.f;
-#pragma unroll
-  for (int j = 0; j < KB; ++j) {
-    if (!live[j]) continue;  // uniform
-    const float vj = in ? v[j] : -INFINITY;
-    bool sel = false;
-    float vmax = 0.f, den = 0.f, rec_v = 0.f;
-    int rec_i = 0;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {  // M <= 16
-      if (i < M) {
-        float cv = (in && !sel) ? vj : -INFINITY;
-        int ci = (in && !sel) ? lane : kBig;
-        wave_argmax(cv, ci);
-        if (lane == ci) sel = true;
-        if (i == 0) vmax = cv;
-        if (lane == i) {
-          rec_v = cv;
-          rec_i = ci;
-        }
-        den += expf(cv - vmax);  // softmax over the m values, slot order
-      }
-    }
-    if (sel) c += expf(vj - vmax) / den;
-    if (lane < M) {
-      edge_idx[static_cast<int64_t>(row[j]) * M + lane] = rec_i;
-      edge_w[static_cast<int64_t>(row[j]) * M + lane] = expf(rec_v - vmax) / den;
-    }
-  }
-  const bool nz = in && c != 0.f;
-  const uint64_t m = __ballot(nz);
-  const int cnt = __popcll(m);
-  if (nz) {
-    const int rank = __popcll(m & ((1ull << lane) - 1));
-    tok_d[static_cast<int64_t>(t) * S + rank] = lane;
-    tok_dc[static_cast<int64_t>(t) * S + rank] = c;
-  }
-  if (lane >= cnt && lane < S) {
-    tok_d[static_cast<int64_t>(t) * S + lane] = -1;
-    tok_dc[static_cast<int64_t>(t) * S + lane] = 0.f;
-  }
+  topm_seg<SEG, KB>(v, row, live, t, ok, E, M, S, edge_idx, edge_w, tok_d, tok_dc, nullptr, nullptr);
 }
 
 int launch_edge_topm(const float* edge_logit, const int32_t* tok_e, const int32_t* e_tokrow,
@@ -209,15 +275,23 @@ int launch_edge_topm(const float* edge_logit, const int32_t* tok_e, const int32_
   if (E < 1 || E > 64 || M < 1 || M > E || M > 16 || S < 1 || S > 64 || K < 1 || K > 16)
     return SMOE_EINVAL;
   if (N <= 0) return SMOE_OK;
-  const dim3 grid((N + 3) / 4), block(256);
-#define SMOE_EDGE_TOPM(KB)                                                                     \
-  hipLaunchKernelGGL(k_edge_topm<KB>, grid, block, 0, s, edge_logit, tok_e, e_tokrow, N, E, K, M, \
-                     S, edge_idx, edge_w, tok_d, tok_dc)
-  if (K <= 1) SMOE_EDGE_TOPM(1);
-  else if (K <= 2) SMOE_EDGE_TOPM(2);
-  else if (K <= 4) SMOE_EDGE_TOPM(4);
-  else if (K <= 8) SMOE_EDGE_TOPM(8);
-  else SMOE_EDGE_TOPM(16);
+  const int seg = seg_of(E), per_block = 4 * (64 / seg);
+  const dim3 grid((N + per_block - 1) / per_block), block(256);
+#define SMOE_EDGE_TOPM(SG, KB)                                                                   \
+  hipLaunchKernelGGL((k_edge_topm<SG, KB>), grid, block, 0, s, edge_logit, tok_e, e_tokrow, N, E, \
+                     K, M, S, edge_idx, edge_w, tok_d, tok_dc)
+#define SMOE_EDGE_TOPM_K(SG)           \
+  do {                                 \
+    if (K <= 1) SMOE_EDGE_TOPM(SG, 1); \
+    else if (K <= 2) SMOE_EDGE_TOPM(SG, 2); \
+    else if (K <= 4) SMOE_EDGE_TOPM(SG, 4); \
+    else if (K <= 8) SMOE_EDGE_TOPM(SG, 8); \
+    else SMOE_EDGE_TOPM(SG, 16);       \
+  } while (0)
+  if (seg == 16) SMOE_EDGE_TOPM_K(16);
+  else if (seg == 32) SMOE_EDGE_TOPM_K(32);
+  else SMOE_EDGE_TOPM_K(64);
+#undef SMOE_EDGE_TOPM_K
 #undef SMOE_EDGE_TOPM
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
@@ -456,17 +530,26 @@ __global__ __launch_bounds__(256) void k_plan_scatter(const int32_t* __restrict_
 // chunk counts in LDS (C <= 64: one chunk per lane in the scan).  Groups are
 // cut into windows of `win` so that the rank work spreads over the waves.
 constexpr int kSmallMaxCells = 8192;
-__global__ __launch_bounds__(1024) void k_plan_small(const int32_t* __restrict__ tok_g,
-                                                     const float* __restrict__ tok_w, int N,
-                                                     int S, int G, int drop, int win,
-                                                     int32_t* __restrict__ cnt,
-                                                     int32_t* __restrict__ acnt,
-                                                     int32_t* __restrict__ off,
-                                                     int32_t* __restrict__ rows,
-                                                     float* __restrict__ roww,
-                                                     int32_t* __restrict__ tokrow) {
-  __shared__ int cc[kSmallMaxCells], ca[kSmallMaxCells];
-  __shared__ int tot[kPlanMaxG], goff[kPlanMaxG + 1], wsum[4];
+struct PlanSmem {
+  int cc[kSmallMaxCells], ca[kSmallMaxCells];
+  int tot[kPlanMaxG], goff[kPlanMaxG + 1], wsum[4];
+};
+
+// Every thread of a 1024-thread workgroup calls it; ends with the plan
+// written (tokrow / rows / roww by the scatter of the calling thread).
+__device__ __forceinline__ void plan_small_body(const int32_t* __restrict__ tok_g,
+                                                const float* __restrict__ tok_w, int N, int S,
+                                                int G, int drop, int win, int32_t* __restrict__ cnt,
+                                                int32_t* __restrict__ acnt,
+                                                int32_t* __restrict__ off,
+                                                int32_t* __restrict__ rows,
+                                                float* __restrict__ roww,
+                                                int32_t* __restrict__ tokrow, PlanSmem& sm) {
+  int* cc = sm.cc;
+  int* ca = sm.ca;
+  int* tot = sm.tot;
+  int* goff = sm.goff;
+  int* wsum = sm.wsum;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int C = (N + 63) / 64;
   const int W = (G + win - 1) / win;
@@ -501,6 +584,133 @@ __global__ __launch_bounds__(1024) void k_plan_small(const int32_t* __restrict__
     scatter_token(tok_g, tok_w, t, S, G, cc + (t >> 6), C, goff, rows, roww, tokrow);
 }
 
+__global__ __launch_bounds__(1024) void k_plan_small(const int32_t* __restrict__ tok_g,
+                                                     const float* __restrict__ tok_w, int N,
+                                                     int S, int G, int drop, int win,
+                                                     int32_t* __restrict__ cnt,
+                                                     int32_t* __restrict__ acnt,
+                                                     int32_t* __restrict__ off,
+                                                     int32_t* __restrict__ rows,
+                                                     float* __restrict__ roww,
+                                                     int32_t* __restrict__ tokrow) {
+  __shared__ PlanSmem sm;
+  plan_small_body(tok_g, tok_w, N, S, G, drop, win, cnt, acnt, off, rows, roww, tokrow, sm);
+}
+
+// Window of the single-workgroup plan: narrower windows until the 16 waves
+// have work.
+inline int plan_small_win(int C, int G) {
+  int win = 64;
+  while (win > 8 && C * ((G + win - 1) / win) < 16) win >>= 1;
+  return win;
+}
+
+// Small decode steps: every routing stage in one workgroup of 16 waves, the
+// phases separated by workgroup barriers; a token is a segment of SEG lanes
+// (64 / SEG tokens per wave, 1024 / SEG per pass).  What a later phase reads
+// (the tokens' sources and destinations, the plans' token rows) also goes to
+// LDS, so only the logits come from memory.  Within a phase a wave issues
+// its logit loads (clamped indices, no branch) before its stores: loads and
+// stores share one in-order counter, so a load issued after a store would
+// wait for it.
+constexpr int kFrontMaxSrc = kFrontMaxN * 16;   // N*K
+constexpr int kFrontMaxDst = kFrontMaxN * 64;   // N*S
+template <int SEG, int KB>
+__global__ __launch_bounds__(1024) void k_front_route(
+    const float* __restrict__ front, int ldf, int N, int E, int K, int M, int S, int win,
+    float* __restrict__ logits, int32_t* __restrict__ top_idx, float* __restrict__ top_w,
+    int32_t* __restrict__ tok_e, float* __restrict__ tok_ew, int32_t* __restrict__ e_cnt,
+    int32_t* __restrict__ e_acnt, int32_t* __restrict__ e_off, int32_t* __restrict__ e_rows,
+    float* __restrict__ e_roww, int32_t* __restrict__ e_tokrow, float* __restrict__ edge_logit,
+    int32_t* __restrict__ edge_idx, float* __restrict__ edge_w, int32_t* __restrict__ tok_d,
+    float* __restrict__ tok_dc, int32_t* __restrict__ d_cnt, int32_t* __restrict__ d_acnt,
+    int32_t* __restrict__ d_off, int32_t* __restrict__ d_rows, float* __restrict__ d_roww,
+    int32_t* __restrict__ d_tokrow) {
+  constexpr int PASS = 1024 / SEG;  // tokens per pass
+  __shared__ PlanSmem sm;
+  __shared__ int32_t s_e[kFrontMaxSrc], s_etr[kFrontMaxSrc], s_d[kFrontMaxDst], s_dtr[kFrontMaxDst];
+  __shared__ float s_ew[kFrontMaxSrc], s_dc[kFrontMaxDst];
+  const int lane = threadIdx.x & 63;
+  const int e = lane & (SEG - 1);
+  const int le = e < E ? e : E - 1;
+  const int tl = threadIdx.x / SEG;  // token of this lane within a pass
+  // 1 router top-k (and the logits region)
+  for (int t0 = 0; t0 < N; t0 += PASS) {
+    const int t = t0 + tl;
+    const bool ok = t < N;
+    const float v = front[static_cast<int64_t>(ok ? t : N - 1) * ldf + le];
+    if (ok && e < E) logits[static_cast<int64_t>(t) * E + e] = v;
+    topk_seg<SEG>(v, t, ok, E, K, top_idx, top_w, tok_e, tok_ew, s_e, s_ew);
+  }
+  __syncthreads();
+  // 2 expert plan
+  plan_small_body(s_e, s_ew, N, K, E, 0, win, e_cnt, e_acnt, e_off, e_rows, e_roww, s_etr, sm);
+  __syncthreads();
+  // 3 top-m over each token's sources (dense logit rows of the front GEMM)
+  const float* dense = front + E;
+  for (int t0 = 0; t0 < N; t0 += PASS) {
+    const int t = t0 + tl;
+    const bool ok = t < N;
+    const int tc = ok ? t : N - 1;
+    float v[KB];
+    int row[KB];
+    bool live[KB];
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+      const int jj = j < K ? j : K - 1;
+      const int sj = s_e[tc * K + jj], rj = s_etr[tc * K + jj];
+      live[j] = ok && j < K && sj >= 0;
+      row[j] = live[j] ? rj : 0;
+      v[j] = dense[static_cast<int64_t>(tc) * ldf + (live[j] ? sj : 0) * E + le];
+    }
+#pragma unroll
+    for (int j = 0; j < KB; ++j)
+      if (live[j] && e < E) edge_logit[static_cast<int64_t>(row[j]) * E + e] = v[j];
+    topm_seg<SEG, KB>(v, row, live, t, ok, E, M, S, edge_idx, edge_w, tok_d, tok_dc, s_d, s_dc);
+  }
+  for (int i = threadIdx.x; i < N * K; i += 1024) e_tokrow[i] = s_etr[i];
+  __syncthreads();
+  // 4 destination plan
+  plan_small_body(s_d, s_dc, N, S, E, 1, win, d_cnt, d_acnt, d_off, d_rows, d_roww, s_dtr, sm);
+  __syncthreads();
+  for (int i = threadIdx.x; i < N * S; i += 1024) d_tokrow[i] = s_dtr[i];
+}
+
+int launch_front_route(const float* front, int ldf, int N, int E, int K, int M, int S,
+                       float* logits, int32_t* top_idx, float* top_w, int32_t* tok_e,
+                       float* tok_ew, int32_t* e_cnt, int32_t* e_acnt, int32_t* e_off,
+                       int32_t* e_rows, float* e_roww, int32_t* e_tokrow, float* edge_logit,
+                       int32_t* edge_idx, float* edge_w, int32_t* tok_d, float* tok_dc,
+                       int32_t* d_cnt, int32_t* d_acnt, int32_t* d_off, int32_t* d_rows,
+                       float* d_roww, int32_t* d_tokrow, hipStream_t s) {
+  if (N < 1 || N > kFrontMaxN || E < 1 || E > 64 || K < 1 || K > 16 || K > E || M < 1 || M > 16 ||
+      M > E || S < 1 || S > 64 || ldf < E + E * E)
+    return SMOE_EINVAL;
+  const int C = (N + 63) / 64;
+  if (C * E > kSmallMaxCells) return SMOE_EINVAL;
+  const int win = plan_small_win(C, E);
+#define SMOE_FRONT(SG, KB)                                                                      \
+  hipLaunchKernelGGL((k_front_route<SG, KB>), dim3(1), dim3(1024), 0, s, front, ldf, N, E, K, M, S, \
+                     win, logits, top_idx, top_w, tok_e, tok_ew, e_cnt, e_acnt, e_off, e_rows,     \
+                     e_roww, e_tokrow, edge_logit, edge_idx, edge_w, tok_d, tok_dc, d_cnt, d_acnt, \
+                     d_off, d_rows, d_roww, d_tokrow)
+#define SMOE_FRONT_K(SG)           \
+  do {                             \
+    if (K <= 1) SMOE_FRONT(SG, 1); \
+    else if (K <= 2) SMOE_FRONT(SG, 2); \
+    else if (K <= 4) SMOE_FRONT(SG, 4); \
+    else if (K <= 8) SMOE_FRONT(SG, 8); \
+    else SMOE_FRONT(SG, 16);       \
+  } while (0)
+  const int seg = seg_of(E);
+  if (seg == 16) SMOE_FRONT_K(16);
+  else if (seg == 32) SMOE_FRONT_K(32);
+  else SMOE_FRONT_K(64);
+#undef SMOE_FRONT_K
+#undef SMOE_FRONT
+  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
 size_t plan_scratch_bytes(int N, int G) {
   const size_t C = (static_cast<size_t>(N > 0 ? N : 1) + 63) / 64;
   return 2 * C * static_cast<size_t>(G) * sizeof(int32_t);
@@ -514,8 +724,7 @@ int launch_plan(const int32_t* tok_g, const float* tok_w, int N, int S, int G, i
   // One workgroup while its rank work (C x G ballots) stays small; the
   // three-kernel form spreads larger plans over the chip.
   if (C * G <= 512) {
-    int win = 64;  // narrower windows until the 16 waves have work
-    while (win > 8 && C * ((G + win - 1) / win) < 16) win >>= 1;
+    const int win = plan_small_win(C, G);
     hipLaunchKernelGGL(k_plan_small, dim3(1), dim3(1024), 0, s, tok_g, tok_w, N, S, G, drop, win,
                        cnt, acnt, off, rows, roww, tokrow);
     return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;

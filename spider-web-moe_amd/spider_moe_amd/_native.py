@@ -42,7 +42,7 @@ class SmoeBlock(ctypes.Structure):
 _LAYOUT_FIELDS = ["total", "logits", "top_idx", "top_w", "tok_e", "tok_ew", "e_cnt", "e_acnt",
                   "e_off", "e_rows", "e_roww", "e_tokrow", "edge_logit", "edge_idx", "edge_w",
                   "tok_d", "tok_dc", "d_cnt", "d_acnt", "d_off", "d_rows", "d_roww", "d_tokrow",
-                  "proj", "msg", "act", "y", "h_tmp", "scratch"]
+                  "proj", "msg", "act", "y", "h_tmp", "scratch", "front"]
 
 
 class SmoeWsLayout(ctypes.Structure):
@@ -79,8 +79,11 @@ SIGNATURES = {
 }
 
 STAGES = ["router_gemm", "route_topk", "expert_plan", "edge_logits", "edge_topm", "dest_plan",
-          "edge_gemm", "msg_combine", "up_gemm", "down_gemm", "epilogue"]
+          "edge_gemm", "msg_combine", "up_gemm", "down_gemm", "epilogue",
+          # bf16 steps of N <= 64: stages 0-5 as one GEMM and one routing workgroup
+          "front_gemm", "front_route"]
 
+ABI_VERSION = 2
 _LIB = None
 
 
@@ -97,7 +100,7 @@ def lib():
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
-        if handle.smoe_abi_version() != 1:
+        if handle.smoe_abi_version() != ABI_VERSION:
             raise RuntimeError("libsmoe.so ABI version mismatch")
         _LIB = handle
     return _LIB

@@ -115,6 +115,26 @@ def test_block_small_bf16_per_loop(spec):
         h, rep = _check_loop(wl.layer, h, wl.x0, r, 1e-2)
 
 
+@pytest.mark.parametrize("n,e,k,m", [(1, 16, 2, 2), (37, 16, 2, 2), (64, 32, 4, 2), (48, 64, 2, 4),
+                                     (64, 16, 3, 3), (65, 16, 2, 2), (200, 64, 2, 4)])
+def test_block_small_steps_fused_front(n, e, k, m):
+    """bf16 steps of N <= 64 tokens run stages 1-6 as one logits GEMM over
+    the router and every edge-generator row plus one routing workgroup
+    (top-k, expert plan, top-m, destination plan); N = 65 and 200 take the
+    separate stages.  Routing, plans and outputs against the oracle for two
+    loops, at E 16 / 32 / 64."""
+    from spider_moe_amd.workloads import make_block
+    say("fused front", n, e, k, m)
+    wl = make_block("c1", tokens=n, hidden_size=128, num_experts=e, top_k=k, edges_per_expert=m,
+                    expert_ffn_size=256, num_loops=2, expert_activation="swiglu", experts="bf16")
+    h = wl.h
+    for r in range(2):
+        h, rep = _check_loop(wl.layer, h, wl.x0, r, 1e-2)
+    rt = wl.layer.last_routing()
+    assert int(rt["e_cnt"].sum()) == n * k
+    assert int(rt["d_cnt"].sum()) == int((rt["tok_d"] >= 0).sum())
+
+
 def test_block_skewed_empty_experts():
     from spider_moe_amd.workloads import make_block
     say("skewed small")

@@ -38,7 +38,7 @@ def test_exports_every_declared_symbol(nat):
 
 def test_identity(nat):
     lib = nat.lib()
-    assert lib.smoe_abi_version() == 1
+    assert lib.smoe_abi_version() == 2
     assert lib.smoe_backend_name() == b"hip-gfx950"
     assert lib.smoe_backend_caps() == 0b1111
 
@@ -69,12 +69,17 @@ def test_workspace_layout_is_consistent(nat):
     assert lay.total == lib.smoe_block_workspace_bytes(ctypes.byref(b), n)
     offs = sorted((getattr(lay, f), f) for f in nat._LAYOUT_FIELDS if f != "total")
     assert all(o % 256 == 0 for o, _ in offs)
-    assert offs[-1][0] < lay.total
+    assert lay.front == lay.total  # the fused small-step front is off at this N: empty region
+    assert max(o for o, f in offs if f != "front") < lay.total
     assert lay.S == 4 and lay.ffn_dtype == nat.BF16
     # regions do not overlap: each is at least its size from the next
     assert lay.top_idx - lay.logits >= n * 16 * 4
     assert lay.act + n * 2 * 2816 * 2 <= lay.y
     assert lay.proj + n * 4 * 1024 * 2 <= lay.msg
+    # a decode-size step (N <= 256, bf16) gets the front region: [N, E + E*E] f32
+    small = nat.SmoeWsLayout()
+    assert lib.smoe_block_workspace_layout(ctypes.byref(b), 64, ctypes.byref(small)) == 0
+    assert small.total - small.front >= 64 * (16 + 16 * 16) * 4
 
 
 @pytest.mark.parametrize("bad", [dict(K=0), dict(K=17), dict(E=65), dict(M=0), dict(H=1000),
