@@ -158,6 +158,32 @@ __device__ __forceinline__ void seg_argmax(float& v, int& i) {
   if constexpr (SEG >= 64) argmax_take(v, i, __shfl_xor(v, 32), __shfl_xor(i, 32));
 }
 
+// Inclusive prefix sum over the wave in lane order: Hillis-Steele within
+// each 16-lane row (DPP row_shr 1, 2, 4, 8, zero fill), then row_bcast15 /
+// row_bcast31 carry the row totals into the rows above.
+template <int CTRL>
+__device__ __forceinline__ int dpp_shr0(int x) {  // out-of-row sources read 0
+  return __builtin_amdgcn_update_dpp(0, x, CTRL, 0xF, 0xF, true);
+}
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  v += dpp_shr0<0x111>(v);
+  v += dpp_shr0<0x112>(v);
+  v += dpp_shr0<0x114>(v);
+  v += dpp_shr0<0x118>(v);
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast15 -> rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast31 -> rows 2, 3
+  return v;
+}
+
+// Workgroup barrier ordering LDS only: waits for the wave's LDS accesses
+// (lgkmcnt) but not for its global stores, which no other wave of the
+// workgroup reads back.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ void wave_argmax(float& v, int& i) {
   argmax_dpp<kDppXor1>(v, i);
   argmax_dpp<kDppXor2>(v, i);

@@ -427,27 +427,26 @@ __device__ __forceinline__ void scatter_token(const int32_t* __restrict__ tok_g,
 }
 
 // Exclusive scan of tot[0..G) into goff[0..G].  Every thread of the
-// workgroup calls it (it holds barriers); the first 256 do the work.
+// workgroup calls it (it holds barriers); the first 256 do the work.  With
+// LDS_ONLY the barriers order LDS alone (tot, goff and wsum in LDS).
+template <bool LDS_ONLY = false>
 __device__ __forceinline__ void block_group_offsets(const int32_t* tot, int G, int* goff,
                                                     int* wsum) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const bool act = tid < 256;
   const int v = (act && tid < G) ? tot[tid] : 0;
-  int incl = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int u = __shfl_up(incl, o);
-    if (lane >= o) incl += u;
-  }
+  const int incl = wave_incl_scan(v);
   if (act && lane == 63) wsum[wave] = incl;
-  __syncthreads();
+  if constexpr (LDS_ONLY) lds_barrier();
+  else __syncthreads();
   if (act) {
     int before = 0;
     for (int w = 0; w < wave; ++w) before += wsum[w];
     if (tid < G) goff[tid] = before + incl - v;
     if (tid == 0) goff[G] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
   }
-  __syncthreads();
+  if constexpr (LDS_ONLY) lds_barrier();
+  else __syncthreads();
 }
 
 // ccnt / cacnt are [G, C] (group-major).  Wave w of the grid ranks chunk
@@ -485,12 +484,7 @@ __global__ __launch_bounds__(64) void k_plan_scan(int C, int32_t* __restrict__ c
       a += c < C ? arow[c] : 0;
     }
     const int s = v[0] + v[1] + v[2] + v[3];
-    int incl = s;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int u = __shfl_up(incl, o);
-      if (lane >= o) incl += u;
-    }
+    const int incl = wave_incl_scan(s);
     int p = run + incl - s;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -498,10 +492,9 @@ __global__ __launch_bounds__(64) void k_plan_scan(int C, int32_t* __restrict__ c
       if (c < C) row[c] = p;
       p += v[k];
     }
-    run += __shfl(incl, 63);
+    run += __builtin_amdgcn_readlane(incl, 63);
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o);
+  a = __builtin_amdgcn_readlane(wave_incl_scan(a), 63);
   if (lane == 0) {
     cnt[g] = run;
     acnt[g] = a;
@@ -536,7 +529,10 @@ struct PlanSmem {
 };
 
 // Every thread of a 1024-thread workgroup calls it; ends with the plan
-// written (tokrow / rows / roww by the scatter of the calling thread).
+// written (tokrow / rows / roww by the scatter of the calling thread).  With
+// LDS_ONLY (tok_g, tok_w and tokrow in LDS; cnt, acnt, off, rows and roww
+// only written) its barriers order LDS alone.
+template <bool LDS_ONLY>
 __device__ __forceinline__ void plan_small_body(const int32_t* __restrict__ tok_g,
                                                 const float* __restrict__ tok_w, int N, int S,
                                                 int G, int drop, int win, int32_t* __restrict__ cnt,
@@ -558,18 +554,13 @@ __device__ __forceinline__ void plan_small_body(const int32_t* __restrict__ tok_
     rank_chunk(tok_g, tok_w, N, S, G, drop, c * 64, (item % W) * win, win, cc + c, ca + c, C,
                tokrow);
   }
-  __syncthreads();
+  if constexpr (LDS_ONLY) lds_barrier();
+  else __syncthreads();
   for (int g = wave; g < G; g += 16) {
     const int v = lane < C ? cc[g * C + lane] : 0;
     int a = lane < C ? ca[g * C + lane] : 0;
-    int incl = v;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int u = __shfl_up(incl, o);
-      if (lane >= o) incl += u;
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) a += __shfl_xor(a, o);
+    const int incl = wave_incl_scan(v);
+    a = __builtin_amdgcn_readlane(wave_incl_scan(a), 63);
     if (lane < C) cc[g * C + lane] = incl - v;
     if (lane == 63) {
       tot[g] = incl;
@@ -577,8 +568,9 @@ __device__ __forceinline__ void plan_small_body(const int32_t* __restrict__ tok_
       acnt[g] = a;
     }
   }
-  __syncthreads();
-  block_group_offsets(tot, G, goff, wsum);
+  if constexpr (LDS_ONLY) lds_barrier();
+  else __syncthreads();
+  block_group_offsets<LDS_ONLY>(tot, G, goff, wsum);
   for (int g = threadIdx.x; g <= G; g += 1024) off[g] = goff[g];
   for (int t = threadIdx.x; t < N; t += 1024)
     scatter_token(tok_g, tok_w, t, S, G, cc + (t >> 6), C, goff, rows, roww, tokrow);
@@ -594,7 +586,7 @@ __global__ __launch_bounds__(1024) void k_plan_small(const int32_t* __restrict__
                                                      float* __restrict__ roww,
                                                      int32_t* __restrict__ tokrow) {
   __shared__ PlanSmem sm;
-  plan_small_body(tok_g, tok_w, N, S, G, drop, win, cnt, acnt, off, rows, roww, tokrow, sm);
+  plan_small_body<false>(tok_g, tok_w, N, S, G, drop, win, cnt, acnt, off, rows, roww, tokrow, sm);
 }
 
 // Window of the single-workgroup plan: narrower windows until the 16 waves
@@ -642,10 +634,11 @@ __global__ __launch_bounds__(1024) void k_front_route(
     if (ok && e < E) logits[static_cast<int64_t>(t) * E + e] = v;
     topk_seg<SEG>(v, t, ok, E, K, top_idx, top_w, tok_e, tok_ew, s_e, s_ew);
   }
-  __syncthreads();
+  lds_barrier();
   // 2 expert plan
-  plan_small_body(s_e, s_ew, N, K, E, 0, win, e_cnt, e_acnt, e_off, e_rows, e_roww, s_etr, sm);
-  __syncthreads();
+  plan_small_body<true>(s_e, s_ew, N, K, E, 0, win, e_cnt, e_acnt, e_off, e_rows, e_roww, s_etr,
+                        sm);
+  lds_barrier();
   // 3 top-m over each token's sources (dense logit rows of the front GEMM)
   const float* dense = front + E;
   for (int t0 = 0; t0 < N; t0 += PASS) {
@@ -669,10 +662,11 @@ __global__ __launch_bounds__(1024) void k_front_route(
     topm_seg<SEG, KB>(v, row, live, t, ok, E, M, S, edge_idx, edge_w, tok_d, tok_dc, s_d, s_dc);
   }
   for (int i = threadIdx.x; i < N * K; i += 1024) e_tokrow[i] = s_etr[i];
-  __syncthreads();
+  lds_barrier();
   // 4 destination plan
-  plan_small_body(s_d, s_dc, N, S, E, 1, win, d_cnt, d_acnt, d_off, d_rows, d_roww, s_dtr, sm);
-  __syncthreads();
+  plan_small_body<true>(s_d, s_dc, N, S, E, 1, win, d_cnt, d_acnt, d_off, d_rows, d_roww, s_dtr,
+                        sm);
+  lds_barrier();
   for (int i = threadIdx.x; i < N * S; i += 1024) d_tokrow[i] = s_dtr[i];
 }
 
