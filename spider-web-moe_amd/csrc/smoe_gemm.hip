@@ -881,8 +881,12 @@ __global__ __launch_bounds__(256, WGS) void k_gemm_stream(const GemmArgs p) {
   static_assert(W_BYTES % 4096 == 0 && A_BYTES % 4096 == 0, "whole DMA instructions per wave");
   static_assert(NS >= 3, "ring depth");
   static_assert(EPI != EPI_SWIGLU || TN == 4, "SwiGLU pairs channel c with c + 32");
-  __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE];
-  __shared__ float sc[FMT == SMOE_INT4 ? kStreamScaleMax : 1];
+  // one LDS object: the ring, then the int4 scale table (with a second LDS
+  // object the compiler waits for every outstanding DMA before reads of the
+  // table, draining the ring's prefetch)
+  constexpr int SC_BYTES = (FMT == SMOE_INT4 ? kStreamScaleMax : 1) * 4;
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE + SC_BYTES];
+  float* sc = reinterpret_cast<float*>(ring + NS * STAGE);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int q = lane >> 4, l16 = lane & 15;
