@@ -18,6 +18,8 @@
 // and workgroups past the real tile count exit at once, so no host ever
 // reads the routing.  Operands stream through double-buffered LDS with a
 // register prefetch of the next K slice.
+#include <type_traits>
+
 #include "smoe_common.hpp"
 #include "smoe_internal.hpp"
 
@@ -306,25 +308,37 @@ __device__ __forceinline__ void store4(const GemmArgs& p, int fmt, int g, int ro
 // layout: row r, 16-byte chunk c at chunk c ^ (r & 15) (rows of OW bf16, no
 // padding; r & 7 for 8-chunk rows).  The caller has synchronised the
 // workgroup after its last read of the ring.  16-row tiles past the last
-// row are skipped.
-template <int BM, int BN, int TM, int TN, int NT, int EPI>
+// row are skipped.  With PASSES = 2 (a tile larger than the ring) the wave
+// rows wm = 0, 1 stage and store their TM rows one after the other.
+template <int BM, int BN, int TM, int TN, int NT, int EPI, int PASSES = 1>
 __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const f32x4 (&acc)[TN / 16][TM / 16],
                                               int g, int m0, int mrows, int n0, int wm, int wn,
                                               uint8_t* ring) {
+  static_assert(PASSES == 1 || PASSES == 2, "staging passes");
   constexpr int FM = TM / 16, FN = TN / 16;
   constexpr int OW = (EPI == EPI_SWIGLU) ? BN / 2 : BN;  // output columns of the tile
   constexpr int SWM = (OW / 8 >= 16 ? 16 : OW / 8) - 1;  // chunk swizzle mask
+  constexpr int SROWS = PASSES == 1 ? BM : TM;            // rows staged per pass
   const int tid = threadIdx.x, lane = tid & 63;
   const int fr = lane & 15, fc = lane >> 4;
   uint16_t* stg = reinterpret_cast<uint16_t*>(ring);
-  auto stg_at = [&](int r, int col) {  // col: multiple of 4
+  auto stg_at = [&](int r, int col) {  // staging row r, col: multiple of 4
     return stg + r * OW + ((((col >> 3) ^ (r & SWM)) << 3) | (col & 7));
   };
+  constexpr int CPR_OUT = OW / 8;  // 16-byte chunks per output row
+  const int ncol0 = (EPI == EPI_SWIGLU) ? (n0 >> 1) : n0;
+  const int ncols = (EPI == EPI_SWIGLU) ? (p.N_out >> 1) : p.N_out;  // a last tile may be partial
+  uint16_t* out = reinterpret_cast<uint16_t*>(p.out);
+#pragma unroll 1
+  for (int ps = 0; ps < PASSES; ++ps) {
+  const int srow0 = PASSES == 1 ? 0 : ps * TM;  // first tile row of this pass
+  if (PASSES == 1 || wm == ps) {
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int tr0 = wm * TM + i * 16;
     if (tr0 >= mrows) continue;  // wave-uniform
     const int lr = tr0 + fr;
+    const int sr = lr - srow0;   // staging row
     const bool live = lr < mrows;
     const int row = m0 + (live ? lr : 0);
     float rs = 0.f;
@@ -340,7 +354,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const f32x4 (&a
         const int u = (n0 >> 1) + ul;
 #pragma unroll
         for (int q = 0; q < 4; ++q) r[q] = silu(acc[j][i][q]) * (acc[j + 2][i][q] + bias_at(p, g, u + q));
-        *reinterpret_cast<u32x2*>(stg_at(lr, ul)) = u32x2{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3])};
+        *reinterpret_cast<u32x2*>(stg_at(sr, ul)) = u32x2{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3])};
       } else {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -350,20 +364,20 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const f32x4 (&a
           else if constexpr (EPI == EPI_DOWN) r[q] = (a + bias_at(p, g, c + q)) * rs;
           else r[q] = a + bias_at(p, g, c + q);
         }
-        *reinterpret_cast<u32x2*>(stg_at(lr, cl)) = u32x2{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3])};
+        *reinterpret_cast<u32x2*>(stg_at(sr, cl)) = u32x2{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3])};
       }
     }
   }
+  }
   __syncthreads();
-  constexpr int CPR_OUT = OW / 8;  // 16-byte chunks per output row
-  const int ncol0 = (EPI == EPI_SWIGLU) ? (n0 >> 1) : n0;
-  const int ncols = (EPI == EPI_SWIGLU) ? (p.N_out >> 1) : p.N_out;  // a last tile may be partial
-  uint16_t* out = reinterpret_cast<uint16_t*>(p.out);
-  for (int q = tid; q < BM * CPR_OUT; q += NT) {
-    const int r = q / CPR_OUT, cc = (q % CPR_OUT) * 8;
+  for (int q = tid; q < SROWS * CPR_OUT; q += NT) {
+    const int sr = q / CPR_OUT, cc = (q % CPR_OUT) * 8;
+    const int r = srow0 + sr;
     if (r < mrows && ncol0 + cc < ncols)
       *reinterpret_cast<u32x4*>(out + static_cast<int64_t>(m0 + r) * p.ldo + ncol0 + cc) =
-          *reinterpret_cast<const u32x4*>(stg_at(r, cc));
+          *reinterpret_cast<const u32x4*>(stg_at(sr, cc));
+  }
+  if (ps + 1 < PASSES) __syncthreads();  // the next pass restages into the ring
   }
 }
 
@@ -540,12 +554,19 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
   constexpr int BN = 256, TM = BM / 2, TN = 64;
   constexpr int FM = TM / 16, FN = TN / 16;
   constexpr int A_BYTES = BM * 64, B_BYTES = BN * 64, STAGE = A_BYTES + B_BYTES;
-  constexpr int A_LD = BM / 16 / 8, B_LD = BN / 16 / 8;  // DMA instructions per wave per stage
-  constexpr int LD = A_LD + B_LD;
+  // DMA instructions (16 rows each) per stage: A_INS of A, B_LD per wave of
+  // W.  With BM = 320 the 20 A instructions do not split evenly over the 8
+  // waves: waves 0-3 issue 3, waves 4-7 issue 2, and each wave's vmcnt waits
+  // count its own.
+  constexpr int A_INS = BM / 16, B_LD = BN / 16 / 8;
+  constexpr int A_LD = (A_INS + 7) / 8;                  // most per wave
+  constexpr int A_HI = A_INS % 8 == 0 ? 8 : A_INS % 8;   // waves issuing A_LD of them
+  constexpr int LD = A_LD + B_LD, LD_LO = (A_INS / 8) + B_LD;
+  constexpr int OUT_BYTES = BM * ((EPI == EPI_SWIGLU) ? BN / 2 : BN) * 2;
+  constexpr int PASSES = OUT_BYTES <= NS * STAGE ? 1 : 2;
   static_assert(NS >= 2, "ring depth");
-  static_assert(BM == 128 || BM == 256, "block rows");
-  static_assert(BM * ((EPI == EPI_SWIGLU) ? BN / 2 : BN) * 2 <= NS * STAGE,
-                "output staging fits in the ring");
+  static_assert(BM == 128 || BM == 256 || BM == 320, "block rows");
+  static_assert(OUT_BYTES <= 2 * NS * STAGE, "output staging fits in the ring in two passes");
   __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE];
 
   int g, m0, mrows, n0;
@@ -553,6 +574,17 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int grp = wave >> 2;
   const int wm = grp, wn = wave & 3;
+  const bool a_hi = wave < A_HI;  // issues A_LD A instructions (else A_LD - 1)
+  // s_waitcnt vmcnt(n stages of this wave's DMA in flight)
+  auto wait_stages = [&](auto n_stages) {
+    constexpr int n = decltype(n_stages)::value;
+    if constexpr (LD == LD_LO) {
+      wait_vmcnt<n * LD>();
+    } else {
+      if (a_hi) wait_vmcnt<n * LD>();
+      else wait_vmcnt<n * LD_LO>();
+    }
+  };
 
   // DMA sources: instruction j of wave w covers rows 16 (8 j + w) ..
   const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A);
@@ -563,7 +595,7 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
     const int pr = lane >> 2, pc = lane & 3;
 #pragma unroll
     for (int j = 0; j < A_LD; ++j) {
-      const int r = (8 * j + wave) * 16 + pr;
+      const int r = min(8 * j + wave, A_INS - 1) * 16 + pr;  // past A_INS: never issued
       const int rr = r < mrows ? r : 0;  // rows past the group end: valid data, never stored
       const int ar = p.a_rows ? p.a_rows[m0 + rr] : (m0 + rr);
       asrc[j] = A + static_cast<int64_t>(ar) * p.lda + ((pc ^ ((r >> 1) & 3)) << 3);
@@ -580,8 +612,9 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
     const int k0 = stage * 32;
 #pragma unroll
     for (int j = 0; j < A_LD; ++j)
-      __builtin_amdgcn_global_load_lds((gbl_vptr)(asrc[j] + k0),
-                                       (lds_vptr)(base + (8 * j + wave) * 1024), 16, 0, 0);
+      if (j + 1 < A_LD || a_hi)  // wave-uniform
+        __builtin_amdgcn_global_load_lds((gbl_vptr)(asrc[j] + k0),
+                                         (lds_vptr)(base + (8 * j + wave) * 1024), 16, 0, 0);
 #pragma unroll
     for (int j = 0; j < B_LD; ++j)
       __builtin_amdgcn_global_load_lds((gbl_vptr)(bsrc[j] + k0),
@@ -611,7 +644,7 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
 #pragma unroll
   for (int st = 0; st < NS - 1; ++st)
     if (st < KT) issue(st);
-  if (KT >= NS - 1) wait_vmcnt<(NS - 2) * LD>();
+  if (KT >= NS - 1) wait_stages(std::integral_constant<int, NS - 2>{});
   else wait_vmcnt<0>();
   __builtin_amdgcn_s_barrier();
   if (grp == 1) __builtin_amdgcn_s_barrier();  // group 1 starts half a step behind
@@ -620,7 +653,7 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
     if (k + NS - 1 < KT) issue(k + NS - 1);
     read_frags(k);
     if (k + 1 < KT) {  // own part of stage k+1 landed (stages k+2 .. k+NS-1 may fly)
-      if (k + NS - 1 < KT) wait_vmcnt<(NS - 2) * LD>();
+      if (k + NS - 1 < KT) wait_stages(std::integral_constant<int, NS - 2>{});
       else wait_vmcnt<0>();
     }
     wait_lgkm0();
@@ -634,7 +667,7 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
     if (grp == 0 || k + 1 < KT) __builtin_amdgcn_s_barrier();
   }
   __syncthreads();  // every wave is done with the ring (no DMA is outstanding here)
-  tile_epilogue<BM, BN, TM, TN, 512, EPI>(p, acc, g, m0, mrows, n0, wm, wn, ring);
+  tile_epilogue<BM, BN, TM, TN, 512, EPI, PASSES>(p, acc, g, m0, mrows, n0, wm, wn, ring);
 }
 
 // --------------------------------------------------------------- skinny ----
@@ -1282,6 +1315,37 @@ int launch_front_gemm(const GemmArgs& a, hipStream_t s) {
   return a.single_rows <= 16 ? launch_skinny<1, 1>(a, s) : launch_skinny<1, 2>(a, s);
 }
 
+// CUs of the current device (cached per device; 0 if unknown).
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// 320- or 256-row ping-pong tiles for groups of >= 512 rows and K >= 2048:
+// the estimated tile count (each group's last tile partial) in rounds of one
+// workgroup per CU, a 320-row round costing 1.15 256-row rounds (measured at
+// 2048-row groups, K 2816).  The taller tile wins where it saves a round
+// (C1 down: 576 tiles = 3 rounds at 256 rows, 448 = 2 at 320).  At K 1024
+// and 1408 its two-pass epilogue weighs more and it measured slower even
+// where it saves a round (C1 / C3 edge and up, C3 down).
+bool pp_rows_320(const GemmArgs& a, int rpg) {
+  const int cus = device_cus();
+  if (cus <= 0) return false;
+  const int64_t groups = a.G == 0 ? 1 : a.G, tn = (a.N_out + 255) / 256;
+  auto rounds = [&](int bm) {
+    const int64_t tiles = groups * (rpg / bm + 1) * tn;
+    return (tiles + cus - 1) / cus;
+  };
+  return 115 * rounds(320) < 100 * rounds(256);
+}
+
 int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
   if (a.N_out <= 0 || a.K <= 0) return SMOE_EINVAL;
   if (a.W2) return SMOE_EINVAL;  // two weight segments: launch_front_gemm
@@ -1330,8 +1394,12 @@ int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
       a.ldw % 8 == 0 && a.lda % 8 == 0 && a.ldo % 8 == 0 &&
       (a.G == 0 ? a.single_rows : a.max_rows / (a.G > 0 ? a.G : 1)) >= 256) {
     const int rpg = a.G == 0 ? a.single_rows : a.max_rows / a.G;
-    if (a.N_out % 256 == 0)
-      return rpg < 512 ? launch_pp<3, 4, 128>(a, s) : launch_pp<4, 4, 256>(a, s);
+    if (a.N_out % 256 == 0) {
+      if (rpg > 256 && rpg <= 320) return launch_pp<4, 4, 320>(a, s);
+      if (rpg < 512) return launch_pp<3, 4, 128>(a, s);
+      return a.K >= 2048 && pp_rows_320(a, rpg) ? launch_pp<4, 4, 320>(a, s)
+                                                : launch_pp<4, 4, 256>(a, s);
+    }
     if (a.N_out % 128 == 0) return launch_ring<128, 3, 4>(a, s);
   }
   const bool b64 = bk == 64;
