@@ -681,8 +681,10 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
 // steps are issued before the first MFMA of the batch.  The waves' partial
 // sums meet in LDS and are added in wave order, so results are bit-identical
 // run to run; the epilogue writes 4 consecutive channels per lane.
-// Rows go in passes of 16*RT (a single-group GEMM spreads its passes over
-// grid.z; a grouped one loops over them).
+// A workgroup takes one tile of at most 16*RT rows of one group; the tiles
+// of all groups form one flat list (grid.y), so at many rows (router / edge
+// logits at prefill: narrow outputs, the activations are the stream) and
+// skewed groups the work still spreads evenly.
 // A lane's raw 16 consecutive k of one weight row, in its storage format
 // (only what the format needs stays in registers).
 template <int FMT> struct WRaw;
@@ -739,17 +741,16 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(const GemmArgs p) {
   __shared__ f32x4 red[NW][TN * RT][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int q = lane >> 4, l16 = lane & 15;
-  const int g = blockIdx.y;
   const int n0 = blockIdx.x * BN;
-  int r_lo, r_hi;
-  if (p.G == 0) {
-    r_lo = 0;
-    r_hi = p.single_rows;
-  } else {
-    r_lo = p.grp_off[g];
-    r_hi = p.grp_off[g + 1];
+  // one tile of <= 16*RT rows of one group: the tiles of all groups form one
+  // flat list over grid.y, so skewed groups spread over many workgroups
+  int g, r_lo, r_hi;
+  {
+    int m0, mrows;
+    if (!find_tile(p, 16 * RT, blockIdx.y, g, m0, mrows)) return;  // uniform, before any barrier
+    r_lo = m0;
+    r_hi = m0 + mrows;
   }
-  if (r_hi <= r_lo) return;  // workgroup-uniform, before any barrier
   const uint8_t* wrow[TN];
   int wn[TN];
 #pragma unroll
@@ -765,9 +766,7 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(const GemmArgs p) {
   const int KS = p.K / 64;
   const int s_begin = wave * KS / NW, s_end = (wave + 1) * KS / NW;
   const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A);
-  const int pass0 = p.G == 0 ? static_cast<int>(blockIdx.z) : 0;
-  const int pstep = p.G == 0 ? static_cast<int>(gridDim.z) : 1;
-  for (int m0 = r_lo + pass0 * 16 * RT; m0 < r_hi; m0 += pstep * 16 * RT) {
+  for (int m0 = r_lo; m0 < r_hi; m0 += 16 * RT) {  // one pass (the tile)
     const uint16_t* arow[RT];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
@@ -1219,12 +1218,12 @@ int launch_f32_bn(const GemmArgs& a, hipStream_t s) {
 
 }  // namespace
 
-// Passes of 16 * RT rows; a single-group GEMM puts one pass per grid.z.
 template <int FMT, int TN, int RT, int NW, int U>
 int launch_skinny_fmt(const GemmArgs& a, hipStream_t s) {
-  const int passes = a.G == 0 ? (a.single_rows + 16 * RT - 1) / (16 * RT) : 1;
-  if (passes == 0) return SMOE_OK;
-  const dim3 grid((a.N_out + 16 * TN - 1) / (16 * TN), a.G == 0 ? 1 : a.G, passes);
+  // one workgroup per (strip of 16*TN channels, tile of 16*RT rows)
+  const int tiles = max_tiles(a, 16 * RT);
+  if (tiles == 0) return SMOE_OK;
+  const dim3 grid((a.N_out + 16 * TN - 1) / (16 * TN), tiles, 1);
   const dim3 block(NW * 64);
   switch (a.epi) {
     case EPI_F32_BIAS: hipLaunchKernelGGL((k_gemm_skinny<FMT, EPI_F32_BIAS, TN, RT, NW, U>), grid, block, 0, s, a); break;
@@ -1291,16 +1290,22 @@ bool stream_aligned(const GemmArgs& a) {
   return a.fmt == SMOE_BF16 || a.fmt == SMOE_FP8_E4M3 || a.fmt == SMOE_INT4;
 }
 
-// Whether the skinny kernel takes the GEMM: few rows per group, and every
-// 16-byte (int4: 8-byte) load it issues aligned.
-bool skinny_fits(const GemmArgs& a) {
-  const int rows_per_group = a.G == 0 ? a.single_rows : a.max_rows / a.G;
-  if (rows_per_group > (a.G == 0 ? 64 : 32)) return false;
+// Whether every 16-byte (int4: 8-byte) load the skinny kernel issues is
+// aligned and K comes in 64-wide steps.
+bool skinny_aligned(const GemmArgs& a) {
   if (a.K % 64 || a.N_out % 4 || a.ldo % 4 || a.lda % 8) return false;
   const int walign = a.fmt == SMOE_BF16 ? 8 : 16;  // elements per aligned load
   if (a.ldw % walign || a.w_gstride % walign) return false;
   if (a.fmt == SMOE_INT4 && a.group_size % 16) return false;
-  return true;
+  return a.fmt == SMOE_BF16 || a.fmt == SMOE_FP8_E4M3 || a.fmt == SMOE_INT4;
+}
+
+// Whether the skinny kernel takes the GEMM as a weight stream: few rows per
+// group, aligned.
+bool skinny_fits(const GemmArgs& a) {
+  const int rows_per_group = a.G == 0 ? a.single_rows : a.max_rows / a.G;
+  if (rows_per_group > (a.G == 0 ? 64 : 32)) return false;
+  return skinny_aligned(a);
 }
 
 int launch_front_gemm(const GemmArgs& a, hipStream_t s) {
@@ -1366,8 +1371,13 @@ int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
   const int bk = (a.K % 64 == 0) ? 64 : (a.K % 32 == 0 ? 32 : 0);
   if (!bk) return SMOE_EINVAL;
   if (a.epi == EPI_SWIGLU && a.N_out % 128) return SMOE_EINVAL;
-  // decode: a few rows per group, weight streaming
-  if (skinny_fits(a)) {
+  // decode: a few rows per group, weight streaming; also narrow outputs
+  // (router / edge logits, N_out <= 64) of one group at any row count or of
+  // groups of up to 256 rows, where the activations are the stream (grouped
+  // ones with thousands of rows per group run faster as 64-row MFMA tiles)
+  const int rpg_all = a.G == 0 ? a.single_rows : a.max_rows / a.G;
+  if (skinny_fits(a) || (a.N_out <= 64 && a.epi != EPI_SWIGLU && (a.G == 0 || rpg_all <= 256) &&
+                         skinny_aligned(a))) {
     const int rpg = a.G == 0 ? a.single_rows : a.max_rows / a.G;
     if (a.N_out <= 16) return rpg <= 16 ? launch_skinny<1, 1>(a, s) : launch_skinny<1, 2>(a, s);
     if (a.N_out <= 32 && a.epi != EPI_SWIGLU)
