@@ -25,7 +25,35 @@
 
 namespace smoe {
 
-// Block-uniform tile lookup: the tile-th BM-row tile in group order.
+// Tile lookups over the plan's groups, wave-parallel: lane i holds group
+// b + i of a 64-group chunk (offsets by one clamped load per lane), the
+// per-group tile counts are prefix-summed by DPP, and the group holding a
+// tile is the first lane whose inclusive count exceeds it (a ballot).  A
+// serial loop over the groups would wait on one scalar load per group at the
+// start of every workgroup.  Every lane of the wave must be active; the
+// results are wave-uniform.
+__device__ __forceinline__ void group_chunk(const GemmArgs& p, int BM, int b, int& lo, int& hi,
+                                            int& t) {
+  const int i = b + static_cast<int>(threadIdx.x & 63);
+  const int ic = i < p.G ? i : p.G - 1;
+  lo = p.grp_off[ic];
+  hi = p.grp_off[ic + 1];
+  t = i < p.G ? (hi - lo + BM - 1) / BM : 0;
+}
+
+// Number of BM-row tiles over all groups.
+__device__ __forceinline__ int count_tiles(const GemmArgs& p, int BM) {
+  if (p.G == 0) return (p.single_rows + BM - 1) / BM;
+  int total = 0;
+  for (int b = 0; b < p.G; b += 64) {
+    int lo, hi, t;
+    group_chunk(p, BM, b, lo, hi, t);
+    total += __builtin_amdgcn_readlane(wave_incl_scan(t), 63);
+  }
+  return total;
+}
+
+// The tile-th BM-row tile in group order: group, first row, rows.
 __device__ __forceinline__ bool find_tile(const GemmArgs& p, int BM, int tile, int& g, int& m0,
                                           int& mrows) {
   if (p.G == 0) {
@@ -37,18 +65,21 @@ __device__ __forceinline__ bool find_tile(const GemmArgs& p, int BM, int tile, i
     return true;
   }
   int acc = 0;
-  int lo = p.grp_off[0];
-  for (int i = 0; i < p.G; ++i) {
-    const int hi = p.grp_off[i + 1];
-    const int t = (hi - lo + BM - 1) / BM;
-    if (tile < acc + t) {
-      g = i;
-      m0 = lo + (tile - acc) * BM;
-      mrows = min(BM, hi - m0);
+  for (int b = 0; b < p.G; b += 64) {
+    int lo, hi, t;
+    group_chunk(p, BM, b, lo, hi, t);
+    const int incl = wave_incl_scan(t) + acc;
+    const uint64_t m = __ballot(tile < incl);  // empty groups never come first
+    if (m) {
+      const int f = __builtin_ctzll(m);
+      g = b + f;
+      const int excl = __builtin_amdgcn_readlane(incl - t, f);
+      const int glo = __builtin_amdgcn_readlane(lo, f), ghi = __builtin_amdgcn_readlane(hi, f);
+      m0 = glo + (tile - excl) * BM;
+      mrows = min(BM, ghi - m0);
       return true;
     }
-    acc += t;
-    lo = hi;
+    acc = __builtin_amdgcn_readlane(incl, 63);
   }
   return false;
 }
@@ -255,10 +286,7 @@ __global__ __launch_bounds__(WM* WN * 64) void k_gemm_mfma(const GemmArgs p) {
 // while weight tiles stream.
 template <int BM>
 __device__ __forceinline__ int count_m_tiles(const GemmArgs& p) {
-  if (p.G == 0) return (p.single_rows + BM - 1) / BM;
-  int t = 0;
-  for (int i = 0; i < p.G; ++i) t += (p.grp_off[i + 1] - p.grp_off[i] + BM - 1) / BM;
-  return t;
+  return count_tiles(p, BM);
 }
 
 template <int BM, int BN, int GM>
