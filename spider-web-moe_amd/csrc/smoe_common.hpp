@@ -22,8 +22,12 @@ __device__ __forceinline__ float bf2f(uint16_t b) {
 __device__ __forceinline__ uint16_t f2bf(float f) {  // RNE (v_cvt_pk_bf16_f32)
   return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
+// Two floats -> two RNE bf16 in one u32 (lo in the low half), as one
+// v_cvt_pk_bf16_f32 (two scalar conversions would add shifts and ors).
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
-  return static_cast<uint32_t>(f2bf(lo)) | (static_cast<uint32_t>(f2bf(hi)) << 16);
+  typedef float f32v2 __attribute__((ext_vector_type(2)));
+  typedef __bf16 bf16v2 __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32v2{lo, hi}, bf16v2));
 }
 
 // ------------------------------------------------------------ fp8 e4m3 ----
