@@ -45,7 +45,7 @@ BOUND = {"c1": "mfma", "c2": "hbm", "c3": "mfma", "c4": "hbm"}
 # (rows per expert, N_out, format); rocprof summaries under profiles/ name it too
 UP_KERNEL = {
     "c1": "k_gemm_pp<4,4,SwiGLU,256> (bf16, 8-wave ping-pong, LDS-DMA ring)",
-    "c2": "k_gemm_skinny<fp8,SwiGLU,4,1> (weight streaming)",
+    "c2": "k_gemm_decode<fp8,SwiGLU,4,1,4,3> (weight streaming, 3-step register ring per wave)",
     "c3": "k_gemm_ring<128,3,4> (bf16 GELU, LDS-DMA ring, 2 workgroups/CU)",
     "c4": "k_gemm_stream<int4,GELU,6,3,2> (weight streaming, both operands by LDS-DMA ring, 2 workgroups/CU)",
 }

@@ -895,6 +895,208 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(const GemmArgs p) {
   }
 }
 
+// ------------------------------------------------------ decode stream ----
+// Weight streams of decode steps (a few rows per group, wide outputs): the
+// weights are nearly all of the traffic.  Each wave streams its own slice,
+// TNW 16-channel tiles of one group (SwiGLU: TNW / 2 gate tiles and the up
+// tiles 32 channels on) over one KSPLIT-th of K, for one tile of <= 16*RT rows,
+// through a D-step register ring: step s + D is requested as step s is
+// widened and multiplied, so every wave keeps D steps in flight and its MFMAs
+// run while the rest of its stream arrives (a wave that requested its whole
+// slice at once would wait for the last byte before its first MFMA, and all
+// waves of the grid would do their arithmetic at the end).  The KSPLIT waves
+// of a slice add their partial sums through LDS in wave order (bit-identical
+// run to run); with KSPLIT 1 no wave waits for another.  k order inside a
+// 64-wide step, the same for both operands: bf16 weights take k 8q..8q+7
+// (first MFMA) and 32+8q.. (second), so each of their two 16-byte loads
+// covers 64 contiguous bytes of 16 rows; fp8 / int4 take the 16 consecutive
+// k at 16q.  Only the last 2D - 1 steps' refills sit under a branch, so the
+// main loop's waits count the loads in flight exactly.
+template <int FMT>
+struct DRaw;
+template <> struct DRaw<SMOE_BF16> { u32x4 a, b; };
+template <> struct DRaw<SMOE_FP8_E4M3> { u32x4 a; };
+template <> struct DRaw<SMOE_INT4> { u32x2 a; float s; };
+
+template <int FMT, int EPI, int TNW, int RT, int KSPLIT, int D>
+__global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
+  constexpr int ESZ2 = FMT == SMOE_BF16 ? 4 : (FMT == SMOE_FP8_E4M3 ? 2 : 1);  // 2 x bytes/elt
+  constexpr int CS = 4 / KSPLIT;  // channel slices per workgroup
+  static_assert(4 % KSPLIT == 0, "KSPLIT divides the 4 waves");
+  static_assert(EPI != EPI_SWIGLU || TNW == 2 || TNW == 4, "SwiGLU slices pair gate and up tiles");
+  __shared__ f32x4 red[KSPLIT > 1 ? 4 : 1][TNW * RT][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q = lane >> 4, l16 = lane & 15;
+  const int kp = wave % KSPLIT, slice = blockIdx.x * CS + wave / KSPLIT;
+  int g, r_lo, r_hi;
+  {
+    int m0, mrows;
+    if (!find_tile(p, 16 * RT, blockIdx.y, g, m0, mrows)) return;  // uniform, before any barrier
+    r_lo = m0;
+    r_hi = m0 + mrows;
+  }
+  int c0[TNW];  // first channel of each tile (slices past N_out: clamped rows, never stored)
+#pragma unroll
+  for (int t = 0; t < TNW; ++t)
+    c0[t] = EPI == EPI_SWIGLU ? 64 * (slice / (4 / TNW)) + 8 * TNW * (slice % (4 / TNW)) +
+                                    16 * (t % (TNW / 2)) + 32 * (t / (TNW / 2))
+                              : 16 * (TNW * slice + t);
+  const uint8_t* wrow[TNW];
+  int wn[TNW];
+#pragma unroll
+  for (int t = 0; t < TNW; ++t) {
+    const int n = min(c0[t] + l16, p.N_out - 1);
+    wn[t] = n;
+    wrow[t] = reinterpret_cast<const uint8_t*>(p.W) +
+              (g * p.w_gstride + static_cast<int64_t>(n) * p.ldw) * ESZ2 / 2;
+  }
+  const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A);
+  const uint16_t* arow[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    int r = r_lo + 16 * rt + l16;
+    r = r < r_hi ? r : r_lo;  // rows past the tile: a valid row, never stored
+    const int ar = p.a_rows ? p.a_rows[r] : r;
+    arow[rt] = A + static_cast<int64_t>(ar) * p.lda;
+  }
+  const int steps = p.K / 64;
+  const int s_begin = kp * steps / KSPLIT, nst = (kp + 1) * steps / KSPLIT - s_begin;
+  const int last = min(s_begin + max(nst - 1, 0), steps - 1);
+  DRaw<FMT> wr[D][TNW];
+  u32x4 av[D][RT][2];
+  auto fetch = [&](int d, int i) {  // ring slot d <- step s_begin + i (clamped to the slice)
+    const int k0 = 64 * min(s_begin + i, last);
+#pragma unroll
+    for (int t = 0; t < TNW; ++t) {
+      if constexpr (FMT == SMOE_BF16) {
+        wr[d][t].a = *reinterpret_cast<const u32x4*>(wrow[t] + 2 * (k0 + 8 * q));
+        wr[d][t].b = *reinterpret_cast<const u32x4*>(wrow[t] + 2 * (k0 + 32 + 8 * q));
+      } else if constexpr (FMT == SMOE_FP8_E4M3) {
+        wr[d][t].a = *reinterpret_cast<const u32x4*>(wrow[t] + k0 + 16 * q);
+      } else {
+        const int k = k0 + 16 * q;
+        wr[d][t].a = *reinterpret_cast<const u32x2*>(wrow[t] + (k >> 1));
+        wr[d][t].s = load_scale(p.S,
+                                g * p.s_gstride + static_cast<int64_t>(wn[t]) * (p.K / p.group_size) +
+                                    k / p.group_size,
+                                p.s_f16);
+      }
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      if constexpr (FMT == SMOE_BF16) {
+        av[d][rt][0] = *reinterpret_cast<const u32x4*>(arow[rt] + k0 + 8 * q);
+        av[d][rt][1] = *reinterpret_cast<const u32x4*>(arow[rt] + k0 + 32 + 8 * q);
+      } else {
+        const u32x4* ap = reinterpret_cast<const u32x4*>(arow[rt] + k0 + 16 * q);
+        av[d][rt][0] = ap[0];
+        av[d][rt][1] = ap[1];
+      }
+    }
+  };
+  f32x4 acc[TNW][RT];
+#pragma unroll
+  for (int t = 0; t < TNW; ++t)
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) acc[t][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto step = [&](int d) {  // widen ring slot d and multiply it into acc
+#pragma unroll
+    for (int t = 0; t < TNW; ++t) {
+      u32x4 l, h;
+      if constexpr (FMT == SMOE_BF16) {
+        l = wr[d][t].a;
+        h = wr[d][t].b;
+      } else if constexpr (FMT == SMOE_FP8_E4M3) {
+        const u32x2 a0 = fp8x4_to_bf16x4(wr[d][t].a.x), a1 = fp8x4_to_bf16x4(wr[d][t].a.y);
+        const u32x2 b0 = fp8x4_to_bf16x4(wr[d][t].a.z), b1 = fp8x4_to_bf16x4(wr[d][t].a.w);
+        l = u32x4{a0.x, a0.y, a1.x, a1.y};
+        h = u32x4{b0.x, b0.y, b1.x, b1.y};
+      } else {
+        l = int4x8_to_bf16x8(wr[d][t].a.x, wr[d][t].s);
+        h = int4x8_to_bf16x8(wr[d][t].a.y, wr[d][t].s);
+      }
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        acc[t][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8, l), __builtin_bit_cast(bf16x8, av[d][rt][0]), acc[t][rt],
+            0, 0, 0);
+        acc[t][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8, h), __builtin_bit_cast(bf16x8, av[d][rt][1]), acc[t][rt],
+            0, 0, 0);
+      }
+    }
+  };
+#pragma unroll
+  for (int d = 0; d < D; ++d) fetch(d, d);  // a slice of < D steps: its last step again (unused)
+  int s = 0;
+  for (; s + 2 * D <= nst; s += D) {  // slot d holds step s + d; every refill is a real step
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      step(d);
+      fetch(d, s + d + D);
+    }
+  }
+  // the last 2D - 1 steps at most: refills only where a step is left
+#pragma unroll
+  for (int d = 0; d < D; ++d) {
+    if (s + d < nst) step(d);
+    if (s + d + D < nst) fetch(d, s + d + D);
+  }
+#pragma unroll
+  for (int d = 0; d < D - 1; ++d)
+    if (s + D + d < nst) step(d);
+  if constexpr (KSPLIT > 1) {
+    if (kp > 0)
+#pragma unroll
+      for (int t = 0; t < TNW; ++t)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) red[wave][t * RT + rt][lane] = acc[t][rt];
+    __syncthreads();
+    if (kp > 0) return;
+#pragma unroll
+    for (int j = 1; j < KSPLIT; ++j)
+#pragma unroll
+      for (int t = 0; t < TNW; ++t)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) acc[t][rt] += red[wave + j][t * RT + rt][lane];
+  }
+  // lane: channels c0[t] + 4 q + (0..3) of row r_lo + 16 rt + l16
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int row = r_lo + 16 * rt + l16;
+    if (row >= r_hi) continue;
+    if constexpr (EPI == EPI_SWIGLU) {
+#pragma unroll
+      for (int t = 0; t < TNW / 2; ++t) {  // gate tile t, up tile t + TNW / 2
+        const int c = c0[t] + 4 * q;
+        if (c >= p.N_out) continue;
+        const int u0 = (c >> 6) * 32 + (c & 31);
+        float o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float gs = acc[t][rt][i] * col_scale(p, FMT, g, c + i);
+          const float us =
+              acc[t + TNW / 2][rt][i] * col_scale(p, FMT, g, c + 32 + i) + bias_at(p, g, u0 + i);
+          o[i] = silu(gs) * us;
+        }
+        const int64_t off = static_cast<int64_t>(row) * p.ldo + u0;
+        if (p.out_dtype == SMOE_F32)
+          *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + off) =
+              f32x4{o[0], o[1], o[2], o[3]};
+        else
+          *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + off) =
+              u32x2{pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3])};
+      }
+    } else {
+#pragma unroll
+      for (int t = 0; t < TNW; ++t) {
+        const int c = c0[t] + 4 * q;
+        if (c < p.N_out) store4<EPI>(p, FMT, g, row, c, acc[t][rt]);
+      }
+    }
+  }
+}
+
 // ------------------------------------------------------- weight stream ----
 // Medium rows per group (a few dozen to ~128: mixed decode + prefill steps,
 // quantized experts).  The weights dominate the traffic and every weight is
@@ -1244,7 +1446,59 @@ int launch_f32_bn(const GemmArgs& a, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 
+template <int FMT, int RT, int KSPLIT>
+int launch_decode_fmt(const GemmArgs& a, hipStream_t s) {
+  // one workgroup per (4 / KSPLIT slices of 64 channels, tile of 16*RT rows);
+  // 3 steps in flight per wave
+  constexpr int TNW = 4, D = 3, CS = 4 / KSPLIT;
+  const int tiles = max_tiles(a, 16 * RT);
+  if (tiles == 0) return SMOE_OK;
+  const int slices = (a.N_out + 16 * TNW - 1) / (16 * TNW);
+  const dim3 grid((slices + CS - 1) / CS, tiles, 1);
+  switch (a.epi) {
+    case EPI_F32_BIAS: hipLaunchKernelGGL((k_gemm_decode<FMT, EPI_F32_BIAS, TNW, RT, KSPLIT, D>), grid, dim3(256), 0, s, a); break;
+    case EPI_ROWSCALE: hipLaunchKernelGGL((k_gemm_decode<FMT, EPI_ROWSCALE, TNW, RT, KSPLIT, D>), grid, dim3(256), 0, s, a); break;
+    case EPI_GELU: hipLaunchKernelGGL((k_gemm_decode<FMT, EPI_GELU, TNW, RT, KSPLIT, D>), grid, dim3(256), 0, s, a); break;
+    case EPI_DOWN: hipLaunchKernelGGL((k_gemm_decode<FMT, EPI_DOWN, TNW, RT, KSPLIT, D>), grid, dim3(256), 0, s, a); break;
+    case EPI_SWIGLU: hipLaunchKernelGGL((k_gemm_decode<FMT, EPI_SWIGLU, TNW, RT, KSPLIT, D>), grid, dim3(256), 0, s, a); break;
+    default: return SMOE_EINVAL;
+  }
+  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
+template <int FMT, int RT>
+int launch_decode_split(const GemmArgs& a, int ksplit, hipStream_t s) {
+  if (ksplit == 1) return launch_decode_fmt<FMT, RT, 1>(a, s);
+  if (ksplit == 2) return launch_decode_fmt<FMT, RT, 2>(a, s);
+  return launch_decode_fmt<FMT, RT, 4>(a, s);
+}
+
 }  // namespace
+
+// Decode weight streams (few rows per group, N_out >= 128): 64 channels per
+// wave and K split over 4 waves wherever each part keeps >= 3 steps (C2's up,
+// down and edge GEMMs: 5632, 1024 and 1024 waves).  Measured at those shapes:
+// 64-channel slices beat 32-channel ones (half the activation loads per
+// weight byte), a split of 4 beats 2 and 1, and a ring of 3 steps is as fast
+// as 4 to 6.
+int launch_decode(const GemmArgs& a, hipStream_t s) {
+  const int rpg = a.G == 0 ? a.single_rows : a.max_rows / a.G;
+  const int rt = rpg <= 16 ? 1 : 2;
+  const int steps = a.K / 64;
+  const int ksplit = steps >= 12 ? 4 : (steps >= 6 ? 2 : 1);
+  switch (a.fmt) {
+    case SMOE_BF16:
+      return rt == 1 ? launch_decode_split<SMOE_BF16, 1>(a, ksplit, s)
+                     : launch_decode_split<SMOE_BF16, 2>(a, ksplit, s);
+    case SMOE_FP8_E4M3:
+      return rt == 1 ? launch_decode_split<SMOE_FP8_E4M3, 1>(a, ksplit, s)
+                     : launch_decode_split<SMOE_FP8_E4M3, 2>(a, ksplit, s);
+    case SMOE_INT4:
+      return rt == 1 ? launch_decode_split<SMOE_INT4, 1>(a, ksplit, s)
+                     : launch_decode_split<SMOE_INT4, 2>(a, ksplit, s);
+    default: return SMOE_EUNSUPPORTED;
+  }
+}
 
 template <int FMT, int TN, int RT, int NW, int U>
 int launch_skinny_fmt(const GemmArgs& a, hipStream_t s) {
@@ -1407,6 +1661,7 @@ int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
   if (skinny_fits(a) || (a.N_out <= 64 && a.epi != EPI_SWIGLU && (a.G == 0 || rpg_all <= 256) &&
                          skinny_aligned(a))) {
     const int rpg = a.G == 0 ? a.single_rows : a.max_rows / a.G;
+    if (a.N_out >= 128 && skinny_fits(a)) return launch_decode(a, s);
     if (a.N_out <= 16) return rpg <= 16 ? launch_skinny<1, 1>(a, s) : launch_skinny<1, 2>(a, s);
     if (a.N_out <= 32 && a.epi != EPI_SWIGLU)
       return rpg <= 16 ? launch_skinny<2, 1>(a, s) : launch_skinny<2, 2>(a, s);
