@@ -459,8 +459,9 @@ __global__ __launch_bounds__(256) void k_plan_rank(const int32_t* __restrict__ t
                                                    int32_t* __restrict__ tokrow) {
   const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (item >= C * W) return;
-  const int chunk = item / W, g0 = (item % W) * 64;
-  rank_chunk(tok_g, tok_w, N, S, G, drop, chunk * 64, g0, 64, ccnt + chunk, cacnt + chunk, C,
+  const int win = (G + W - 1) / W;
+  const int chunk = item / W, g0 = (item % W) * win;
+  rank_chunk(tok_g, tok_w, N, S, G, drop, chunk * 64, g0, win, ccnt + chunk, cacnt + chunk, C,
              tokrow);
 }
 
@@ -723,7 +724,11 @@ int launch_plan(const int32_t* tok_g, const float* tok_w, int N, int S, int G, i
                        cnt, acnt, off, rows, roww, tokrow);
     return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
   }
-  const int W = (G + 63) / 64;
+  // group windows per chunk: narrower windows (fewer ballots per wave) until
+  // the rank kernel has about 256 waves (C4: 34 chunks x 64 groups -> 8
+  // windows of 8)
+  int W = (G + 63) / 64;
+  while (C * W < 256 && (G + W - 1) / W > 8) W *= 2;
   int32_t* ccnt = reinterpret_cast<int32_t*>(scratch);
   int32_t* cacnt = ccnt + static_cast<int64_t>(C) * G;
   hipLaunchKernelGGL(k_plan_rank, dim3((C * W + 3) / 4), dim3(256), 0, s, tok_g, tok_w, N, S, G,
