@@ -1482,8 +1482,12 @@ int launch_decode_split(const GemmArgs& a, int ksplit, hipStream_t s) {
 // weight byte), a split of 4 beats 2 and 1, and a ring of 3 steps is as fast
 // as 4 to 6.
 int launch_decode(const GemmArgs& a, hipStream_t s) {
+  // 32-row tiles above 8 rows per group on average: routed groups are ragged,
+  // and a group past its tile takes a second tile that streams the same
+  // weights again (C2's destination groups, 16 rows on average: 12.4 us with
+  // 16-row tiles)
   const int rpg = a.G == 0 ? a.single_rows : a.max_rows / a.G;
-  const int rt = rpg <= 16 ? 1 : 2;
+  const int rt = rpg <= 8 ? 1 : 2;
   const int steps = a.K / 64;
   const int ksplit = steps >= 12 ? 4 : (steps >= 6 ? 2 : 1);
   switch (a.fmt) {

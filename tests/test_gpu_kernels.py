@@ -248,7 +248,7 @@ def test_int4_experts_match_oracle(group, sdt):
     assert (got - ref).abs().max() < max(float(env), 1e-3)
 
 
-@pytest.mark.parametrize("shape", [(60, 384, 640, 8), (40, 768, 1664, 4)])
+@pytest.mark.parametrize("shape", [(24, 384, 640, 8), (60, 384, 640, 8), (40, 768, 1664, 4)])
 @pytest.mark.parametrize("fmt,act", [("bf16", "gelu"), ("bf16", "swiglu"), ("fp8", "gelu"),
                                      ("fp8", "swiglu"), ("int4-g32-f32", "gelu"),
                                      ("int4-g128-f16", "gelu")])
@@ -256,9 +256,9 @@ def test_decode_experts_match_oracle(fmt, act, shape):
     """Decode shapes (a few rows per expert) take the weight-streaming GEMM,
     K split over 2 or 4 waves with ragged parts: up K = 384 (6 steps of 64)
     and 768 (12), down K = 640 (10) and 1664 (26: parts of 6 and 7 steps,
-    so the ring's main loop runs); 16-row tiles (15 rows per expert on
-    average) and 32-row tiles (20); an expert with more rows than one tile
-    holds, an empty expert, a one-row expert."""
+    so the ring's main loop runs); 16-row tiles (6 rows per expert on
+    average) and 32-row tiles (15 and 20); an expert with more rows than one
+    tile holds, an empty expert, a one-row expert."""
     from spider_moe_amd.quant import interleave_gate_up, interleave_gate_up_rows, quantize_int4
     n8 = nat()
     say("decode experts", fmt, act, shape)
