@@ -427,9 +427,7 @@ __device__ __forceinline__ void scatter_token(const int32_t* __restrict__ tok_g,
 }
 
 // Exclusive scan of tot[0..G) into goff[0..G].  Every thread of the
-// workgroup calls it (it holds barriers); the first 256 do the work.  With
-// LDS_ONLY the barriers order LDS alone (tot, goff and wsum in LDS).
-template <bool LDS_ONLY = false>
+// workgroup calls it (it holds barriers); the first 256 do the work.
 __device__ __forceinline__ void block_group_offsets(const int32_t* tot, int G, int* goff,
                                                     int* wsum) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -437,16 +435,14 @@ __device__ __forceinline__ void block_group_offsets(const int32_t* tot, int G, i
   const int v = (act && tid < G) ? tot[tid] : 0;
   const int incl = wave_incl_scan(v);
   if (act && lane == 63) wsum[wave] = incl;
-  if constexpr (LDS_ONLY) lds_barrier();
-  else __syncthreads();
+  __syncthreads();
   if (act) {
     int before = 0;
     for (int w = 0; w < wave; ++w) before += wsum[w];
     if (tid < G) goff[tid] = before + incl - v;
     if (tid == 0) goff[G] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
   }
-  if constexpr (LDS_ONLY) lds_barrier();
-  else __syncthreads();
+  __syncthreads();
 }
 
 // ccnt / cacnt are [G, C] (group-major).  Wave w of the grid ranks chunk
@@ -529,54 +525,8 @@ struct PlanSmem {
   int tot[kPlanMaxG], goff[kPlanMaxG + 1], wsum[4];
 };
 
-// Every thread of a 1024-thread workgroup calls it; ends with the plan
-// written (tokrow / rows / roww by the scatter of the calling thread).  With
-// LDS_ONLY (tok_g, tok_w and tokrow in LDS; cnt, acnt, off, rows and roww
-// only written) its barriers order LDS alone.
-template <bool LDS_ONLY>
-__device__ __forceinline__ void plan_small_body(const int32_t* __restrict__ tok_g,
-                                                const float* __restrict__ tok_w, int N, int S,
-                                                int G, int drop, int win, int32_t* __restrict__ cnt,
-                                                int32_t* __restrict__ acnt,
-                                                int32_t* __restrict__ off,
-                                                int32_t* __restrict__ rows,
-                                                float* __restrict__ roww,
-                                                int32_t* __restrict__ tokrow, PlanSmem& sm) {
-  int* cc = sm.cc;
-  int* ca = sm.ca;
-  int* tot = sm.tot;
-  int* goff = sm.goff;
-  int* wsum = sm.wsum;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int C = (N + 63) / 64;
-  const int W = (G + win - 1) / win;
-  for (int item = wave; item < C * W; item += 16) {
-    const int c = item / W;
-    rank_chunk(tok_g, tok_w, N, S, G, drop, c * 64, (item % W) * win, win, cc + c, ca + c, C,
-               tokrow);
-  }
-  if constexpr (LDS_ONLY) lds_barrier();
-  else __syncthreads();
-  for (int g = wave; g < G; g += 16) {
-    const int v = lane < C ? cc[g * C + lane] : 0;
-    int a = lane < C ? ca[g * C + lane] : 0;
-    const int incl = wave_incl_scan(v);
-    a = __builtin_amdgcn_readlane(wave_incl_scan(a), 63);
-    if (lane < C) cc[g * C + lane] = incl - v;
-    if (lane == 63) {
-      tot[g] = incl;
-      cnt[g] = incl;
-      acnt[g] = a;
-    }
-  }
-  if constexpr (LDS_ONLY) lds_barrier();
-  else __syncthreads();
-  block_group_offsets<LDS_ONLY>(tot, G, goff, wsum);
-  for (int g = threadIdx.x; g <= G; g += 1024) off[g] = goff[g];
-  for (int t = threadIdx.x; t < N; t += 1024)
-    scatter_token(tok_g, tok_w, t, S, G, cc + (t >> 6), C, goff, rows, roww, tokrow);
-}
-
+// One workgroup of 16 waves: rank (wave per (chunk, window)), scan (wave per
+// group), group offsets, scatter (thread per token).
 __global__ __launch_bounds__(1024) void k_plan_small(const int32_t* __restrict__ tok_g,
                                                      const float* __restrict__ tok_w, int N,
                                                      int S, int G, int drop, int win,
@@ -587,7 +537,34 @@ __global__ __launch_bounds__(1024) void k_plan_small(const int32_t* __restrict__
                                                      float* __restrict__ roww,
                                                      int32_t* __restrict__ tokrow) {
   __shared__ PlanSmem sm;
-  plan_small_body<false>(tok_g, tok_w, N, S, G, drop, win, cnt, acnt, off, rows, roww, tokrow, sm);
+  int* cc = sm.cc;
+  int* ca = sm.ca;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int C = (N + 63) / 64;
+  const int W = (G + win - 1) / win;
+  for (int item = wave; item < C * W; item += 16) {
+    const int c = item / W;
+    rank_chunk(tok_g, tok_w, N, S, G, drop, c * 64, (item % W) * win, win, cc + c, ca + c, C,
+               tokrow);
+  }
+  __syncthreads();
+  for (int g = wave; g < G; g += 16) {
+    const int v = lane < C ? cc[g * C + lane] : 0;
+    int a = lane < C ? ca[g * C + lane] : 0;
+    const int incl = wave_incl_scan(v);
+    a = __builtin_amdgcn_readlane(wave_incl_scan(a), 63);
+    if (lane < C) cc[g * C + lane] = incl - v;
+    if (lane == 63) {
+      sm.tot[g] = incl;
+      cnt[g] = incl;
+      acnt[g] = a;
+    }
+  }
+  __syncthreads();
+  block_group_offsets(sm.tot, G, sm.goff, sm.wsum);
+  for (int g = threadIdx.x; g <= G; g += 1024) off[g] = sm.goff[g];
+  for (int t = threadIdx.x; t < N; t += 1024)
+    scatter_token(tok_g, tok_w, t, S, G, cc + (t >> 6), C, sm.goff, rows, roww, tokrow);
 }
 
 // Window of the single-workgroup plan: narrower windows until the 16 waves
@@ -596,6 +573,80 @@ inline int plan_small_win(int C, int G) {
   int win = 64;
   while (win > 8 && C * ((G + win - 1) / win) < 16) win >>= 1;
   return win;
+}
+
+// Plan of <= 64 tokens over <= 64 groups by one wave, lane t = token t
+// (tok_g, tok_w and tokrow in LDS or global memory): each valid entry sets bit t of its
+// group's token masks (kept, positive weight) by an LDS atomic OR; lane g
+// counts group g by popcount and a wave scan gives the offsets; a kept
+// entry's row is off[g] + the number of earlier tokens in its group's mask.
+// The plan the multi-wave forms write (stable token order, tokrow -1 for
+// every entry not kept), in one wave and without a workgroup barrier: the
+// wave's LDS operations complete in order.  km / am: 64 words of LDS each;
+// soff: 64.
+__device__ __forceinline__ void plan64_wave(const int32_t* tok_g, const float* tok_w, int N, int S,
+                                            int G, int drop, int32_t* __restrict__ cnt,
+                                            int32_t* __restrict__ acnt, int32_t* __restrict__ off,
+                                            int32_t* __restrict__ rows, float* __restrict__ roww,
+                                            int32_t* tokrow, uint64_t* km, uint64_t* am,
+                                            int* soff) {
+  const int t = threadIdx.x & 63;
+  const bool tv = t < N;
+  km[t] = 0ull;
+  am[t] = 0ull;
+  const uint64_t bit = 1ull << t, below = bit - 1ull;
+  int prev = -1;
+  bool open = tv;
+  for (int j = 0; j < S; ++j) {
+    const int g = tv ? tok_g[t * S + j] : -1;
+    const float w = tv ? tok_w[t * S + j] : 0.f;
+    open = open && g > prev && g < G;  // g > prev >= -1, so g >= 0
+    prev = open ? g : prev;
+    if (open && (!drop || w > 0.f)) atomicOr(&km[g], bit);
+    if (open && !drop && w > 0.f) atomicOr(&am[g], bit);
+  }
+  const int gl = t < G ? t : 0;
+  const int c = t < G ? __popcll(km[gl]) : 0;
+  const int a = t < G ? (drop ? c : __popcll(am[gl])) : 0;
+  const int incl = wave_incl_scan(c);
+  if (t < G) {
+    cnt[t] = c;
+    acnt[t] = a;
+    off[t] = incl - c;
+    soff[t] = incl - c;
+  }
+  if (t == 0) off[G] = __builtin_amdgcn_readlane(incl, 63);
+  prev = -1;
+  open = tv;
+  for (int j = 0; j < S; ++j) {
+    const int g = tv ? tok_g[t * S + j] : -1;
+    const float w = tv ? tok_w[t * S + j] : 0.f;
+    open = open && g > prev && g < G;
+    prev = open ? g : prev;
+    const bool kept = open && (!drop || w > 0.f);
+    const int gc = kept ? g : 0;
+    const int row = soff[gc] + __popcll(km[gc] & below);
+    if (tv) tokrow[t * S + j] = kept ? row : -1;
+    if (kept) {
+      rows[row] = t;
+      roww[row] = w;
+    }
+  }
+}
+
+// Plans of <= 64 tokens over <= 64 groups outside the fused front (fp32
+// blocks, the standalone plan entry point): one wave.
+__global__ __launch_bounds__(64) void k_plan64(const int32_t* __restrict__ tok_g,
+                                               const float* __restrict__ tok_w, int N, int S,
+                                               int G, int drop, int32_t* __restrict__ cnt,
+                                               int32_t* __restrict__ acnt,
+                                               int32_t* __restrict__ off,
+                                               int32_t* __restrict__ rows,
+                                               float* __restrict__ roww,
+                                               int32_t* __restrict__ tokrow) {
+  __shared__ uint64_t km[64], am[64];
+  __shared__ int soff[64];
+  plan64_wave(tok_g, tok_w, N, S, G, drop, cnt, acnt, off, rows, roww, tokrow, km, am, soff);
 }
 
 // Small decode steps: every routing stage in one workgroup of 16 waves, the
@@ -610,7 +661,7 @@ constexpr int kFrontMaxSrc = kFrontMaxN * 16;   // N*K
 constexpr int kFrontMaxDst = kFrontMaxN * 64;   // N*S
 template <int SEG, int KB>
 __global__ __launch_bounds__(1024) void k_front_route(
-    const float* __restrict__ front, int ldf, int N, int E, int K, int M, int S, int win,
+    const float* __restrict__ front, int ldf, int N, int E, int K, int M, int S,
     float* __restrict__ logits, int32_t* __restrict__ top_idx, float* __restrict__ top_w,
     int32_t* __restrict__ tok_e, float* __restrict__ tok_ew, int32_t* __restrict__ e_cnt,
     int32_t* __restrict__ e_acnt, int32_t* __restrict__ e_off, int32_t* __restrict__ e_rows,
@@ -620,9 +671,10 @@ __global__ __launch_bounds__(1024) void k_front_route(
     int32_t* __restrict__ d_off, int32_t* __restrict__ d_rows, float* __restrict__ d_roww,
     int32_t* __restrict__ d_tokrow) {
   constexpr int PASS = 1024 / SEG;  // tokens per pass
-  __shared__ PlanSmem sm;
   __shared__ int32_t s_e[kFrontMaxSrc], s_etr[kFrontMaxSrc], s_d[kFrontMaxDst], s_dtr[kFrontMaxDst];
   __shared__ float s_ew[kFrontMaxSrc], s_dc[kFrontMaxDst];
+  __shared__ uint64_t s_km[64], s_am[64];
+  __shared__ int s_off[64];
   const int lane = threadIdx.x & 63;
   const int e = lane & (SEG - 1);
   const int le = e < E ? e : E - 1;
@@ -636,9 +688,10 @@ __global__ __launch_bounds__(1024) void k_front_route(
     topk_seg<SEG>(v, t, ok, E, K, top_idx, top_w, tok_e, tok_ew, s_e, s_ew);
   }
   lds_barrier();
-  // 2 expert plan
-  plan_small_body<true>(s_e, s_ew, N, K, E, 0, win, e_cnt, e_acnt, e_off, e_rows, e_roww, s_etr,
-                        sm);
+  // 2 expert plan (wave 0)
+  if (threadIdx.x < 64)
+    plan64_wave(s_e, s_ew, N, K, E, 0, e_cnt, e_acnt, e_off, e_rows, e_roww, s_etr, s_km, s_am,
+                s_off);
   lds_barrier();
   // 3 top-m over each token's sources (dense logit rows of the front GEMM)
   const float* dense = front + E;
@@ -664,9 +717,10 @@ __global__ __launch_bounds__(1024) void k_front_route(
   }
   for (int i = threadIdx.x; i < N * K; i += 1024) e_tokrow[i] = s_etr[i];
   lds_barrier();
-  // 4 destination plan
-  plan_small_body<true>(s_d, s_dc, N, S, E, 1, win, d_cnt, d_acnt, d_off, d_rows, d_roww, s_dtr,
-                        sm);
+  // 4 destination plan (wave 0)
+  if (threadIdx.x < 64)
+    plan64_wave(s_d, s_dc, N, S, E, 1, d_cnt, d_acnt, d_off, d_rows, d_roww, s_dtr, s_km, s_am,
+                s_off);
   lds_barrier();
   for (int i = threadIdx.x; i < N * S; i += 1024) d_tokrow[i] = s_dtr[i];
 }
@@ -681,12 +735,9 @@ int launch_front_route(const float* front, int ldf, int N, int E, int K, int M, 
   if (N < 1 || N > kFrontMaxN || E < 1 || E > 64 || K < 1 || K > 16 || K > E || M < 1 || M > 16 ||
       M > E || S < 1 || S > 64 || ldf < E + E * E)
     return SMOE_EINVAL;
-  const int C = (N + 63) / 64;
-  if (C * E > kSmallMaxCells) return SMOE_EINVAL;
-  const int win = plan_small_win(C, E);
 #define SMOE_FRONT(SG, KB)                                                                      \
   hipLaunchKernelGGL((k_front_route<SG, KB>), dim3(1), dim3(1024), 0, s, front, ldf, N, E, K, M, S, \
-                     win, logits, top_idx, top_w, tok_e, tok_ew, e_cnt, e_acnt, e_off, e_rows,     \
+                     logits, top_idx, top_w, tok_e, tok_ew, e_cnt, e_acnt, e_off, e_rows,          \
                      e_roww, e_tokrow, edge_logit, edge_idx, edge_w, tok_d, tok_dc, d_cnt, d_acnt, \
                      d_off, d_rows, d_roww, d_tokrow)
 #define SMOE_FRONT_K(SG)           \
@@ -716,8 +767,14 @@ int launch_plan(const int32_t* tok_g, const float* tok_w, int N, int S, int G, i
                 int32_t* tokrow, void* scratch, hipStream_t s) {
   if (G < 1 || G > kPlanMaxG || S < 1 || S > kPlanMaxS || N < 0) return SMOE_EINVAL;
   const int C = (N + 63) / 64;
-  // One workgroup while its rank work (C x G ballots) stays small; the
-  // three-kernel form spreads larger plans over the chip.
+  // One wave for a single chunk over <= 64 groups; one workgroup while its
+  // rank work (C x G ballots) stays small; the three-kernel form spreads
+  // larger plans over the chip.
+  if (N <= 64 && G <= 64) {
+    hipLaunchKernelGGL(k_plan64, dim3(1), dim3(64), 0, s, tok_g, tok_w, N, S, G, drop, cnt, acnt,
+                       off, rows, roww, tokrow);
+    return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+  }
   if (C * G <= 512) {
     const int win = plan_small_win(C, G);
     hipLaunchKernelGGL(k_plan_small, dim3(1), dim3(1024), 0, s, tok_g, tok_w, N, S, G, drop, win,
