@@ -46,18 +46,49 @@ int g_prof_cap = 0;
 int g_prof_n = 0;
 int32_t g_prof_stage[1 << 16];
 
+}  // namespace
+
+namespace smoe {
+hipEvent_t g_launch_ev[2] = {nullptr, nullptr};
+}  // namespace smoe
+
+namespace {
+
+// Stages that are one GEMM launch: their events go with the launch itself
+// (SMOE_LAUNCH), so the interval is the kernel's execution.  The others are
+// bracketed by two recorded events.
+bool one_gemm_stage(int stage) {
+  return stage == SMOE_STAGE_ROUTER_GEMM || stage == SMOE_STAGE_EDGE_LOGITS ||
+         stage == SMOE_STAGE_EDGE_GEMM || stage == SMOE_STAGE_UP_GEMM ||
+         stage == SMOE_STAGE_DOWN_GEMM || stage == SMOE_STAGE_FRONT_GEMM;
+}
+
 struct StageScope {
   int i = -1;
+  bool ext = false;
   hipStream_t s;
   StageScope(int stage, hipStream_t st) : s(st) {
     if (g_prof_ev && (g_prof_mask >> stage & 1u) && g_prof_n < g_prof_cap && g_prof_n < (1 << 16)) {
       i = g_prof_n++;
       g_prof_stage[i] = stage;
-      (void)hipEventRecord(g_prof_ev[2 * i], s);
+      ext = one_gemm_stage(stage);
+      if (ext) {
+        g_launch_ev[0] = g_prof_ev[2 * i];
+        g_launch_ev[1] = g_prof_ev[2 * i + 1];
+      } else {
+        (void)hipEventRecord(g_prof_ev[2 * i], s);
+      }
     }
   }
   ~StageScope() {
-    if (i >= 0) (void)hipEventRecord(g_prof_ev[2 * i + 1], s);
+    if (i < 0) return;
+    if (!ext) {
+      (void)hipEventRecord(g_prof_ev[2 * i + 1], s);
+    } else if (g_launch_ev[0]) {  // nothing launched (no rows): an empty interval
+      (void)hipEventRecord(g_prof_ev[2 * i], s);
+      (void)hipEventRecord(g_prof_ev[2 * i + 1], s);
+      g_launch_ev[0] = g_launch_ev[1] = nullptr;
+    }
   }
 };
 

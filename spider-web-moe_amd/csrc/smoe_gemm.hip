@@ -1376,13 +1376,13 @@ int launch_mfma_fmt(const GemmArgs& a, hipStream_t s) {
   const dim3 block(WM * WN * 64);
   if (grid.x == 0) return SMOE_OK;
   switch (a.epi) {
-    case EPI_F32_BIAS: hipLaunchKernelGGL((k_gemm_mfma<BM, BN, BK, WM, WN, FMT, EPI_F32_BIAS>), grid, block, 0, s, a); break;
-    case EPI_ROWSCALE: hipLaunchKernelGGL((k_gemm_mfma<BM, BN, BK, WM, WN, FMT, EPI_ROWSCALE>), grid, block, 0, s, a); break;
-    case EPI_GELU: hipLaunchKernelGGL((k_gemm_mfma<BM, BN, BK, WM, WN, FMT, EPI_GELU>), grid, block, 0, s, a); break;
-    case EPI_DOWN: hipLaunchKernelGGL((k_gemm_mfma<BM, BN, BK, WM, WN, FMT, EPI_DOWN>), grid, block, 0, s, a); break;
+    case EPI_F32_BIAS: SMOE_LAUNCH((k_gemm_mfma<BM, BN, BK, WM, WN, FMT, EPI_F32_BIAS>), grid, block, 0, s, a); break;
+    case EPI_ROWSCALE: SMOE_LAUNCH((k_gemm_mfma<BM, BN, BK, WM, WN, FMT, EPI_ROWSCALE>), grid, block, 0, s, a); break;
+    case EPI_GELU: SMOE_LAUNCH((k_gemm_mfma<BM, BN, BK, WM, WN, FMT, EPI_GELU>), grid, block, 0, s, a); break;
+    case EPI_DOWN: SMOE_LAUNCH((k_gemm_mfma<BM, BN, BK, WM, WN, FMT, EPI_DOWN>), grid, block, 0, s, a); break;
     case EPI_SWIGLU:
       if constexpr ((BN / WN) % 64 == 0) {
-        hipLaunchKernelGGL((k_gemm_mfma<BM, BN, BK, WM, WN, FMT, EPI_SWIGLU>), grid, block, 0, s, a);
+        SMOE_LAUNCH((k_gemm_mfma<BM, BN, BK, WM, WN, FMT, EPI_SWIGLU>), grid, block, 0, s, a);
         break;
       }
       return SMOE_EINVAL;
@@ -1407,11 +1407,11 @@ int launch_ring(const GemmArgs& a, hipStream_t s) {
   if (tiles == 0) return SMOE_OK;
   const dim3 grid(tiles), block(256);
   switch (a.epi) {
-    case EPI_F32_BIAS: hipLaunchKernelGGL((k_gemm_ring<BN, NS, GM, EPI_F32_BIAS>), grid, block, 0, s, a); break;
-    case EPI_ROWSCALE: hipLaunchKernelGGL((k_gemm_ring<BN, NS, GM, EPI_ROWSCALE>), grid, block, 0, s, a); break;
-    case EPI_GELU: hipLaunchKernelGGL((k_gemm_ring<BN, NS, GM, EPI_GELU>), grid, block, 0, s, a); break;
-    case EPI_SWIGLU: hipLaunchKernelGGL((k_gemm_ring<BN, NS, GM, EPI_SWIGLU>), grid, block, 0, s, a); break;
-    case EPI_DOWN: hipLaunchKernelGGL((k_gemm_ring<BN, NS, GM, EPI_DOWN>), grid, block, 0, s, a); break;
+    case EPI_F32_BIAS: SMOE_LAUNCH((k_gemm_ring<BN, NS, GM, EPI_F32_BIAS>), grid, block, 0, s, a); break;
+    case EPI_ROWSCALE: SMOE_LAUNCH((k_gemm_ring<BN, NS, GM, EPI_ROWSCALE>), grid, block, 0, s, a); break;
+    case EPI_GELU: SMOE_LAUNCH((k_gemm_ring<BN, NS, GM, EPI_GELU>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU: SMOE_LAUNCH((k_gemm_ring<BN, NS, GM, EPI_SWIGLU>), grid, block, 0, s, a); break;
+    case EPI_DOWN: SMOE_LAUNCH((k_gemm_ring<BN, NS, GM, EPI_DOWN>), grid, block, 0, s, a); break;
     default: return SMOE_EINVAL;
   }
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
@@ -1423,10 +1423,10 @@ int launch_pp(const GemmArgs& a, hipStream_t s) {
   if (tiles == 0) return SMOE_OK;
   const dim3 grid(tiles), block(512);
   switch (a.epi) {
-    case EPI_ROWSCALE: hipLaunchKernelGGL((k_gemm_pp<NS, GM, EPI_ROWSCALE, BM>), grid, block, 0, s, a); break;
-    case EPI_GELU: hipLaunchKernelGGL((k_gemm_pp<NS, GM, EPI_GELU, BM>), grid, block, 0, s, a); break;
-    case EPI_SWIGLU: hipLaunchKernelGGL((k_gemm_pp<NS, GM, EPI_SWIGLU, BM>), grid, block, 0, s, a); break;
-    case EPI_DOWN: hipLaunchKernelGGL((k_gemm_pp<NS, GM, EPI_DOWN, BM>), grid, block, 0, s, a); break;
+    case EPI_ROWSCALE: SMOE_LAUNCH((k_gemm_pp<NS, GM, EPI_ROWSCALE, BM>), grid, block, 0, s, a); break;
+    case EPI_GELU: SMOE_LAUNCH((k_gemm_pp<NS, GM, EPI_GELU, BM>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU: SMOE_LAUNCH((k_gemm_pp<NS, GM, EPI_SWIGLU, BM>), grid, block, 0, s, a); break;
+    case EPI_DOWN: SMOE_LAUNCH((k_gemm_pp<NS, GM, EPI_DOWN, BM>), grid, block, 0, s, a); break;
     default: return SMOE_EINVAL;
   }
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
@@ -1437,10 +1437,10 @@ int launch_f32_bn(const GemmArgs& a, hipStream_t s) {
   const dim3 grid(max_tiles(a, BM), (a.N_out + BN - 1) / BN);
   if (grid.x == 0) return SMOE_OK;
   switch (a.epi) {
-    case EPI_F32_BIAS: hipLaunchKernelGGL((k_gemm_f32<BM, BN, EPI_F32_BIAS>), grid, dim3(256), 0, s, a); break;
-    case EPI_ROWSCALE: hipLaunchKernelGGL((k_gemm_f32<BM, BN, EPI_ROWSCALE>), grid, dim3(256), 0, s, a); break;
-    case EPI_GELU: hipLaunchKernelGGL((k_gemm_f32<BM, BN, EPI_GELU>), grid, dim3(256), 0, s, a); break;
-    case EPI_DOWN: hipLaunchKernelGGL((k_gemm_f32<BM, BN, EPI_DOWN>), grid, dim3(256), 0, s, a); break;
+    case EPI_F32_BIAS: SMOE_LAUNCH((k_gemm_f32<BM, BN, EPI_F32_BIAS>), grid, dim3(256), 0, s, a); break;
+    case EPI_ROWSCALE: SMOE_LAUNCH((k_gemm_f32<BM, BN, EPI_ROWSCALE>), grid, dim3(256), 0, s, a); break;
+    case EPI_GELU: SMOE_LAUNCH((k_gemm_f32<BM, BN, EPI_GELU>), grid, dim3(256), 0, s, a); break;
+    case EPI_DOWN: SMOE_LAUNCH((k_gemm_f32<BM, BN, EPI_DOWN>), grid, dim3(256), 0, s, a); break;
     default: return SMOE_EUNSUPPORTED;  // SwiGLU on fp32 experts is not provided
   }
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
@@ -1456,11 +1456,11 @@ int launch_decode_fmt(const GemmArgs& a, hipStream_t s) {
   const int slices = (a.N_out + 16 * TNW - 1) / (16 * TNW);
   const dim3 grid((slices + CS - 1) / CS, tiles, 1);
   switch (a.epi) {
-    case EPI_F32_BIAS: hipLaunchKernelGGL((k_gemm_decode<FMT, EPI_F32_BIAS, TNW, RT, KSPLIT, D>), grid, dim3(256), 0, s, a); break;
-    case EPI_ROWSCALE: hipLaunchKernelGGL((k_gemm_decode<FMT, EPI_ROWSCALE, TNW, RT, KSPLIT, D>), grid, dim3(256), 0, s, a); break;
-    case EPI_GELU: hipLaunchKernelGGL((k_gemm_decode<FMT, EPI_GELU, TNW, RT, KSPLIT, D>), grid, dim3(256), 0, s, a); break;
-    case EPI_DOWN: hipLaunchKernelGGL((k_gemm_decode<FMT, EPI_DOWN, TNW, RT, KSPLIT, D>), grid, dim3(256), 0, s, a); break;
-    case EPI_SWIGLU: hipLaunchKernelGGL((k_gemm_decode<FMT, EPI_SWIGLU, TNW, RT, KSPLIT, D>), grid, dim3(256), 0, s, a); break;
+    case EPI_F32_BIAS: SMOE_LAUNCH((k_gemm_decode<FMT, EPI_F32_BIAS, TNW, RT, KSPLIT, D>), grid, dim3(256), 0, s, a); break;
+    case EPI_ROWSCALE: SMOE_LAUNCH((k_gemm_decode<FMT, EPI_ROWSCALE, TNW, RT, KSPLIT, D>), grid, dim3(256), 0, s, a); break;
+    case EPI_GELU: SMOE_LAUNCH((k_gemm_decode<FMT, EPI_GELU, TNW, RT, KSPLIT, D>), grid, dim3(256), 0, s, a); break;
+    case EPI_DOWN: SMOE_LAUNCH((k_gemm_decode<FMT, EPI_DOWN, TNW, RT, KSPLIT, D>), grid, dim3(256), 0, s, a); break;
+    case EPI_SWIGLU: SMOE_LAUNCH((k_gemm_decode<FMT, EPI_SWIGLU, TNW, RT, KSPLIT, D>), grid, dim3(256), 0, s, a); break;
     default: return SMOE_EINVAL;
   }
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
@@ -1512,13 +1512,13 @@ int launch_skinny_fmt(const GemmArgs& a, hipStream_t s) {
   const dim3 grid((a.N_out + 16 * TN - 1) / (16 * TN), tiles, 1);
   const dim3 block(NW * 64);
   switch (a.epi) {
-    case EPI_F32_BIAS: hipLaunchKernelGGL((k_gemm_skinny<FMT, EPI_F32_BIAS, TN, RT, NW, U>), grid, block, 0, s, a); break;
-    case EPI_ROWSCALE: hipLaunchKernelGGL((k_gemm_skinny<FMT, EPI_ROWSCALE, TN, RT, NW, U>), grid, block, 0, s, a); break;
-    case EPI_GELU: hipLaunchKernelGGL((k_gemm_skinny<FMT, EPI_GELU, TN, RT, NW, U>), grid, block, 0, s, a); break;
-    case EPI_DOWN: hipLaunchKernelGGL((k_gemm_skinny<FMT, EPI_DOWN, TN, RT, NW, U>), grid, block, 0, s, a); break;
+    case EPI_F32_BIAS: SMOE_LAUNCH((k_gemm_skinny<FMT, EPI_F32_BIAS, TN, RT, NW, U>), grid, block, 0, s, a); break;
+    case EPI_ROWSCALE: SMOE_LAUNCH((k_gemm_skinny<FMT, EPI_ROWSCALE, TN, RT, NW, U>), grid, block, 0, s, a); break;
+    case EPI_GELU: SMOE_LAUNCH((k_gemm_skinny<FMT, EPI_GELU, TN, RT, NW, U>), grid, block, 0, s, a); break;
+    case EPI_DOWN: SMOE_LAUNCH((k_gemm_skinny<FMT, EPI_DOWN, TN, RT, NW, U>), grid, block, 0, s, a); break;
     case EPI_SWIGLU:
       if constexpr (TN == 4) {
-        hipLaunchKernelGGL((k_gemm_skinny<FMT, EPI_SWIGLU, TN, RT, NW, U>), grid, block, 0, s, a);
+        SMOE_LAUNCH((k_gemm_skinny<FMT, EPI_SWIGLU, TN, RT, NW, U>), grid, block, 0, s, a);
         break;
       }
       return SMOE_EINVAL;
@@ -1541,11 +1541,11 @@ template <int FMT, int RT, int NS, int WGS>
 int launch_stream_fmt(const GemmArgs& a, hipStream_t s) {
   const dim3 grid((a.N_out + 255) / 256, a.G == 0 ? 1 : a.G), block(256);
   switch (a.epi) {
-    case EPI_F32_BIAS: hipLaunchKernelGGL((k_gemm_stream<FMT, EPI_F32_BIAS, RT, NS, WGS>), grid, block, 0, s, a); break;
-    case EPI_ROWSCALE: hipLaunchKernelGGL((k_gemm_stream<FMT, EPI_ROWSCALE, RT, NS, WGS>), grid, block, 0, s, a); break;
-    case EPI_GELU: hipLaunchKernelGGL((k_gemm_stream<FMT, EPI_GELU, RT, NS, WGS>), grid, block, 0, s, a); break;
-    case EPI_SWIGLU: hipLaunchKernelGGL((k_gemm_stream<FMT, EPI_SWIGLU, RT, NS, WGS>), grid, block, 0, s, a); break;
-    case EPI_DOWN: hipLaunchKernelGGL((k_gemm_stream<FMT, EPI_DOWN, RT, NS, WGS>), grid, block, 0, s, a); break;
+    case EPI_F32_BIAS: SMOE_LAUNCH((k_gemm_stream<FMT, EPI_F32_BIAS, RT, NS, WGS>), grid, block, 0, s, a); break;
+    case EPI_ROWSCALE: SMOE_LAUNCH((k_gemm_stream<FMT, EPI_ROWSCALE, RT, NS, WGS>), grid, block, 0, s, a); break;
+    case EPI_GELU: SMOE_LAUNCH((k_gemm_stream<FMT, EPI_GELU, RT, NS, WGS>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU: SMOE_LAUNCH((k_gemm_stream<FMT, EPI_SWIGLU, RT, NS, WGS>), grid, block, 0, s, a); break;
+    case EPI_DOWN: SMOE_LAUNCH((k_gemm_stream<FMT, EPI_DOWN, RT, NS, WGS>), grid, block, 0, s, a); break;
     default: return SMOE_EINVAL;
   }
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;

@@ -1,11 +1,31 @@
 // Host-side launcher interfaces shared by the .hip translation units.
 #pragma once
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "smoe.h"
 
 namespace smoe {
+
+// Start / stop events for the next GEMM launch (stage timing of the
+// single-kernel stages): when set, the launch records them itself
+// (hipExtLaunchKernelGGL), so the interval is the kernel's own execution,
+// without the gaps two separate event packets would add; the launch clears
+// them.  Diagnostics state of one host thread at a time, like the stage
+// profiler that sets it.
+extern hipEvent_t g_launch_ev[2];
+
+#define SMOE_LAUNCH(kernel, grid, block, shm, stream, ...)                                   \
+  do {                                                                                       \
+    if (::smoe::g_launch_ev[0]) {                                                            \
+      hipExtLaunchKernelGGL(kernel, grid, block, shm, stream, ::smoe::g_launch_ev[0],        \
+                            ::smoe::g_launch_ev[1], 0, __VA_ARGS__);                         \
+      ::smoe::g_launch_ev[0] = ::smoe::g_launch_ev[1] = nullptr;                             \
+    } else {                                                                                 \
+      hipLaunchKernelGGL(kernel, grid, block, shm, stream, __VA_ARGS__);                     \
+    }                                                                                        \
+  } while (0)
 
 // Epilogues of the grouped GEMM  C[row, n] = sum_k A[a_row(row), k] * W_g[n, k]
 enum Epi : int {
