@@ -1036,6 +1036,29 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
       fetch(d, s + d + D);
     }
   }
+  // the epilogue's per-channel scales / biases and row weights go out now,
+  // behind the slice's last loads, so they land while the last steps run
+  float esc[TNW][4], ebi[TNW][4], ers[RT];
+#pragma unroll
+  for (int t = 0; t < TNW; ++t) {
+    const int c = min(c0[t] + 4 * q, p.N_out - 4);
+    const bool sw_gate = EPI == EPI_SWIGLU && t < TNW / 2;
+    const int bc = EPI == EPI_SWIGLU ? (c >> 6) * 32 + (c & 31) : c;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      esc[t][i] = (FMT == SMOE_FP8_E4M3 && EPI != EPI_ROWSCALE)
+                      ? reinterpret_cast<const float*>(p.S)[g * p.s_gstride + c + i]
+                      : 1.0f;
+      ebi[t][i] = (p.bias && (EPI == EPI_SWIGLU ? sw_gate : EPI != EPI_ROWSCALE))
+                      ? p.bias[g * p.bias_gstride + bc + i]
+                      : 0.0f;
+    }
+  }
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int r = min(r_lo + 16 * rt + l16, r_hi - 1);
+    ers[rt] = (EPI == EPI_ROWSCALE || EPI == EPI_DOWN) ? p.row_scale[r] : 1.0f;
+  }
   // the last 2D - 1 steps at most: refills only where a step is left
 #pragma unroll
   for (int d = 0; d < D; ++d) {
@@ -1061,6 +1084,15 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
         for (int rt = 0; rt < RT; ++rt) acc[t][rt] += red[wave + j][t * RT + rt][lane];
   }
   // lane: channels c0[t] + 4 q + (0..3) of row r_lo + 16 rt + l16
+  const bool f32o = EPI == EPI_F32_BIAS || p.out_dtype == SMOE_F32;
+  auto put4 = [&](int row, int col, const float (&o)[4]) {
+    const int64_t off = static_cast<int64_t>(row) * p.ldo + col;
+    if (f32o)
+      *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + off) = f32x4{o[0], o[1], o[2], o[3]};
+    else
+      *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + off) =
+          u32x2{pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3])};
+  };
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const int row = r_lo + 16 * rt + l16;
@@ -1070,28 +1102,30 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
       for (int t = 0; t < TNW / 2; ++t) {  // gate tile t, up tile t + TNW / 2
         const int c = c0[t] + 4 * q;
         if (c >= p.N_out) continue;
-        const int u0 = (c >> 6) * 32 + (c & 31);
         float o[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float gs = acc[t][rt][i] * col_scale(p, FMT, g, c + i);
-          const float us =
-              acc[t + TNW / 2][rt][i] * col_scale(p, FMT, g, c + 32 + i) + bias_at(p, g, u0 + i);
+          const float gs = acc[t][rt][i] * esc[t][i];
+          const float us = acc[t + TNW / 2][rt][i] * esc[t + TNW / 2][i] + ebi[t][i];
           o[i] = silu(gs) * us;
         }
-        const int64_t off = static_cast<int64_t>(row) * p.ldo + u0;
-        if (p.out_dtype == SMOE_F32)
-          *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + off) =
-              f32x4{o[0], o[1], o[2], o[3]};
-        else
-          *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + off) =
-              u32x2{pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3])};
+        put4(row, (c >> 6) * 32 + (c & 31), o);
       }
     } else {
 #pragma unroll
       for (int t = 0; t < TNW; ++t) {
         const int c = c0[t] + 4 * q;
-        if (c < p.N_out) store4<EPI>(p, FMT, g, row, c, acc[t][rt]);
+        if (c >= p.N_out) continue;
+        float o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float a = acc[t][rt][i];
+          if constexpr (EPI == EPI_ROWSCALE) o[i] = a * ers[rt];
+          else if constexpr (EPI == EPI_GELU) o[i] = gelu_erf(a * esc[t][i] + ebi[t][i]);
+          else if constexpr (EPI == EPI_DOWN) o[i] = (a * esc[t][i] + ebi[t][i]) * ers[rt];
+          else o[i] = a * esc[t][i] + ebi[t][i];  // EPI_F32_BIAS
+        }
+        put4(row, c, o);
       }
     }
   }
