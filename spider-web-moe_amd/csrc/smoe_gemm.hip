@@ -791,6 +791,31 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(const GemmArgs p) {
                   : reinterpret_cast<const uint8_t*>(p.W) +
                         (g * p.w_gstride + static_cast<int64_t>(n) * p.ldw) * ESZ2 / 2;
   }
+  // the epilogue operands of this wave's channel tile (waves < ET), requested
+  // before the weight stream: they are in registers when the partial sums
+  // meet instead of costing a round trip after them
+  constexpr int ET = EPI == EPI_SWIGLU ? TN / 2 : TN;
+  float esc[4], esc2[4], ebi[4], ers[RT];
+  {
+    const int ce = min(n0 + 16 * (wave < ET ? wave : 0) + 4 * q, p.N_out - 4);
+    const bool seg2 = p.W2 && ce >= p.n_split;  // second weight segment (front GEMM)
+    const int bc = EPI == EPI_SWIGLU ? (ce >> 6) * 32 + (ce & 31) : ce;
+    const int64_t s0 = g * p.s_gstride + ce;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      constexpr bool fp8 = FMT == SMOE_FP8_E4M3 && EPI != EPI_ROWSCALE;
+      esc[i] = fp8 ? reinterpret_cast<const float*>(p.S)[s0 + i] : 1.0f;
+      esc2[i] = (fp8 && EPI == EPI_SWIGLU) ? reinterpret_cast<const float*>(p.S)[s0 + 32 + i] : 1.0f;
+      ebi[i] = EPI == EPI_ROWSCALE ? 0.0f
+               : seg2              ? (p.bias2 ? p.bias2[ce - p.n_split + i] : 0.0f)
+                                   : bias_at(p, g, bc + i);
+    }
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+      ers[rt] = (EPI == EPI_ROWSCALE || EPI == EPI_DOWN)
+                    ? p.row_scale[min(r_lo + 16 * rt + l16, r_hi - 1)]
+                    : 1.0f;
+  }
   const int KS = p.K / 64;
   const int s_begin = wave * KS / NW, s_end = (wave + 1) * KS / NW;
   const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A);
@@ -856,7 +881,6 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(const GemmArgs p) {
       for (int rt = 0; rt < RT; ++rt) red[wave][t * RT + rt][lane] = acc[t][rt];
     __syncthreads();
     // lane: channels n0 + 16 t + 4 q + (0..3) of row m0 + 16 rt + l16
-    constexpr int ET = EPI == EPI_SWIGLU ? TN / 2 : TN;
     if (wave < ET) {
       const int t = wave;
 #pragma unroll
@@ -867,28 +891,31 @@ __global__ __launch_bounds__(NW * 64) void k_gemm_skinny(const GemmArgs p) {
         for (int w = 1; w < NW; ++w) v += red[w][t * RT + rt][lane];
         const int c = n0 + 16 * t + 4 * q;
         if (row >= r_hi || c >= p.N_out) continue;
+        float o[4];
+        int col = c;
         if constexpr (EPI == EPI_SWIGLU) {
           f32x4 up = red[0][(t + TN / 2) * RT + rt][lane];
 #pragma unroll
           for (int w = 1; w < NW; ++w) up += red[w][(t + TN / 2) * RT + rt][lane];
-          const int u0 = (c >> 6) * 32 + (c & 31);
-          float o[4];
+          col = (c >> 6) * 32 + (c & 31);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[i] = silu(v[i] * esc[i]) * (up[i] * esc2[i] + ebi[i]);
+        } else {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float gs = v[i] * col_scale(p, FMT, g, c + i);
-            const float us = up[i] * col_scale(p, FMT, g, c + 32 + i) + bias_at(p, g, u0 + i);
-            o[i] = silu(gs) * us;
+            if constexpr (EPI == EPI_ROWSCALE) o[i] = v[i] * ers[rt];
+            else if constexpr (EPI == EPI_GELU) o[i] = gelu_erf(v[i] * esc[i] + ebi[i]);
+            else if constexpr (EPI == EPI_DOWN) o[i] = (v[i] * esc[i] + ebi[i]) * ers[rt];
+            else o[i] = v[i] * esc[i] + ebi[i];  // EPI_F32_BIAS
           }
-          const int64_t off = static_cast<int64_t>(row) * p.ldo + u0;
-          if (p.out_dtype == SMOE_F32)
-            *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + off) =
-                f32x4{o[0], o[1], o[2], o[3]};
-          else
-            *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + off) =
-                u32x2{pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3])};
-        } else {
-          store4<EPI>(p, FMT, g, row, c, v);
         }
+        const int64_t off = static_cast<int64_t>(row) * p.ldo + col;
+        if (EPI == EPI_F32_BIAS || p.out_dtype == SMOE_F32)
+          *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + off) =
+              f32x4{o[0], o[1], o[2], o[3]};
+        else
+          *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + off) =
+              u32x2{pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3])};
       }
     }
     __syncthreads();  // red is rewritten by the next pass
