@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define SMOE_ABI_VERSION 2
+#define SMOE_ABI_VERSION 3
 
 /* status codes (spider_kernels.h convention; see scalar.cpp:9,45,58) */
 #define SMOE_OK 0
@@ -82,6 +82,11 @@ typedef struct smoe_experts {
   const void* s_down;
   const float* b_up;
   const float* b_down;
+  /* optional (bf16 only, else ignored): w_up / w_down in the decode tile
+   * layout (smoe_pack_decode_tiles), read instead of them by the decode
+   * weight stream; NULL to stream the row-major weights */
+  const void* w_up_tiles;
+  const void* w_down_tiles;
 } smoe_experts;
 
 /* One Spider-MoE block (parameters of model.py:165-185).
@@ -103,6 +108,8 @@ typedef struct smoe_block {
   float alpha;                /* residual_scale  (config.py:18)    */
   float beta;                 /* re_inject_weight (config.py:19)   */
   float eps;                  /* LayerNorm eps (1e-5)              */
+  const void* edge_value_w_tiles; /* optional (bf16): edge_value_w in the decode
+                                     tile layout, or NULL            */
 } smoe_block;
 
 /* Byte offsets of the named regions inside a block workspace (for tests and
@@ -222,6 +229,21 @@ SMOE_API int smoe_expert_delta(const smoe_experts* ex, const void* msg, const in
 #define SMOE_STAGE_FRONT_GEMM 11  /* router + all edge-generator logits, one GEMM */
 #define SMOE_STAGE_FRONT_ROUTE 12 /* top-k, expert plan, top-m, destination plan */
 #define SMOE_NUM_STAGES 13
+
+/* Decode tile layout of bf16 weights w [G,N,K] (N % 16 == 0, K % 64 == 0),
+ * same size: for group g, 16-row tile t, 64-wide K step s, half h and lane
+ * l = 16q + r, the 8 elements e at
+ *   out[((((g*(N/16) + t)*(K/64) + s)*2 + h)*64 + l)*8 + e]
+ *     = w[g][16t + r][64s + 32h + 8q + e],
+ * i.e. each 16-row x 64-k block is two 1 KB halves holding, lane by lane,
+ * the 16-byte MFMA fragments a wave loads.  The decode weight stream reads a
+ * block with two fully contiguous 1 KB loads instead of sixteen 64-byte row
+ * pieces a row pitch apart (C2's bf16 edge projection: 8.5 -> 6.4 us per
+ * launch at uniform 15-row groups).  No counterpart in the reference (its
+ * weights stay nn.Linear row-major); the row-major weights remain the
+ * format every other kernel reads. */
+SMOE_API int smoe_pack_decode_tiles(const void* w, int G, int N, int K, void* out, void* stream);
+
 /* When `events` is not NULL, every later smoe_block_forward records
  * events[2*i] before and events[2*i+1] after the i-th launch of a stage in
  * `stage_mask` (bit s = stage s), for i < capacity, on the call's stream.

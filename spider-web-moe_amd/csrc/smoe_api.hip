@@ -241,6 +241,7 @@ int run_experts(const smoe_experts& ex, const void* msg, const int32_t* off, con
   up.lda = H;
   up.a_rows = rows;
   up.W = ex.w_up;
+  up.Wt = ex.format == SMOE_BF16 ? ex.w_up_tiles : nullptr;
   up.w_gstride = static_cast<int64_t>(nup) * H;
   up.ldw = H;
   up.S = ex.s_up;
@@ -266,6 +267,7 @@ int run_experts(const smoe_experts& ex, const void* msg, const int32_t* off, con
   dn.lda = U;
   dn.a_rows = nullptr;  // act rows are already in plan order
   dn.W = ex.w_down;
+  dn.Wt = ex.format == SMOE_BF16 ? ex.w_down_tiles : nullptr;
   dn.w_gstride = static_cast<int64_t>(H) * U;
   dn.ldw = U;
   dn.S = ex.s_down;
@@ -457,6 +459,7 @@ SMOE_API int smoe_block_forward(const smoe_block* b, const void* h_in, const voi
     pg.lda = H;
     pg.a_rows = at<int32_t>(ws, l.d_rows);
     pg.W = b->edge_value_w;
+    pg.Wt = b->act_dtype == SMOE_BF16 ? b->edge_value_w_tiles : nullptr;
     pg.w_gstride = static_cast<int64_t>(H) * H;
     pg.ldw = H;
     pg.K = H;
@@ -486,6 +489,11 @@ SMOE_API int smoe_block_forward(const smoe_block* b, const void* h_in, const voi
     cur = dst;
   }
   return SMOE_OK;
+}
+
+SMOE_API int smoe_pack_decode_tiles(const void* w, int G, int N, int K, void* out, void* stream) {
+  return hip_rc(launch_pack_decode_tiles(w, G, N, K, out, static_cast<hipStream_t>(stream)),
+                "smoe_pack_decode_tiles");
 }
 
 SMOE_API int smoe_profile_stages(uint32_t stage_mask, void** events, int capacity) {

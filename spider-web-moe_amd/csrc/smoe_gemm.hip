@@ -945,12 +945,13 @@ template <> struct DRaw<SMOE_BF16> { u32x4 a, b; };
 template <> struct DRaw<SMOE_FP8_E4M3> { u32x4 a; };
 template <> struct DRaw<SMOE_INT4> { u32x2 a; float s; };
 
-template <int FMT, int EPI, int TNW, int RT, int KSPLIT, int D>
+template <int FMT, int EPI, int TNW, int RT, int KSPLIT, int D, bool PK = false>
 __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
   constexpr int ESZ2 = FMT == SMOE_BF16 ? 4 : (FMT == SMOE_FP8_E4M3 ? 2 : 1);  // 2 x bytes/elt
   constexpr int CS = 4 / KSPLIT;  // channel slices per workgroup
   static_assert(4 % KSPLIT == 0, "KSPLIT divides the 4 waves");
   static_assert(EPI != EPI_SWIGLU || TNW == 2 || TNW == 4, "SwiGLU slices pair gate and up tiles");
+  static_assert(!PK || FMT == SMOE_BF16, "the decode tile layout holds bf16 weights");
   __shared__ f32x4 red[KSPLIT > 1 ? 4 : 1][TNW * RT][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int q = lane >> 4, l16 = lane & 15;
@@ -977,6 +978,17 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
     wrow[t] = reinterpret_cast<const uint8_t*>(p.W) +
               (g * p.w_gstride + static_cast<int64_t>(n) * p.ldw) * ESZ2 / 2;
   }
+  // decode tile layout: tile t's 64-k step st is the 2 KB block
+  // (g * N_out/16 + t) * K/64 + st, lane l's fragments at 16 l and 1 KB + 16 l
+  const uint8_t* wtile[TNW];
+  if constexpr (PK) {
+#pragma unroll
+    for (int t = 0; t < TNW; ++t) {
+      const int tile = min(c0[t], p.N_out - 16) >> 4;
+      wtile[t] = reinterpret_cast<const uint8_t*>(p.Wt) +
+                 (static_cast<int64_t>(g) * (p.N_out >> 4) + tile) * (p.K >> 6) * 2048 + 16 * lane;
+    }
+  }
   const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A);
   const uint16_t* arow[RT];
 #pragma unroll
@@ -995,7 +1007,11 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
     const int k0 = 64 * min(s_begin + i, last);
 #pragma unroll
     for (int t = 0; t < TNW; ++t) {
-      if constexpr (FMT == SMOE_BF16) {
+      if constexpr (PK) {
+        const uint8_t* blk = wtile[t] + static_cast<int64_t>(k0 >> 6) * 2048;
+        wr[d][t].a = *reinterpret_cast<const u32x4*>(blk);
+        wr[d][t].b = *reinterpret_cast<const u32x4*>(blk + 1024);
+      } else if constexpr (FMT == SMOE_BF16) {
         wr[d][t].a = *reinterpret_cast<const u32x4*>(wrow[t] + 2 * (k0 + 8 * q));
         wr[d][t].b = *reinterpret_cast<const u32x4*>(wrow[t] + 2 * (k0 + 32 + 8 * q));
       } else if constexpr (FMT == SMOE_FP8_E4M3) {
@@ -1423,6 +1439,36 @@ __global__ __launch_bounds__(256) void k_gemm_f32(const GemmArgs p) {
   }
 }
 
+// ------------------------------------------------- decode tile layout ----
+// out[(((g*T + t)*S + s)*2 + h)*64 + l][e] = w[g][16t + l%16][64s + 32h + 8(l/16) + e]
+// (T = N/16, S = K/64): one thread per 16-byte fragment, 16-byte reads from
+// the row-major weights, contiguous writes.
+__global__ __launch_bounds__(256) void k_pack_decode_tiles(const uint16_t* __restrict__ w,
+                                                          int64_t frags, int N, int K,
+                                                          uint16_t* __restrict__ out) {
+  const int64_t f = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (f >= frags) return;
+  const int l = static_cast<int>(f & 63), h = static_cast<int>((f >> 6) & 1);
+  const int64_t blk = f >> 7;  // (g*T + t)*S + s
+  const int S = K / 64, T = N / 16;
+  const int st = static_cast<int>(blk % S);
+  const int64_t gt = blk / S;  // g*T + t
+  const int64_t g = gt / T, t = gt % T;
+  const int64_t row = g * N + 16 * t + (l & 15);
+  const int k = 64 * st + 32 * h + 8 * (l >> 4);
+  *reinterpret_cast<u32x4*>(out + f * 8) = *reinterpret_cast<const u32x4*>(w + row * K + k);
+}
+
+int launch_pack_decode_tiles(const void* w, int G, int N, int K, void* out, hipStream_t s) {
+  if (!w || !out || G < 1 || N < 16 || K < 64 || N % 16 || K % 64) return SMOE_EINVAL;
+  if (reinterpret_cast<uintptr_t>(w) % 16 || reinterpret_cast<uintptr_t>(out) % 16) return SMOE_EINVAL;
+  const int64_t frags = static_cast<int64_t>(G) * N * K / 8;
+  hipLaunchKernelGGL(k_pack_decode_tiles, dim3(static_cast<unsigned>((frags + 255) / 256)), dim3(256),
+                     0, s, reinterpret_cast<const uint16_t*>(w), frags, N, K,
+                     reinterpret_cast<uint16_t*>(out));
+  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
 // --------------------------------------------------------------- launch ----
 namespace {
 
@@ -1507,7 +1553,7 @@ int launch_f32_bn(const GemmArgs& a, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 
-template <int FMT, int RT, int KSPLIT>
+template <int FMT, int RT, int KSPLIT, bool PK>
 int launch_decode_fmt(const GemmArgs& a, hipStream_t s) {
   // one workgroup per (4 / KSPLIT slices of 64 channels, tile of 16*RT rows);
   // 3 steps in flight per wave
@@ -1517,21 +1563,21 @@ int launch_decode_fmt(const GemmArgs& a, hipStream_t s) {
   const int slices = (a.N_out + 16 * TNW - 1) / (16 * TNW);
   const dim3 grid((slices + CS - 1) / CS, tiles, 1);
   switch (a.epi) {
-    case EPI_F32_BIAS: SMOE_LAUNCH((k_gemm_decode<FMT, EPI_F32_BIAS, TNW, RT, KSPLIT, D>), grid, dim3(256), 0, s, a); break;
-    case EPI_ROWSCALE: SMOE_LAUNCH((k_gemm_decode<FMT, EPI_ROWSCALE, TNW, RT, KSPLIT, D>), grid, dim3(256), 0, s, a); break;
-    case EPI_GELU: SMOE_LAUNCH((k_gemm_decode<FMT, EPI_GELU, TNW, RT, KSPLIT, D>), grid, dim3(256), 0, s, a); break;
-    case EPI_DOWN: SMOE_LAUNCH((k_gemm_decode<FMT, EPI_DOWN, TNW, RT, KSPLIT, D>), grid, dim3(256), 0, s, a); break;
-    case EPI_SWIGLU: SMOE_LAUNCH((k_gemm_decode<FMT, EPI_SWIGLU, TNW, RT, KSPLIT, D>), grid, dim3(256), 0, s, a); break;
+    case EPI_F32_BIAS: SMOE_LAUNCH((k_gemm_decode<FMT, EPI_F32_BIAS, TNW, RT, KSPLIT, D, PK>), grid, dim3(256), 0, s, a); break;
+    case EPI_ROWSCALE: SMOE_LAUNCH((k_gemm_decode<FMT, EPI_ROWSCALE, TNW, RT, KSPLIT, D, PK>), grid, dim3(256), 0, s, a); break;
+    case EPI_GELU: SMOE_LAUNCH((k_gemm_decode<FMT, EPI_GELU, TNW, RT, KSPLIT, D, PK>), grid, dim3(256), 0, s, a); break;
+    case EPI_DOWN: SMOE_LAUNCH((k_gemm_decode<FMT, EPI_DOWN, TNW, RT, KSPLIT, D, PK>), grid, dim3(256), 0, s, a); break;
+    case EPI_SWIGLU: SMOE_LAUNCH((k_gemm_decode<FMT, EPI_SWIGLU, TNW, RT, KSPLIT, D, PK>), grid, dim3(256), 0, s, a); break;
     default: return SMOE_EINVAL;
   }
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 
-template <int FMT, int RT>
+template <int FMT, int RT, bool PK = false>
 int launch_decode_split(const GemmArgs& a, int ksplit, hipStream_t s) {
-  if (ksplit == 1) return launch_decode_fmt<FMT, RT, 1>(a, s);
-  if (ksplit == 2) return launch_decode_fmt<FMT, RT, 2>(a, s);
-  return launch_decode_fmt<FMT, RT, 4>(a, s);
+  if (ksplit == 1) return launch_decode_fmt<FMT, RT, 1, PK>(a, s);
+  if (ksplit == 2) return launch_decode_fmt<FMT, RT, 2, PK>(a, s);
+  return launch_decode_fmt<FMT, RT, 4, PK>(a, s);
 }
 
 }  // namespace
@@ -1553,6 +1599,9 @@ int launch_decode(const GemmArgs& a, hipStream_t s) {
   const int ksplit = steps >= 12 ? 4 : (steps >= 6 ? 2 : 1);
   switch (a.fmt) {
     case SMOE_BF16:
+      if (a.Wt && a.N_out % 16 == 0)  // the decode tile layout: contiguous 1 KB loads
+        return rt == 1 ? launch_decode_split<SMOE_BF16, 1, true>(a, ksplit, s)
+                       : launch_decode_split<SMOE_BF16, 2, true>(a, ksplit, s);
       return rt == 1 ? launch_decode_split<SMOE_BF16, 1>(a, ksplit, s)
                      : launch_decode_split<SMOE_BF16, 2>(a, ksplit, s);
     case SMOE_FP8_E4M3:

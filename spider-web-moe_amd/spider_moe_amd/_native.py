@@ -27,7 +27,7 @@ class SmoeExperts(ctypes.Structure):
     _fields_ = [("format", _c_int), ("act", _c_int), ("E", _c_int), ("H", _c_int), ("U", _c_int),
                 ("group_size", _c_int), ("scale_dtype", _c_int),
                 ("w_up", _vp), ("w_gate", _vp), ("w_down", _vp), ("s_up", _vp), ("s_down", _vp),
-                ("b_up", _vp), ("b_down", _vp)]
+                ("b_up", _vp), ("b_down", _vp), ("w_up_tiles", _vp), ("w_down_tiles", _vp)]
 
 
 class SmoeBlock(ctypes.Structure):
@@ -36,7 +36,7 @@ class SmoeBlock(ctypes.Structure):
                 ("router_w", _vp), ("loop_bias", _vp), ("edge_gen_w", _vp),
                 ("edge_loop_bias", _vp), ("edge_value_w", _vp), ("experts", SmoeExperts),
                 ("ln_w", _vp), ("ln_b", _vp), ("alpha", _c_float), ("beta", _c_float),
-                ("eps", _c_float)]
+                ("eps", _c_float), ("edge_value_w_tiles", _vp)]
 
 
 _LAYOUT_FIELDS = ["total", "logits", "top_idx", "top_w", "tok_e", "tok_ew", "e_cnt", "e_acnt",
@@ -71,6 +71,7 @@ SIGNATURES = {
     "smoe_expert_delta_workspace_bytes": (_sz, [ctypes.POINTER(SmoeExperts), _c_int, _c_int]),
     "smoe_expert_delta": (_c_int, [ctypes.POINTER(SmoeExperts), _vp, _vp, _vp, _c_int, _c_int,
                                    _vp, _c_int, _vp, _sz, _vp]),
+    "smoe_pack_decode_tiles": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp]),
     "smoe_profile_stages": (_c_int, [ctypes.c_uint32, ctypes.POINTER(_vp), _c_int]),
     "smoe_profile_count": (_c_int, [ctypes.POINTER(ctypes.c_int32), _c_int]),
     "smoe_events_create": (_c_int, [_c_int, ctypes.POINTER(_vp)]),
@@ -83,7 +84,7 @@ STAGES = ["router_gemm", "route_topk", "expert_plan", "edge_logits", "edge_topm"
           # bf16 steps of N <= 64: stages 0-5 as one GEMM and one routing workgroup
           "front_gemm", "front_route"]
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 _LIB = None
 
 

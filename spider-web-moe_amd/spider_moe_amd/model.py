@@ -98,6 +98,10 @@ class SpiderMoELayer(nn.Module):
         self._int4_b_up = None
         self._int4_b_down = None
         self._fp8 = None  # (codes_up, scale_up, codes_down, scale_down)
+        # bf16 weights also get a copy in the decode tile layout, which the
+        # decode weight stream (a few rows per group) reads with contiguous
+        # 1 KB loads; False saves that memory (same results either way)
+        self.decode_tiles = True
         self._packed: _Packed | None = None
         self._packed_key = None
         self._ws: torch.Tensor | None = None
@@ -142,7 +146,7 @@ class SpiderMoELayer(nn.Module):
 
     # ----------------------------------------------------------- packing ----
     def _state_key(self):
-        return (self.expert_format, id(self._int4_w_up), id(self._fp8),
+        return (self.expert_format, id(self._int4_w_up), id(self._fp8), self.decode_tiles,
                 tuple((p.data_ptr(), p._version, p.dtype) for p in self.parameters()))
 
     @torch.no_grad()
@@ -225,12 +229,26 @@ class SpiderMoELayer(nn.Module):
         ex.s_up, ex.s_down = nat.ptr(s_up), nat.ptr(s_down)
         ex.b_up, ex.b_down = nat.ptr(b_up), nat.ptr(b_down)
 
+        def tiles(w):  # bf16 copy in the decode tile layout (smoe_pack_decode_tiles)
+            if not self.decode_tiles or w.dtype != torch.bfloat16 or w.shape[1] % 16 or w.shape[2] % 64:
+                return None
+            out = keep(torch.empty_like(w))
+            nat.check(lib.smoe_pack_decode_tiles(w.data_ptr(), w.shape[0], w.shape[1], w.shape[2],
+                                                 out.data_ptr(), nat.stream_of(dev)),
+                      "smoe_pack_decode_tiles")
+            return out
+
+        if ex.format == nat.BF16:
+            ex.w_up_tiles = nat.ptr(tiles(w_up))
+            ex.w_down_tiles = nat.ptr(tiles(w_down))
+
         d = k.desc
         d.act_dtype = adt
         d.H, d.E, d.K, d.M, d.L, d.R = h, e, self.top_k, self.edges_per_expert, lemb, r
         d.router_w, d.loop_bias = router_w.data_ptr(), loop_bias.data_ptr()
         d.edge_gen_w, d.edge_loop_bias = edge_w.data_ptr(), edge_lb.data_ptr()
         d.edge_value_w = edge_value.data_ptr()
+        d.edge_value_w_tiles = nat.ptr(tiles(edge_value))
         d.experts = ex
         d.ln_w, d.ln_b = f32(self.norm.weight).data_ptr(), f32(self.norm.bias).data_ptr()
         d.alpha, d.beta, d.eps = self.residual_scale, self.reinject_weight, self.norm.eps

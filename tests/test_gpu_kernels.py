@@ -172,6 +172,37 @@ def _experts_struct(n8, fmt, act, e, h, u, w_up, w_down, s_up=None, s_down=None,
     return ex
 
 
+def _tiles(n8, w):
+    """bf16 [G,N,K] -> the decode tile layout through smoe_pack_decode_tiles."""
+    out = torch.empty_like(w)
+    n8.check(n8.lib().smoe_pack_decode_tiles(w.data_ptr(), w.shape[0], w.shape[1], w.shape[2],
+                                             out.data_ptr(), n8.stream_of(torch.device(dev))),
+             "pack_decode_tiles")
+    torch.cuda.synchronize()
+    return out
+
+
+def test_pack_decode_tiles_layout():
+    """out[(((g*T + t)*S + s)*2 + h)*64 + l][e] = w[g][16t + l%16][64s + 32h + 8(l/16) + e]
+    (include/smoe.h), checked element by element on a small case and as one
+    permutation of the whole tensor."""
+    n8 = nat()
+    say("pack decode tiles")
+    g_, n_, k_ = 3, 48, 192
+    w = torch.randn(g_, n_, k_, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).to(dev)
+    got = _tiles(n8, w).cpu().view(-1, 8)
+    wc = w.cpu()
+    t_, s_ = n_ // 16, k_ // 64
+    rng = np.random.default_rng(9)
+    for _ in range(200):
+        g, t, s, h, l = (int(rng.integers(0, x)) for x in (g_, t_, s_, 2, 64))
+        f = (((g * t_ + t) * s_ + s) * 2 + h) * 64 + l
+        ref = wc[g, 16 * t + l % 16, 64 * s + 32 * h + 8 * (l // 16): 64 * s + 32 * h + 8 * (l // 16) + 8]
+        assert torch.equal(got[f], ref), (g, t, s, h, l)
+    perm = wc.view(g_, t_, 16, s_, 2, 4, 8).permute(0, 1, 3, 4, 5, 2, 6).reshape(-1, 8)
+    assert torch.equal(got, perm)
+
+
 def _run_delta(n8, ex, msg_bf16, idx, w):
     n, k = idx.shape
     h = msg_bf16.shape[1]
@@ -318,6 +349,11 @@ def test_decode_experts_match_oracle(fmt, act, shape):
                          up_d, dn_d, b_up=bu_d, b_down=bd_d, **kw)
     got = _run_delta(n8, ex, msg.to(dev), idx.to(torch.int32).to(dev), w.to(dev))
     torch.testing.assert_close(got, ref, rtol=1e-2, atol=1e-2)
+    if fmt == "bf16":  # the decode tile layout: the same fragments, so the same bits
+        tu, td = _tiles(n8, up_d), _tiles(n8, dn_d)
+        ex.w_up_tiles, ex.w_down_tiles = tu.data_ptr(), td.data_ptr()
+        got_t = _run_delta(n8, ex, msg.to(dev), idx.to(torch.int32).to(dev), w.to(dev))
+        assert torch.equal(got_t, got)
 
 
 def test_invalid_arguments_are_rejected():

@@ -38,7 +38,7 @@ def test_exports_every_declared_symbol(nat):
 
 def test_identity(nat):
     lib = nat.lib()
-    assert lib.smoe_abi_version() == 2
+    assert lib.smoe_abi_version() == 3
     assert lib.smoe_backend_name() == b"hip-gfx950"
     assert lib.smoe_backend_caps() == 0b1111
 
@@ -94,6 +94,14 @@ def test_invalid_block_is_rejected_without_launch(nat, bad):
     rc = lib.smoe_block_forward(ctypes.byref(b), 0x1000, 0x1000, 0x1000, 64, 0, 1, 0x1000, 1 << 40, None)
     assert rc in (1, -2)
     assert lib.smoe_last_error()
+
+
+def test_pack_decode_tiles_rejects_bad_shapes(nat):
+    lib = nat.lib()
+    for g, n, k in [(0, 16, 64), (1, 10, 64), (1, 16, 100), (1, 8, 64)]:
+        assert lib.smoe_pack_decode_tiles(0x1000, g, n, k, 0x2000, None) == 1
+    assert lib.smoe_pack_decode_tiles(None, 1, 16, 64, 0x2000, None) == 1
+    assert lib.smoe_pack_decode_tiles(0x1008, 1, 16, 64, 0x2000, None) == 1  # 16-byte alignment
 
 
 def test_capacity_and_range_errors(nat):
