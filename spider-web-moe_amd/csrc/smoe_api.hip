@@ -491,9 +491,9 @@ SMOE_API int smoe_block_forward(const smoe_block* b, const void* h_in, const voi
   return SMOE_OK;
 }
 
-SMOE_API int smoe_pack_decode_tiles(const void* w, int G, int N, int K, void* out, void* stream) {
-  return hip_rc(launch_pack_decode_tiles(w, G, N, K, out, static_cast<hipStream_t>(stream)),
-                "smoe_pack_decode_tiles");
+SMOE_API int smoe_pack_weight_tiles(const void* w, int G, int N, int K, void* out, void* stream) {
+  return hip_rc(launch_pack_weight_tiles(w, G, N, K, out, static_cast<hipStream_t>(stream)),
+                "smoe_pack_weight_tiles");
 }
 
 SMOE_API int smoe_profile_stages(uint32_t stage_mask, void** events, int capacity) {

@@ -577,7 +577,7 @@ __global__ __launch_bounds__(256, NS <= 3 ? 2 : 1) void k_gemm_ring(const GemmAr
 // BM = 256 (wave tile 128 x 64) for many rows per group; BM = 128 (wave tile
 // 64 x 64, two workgroups per CU) when groups hold a few hundred rows and a
 // 256-row tile would be mostly padding.
-template <int NS, int GM, int EPI, int BM>
+template <int NS, int GM, int EPI, int BM, bool PK = false>
 __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmArgs p) {
   constexpr int BN = 256, TM = BM / 2, TN = 64;
   constexpr int FM = TM / 16, FN = TN / 16;
@@ -631,8 +631,14 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
 #pragma unroll
     for (int j = 0; j < B_LD; ++j) {
       const int r = (8 * j + wave) * 16 + pr;
-      const int n = n0 + r < p.N_out ? n0 + r : n0;
-      bsrc[j] = W + static_cast<int64_t>(n) * p.ldw + ((pc ^ ((r >> 1) & 3)) << 3);
+      if constexpr (PK) {  // weight tile layout: 16 rows x 32 k = 1 KB of lane-ordered fragments
+        const int tile = (n0 + (8 * j + wave) * 16 < p.N_out ? n0 + (8 * j + wave) * 16 : n0) >> 4;
+        bsrc[j] = reinterpret_cast<const uint16_t*>(p.Wt) +
+                  ((static_cast<int64_t>(g) * (p.N_out >> 4) + tile) * (p.K >> 5)) * 512 + 8 * lane;
+      } else {
+        const int n = n0 + r < p.N_out ? n0 + r : n0;
+        bsrc[j] = W + static_cast<int64_t>(n) * p.ldw + ((pc ^ ((r >> 1) & 3)) << 3);
+      }
     }
   }
   auto issue = [&](int stage) {  // DMA of K slice `stage` into ring slot stage % NS
@@ -644,8 +650,8 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
         __builtin_amdgcn_global_load_lds((gbl_vptr)(asrc[j] + k0),
                                          (lds_vptr)(base + (8 * j + wave) * 1024), 16, 0, 0);
 #pragma unroll
-    for (int j = 0; j < B_LD; ++j)
-      __builtin_amdgcn_global_load_lds((gbl_vptr)(bsrc[j] + k0),
+    for (int j = 0; j < B_LD; ++j)  // tile layout: each stage's block is the next 1 KB (512 elements)
+      __builtin_amdgcn_global_load_lds((gbl_vptr)(bsrc[j] + (PK ? stage * 512 : k0)),
                                        (lds_vptr)(base + A_BYTES + (8 * j + wave) * 1024), 16, 0, 0);
   };
   const int fr = lane & 15, fc = lane >> 4;
@@ -654,8 +660,9 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
     const uint8_t* sa = ring + (stage % NS) * STAGE;
     const uint8_t* sb = sa + A_BYTES;
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
-      wf[j] = *reinterpret_cast<const bf16x8*>(sb + swz32(wn * TN + j * 16 + fr, fc));
+    for (int j = 0; j < FN; ++j)  // tile layout: block (wn * TN + 16 j) / 16 holds lane l's fragment at 16 l
+      wf[j] = *reinterpret_cast<const bf16x8*>(
+          sb + (PK ? (wn * TN / 16 + j) * 1024 + 16 * lane : swz32(wn * TN + j * 16 + fr, fc)));
 #pragma unroll
     for (int i = 0; i < FM; ++i)
       af[i] = *reinterpret_cast<const bf16x8*>(sa + swz32(wm * TM + i * 16 + fr, fc));
@@ -951,7 +958,7 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
   constexpr int CS = 4 / KSPLIT;  // channel slices per workgroup
   static_assert(4 % KSPLIT == 0, "KSPLIT divides the 4 waves");
   static_assert(EPI != EPI_SWIGLU || TNW == 2 || TNW == 4, "SwiGLU slices pair gate and up tiles");
-  static_assert(!PK || FMT == SMOE_BF16, "the decode tile layout holds bf16 weights");
+  static_assert(!PK || FMT == SMOE_BF16, "the weight tile layout holds bf16 weights");
   __shared__ f32x4 red[KSPLIT > 1 ? 4 : 1][TNW * RT][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int q = lane >> 4, l16 = lane & 15;
@@ -978,7 +985,7 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
     wrow[t] = reinterpret_cast<const uint8_t*>(p.W) +
               (g * p.w_gstride + static_cast<int64_t>(n) * p.ldw) * ESZ2 / 2;
   }
-  // decode tile layout: tile t's 64-k step st is the 2 KB block
+  // weight tile layout: tile t's 64-k step st is the 2 KB block
   // (g * N_out/16 + t) * K/64 + st, lane l's fragments at 16 l and 1 KB + 16 l
   const uint8_t* wtile[TNW];
   if constexpr (PK) {
@@ -1439,11 +1446,11 @@ __global__ __launch_bounds__(256) void k_gemm_f32(const GemmArgs p) {
   }
 }
 
-// ------------------------------------------------- decode tile layout ----
+// ------------------------------------------------- weight tile layout ----
 // out[(((g*T + t)*S + s)*2 + h)*64 + l][e] = w[g][16t + l%16][64s + 32h + 8(l/16) + e]
 // (T = N/16, S = K/64): one thread per 16-byte fragment, 16-byte reads from
 // the row-major weights, contiguous writes.
-__global__ __launch_bounds__(256) void k_pack_decode_tiles(const uint16_t* __restrict__ w,
+__global__ __launch_bounds__(256) void k_pack_weight_tiles(const uint16_t* __restrict__ w,
                                                           int64_t frags, int N, int K,
                                                           uint16_t* __restrict__ out) {
   const int64_t f = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
@@ -1459,11 +1466,11 @@ __global__ __launch_bounds__(256) void k_pack_decode_tiles(const uint16_t* __res
   *reinterpret_cast<u32x4*>(out + f * 8) = *reinterpret_cast<const u32x4*>(w + row * K + k);
 }
 
-int launch_pack_decode_tiles(const void* w, int G, int N, int K, void* out, hipStream_t s) {
+int launch_pack_weight_tiles(const void* w, int G, int N, int K, void* out, hipStream_t s) {
   if (!w || !out || G < 1 || N < 16 || K < 64 || N % 16 || K % 64) return SMOE_EINVAL;
   if (reinterpret_cast<uintptr_t>(w) % 16 || reinterpret_cast<uintptr_t>(out) % 16) return SMOE_EINVAL;
   const int64_t frags = static_cast<int64_t>(G) * N * K / 8;
-  hipLaunchKernelGGL(k_pack_decode_tiles, dim3(static_cast<unsigned>((frags + 255) / 256)), dim3(256),
+  hipLaunchKernelGGL(k_pack_weight_tiles, dim3(static_cast<unsigned>((frags + 255) / 256)), dim3(256),
                      0, s, reinterpret_cast<const uint16_t*>(w), frags, N, K,
                      reinterpret_cast<uint16_t*>(out));
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
@@ -1524,19 +1531,27 @@ int launch_ring(const GemmArgs& a, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 
-template <int NS, int GM, int BM>
-int launch_pp(const GemmArgs& a, hipStream_t s) {
+template <int NS, int GM, int BM, bool PK>
+int launch_pp_fmt(const GemmArgs& a, hipStream_t s) {
   const int tiles = max_tiles(a, BM) * ((a.N_out + 255) / 256);
   if (tiles == 0) return SMOE_OK;
   const dim3 grid(tiles), block(512);
   switch (a.epi) {
-    case EPI_ROWSCALE: SMOE_LAUNCH((k_gemm_pp<NS, GM, EPI_ROWSCALE, BM>), grid, block, 0, s, a); break;
-    case EPI_GELU: SMOE_LAUNCH((k_gemm_pp<NS, GM, EPI_GELU, BM>), grid, block, 0, s, a); break;
-    case EPI_SWIGLU: SMOE_LAUNCH((k_gemm_pp<NS, GM, EPI_SWIGLU, BM>), grid, block, 0, s, a); break;
-    case EPI_DOWN: SMOE_LAUNCH((k_gemm_pp<NS, GM, EPI_DOWN, BM>), grid, block, 0, s, a); break;
+    case EPI_ROWSCALE: SMOE_LAUNCH((k_gemm_pp<NS, GM, EPI_ROWSCALE, BM, PK>), grid, block, 0, s, a); break;
+    case EPI_GELU: SMOE_LAUNCH((k_gemm_pp<NS, GM, EPI_GELU, BM, PK>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU: SMOE_LAUNCH((k_gemm_pp<NS, GM, EPI_SWIGLU, BM, PK>), grid, block, 0, s, a); break;
+    case EPI_DOWN: SMOE_LAUNCH((k_gemm_pp<NS, GM, EPI_DOWN, BM, PK>), grid, block, 0, s, a); break;
     default: return SMOE_EINVAL;
   }
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
+// bf16 weights with a weight tile copy: the W operand's DMA reads each
+// 16-row x 32-k block as one contiguous 1 KB of lane-ordered fragments
+template <int NS, int GM, int BM>
+int launch_pp(const GemmArgs& a, hipStream_t s) {
+  return a.Wt && a.N_out % 16 == 0 ? launch_pp_fmt<NS, GM, BM, true>(a, s)
+                                   : launch_pp_fmt<NS, GM, BM, false>(a, s);
 }
 
 template <int BM, int BN>
@@ -1599,7 +1614,7 @@ int launch_decode(const GemmArgs& a, hipStream_t s) {
   const int ksplit = steps >= 12 ? 4 : (steps >= 6 ? 2 : 1);
   switch (a.fmt) {
     case SMOE_BF16:
-      if (a.Wt && a.N_out % 16 == 0)  // the decode tile layout: contiguous 1 KB loads
+      if (a.Wt && a.N_out % 16 == 0)  // the weight tile layout: contiguous 1 KB loads
         return rt == 1 ? launch_decode_split<SMOE_BF16, 1, true>(a, ksplit, s)
                        : launch_decode_split<SMOE_BF16, 2, true>(a, ksplit, s);
       return rt == 1 ? launch_decode_split<SMOE_BF16, 1>(a, ksplit, s)

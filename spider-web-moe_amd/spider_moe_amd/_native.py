@@ -71,7 +71,7 @@ SIGNATURES = {
     "smoe_expert_delta_workspace_bytes": (_sz, [ctypes.POINTER(SmoeExperts), _c_int, _c_int]),
     "smoe_expert_delta": (_c_int, [ctypes.POINTER(SmoeExperts), _vp, _vp, _vp, _c_int, _c_int,
                                    _vp, _c_int, _vp, _sz, _vp]),
-    "smoe_pack_decode_tiles": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp]),
+    "smoe_pack_weight_tiles": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp]),
     "smoe_profile_stages": (_c_int, [ctypes.c_uint32, ctypes.POINTER(_vp), _c_int]),
     "smoe_profile_count": (_c_int, [ctypes.POINTER(ctypes.c_int32), _c_int]),
     "smoe_events_create": (_c_int, [_c_int, ctypes.POINTER(_vp)]),

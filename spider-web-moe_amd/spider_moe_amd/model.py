@@ -98,10 +98,11 @@ class SpiderMoELayer(nn.Module):
         self._int4_b_up = None
         self._int4_b_down = None
         self._fp8 = None  # (codes_up, scale_up, codes_down, scale_down)
-        # bf16 weights also get a copy in the decode tile layout, which the
-        # decode weight stream (a few rows per group) reads with contiguous
-        # 1 KB loads; False saves that memory (same results either way)
-        self.decode_tiles = True
+        # bf16 weights also get a copy in the weight tile layout (lane-ordered
+        # MFMA fragments, 1 KB per 16 rows x 32 k), which the decode weight
+        # stream and the prefill GEMM read with contiguous 1 KB loads; False
+        # saves that memory (same results either way)
+        self.weight_tiles = True
         self._packed: _Packed | None = None
         self._packed_key = None
         self._ws: torch.Tensor | None = None
@@ -146,7 +147,7 @@ class SpiderMoELayer(nn.Module):
 
     # ----------------------------------------------------------- packing ----
     def _state_key(self):
-        return (self.expert_format, id(self._int4_w_up), id(self._fp8), self.decode_tiles,
+        return (self.expert_format, id(self._int4_w_up), id(self._fp8), self.weight_tiles,
                 tuple((p.data_ptr(), p._version, p.dtype) for p in self.parameters()))
 
     @torch.no_grad()
@@ -229,13 +230,13 @@ class SpiderMoELayer(nn.Module):
         ex.s_up, ex.s_down = nat.ptr(s_up), nat.ptr(s_down)
         ex.b_up, ex.b_down = nat.ptr(b_up), nat.ptr(b_down)
 
-        def tiles(w):  # bf16 copy in the decode tile layout (smoe_pack_decode_tiles)
-            if not self.decode_tiles or w.dtype != torch.bfloat16 or w.shape[1] % 16 or w.shape[2] % 64:
+        def tiles(w):  # bf16 copy in the weight tile layout (smoe_pack_weight_tiles)
+            if not self.weight_tiles or w.dtype != torch.bfloat16 or w.shape[1] % 16 or w.shape[2] % 64:
                 return None
             out = keep(torch.empty_like(w))
-            nat.check(lib.smoe_pack_decode_tiles(w.data_ptr(), w.shape[0], w.shape[1], w.shape[2],
+            nat.check(lib.smoe_pack_weight_tiles(w.data_ptr(), w.shape[0], w.shape[1], w.shape[2],
                                                  out.data_ptr(), nat.stream_of(dev)),
-                      "smoe_pack_decode_tiles")
+                      "smoe_pack_weight_tiles")
             return out
 
         if ex.format == nat.BF16:

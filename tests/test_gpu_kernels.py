@@ -173,21 +173,21 @@ def _experts_struct(n8, fmt, act, e, h, u, w_up, w_down, s_up=None, s_down=None,
 
 
 def _tiles(n8, w):
-    """bf16 [G,N,K] -> the decode tile layout through smoe_pack_decode_tiles."""
+    """bf16 [G,N,K] -> the weight tile layout through smoe_pack_weight_tiles."""
     out = torch.empty_like(w)
-    n8.check(n8.lib().smoe_pack_decode_tiles(w.data_ptr(), w.shape[0], w.shape[1], w.shape[2],
+    n8.check(n8.lib().smoe_pack_weight_tiles(w.data_ptr(), w.shape[0], w.shape[1], w.shape[2],
                                              out.data_ptr(), n8.stream_of(torch.device(dev))),
-             "pack_decode_tiles")
+             "pack_weight_tiles")
     torch.cuda.synchronize()
     return out
 
 
-def test_pack_decode_tiles_layout():
+def test_pack_weight_tiles_layout():
     """out[(((g*T + t)*S + s)*2 + h)*64 + l][e] = w[g][16t + l%16][64s + 32h + 8(l/16) + e]
     (include/smoe.h), checked element by element on a small case and as one
     permutation of the whole tensor."""
     n8 = nat()
-    say("pack decode tiles")
+    say("pack weight tiles")
     g_, n_, k_ = 3, 48, 192
     w = torch.randn(g_, n_, k_, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).to(dev)
     got = _tiles(n8, w).cpu().view(-1, 8)
@@ -349,7 +349,7 @@ def test_decode_experts_match_oracle(fmt, act, shape):
                          up_d, dn_d, b_up=bu_d, b_down=bd_d, **kw)
     got = _run_delta(n8, ex, msg.to(dev), idx.to(torch.int32).to(dev), w.to(dev))
     torch.testing.assert_close(got, ref, rtol=1e-2, atol=1e-2)
-    if fmt == "bf16":  # the decode tile layout: the same fragments, so the same bits
+    if fmt == "bf16":  # the weight tile layout: the same fragments, so the same bits
         tu, td = _tiles(n8, up_d), _tiles(n8, dn_d)
         ex.w_up_tiles, ex.w_down_tiles = tu.data_ptr(), td.data_ptr()
         got_t = _run_delta(n8, ex, msg.to(dev), idx.to(torch.int32).to(dev), w.to(dev))
@@ -410,3 +410,9 @@ def test_large_bf16_experts_ragged_groups(act, u, n):
                          wu_dev, wd_dev, b_up=bu_d, b_down=bd_d)
     got = _run_delta(n8, ex, msg.to(dev), idx.to(torch.int32).to(dev), w.to(dev))
     torch.testing.assert_close(got, ref, rtol=1e-2, atol=1e-2)
+    # the ping-pong kernel with its W operand read from the weight tile copy
+    # (lane-ordered 1 KB fragment blocks): the same fragments, the same bits
+    tu, td = _tiles(n8, wu_dev), _tiles(n8, wd_dev)
+    ex.w_up_tiles, ex.w_down_tiles = tu.data_ptr(), td.data_ptr()
+    got_t = _run_delta(n8, ex, msg.to(dev), idx.to(torch.int32).to(dev), w.to(dev))
+    assert torch.equal(got_t, got)

@@ -96,12 +96,12 @@ def test_invalid_block_is_rejected_without_launch(nat, bad):
     assert lib.smoe_last_error()
 
 
-def test_pack_decode_tiles_rejects_bad_shapes(nat):
+def test_pack_weight_tiles_rejects_bad_shapes(nat):
     lib = nat.lib()
     for g, n, k in [(0, 16, 64), (1, 10, 64), (1, 16, 100), (1, 8, 64)]:
-        assert lib.smoe_pack_decode_tiles(0x1000, g, n, k, 0x2000, None) == 1
-    assert lib.smoe_pack_decode_tiles(None, 1, 16, 64, 0x2000, None) == 1
-    assert lib.smoe_pack_decode_tiles(0x1008, 1, 16, 64, 0x2000, None) == 1  # 16-byte alignment
+        assert lib.smoe_pack_weight_tiles(0x1000, g, n, k, 0x2000, None) == 1
+    assert lib.smoe_pack_weight_tiles(None, 1, 16, 64, 0x2000, None) == 1
+    assert lib.smoe_pack_weight_tiles(0x1008, 1, 16, 64, 0x2000, None) == 1  # 16-byte alignment
 
 
 def test_capacity_and_range_errors(nat):
