@@ -1747,13 +1747,13 @@ int device_cus() {
   return cus[dev];
 }
 
-// 320- or 256-row ping-pong tiles for groups of >= 512 rows and K >= 2048:
-// the estimated tile count (each group's last tile partial) in rounds of one
-// workgroup per CU, a 320-row round costing 1.15 256-row rounds (measured at
-// 2048-row groups, K 2816).  The taller tile wins where it saves a round
-// (C1 down: 576 tiles = 3 rounds at 256 rows, 448 = 2 at 320).  At K 1024
-// and 1408 its two-pass epilogue weighs more and it measured slower even
-// where it saves a round (C1 / C3 edge and up, C3 down).
+// 320- or 256-row ping-pong tiles for groups of >= 512 rows: the estimated
+// tile count (each group's last tile partial) in rounds of one workgroup per
+// CU, a 320-row round costing 1.15 256-row rounds (measured at 2048-row
+// groups, K 2816, and with the SwiGLU epilogue at K 1024: C1 up 393 -> 383 us
+// per launch).  A 320-row tile's output is staged in two passes unless it is
+// SwiGLU's half-width one; at K 1024 / 1408 that second pass outweighs the
+// saved round (C1 edge 134 -> 157 us, C3 down and edge slower too).
 bool pp_rows_320(const GemmArgs& a, int rpg) {
   const int cus = device_cus();
   if (cus <= 0) return false;
@@ -1826,7 +1826,9 @@ int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
     if (a.N_out % 256 == 0) {
       if (rpg > 256 && rpg <= 320) return launch_pp<4, 4, 320>(a, s);
       if (rpg < 512) return launch_pp<3, 4, 128>(a, s);
-      return a.K >= 2048 && pp_rows_320(a, rpg) ? launch_pp<4, 4, 320>(a, s)
+      // 320-row tiles where they save rounds and either K is long or the
+      // SwiGLU output (half the channels) is staged in one pass
+      return (a.K >= 2048 || a.epi == EPI_SWIGLU) && pp_rows_320(a, rpg) ? launch_pp<4, 4, 320>(a, s)
                                                 : launch_pp<4, 4, 256>(a, s);
     }
     if (a.N_out % 128 == 0) return launch_ring<128, 3, 4>(a, s);
