@@ -591,11 +591,16 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
   constexpr int A_HI = A_INS % 8 == 0 ? 8 : A_INS % 8;   // waves issuing A_LD of them
   constexpr int LD = A_LD + B_LD, LD_LO = (A_INS / 8) + B_LD;
   constexpr int OUT_BYTES = BM * ((EPI == EPI_SWIGLU) ? BN / 2 : BN) * 2;
-  constexpr int PASSES = OUT_BYTES <= NS * STAGE ? 1 : 2;
+  // the ring also stages the output tile: sized for one staging pass when the
+  // 160 KB of LDS allow it (320 x 256 bf16 is exactly 160 KB; two passes
+  // through the 144 KB ring cost a barrier and a half-idle store phase)
+  constexpr int RING = NS * STAGE > OUT_BYTES ? NS * STAGE : OUT_BYTES;
+  static_assert(RING <= 163840, "LDS of one workgroup");
+  constexpr int PASSES = OUT_BYTES <= RING ? 1 : 2;
   static_assert(NS >= 2, "ring depth");
   static_assert(BM == 128 || BM == 256 || BM == 320, "block rows");
   static_assert(OUT_BYTES <= 2 * NS * STAGE, "output staging fits in the ring in two passes");
-  __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE];
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[RING];
 
   int g, m0, mrows, n0;
   if (!big_tile<BM, BN, GM>(p, g, m0, mrows, n0)) return;  // workgroup-uniform
@@ -1751,9 +1756,10 @@ int device_cus() {
 // tile count (each group's last tile partial) in rounds of one workgroup per
 // CU, a 320-row round costing 1.15 256-row rounds (measured at 2048-row
 // groups, K 2816, and with the SwiGLU epilogue at K 1024: C1 up 393 -> 383 us
-// per launch).  A 320-row tile's output is staged in two passes unless it is
-// SwiGLU's half-width one; at K 1024 / 1408 that second pass outweighs the
-// saved round (C1 edge 134 -> 157 us, C3 down and edge slower too).
+// per launch; C3 down, K 1408: 0.928 -> 0.895 ms per step).  The edge
+// projections (C1 / C3, K 1024) measured slower with 320 rows (C1 124 ->
+// 143 us per launch): their worst-case rows per group (N*S / E) overstate the
+// real ones, so the estimate picks 320 where 256 already had few rounds.
 bool pp_rows_320(const GemmArgs& a, int rpg) {
   const int cus = device_cus();
   if (cus <= 0) return false;
@@ -1826,9 +1832,9 @@ int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
     if (a.N_out % 256 == 0) {
       if (rpg > 256 && rpg <= 320) return launch_pp<4, 4, 320>(a, s);
       if (rpg < 512) return launch_pp<3, 4, 128>(a, s);
-      // 320-row tiles where they save rounds and either K is long or the
-      // SwiGLU output (half the channels) is staged in one pass
-      return (a.K >= 2048 || a.epi == EPI_SWIGLU) && pp_rows_320(a, rpg) ? launch_pp<4, 4, 320>(a, s)
+      // 320-row tiles where they save rounds, except for the edge projection
+      // (EPI_ROWSCALE), whose worst-case row count overstates its groups
+      return a.epi != EPI_ROWSCALE && pp_rows_320(a, rpg) ? launch_pp<4, 4, 320>(a, s)
                                                 : launch_pp<4, 4, 256>(a, s);
     }
     if (a.N_out % 128 == 0) return launch_ring<128, 3, 4>(a, s);
