@@ -440,7 +440,7 @@ __device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F
 typedef __attribute__((address_space(3))) void* lds_vptr;
 typedef __attribute__((address_space(1))) void* gbl_vptr;
 
-template <int BN, int NS, int GM, int EPI>
+template <int BN, int NS, int GM, int EPI, bool PK = false>
 // A ring of 3 stages (72 KB of LDS at BN = 128) lets two workgroups share a
 // CU (registers are held to 256 per lane by the launch bound), so one's
 // epilogue math and DMA waits overlap the other's MFMAs.
@@ -478,8 +478,15 @@ __global__ __launch_bounds__(256, NS <= 3 ? 2 : 1) void k_gemm_ring(const GemmAr
 #pragma unroll
     for (int j = 0; j < B_LD; ++j) {
       const int r = (4 * j + wave) * 16 + pr;
-      const int n = n0 + r < p.N_out ? n0 + r : n0;
-      bsrc[j] = W + static_cast<int64_t>(n) * p.ldw + ((pc ^ ((r >> 1) & 3)) << 3);
+      if constexpr (PK) {  // weight tile layout: 16 rows x 32 k = 1 KB of lane-ordered fragments
+        const int r0 = n0 + (4 * j + wave) * 16;
+        const int tile = (r0 < p.N_out ? r0 : n0) >> 4;
+        bsrc[j] = reinterpret_cast<const uint16_t*>(p.Wt) +
+                  ((static_cast<int64_t>(g) * (p.N_out >> 4) + tile) * (p.K >> 5)) * 512 + 8 * lane;
+      } else {
+        const int n = n0 + r < p.N_out ? n0 + r : n0;
+        bsrc[j] = W + static_cast<int64_t>(n) * p.ldw + ((pc ^ ((r >> 1) & 3)) << 3);
+      }
     }
   }
   auto issue = [&](int stage) {  // DMA of K slice `stage` into ring slot stage % NS
@@ -490,8 +497,8 @@ __global__ __launch_bounds__(256, NS <= 3 ? 2 : 1) void k_gemm_ring(const GemmAr
       __builtin_amdgcn_global_load_lds((gbl_vptr)(asrc[j] + k0),
                                        (lds_vptr)(base + (4 * j + wave) * 1024), 16, 0, 0);
 #pragma unroll
-    for (int j = 0; j < B_LD; ++j)
-      __builtin_amdgcn_global_load_lds((gbl_vptr)(bsrc[j] + k0),
+    for (int j = 0; j < B_LD; ++j)  // tile layout: each stage's block is the next 1 KB
+      __builtin_amdgcn_global_load_lds((gbl_vptr)(bsrc[j] + (PK ? stage * 512 : k0)),
                                        (lds_vptr)(base + A_BYTES + (4 * j + wave) * 1024), 16, 0, 0);
   };
 
@@ -503,7 +510,8 @@ __global__ __launch_bounds__(256, NS <= 3 ? 2 : 1) void k_gemm_ring(const GemmAr
     const uint8_t* sb = sa + A_BYTES;
 #pragma unroll
     for (int j = 0; j < FN; ++j)
-      wf[j] = *reinterpret_cast<const bf16x8*>(sb + swz32(wn * TN + j * 16 + fr, fc));
+      wf[j] = *reinterpret_cast<const bf16x8*>(
+          sb + (PK ? (wn * TN / 16 + j) * 1024 + 16 * lane : swz32(wn * TN + j * 16 + fr, fc)));
 #pragma unroll
     for (int i = 0; i < FM; ++i)
       af[i] = *reinterpret_cast<const bf16x8*>(sa + swz32(wm * TM + i * 16 + fr, fc));
@@ -1520,20 +1528,27 @@ int launch_mfma(const GemmArgs& a, hipStream_t s) {
   }
 }
 
-template <int BN, int NS, int GM>
-int launch_ring(const GemmArgs& a, hipStream_t s) {
+template <int BN, int NS, int GM, bool PK>
+int launch_ring_fmt(const GemmArgs& a, hipStream_t s) {
   const int tiles = max_tiles(a, 256) * ((a.N_out + BN - 1) / BN);
   if (tiles == 0) return SMOE_OK;
   const dim3 grid(tiles), block(256);
   switch (a.epi) {
-    case EPI_F32_BIAS: SMOE_LAUNCH((k_gemm_ring<BN, NS, GM, EPI_F32_BIAS>), grid, block, 0, s, a); break;
-    case EPI_ROWSCALE: SMOE_LAUNCH((k_gemm_ring<BN, NS, GM, EPI_ROWSCALE>), grid, block, 0, s, a); break;
-    case EPI_GELU: SMOE_LAUNCH((k_gemm_ring<BN, NS, GM, EPI_GELU>), grid, block, 0, s, a); break;
-    case EPI_SWIGLU: SMOE_LAUNCH((k_gemm_ring<BN, NS, GM, EPI_SWIGLU>), grid, block, 0, s, a); break;
-    case EPI_DOWN: SMOE_LAUNCH((k_gemm_ring<BN, NS, GM, EPI_DOWN>), grid, block, 0, s, a); break;
+    case EPI_F32_BIAS: SMOE_LAUNCH((k_gemm_ring<BN, NS, GM, EPI_F32_BIAS, PK>), grid, block, 0, s, a); break;
+    case EPI_ROWSCALE: SMOE_LAUNCH((k_gemm_ring<BN, NS, GM, EPI_ROWSCALE, PK>), grid, block, 0, s, a); break;
+    case EPI_GELU: SMOE_LAUNCH((k_gemm_ring<BN, NS, GM, EPI_GELU, PK>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU: SMOE_LAUNCH((k_gemm_ring<BN, NS, GM, EPI_SWIGLU, PK>), grid, block, 0, s, a); break;
+    case EPI_DOWN: SMOE_LAUNCH((k_gemm_ring<BN, NS, GM, EPI_DOWN, PK>), grid, block, 0, s, a); break;
     default: return SMOE_EINVAL;
   }
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
+// bf16 weights with a weight tile copy: contiguous 1 KB weight-operand DMA
+template <int BN, int NS, int GM>
+int launch_ring(const GemmArgs& a, hipStream_t s) {
+  return a.Wt && a.N_out % 16 == 0 ? launch_ring_fmt<BN, NS, GM, true>(a, s)
+                                   : launch_ring_fmt<BN, NS, GM, false>(a, s);
 }
 
 template <int NS, int GM, int BM, bool PK>
