@@ -44,8 +44,8 @@ BOUND = {"c1": "mfma", "c2": "hbm", "c3": "mfma", "c4": "hbm"}
 # the up / gate GEMM kernel the launcher picks for each workload's shapes
 # (rows per expert, N_out, format); rocprof summaries under profiles/ name it too
 UP_KERNEL = {
-    "c1": "k_gemm_pp<4,4,SwiGLU,256> (bf16, 8-wave ping-pong, LDS-DMA ring)",
-    "c2": "k_gemm_decode<fp8,SwiGLU,4,1,4,3> (weight streaming, 3-step register ring per wave)",
+    "c1": "k_gemm_pp<4,4,SwiGLU,320> (bf16 weight tiles, 8-wave ping-pong, LDS-DMA ring)",
+    "c2": "k_gemm_decode<fp8,SwiGLU,4,1,2,3> (weight streaming, K split over 2 waves, 3-step register ring per wave)",
     "c3": "k_gemm_ring<128,3,4> (bf16 GELU, LDS-DMA ring, 2 workgroups/CU)",
     "c4": "k_gemm_stream<int4,GELU,6,3,2> (weight streaming, both operands by LDS-DMA ring, 2 workgroups/CU)",
 }

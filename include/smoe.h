@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define SMOE_ABI_VERSION 3
+#define SMOE_ABI_VERSION 4
 
 /* status codes (spider_kernels.h convention; see scalar.cpp:9,45,58) */
 #define SMOE_OK 0
@@ -82,10 +82,10 @@ typedef struct smoe_experts {
   const void* s_down;
   const float* b_up;
   const float* b_down;
-  /* optional (bf16 only, else ignored): w_up / w_down in the weight tile
-   * layout (smoe_pack_weight_tiles), read instead of them by the decode
-   * weight stream and as the ping-pong GEMM's weight operand; NULL to read
-   * the row-major weights (same results, bit for bit) */
+  /* optional (bf16 and fp8, else ignored): w_up / w_down in the weight
+   * tile layout (smoe_pack_weight_tiles), read instead of them by the decode
+   * weight stream and (bf16) as the ping-pong GEMM's weight operand; NULL to
+   * read the row-major weights (same results, bit for bit) */
   const void* w_up_tiles;
   const void* w_down_tiles;
 } smoe_experts;
@@ -231,21 +231,28 @@ SMOE_API int smoe_expert_delta(const smoe_experts* ex, const void* msg, const in
 #define SMOE_STAGE_FRONT_ROUTE 12 /* top-k, expert plan, top-m, destination plan */
 #define SMOE_NUM_STAGES 13
 
-/* Weight tile layout of bf16 weights w [G,N,K] (N % 16 == 0, K % 64 == 0),
- * same size: for group g, 16-row tile t, 64-wide K step s, half h and lane
- * l = 16q + r, the 8 elements e at
- *   out[((((g*(N/16) + t)*(K/64) + s)*2 + h)*64 + l)*8 + e]
- *     = w[g][16t + r][64s + 32h + 8q + e],
- * i.e. each 16-row x 32-k block is 1 KB holding, lane by lane, the 16-byte
+/* Weight tile layout of weights w [G,N,K] (format SMOE_BF16 or
+ * SMOE_FP8_E4M3 codes; N % 16 == 0, K % 64 == 0), same size.  Rows are cut
+ * into 64-byte pieces; for group g, 16-row tile t, piece c and lane
+ * l = 16q + r, the 16 bytes j at
+ *   out_bytes[(((g*(N/16) + t)*C + c)*64 + l)*16 + j]
+ *     = row_bytes(w[g][16t + r])[64c + 16q + j],      C = K x elt size / 64.
+ * In elements, bf16:  out[((((g*(N/16) + t)*(K/64) + s)*2 + h)*64 + l)*8 + e]
+ *                       = w[g][16t + r][64s + 32h + 8q + e];
+ *              fp8:   out[(((g*(N/16) + t)*(K/64) + s)*64 + l)*16 + e]
+ *                       = w[g][16t + r][64s + 16q + e].
+ * Each 16-row x 64-byte block is 1 KB holding, lane by lane, the 16-byte
  * MFMA fragments a wave loads, and a tile's blocks follow one another along
  * K.  The decode weight stream reads a block with one contiguous 1 KB load
  * instead of sixteen 64-byte row pieces a row pitch apart, and the
- * ping-pong GEMM copies it into LDS as is (its fragment reads need no
- * swizzle).  Measured: C2 0.390 -> 0.377 ms per step, C1 5.25 -> 5.09, C3
- * 4.00 -> 3.93, C4 1.90 -> 1.80 (C4's 537 MB edge projection 178 -> 156 us).
- * No counterpart in the reference (its weights stay nn.Linear row-major);
- * the row-major weights remain the format every other kernel reads. */
-SMOE_API int smoe_pack_weight_tiles(const void* w, int G, int N, int K, void* out, void* stream);
+ * ping-pong GEMM copies bf16 blocks into LDS as they are (its fragment
+ * reads need no swizzle).  Measured (bf16): C2 0.390 -> 0.377 ms per step,
+ * C1 5.25 -> 5.09, C3 4.00 -> 3.93, C4 1.90 -> 1.80 (C4's 537 MB edge
+ * projection 178 -> 156 us).  No counterpart in the reference (its weights
+ * stay nn.Linear row-major); the row-major weights remain the format every
+ * other kernel reads.  Returns -2 for other formats. */
+SMOE_API int smoe_pack_weight_tiles(const void* w, int format, int G, int N, int K, void* out,
+                                    void* stream);
 
 /* When `events` is not NULL, every later smoe_block_forward records
  * events[2*i] before and events[2*i+1] after the i-th launch of a stage in

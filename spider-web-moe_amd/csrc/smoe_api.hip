@@ -241,7 +241,7 @@ int run_experts(const smoe_experts& ex, const void* msg, const int32_t* off, con
   up.lda = H;
   up.a_rows = rows;
   up.W = ex.w_up;
-  up.Wt = ex.format == SMOE_BF16 ? ex.w_up_tiles : nullptr;
+  up.Wt = ex.format == SMOE_BF16 || ex.format == SMOE_FP8_E4M3 ? ex.w_up_tiles : nullptr;
   up.w_gstride = static_cast<int64_t>(nup) * H;
   up.ldw = H;
   up.S = ex.s_up;
@@ -267,7 +267,7 @@ int run_experts(const smoe_experts& ex, const void* msg, const int32_t* off, con
   dn.lda = U;
   dn.a_rows = nullptr;  // act rows are already in plan order
   dn.W = ex.w_down;
-  dn.Wt = ex.format == SMOE_BF16 ? ex.w_down_tiles : nullptr;
+  dn.Wt = ex.format == SMOE_BF16 || ex.format == SMOE_FP8_E4M3 ? ex.w_down_tiles : nullptr;
   dn.w_gstride = static_cast<int64_t>(H) * U;
   dn.ldw = U;
   dn.S = ex.s_down;
@@ -491,8 +491,9 @@ SMOE_API int smoe_block_forward(const smoe_block* b, const void* h_in, const voi
   return SMOE_OK;
 }
 
-SMOE_API int smoe_pack_weight_tiles(const void* w, int G, int N, int K, void* out, void* stream) {
-  return hip_rc(launch_pack_weight_tiles(w, G, N, K, out, static_cast<hipStream_t>(stream)),
+SMOE_API int smoe_pack_weight_tiles(const void* w, int format, int G, int N, int K, void* out,
+                                    void* stream) {
+  return hip_rc(launch_pack_weight_tiles(w, format, G, N, K, out, static_cast<hipStream_t>(stream)),
                 "smoe_pack_weight_tiles");
 }
 

@@ -971,7 +971,8 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
   constexpr int CS = 4 / KSPLIT;  // channel slices per workgroup
   static_assert(4 % KSPLIT == 0, "KSPLIT divides the 4 waves");
   static_assert(EPI != EPI_SWIGLU || TNW == 2 || TNW == 4, "SwiGLU slices pair gate and up tiles");
-  static_assert(!PK || FMT == SMOE_BF16, "the weight tile layout holds bf16 weights");
+  static_assert(!PK || FMT != SMOE_INT4, "the weight tile layout holds bf16 or fp8 weights");
+  constexpr int BLK = 512 * ESZ2;  // bytes of one 64-k step of a 16-row tile
   __shared__ f32x4 red[KSPLIT > 1 ? 4 : 1][TNW * RT][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int q = lane >> 4, l16 = lane & 15;
@@ -998,15 +999,16 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
     wrow[t] = reinterpret_cast<const uint8_t*>(p.W) +
               (g * p.w_gstride + static_cast<int64_t>(n) * p.ldw) * ESZ2 / 2;
   }
-  // weight tile layout: tile t's 64-k step st is the 2 KB block
-  // (g * N_out/16 + t) * K/64 + st, lane l's fragments at 16 l and 1 KB + 16 l
+  // weight tile layout: tile t's 64-k step st is block (g * N_out/16 + t) *
+  // K/64 + st of BLK bytes, lane l's fragments at 16 l (fp8: 64 k) or at
+  // 16 l and 1 KB + 16 l (bf16: k 8q.. and 32 + 8q..)
   const uint8_t* wtile[TNW];
   if constexpr (PK) {
 #pragma unroll
     for (int t = 0; t < TNW; ++t) {
       const int tile = min(c0[t], p.N_out - 16) >> 4;
       wtile[t] = reinterpret_cast<const uint8_t*>(p.Wt) +
-                 (static_cast<int64_t>(g) * (p.N_out >> 4) + tile) * (p.K >> 6) * 2048 + 16 * lane;
+                 (static_cast<int64_t>(g) * (p.N_out >> 4) + tile) * (p.K >> 6) * BLK + 16 * lane;
     }
   }
   const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A);
@@ -1028,9 +1030,9 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
 #pragma unroll
     for (int t = 0; t < TNW; ++t) {
       if constexpr (PK) {
-        const uint8_t* blk = wtile[t] + static_cast<int64_t>(k0 >> 6) * 2048;
+        const uint8_t* blk = wtile[t] + static_cast<int64_t>(k0 >> 6) * BLK;
         wr[d][t].a = *reinterpret_cast<const u32x4*>(blk);
-        wr[d][t].b = *reinterpret_cast<const u32x4*>(blk + 1024);
+        if constexpr (FMT == SMOE_BF16) wr[d][t].b = *reinterpret_cast<const u32x4*>(blk + 1024);
       } else if constexpr (FMT == SMOE_BF16) {
         wr[d][t].a = *reinterpret_cast<const u32x4*>(wrow[t] + 2 * (k0 + 8 * q));
         wr[d][t].b = *reinterpret_cast<const u32x4*>(wrow[t] + 2 * (k0 + 32 + 8 * q));
@@ -1463,29 +1465,34 @@ __global__ __launch_bounds__(256) void k_gemm_f32(const GemmArgs p) {
 // out[(((g*T + t)*S + s)*2 + h)*64 + l][e] = w[g][16t + l%16][64s + 32h + 8(l/16) + e]
 // (T = N/16, S = K/64): one thread per 16-byte fragment, 16-byte reads from
 // the row-major weights, contiguous writes.
-__global__ __launch_bounds__(256) void k_pack_weight_tiles(const uint16_t* __restrict__ w,
-                                                          int64_t frags, int N, int K,
-                                                          uint16_t* __restrict__ out) {
+// One thread per 16-byte fragment f: block (g*T + t)*C + c (16 rows x 64
+// bytes of row bytes 64c..64c+63), lane l = 16q + r taking row r's bytes
+// 64c + 16q .. +15.  rb = bytes per row (K x element size).
+__global__ __launch_bounds__(256) void k_pack_weight_tiles(const uint8_t* __restrict__ w,
+                                                          int64_t frags, int N, int rb,
+                                                          uint8_t* __restrict__ out) {
   const int64_t f = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (f >= frags) return;
-  const int l = static_cast<int>(f & 63), h = static_cast<int>((f >> 6) & 1);
-  const int64_t blk = f >> 7;  // (g*T + t)*S + s
-  const int S = K / 64, T = N / 16;
-  const int st = static_cast<int>(blk % S);
-  const int64_t gt = blk / S;  // g*T + t
+  const int l = static_cast<int>(f & 63);
+  const int64_t blk = f >> 6;  // (g*T + t)*C + c
+  const int C = rb / 64, T = N / 16;
+  const int c = static_cast<int>(blk % C);
+  const int64_t gt = blk / C;  // g*T + t
   const int64_t g = gt / T, t = gt % T;
   const int64_t row = g * N + 16 * t + (l & 15);
-  const int k = 64 * st + 32 * h + 8 * (l >> 4);
-  *reinterpret_cast<u32x4*>(out + f * 8) = *reinterpret_cast<const u32x4*>(w + row * K + k);
+  *reinterpret_cast<u32x4*>(out + f * 16) =
+      *reinterpret_cast<const u32x4*>(w + row * rb + 64 * c + 16 * (l >> 4));
 }
 
-int launch_pack_weight_tiles(const void* w, int G, int N, int K, void* out, hipStream_t s) {
+int launch_pack_weight_tiles(const void* w, int fmt, int G, int N, int K, void* out, hipStream_t s) {
+  if (fmt != SMOE_BF16 && fmt != SMOE_FP8_E4M3) return SMOE_EUNSUPPORTED;
   if (!w || !out || G < 1 || N < 16 || K < 64 || N % 16 || K % 64) return SMOE_EINVAL;
   if (reinterpret_cast<uintptr_t>(w) % 16 || reinterpret_cast<uintptr_t>(out) % 16) return SMOE_EINVAL;
-  const int64_t frags = static_cast<int64_t>(G) * N * K / 8;
+  const int rb = fmt == SMOE_BF16 ? 2 * K : K;
+  const int64_t frags = static_cast<int64_t>(G) * N * rb / 16;
   hipLaunchKernelGGL(k_pack_weight_tiles, dim3(static_cast<unsigned>((frags + 255) / 256)), dim3(256),
-                     0, s, reinterpret_cast<const uint16_t*>(w), frags, N, K,
-                     reinterpret_cast<uint16_t*>(out));
+                     0, s, reinterpret_cast<const uint8_t*>(w), frags, N, rb,
+                     reinterpret_cast<uint8_t*>(out));
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 
@@ -1547,7 +1554,7 @@ int launch_ring_fmt(const GemmArgs& a, hipStream_t s) {
 // bf16 weights with a weight tile copy: contiguous 1 KB weight-operand DMA
 template <int BN, int NS, int GM>
 int launch_ring(const GemmArgs& a, hipStream_t s) {
-  return a.Wt && a.N_out % 16 == 0 ? launch_ring_fmt<BN, NS, GM, true>(a, s)
+  return a.Wt && a.fmt == SMOE_BF16 && a.N_out % 16 == 0 ? launch_ring_fmt<BN, NS, GM, true>(a, s)
                                    : launch_ring_fmt<BN, NS, GM, false>(a, s);
 }
 
@@ -1570,7 +1577,7 @@ int launch_pp_fmt(const GemmArgs& a, hipStream_t s) {
 // 16-row x 32-k block as one contiguous 1 KB of lane-ordered fragments
 template <int NS, int GM, int BM>
 int launch_pp(const GemmArgs& a, hipStream_t s) {
-  return a.Wt && a.N_out % 16 == 0 ? launch_pp_fmt<NS, GM, BM, true>(a, s)
+  return a.Wt && a.fmt == SMOE_BF16 && a.N_out % 16 == 0 ? launch_pp_fmt<NS, GM, BM, true>(a, s)
                                    : launch_pp_fmt<NS, GM, BM, false>(a, s);
 }
 
@@ -1617,12 +1624,16 @@ int launch_decode_split(const GemmArgs& a, int ksplit, hipStream_t s) {
 
 }  // namespace
 
+int device_cus();
+
 // Decode weight streams (few rows per group, N_out >= 128): 64 channels per
-// wave and K split over 4 waves wherever each part keeps >= 3 steps (C2's up,
-// down and edge GEMMs: 5632, 1024 and 1024 waves).  Measured at those shapes:
-// 64-channel slices beat 32-channel ones (half the activation loads per
-// weight byte), a split of 4 beats 2 and 1, and a ring of 3 steps is as fast
-// as 4 to 6.
+// wave and K split over the fewest waves (1, 2 or 4) that still give the
+// chip 8 waves per CU, each part keeping >= 3 steps.  C2's up GEMM (88 x 64
+// channels x 16 groups, K 1024) takes a split of 2: 19.9 us against 22.3 at
+// 4 and 23.7 at 1; its down and edge GEMMs (16 x 64 channels x 16 groups)
+// take 4: 11.3 us against 16.8 at 2.  64-channel slices beat 32-channel
+// ones (half the activation loads per weight byte), and a ring of 3 steps
+// beats 2 and 4.
 int launch_decode(const GemmArgs& a, hipStream_t s) {
   // 32-row tiles above 8 rows per group on average: routed groups are ragged,
   // and a group past its tile takes a second tile that streams the same
@@ -1631,7 +1642,15 @@ int launch_decode(const GemmArgs& a, hipStream_t s) {
   const int rpg = a.G == 0 ? a.single_rows : a.max_rows / a.G;
   const int rt = rpg <= 8 ? 1 : 2;
   const int steps = a.K / 64;
-  const int ksplit = steps >= 12 ? 4 : (steps >= 6 ? 2 : 1);
+  // waves per split: 64-channel strips x row tiles (every group of a dispatch
+  // holds at least one tile, ragged groups rarely more at these sizes)
+  const int tiles = a.G == 0 ? (a.single_rows + 16 * rt - 1) / (16 * rt)
+                             : max(min(a.G, a.max_rows), (a.max_rows + 16 * rt - 1) / (16 * rt));
+  const long long strips = (long long)((a.N_out + 63) / 64) * tiles;
+  const int cus = device_cus();
+  const long long want = 8LL * (cus > 0 ? cus : 256);
+  int ksplit = 1;
+  while (ksplit < 4 && strips * ksplit < want && steps / (2 * ksplit) >= 3) ksplit *= 2;
   switch (a.fmt) {
     case SMOE_BF16:
       if (a.Wt && a.N_out % 16 == 0)  // the weight tile layout: contiguous 1 KB loads
@@ -1640,6 +1659,9 @@ int launch_decode(const GemmArgs& a, hipStream_t s) {
       return rt == 1 ? launch_decode_split<SMOE_BF16, 1>(a, ksplit, s)
                      : launch_decode_split<SMOE_BF16, 2>(a, ksplit, s);
     case SMOE_FP8_E4M3:
+      if (a.Wt && a.N_out % 16 == 0)
+        return rt == 1 ? launch_decode_split<SMOE_FP8_E4M3, 1, true>(a, ksplit, s)
+                       : launch_decode_split<SMOE_FP8_E4M3, 2, true>(a, ksplit, s);
       return rt == 1 ? launch_decode_split<SMOE_FP8_E4M3, 1>(a, ksplit, s)
                      : launch_decode_split<SMOE_FP8_E4M3, 2>(a, ksplit, s);
     case SMOE_INT4:

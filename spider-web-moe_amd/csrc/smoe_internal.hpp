@@ -43,7 +43,7 @@ struct GemmArgs {
   int lda = 0;                   // elements
   const int32_t* a_rows = nullptr;  // plan row -> A row; nullptr = identity
   const void* W = nullptr;
-  const void* Wt = nullptr;      // bf16: W in the weight tile layout (or nullptr)
+  const void* Wt = nullptr;      // bf16 / fp8: W in the weight tile layout (or nullptr)
   int64_t w_gstride = 0;         // elements between groups
   int ldw = 0;                   // elements between rows of W
   const void* S = nullptr;       // fp8: f32 [G, N_out]; int4: [G, N_out, K/gs]
@@ -70,8 +70,8 @@ struct GemmArgs {
 };
 
 int launch_grouped_gemm(const GemmArgs& a, hipStream_t s);
-// bf16 w [G,N,K] -> the weight tile layout (smoe_pack_weight_tiles)
-int launch_pack_weight_tiles(const void* w, int G, int N, int K, void* out, hipStream_t s);
+// bf16 / fp8 w [G,N,K] -> the weight tile layout (smoe_pack_weight_tiles)
+int launch_pack_weight_tiles(const void* w, int fmt, int G, int N, int K, void* out, hipStream_t s);
 // One bf16 GEMM over a few rows (G == 0, single_rows <= 64) with f32 logits
 // out (EPI_F32_BIAS) from two weight segments: the router and all edge
 // generator rows of a small decode step in one pass.

@@ -230,16 +230,21 @@ class SpiderMoELayer(nn.Module):
         ex.s_up, ex.s_down = nat.ptr(s_up), nat.ptr(s_down)
         ex.b_up, ex.b_down = nat.ptr(b_up), nat.ptr(b_down)
 
-        def tiles(w):  # bf16 copy in the weight tile layout (smoe_pack_weight_tiles)
-            if not self.weight_tiles or w.dtype != torch.bfloat16 or w.shape[1] % 16 or w.shape[2] % 64:
+        def tiles(w, code=nat.BF16):  # copy in the weight tile layout (smoe_pack_weight_tiles)
+            if not self.weight_tiles or w.shape[1] % 16 or w.shape[2] % 64:
+                return None
+            if w.dtype != (torch.bfloat16 if code == nat.BF16 else torch.uint8):
                 return None
             out = keep(torch.empty_like(w))
-            nat.check(lib.smoe_pack_weight_tiles(w.data_ptr(), w.shape[0], w.shape[1], w.shape[2],
-                                                 out.data_ptr(), nat.stream_of(dev)),
+            nat.check(lib.smoe_pack_weight_tiles(w.data_ptr(), code, w.shape[0], w.shape[1],
+                                                 w.shape[2], out.data_ptr(), nat.stream_of(dev)),
                       "smoe_pack_weight_tiles")
             return out
 
-        if ex.format == nat.BF16:
+        if ex.format == nat.FP8_E4M3:
+            ex.w_up_tiles = nat.ptr(tiles(w_up, nat.FP8_E4M3))
+            ex.w_down_tiles = nat.ptr(tiles(w_down, nat.FP8_E4M3))
+        elif ex.format == nat.BF16:
             ex.w_up_tiles = nat.ptr(tiles(w_up))
             ex.w_down_tiles = nat.ptr(tiles(w_down))
 

@@ -172,11 +172,14 @@ def _experts_struct(n8, fmt, act, e, h, u, w_up, w_down, s_up=None, s_down=None,
     return ex
 
 
-def _tiles(n8, w):
-    """bf16 [G,N,K] -> the weight tile layout through smoe_pack_weight_tiles."""
+def _tiles(n8, w, code=None):
+    """bf16 (or fp8 codes, code FP8_E4M3) [G,N,K] -> the weight tile layout
+    through smoe_pack_weight_tiles."""
     out = torch.empty_like(w)
-    n8.check(n8.lib().smoe_pack_weight_tiles(w.data_ptr(), w.shape[0], w.shape[1], w.shape[2],
-                                             out.data_ptr(), n8.stream_of(torch.device(dev))),
+    code = n8.BF16 if code is None else code
+    n8.check(n8.lib().smoe_pack_weight_tiles(w.data_ptr(), code, w.shape[0], w.shape[1],
+                                             w.shape[2], out.data_ptr(),
+                                             n8.stream_of(torch.device(dev))),
              "pack_weight_tiles")
     torch.cuda.synchronize()
     return out
@@ -201,6 +204,33 @@ def test_pack_weight_tiles_layout():
         assert torch.equal(got[f], ref), (g, t, s, h, l)
     perm = wc.view(g_, t_, 16, s_, 2, 4, 8).permute(0, 1, 3, 4, 5, 2, 6).reshape(-1, 8)
     assert torch.equal(got, perm)
+
+
+def test_pack_weight_tiles_layout_fp8():
+    """fp8 codes: out[((g*T + t)*S + s)*64 + l][e] = w[g][16t + l%16][64s + 16(l/16) + e]
+    (include/smoe.h), element by element and as one permutation; int4 and
+    f32 are refused."""
+    n8 = nat()
+    say("pack weight tiles fp8")
+    g_, n_, k_ = 2, 32, 320
+    w = torch.randint(0, 256, (g_, n_, k_), dtype=torch.uint8,
+                      generator=torch.Generator().manual_seed(6)).to(dev)
+    got = _tiles(n8, w, n8.FP8_E4M3).cpu().view(-1, 16)
+    wc = w.cpu()
+    t_, s_ = n_ // 16, k_ // 64
+    rng = np.random.default_rng(10)
+    for _ in range(200):
+        g, t, s, l = (int(rng.integers(0, x)) for x in (g_, t_, s_, 64))
+        f = ((g * t_ + t) * s_ + s) * 64 + l
+        ref = wc[g, 16 * t + l % 16, 64 * s + 16 * (l // 16): 64 * s + 16 * (l // 16) + 16]
+        assert torch.equal(got[f], ref), (g, t, s, l)
+    perm = wc.view(g_, t_, 16, s_, 4, 16).permute(0, 1, 3, 4, 2, 5).reshape(-1, 16)
+    assert torch.equal(got, perm)
+    out = torch.empty_like(w)
+    for code in (n8.INT4, n8.F32):
+        rc = n8.lib().smoe_pack_weight_tiles(w.data_ptr(), code, g_, n_, k_, out.data_ptr(),
+                                             n8.stream_of(torch.device(dev)))
+        assert rc == -2
 
 
 def _run_delta(n8, ex, msg_bf16, idx, w):
@@ -279,17 +309,18 @@ def test_int4_experts_match_oracle(group, sdt):
     assert (got - ref).abs().max() < max(float(env), 1e-3)
 
 
-@pytest.mark.parametrize("shape", [(24, 384, 640, 8), (60, 384, 640, 8), (40, 768, 1664, 4)])
+@pytest.mark.parametrize("shape", [(24, 384, 640, 8), (60, 384, 640, 8), (40, 768, 1664, 4),
+                                   (20, 256, 640, 8)])
 @pytest.mark.parametrize("fmt,act", [("bf16", "gelu"), ("bf16", "swiglu"), ("fp8", "gelu"),
                                      ("fp8", "swiglu"), ("int4-g32-f32", "gelu"),
                                      ("int4-g128-f16", "gelu")])
 def test_decode_experts_match_oracle(fmt, act, shape):
     """Decode shapes (a few rows per expert) take the weight-streaming GEMM,
-    K split over 2 or 4 waves with ragged parts: up K = 384 (6 steps of 64)
-    and 768 (12), down K = 640 (10) and 1664 (26: parts of 6 and 7 steps,
-    so the ring's main loop runs); 16-row tiles (6 rows per expert on
-    average) and 32-row tiles (15 and 20); an expert with more rows than one
-    tile holds, an empty expert, a one-row expert."""
+    K split over 1, 2 or 4 waves with ragged parts: up K = 256 (4 steps of
+    64: no split), 384 (6) and 768 (12), down K = 640 (10) and 1664 (26:
+    parts of 6 and 7 steps, so the ring's main loop runs); 16-row tiles (6
+    rows per expert on average) and 32-row tiles (15 and 20); an expert with
+    more rows than one tile holds, an empty expert, a one-row expert."""
     from spider_moe_amd.quant import interleave_gate_up, interleave_gate_up_rows, quantize_int4
     n8 = nat()
     say("decode experts", fmt, act, shape)
@@ -349,8 +380,8 @@ def test_decode_experts_match_oracle(fmt, act, shape):
                          up_d, dn_d, b_up=bu_d, b_down=bd_d, **kw)
     got = _run_delta(n8, ex, msg.to(dev), idx.to(torch.int32).to(dev), w.to(dev))
     torch.testing.assert_close(got, ref, rtol=1e-2, atol=1e-2)
-    if fmt == "bf16":  # the weight tile layout: the same fragments, so the same bits
-        tu, td = _tiles(n8, up_d), _tiles(n8, dn_d)
+    if fmt in ("bf16", "fp8"):  # the weight tile layout: the same fragments, so the same bits
+        tu, td = _tiles(n8, up_d, code), _tiles(n8, dn_d, code)
         ex.w_up_tiles, ex.w_down_tiles = tu.data_ptr(), td.data_ptr()
         got_t = _run_delta(n8, ex, msg.to(dev), idx.to(torch.int32).to(dev), w.to(dev))
         assert torch.equal(got_t, got)
@@ -379,7 +410,7 @@ def test_large_bf16_experts_ragged_groups(act, u, n):
     multiples of 128) the 256 x 128 ring kernel.  With n = 1536 / 1100 (384 /
     275 rows per expert; groups of 0, 1, ~100-400 and ~1000 rows) the
     ping-pong kernel takes 128-row tiles, with n = 1200 (300 rows per expert)
-    its 320-row tiles (the GELU output staged in two passes)."""
+    its 320-row tiles."""
     from spider_moe_amd.quant import interleave_gate_up
     n8 = nat()
     say("large bf16 experts", act, u, n)

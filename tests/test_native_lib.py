@@ -38,7 +38,7 @@ def test_exports_every_declared_symbol(nat):
 
 def test_identity(nat):
     lib = nat.lib()
-    assert lib.smoe_abi_version() == 3
+    assert lib.smoe_abi_version() == 4
     assert lib.smoe_backend_name() == b"hip-gfx950"
     assert lib.smoe_backend_caps() == 0b1111
 
@@ -99,9 +99,12 @@ def test_invalid_block_is_rejected_without_launch(nat, bad):
 def test_pack_weight_tiles_rejects_bad_shapes(nat):
     lib = nat.lib()
     for g, n, k in [(0, 16, 64), (1, 10, 64), (1, 16, 100), (1, 8, 64)]:
-        assert lib.smoe_pack_weight_tiles(0x1000, g, n, k, 0x2000, None) == 1
-    assert lib.smoe_pack_weight_tiles(None, 1, 16, 64, 0x2000, None) == 1
-    assert lib.smoe_pack_weight_tiles(0x1008, 1, 16, 64, 0x2000, None) == 1  # 16-byte alignment
+        for code in (nat.BF16, nat.FP8_E4M3):
+            assert lib.smoe_pack_weight_tiles(0x1000, code, g, n, k, 0x2000, None) == 1
+    assert lib.smoe_pack_weight_tiles(None, nat.BF16, 1, 16, 64, 0x2000, None) == 1
+    assert lib.smoe_pack_weight_tiles(0x1008, nat.BF16, 1, 16, 64, 0x2000, None) == 1  # alignment
+    for code in (nat.F32, nat.INT4, nat.F16):  # formats without a tile layout
+        assert lib.smoe_pack_weight_tiles(0x1000, code, 1, 16, 64, 0x2000, None) == -2
 
 
 def test_capacity_and_range_errors(nat):
