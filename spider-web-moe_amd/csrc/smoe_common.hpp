@@ -59,15 +59,25 @@ __device__ __forceinline__ u32x2 fp8x4_to_bf16x4(uint32_t w) {
 
 // ---------------------------------------------------------------- int4 ----
 // 8 signed nibbles of one u32 (element 2i in the low nibble of byte i) times
-// one scale -> 8 bf16 (RNE of q * s computed in fp32).
+// one scale -> 8 bf16 (RNE of q * s computed in fp32).  A nibble n holds
+// q = n - 16 [n >= 8]; u = n ^ 8 = q + 8 in 0..15 sits alone in a byte after
+// one xor and a mask (low nibbles) or a shift and a mask (high nibbles), is
+// widened by a byte-to-float conversion, and q * s = fma(u, s, -8 s) with one
+// rounding (-8 s is exact), the same bits as float(q) * s.  The empty asm
+// hides the masks from the optimizer, which would otherwise fold each byte
+// back into a bit-field extract ahead of a byte-0 conversion (two VALU
+// operations per element instead of one v_cvt_f32_ubyteN).
 __device__ __forceinline__ u32x4 int4x8_to_bf16x8(uint32_t w, float s) {
+  const uint32_t x = w ^ 0x88888888u;
+  uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
+  asm("" : "+v"(lo), "+v"(hi));
+  const float m = -8.f * s;
   u32x4 r;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int b = static_cast<int>((w >> (8 * i)) & 0xFFu);
-    const int lo = ((b & 0xF) ^ 8) - 8;
-    const int hi = (((b >> 4) & 0xF) ^ 8) - 8;
-    r[i] = pack_bf2(static_cast<float>(lo) * s, static_cast<float>(hi) * s);
+    const float fl = static_cast<float>((lo >> (8 * i)) & 0xFFu);
+    const float fh = static_cast<float>((hi >> (8 * i)) & 0xFFu);
+    r[i] = pack_bf2(__builtin_fmaf(fl, s, m), __builtin_fmaf(fh, s, m));
   }
   return r;
 }
