@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define SMOE_ABI_VERSION 4
+#define SMOE_ABI_VERSION 5
 
 /* status codes (spider_kernels.h convention; see scalar.cpp:9,45,58) */
 #define SMOE_OK 0
@@ -212,6 +212,48 @@ SMOE_API size_t smoe_expert_delta_workspace_bytes(const smoe_experts* ex, int N,
 SMOE_API int smoe_expert_delta(const smoe_experts* ex, const void* msg, const int32_t* idx,
                                const float* w, int N, int K, void* delta, int out_dtype,
                                void* workspace, size_t workspace_bytes, void* stream);
+
+/* Edge generator and per-source top-m (model.py:261-266) for the K selected
+ * sources of each token: x [N,H] act_dtype, edge_gen_w [E*E, ldw] act_dtype
+ * (its first H columns; ldw = H + L for the reference's [h; e_loop] input,
+ * ldw % 8 == 0), edge_bias f32 [E*E] = the loop's row of
+ * smoe_edge_loop_bias (b_g plus the loop-embedding half), src_idx i32
+ * [N,K] (a source listed twice is one source; ids outside [0, E): none)
+ * -> out_eidx i32 [N,K,M] (destinations by descending logit, ties to the
+ * lower index) and out_ew f32 [N,K,M] (their softmax weights), slot for
+ * slot with src_idx; -1 / 0 for slots without a source.  The same
+ * kernels as smoe_block_forward's stages 3-5. */
+SMOE_API size_t smoe_edge_topm_workspace_bytes(int N, int K, int E, int M);
+SMOE_API int smoe_edge_topm(const void* x, int act_dtype, int N, int H, const void* edge_gen_w,
+                            int ldw, const float* edge_bias, int E, int K, int M,
+                            const int32_t* src_idx, int32_t* out_eidx, float* out_ew,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/* Destination projections and message aggregation (model.py:271-288):
+ * msg[t] = sum over the token's distinct sources s in src_idx [N,K] and
+ * their edges j < M of ew[t,s,j] * edge_value_w[eidx[t,s,j]] x[t], with
+ * the weights of each destination added first (in ascending source order)
+ * so each (token, destination) projection is computed once.  x [N,H] and
+ * edge_value_w [E,H,H] act_dtype (edge_value_w_tiles: optional bf16 copy in
+ * the weight tile layout, or NULL), eidx i32 / ew f32 [N,K,M] as
+ * smoe_edge_topm writes them -> msg [N,H] in msg_dtype (SMOE_F32 or
+ * SMOE_BF16).  The same kernels as smoe_block_forward's stages 6-8. */
+SMOE_API size_t smoe_edge_message_workspace_bytes(int N, int H, int E, int K, int M,
+                                                  int act_dtype);
+SMOE_API int smoe_edge_message(const void* x, int act_dtype, int N, int H,
+                               const void* edge_value_w, const void* edge_value_w_tiles, int E,
+                               int K, int M, const int32_t* src_idx, const int32_t* eidx,
+                               const float* ew, void* msg, int msg_dtype, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
+/* Residual, re-injection and LayerNorm (model.py:317):
+ * out = LayerNorm(h + alpha * delta + beta * x0) over H (eps; ln_w / ln_b
+ * f32 [H] or NULL for 1 / 0).  h, x0, out [N,H] act_dtype; delta [N,H] in
+ * delta_dtype (SMOE_F32 or SMOE_BF16).  No workspace. */
+SMOE_API int smoe_combine_epilogue(const void* h, const void* x0, int act_dtype,
+                                   const void* delta, int delta_dtype, int N, int H, float alpha,
+                                   float beta, const float* ln_w, const float* ln_b, float eps,
+                                   void* out, void* stream);
 
 /* ---- diagnostics (no counterpart in the reference; used by bench.py) ----
  * Stage ids of smoe_block_forward, in launch order within a loop. */

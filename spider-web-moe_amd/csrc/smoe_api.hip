@@ -648,4 +648,212 @@ SMOE_API int smoe_expert_delta(const smoe_experts* ex, const void* msg, const in
   return SMOE_OK;
 }
 
+// ------------------------------------------------ stage entry points ----
+namespace {
+
+int check_act(int adt, int H) {
+  if (adt != SMOE_F32 && adt != SMOE_BF16) return fail(SMOE_EUNSUPPORTED, "act_dtype");
+  if (H <= 0 || H % 8 || H > 4096) return fail(SMOE_EINVAL, "H");
+  if (adt == SMOE_BF16 && H % 32) return fail(SMOE_EINVAL, "bf16 needs H % 32 == 0");
+  if (adt == SMOE_F32 && H % 16) return fail(SMOE_EINVAL, "fp32 needs H % 16 == 0");
+  return SMOE_OK;
+}
+
+int check_ekm(int E, int K, int M) {
+  if (E < 1 || E > 64) return fail(SMOE_EINVAL, "E must be in [1, 64]");
+  if (K < 1 || K > E || K > 16) return fail(SMOE_EINVAL, "top_k");
+  if (M < 1 || M > E || M > 16) return fail(SMOE_EINVAL, "edges_per_expert");
+  return SMOE_OK;
+}
+
+// workspace of smoe_edge_topm
+struct TopmWs {
+  size_t tok_e, tok_ew, cnt, acnt, off, rows, roww, tokrow, scratch, logit, eidx, ew, tok_d, tok_dc;
+  size_t total;
+};
+TopmWs topm_ws(int N, int K, int E, int M) {
+  const size_t n = N > 0 ? static_cast<size_t>(N) : 1;
+  const int S = E < K * M ? E : K * M;
+  TopmWs w;
+  Bump z;
+  w.tok_e = z.take(n * K * 4);
+  w.tok_ew = z.take(n * K * 4);
+  w.cnt = z.take(E * 4);
+  w.acnt = z.take(E * 4);
+  w.off = z.take((E + 1) * 4);
+  w.rows = z.take(n * K * 4);
+  w.roww = z.take(n * K * 4);
+  w.tokrow = z.take(n * K * 4);
+  w.scratch = z.take(plan_scratch_bytes(N, E));
+  w.logit = z.take(n * K * E * 4);
+  w.eidx = z.take(n * K * M * 4);
+  w.ew = z.take(n * K * M * 4);
+  w.tok_d = z.take(n * S * 4);
+  w.tok_dc = z.take(n * S * 4);
+  w.total = z.off;
+  return w;
+}
+
+// workspace of smoe_edge_message
+struct MsgWs {
+  size_t tok_d, tok_dc, cnt, acnt, off, rows, roww, tokrow, scratch, proj, total;
+};
+MsgWs msg_ws(int N, int H, int E, int K, int M, int adt) {
+  const size_t n = N > 0 ? static_cast<size_t>(N) : 1;
+  const int S = E < K * M ? E : K * M;
+  MsgWs w;
+  Bump z;
+  w.tok_d = z.take(n * S * 4);
+  w.tok_dc = z.take(n * S * 4);
+  w.cnt = z.take(E * 4);
+  w.acnt = z.take(E * 4);
+  w.off = z.take((E + 1) * 4);
+  w.rows = z.take(n * S * 4);
+  w.roww = z.take(n * S * 4);
+  w.tokrow = z.take(n * S * 4);
+  w.scratch = z.take(plan_scratch_bytes(N, E));
+  w.proj = z.take(n * S * H * esize(adt));
+  w.total = z.off;
+  return w;
+}
+
+}  // namespace
+
+SMOE_API size_t smoe_edge_topm_workspace_bytes(int N, int K, int E, int M) {
+  if (N < 0 || E < 1 || E > 64 || K < 1 || K > 16 || M < 1 || M > 16) return 0;
+  return topm_ws(N, K, E, M).total;
+}
+
+SMOE_API int smoe_edge_topm(const void* x, int act_dtype, int N, int H, const void* edge_gen_w,
+                            int ldw, const float* edge_bias, int E, int K, int M,
+                            const int32_t* src_idx, int32_t* out_eidx, float* out_ew, void* ws,
+                            size_t ws_bytes, void* stream) {
+  int rc = check_act(act_dtype, H);
+  if (rc != SMOE_OK) return rc;
+  rc = check_ekm(E, K, M);
+  if (rc != SMOE_OK) return rc;
+  if (N < 0 || ldw < H || ldw % 8) return fail(SMOE_EINVAL, "shape (ldw >= H, ldw % 8 == 0)");
+  if (N == 0) return SMOE_OK;
+  if (!x || !edge_gen_w || !edge_bias || !src_idx || !out_eidx || !out_ew || !ws)
+    return fail(SMOE_EINVAL, "null buffer");
+  const TopmWs l = topm_ws(N, K, E, M);
+  if (ws_bytes < l.total) return fail(SMOE_ECAPACITY, "workspace");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int S = E < K * M ? E : K * M;
+  // the token's sources: distinct, ascending, each weighing 1 (the edges of
+  // a source do not depend on its router weight)
+  SMOE_TRY(launch_merge_slots(src_idx, nullptr, N, K, E, 0, at<int32_t>(ws, l.tok_e),
+                              at<float>(ws, l.tok_ew), s),
+           "source slots");
+  SMOE_TRY(launch_plan(at<int32_t>(ws, l.tok_e), at<float>(ws, l.tok_ew), N, K, E, 0,
+                       at<int32_t>(ws, l.cnt), at<int32_t>(ws, l.acnt), at<int32_t>(ws, l.off),
+                       at<int32_t>(ws, l.rows), at<float>(ws, l.roww), at<int32_t>(ws, l.tokrow),
+                       at<void>(ws, l.scratch), s),
+           "source plan");
+  GemmArgs eg;
+  eg.fmt = act_dtype == SMOE_F32 ? SMOE_F32 : SMOE_BF16;
+  eg.epi = EPI_F32_BIAS;
+  eg.A = x;
+  eg.lda = H;
+  eg.a_rows = at<int32_t>(ws, l.rows);
+  eg.W = edge_gen_w;
+  eg.w_gstride = static_cast<int64_t>(E) * ldw;
+  eg.ldw = ldw;
+  eg.K = H;
+  eg.N_out = E;
+  eg.grp_off = at<int32_t>(ws, l.off);
+  eg.G = E;
+  eg.max_rows = N * K;
+  eg.out = at<float>(ws, l.logit);
+  eg.ldo = E;
+  eg.bias = edge_bias;
+  eg.bias_gstride = E;
+  SMOE_TRY(launch_grouped_gemm(eg, s), "edge-logit GEMM");
+  SMOE_TRY(launch_edge_topm(at<float>(ws, l.logit), at<int32_t>(ws, l.tok_e), at<int32_t>(ws, l.tokrow),
+                            N, E, K, M, S, at<int32_t>(ws, l.eidx), at<float>(ws, l.ew),
+                            at<int32_t>(ws, l.tok_d), at<float>(ws, l.tok_dc), s),
+           "edge top-m");
+  SMOE_TRY(launch_gather_topm(src_idx, at<int32_t>(ws, l.tok_e), at<int32_t>(ws, l.tokrow),
+                              at<int32_t>(ws, l.eidx), at<float>(ws, l.ew), N, K, M, out_eidx,
+                              out_ew, s),
+           "top-m gather");
+  return SMOE_OK;
+}
+
+SMOE_API size_t smoe_edge_message_workspace_bytes(int N, int H, int E, int K, int M,
+                                                  int act_dtype) {
+  if (N < 0 || H <= 0 || E < 1 || E > 64 || K < 1 || K > 16 || M < 1 || M > 16) return 0;
+  if (act_dtype != SMOE_F32 && act_dtype != SMOE_BF16) return 0;
+  return msg_ws(N, H, E, K, M, act_dtype).total;
+}
+
+SMOE_API int smoe_edge_message(const void* x, int act_dtype, int N, int H,
+                               const void* edge_value_w, const void* edge_value_w_tiles, int E,
+                               int K, int M, const int32_t* src_idx, const int32_t* eidx,
+                               const float* ew, void* msg, int msg_dtype, void* ws,
+                               size_t ws_bytes, void* stream) {
+  int rc = check_act(act_dtype, H);
+  if (rc != SMOE_OK) return rc;
+  rc = check_ekm(E, K, M);
+  if (rc != SMOE_OK) return rc;
+  if (msg_dtype != SMOE_F32 && msg_dtype != SMOE_BF16) return fail(SMOE_EUNSUPPORTED, "msg dtype");
+  if (N < 0) return fail(SMOE_EINVAL, "N");
+  if (N == 0) return SMOE_OK;
+  if (!x || !edge_value_w || !src_idx || !eidx || !ew || !msg || !ws)
+    return fail(SMOE_EINVAL, "null buffer");
+  const MsgWs l = msg_ws(N, H, E, K, M, act_dtype);
+  if (ws_bytes < l.total) return fail(SMOE_ECAPACITY, "workspace");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int S = E < K * M ? E : K * M;
+  SMOE_TRY(launch_dest_coeffs(src_idx, eidx, ew, N, K, M, E, S, at<int32_t>(ws, l.tok_d),
+                              at<float>(ws, l.tok_dc), s),
+           "destination coefficients");
+  SMOE_TRY(launch_plan(at<int32_t>(ws, l.tok_d), at<float>(ws, l.tok_dc), N, S, E, 1,
+                       at<int32_t>(ws, l.cnt), at<int32_t>(ws, l.acnt), at<int32_t>(ws, l.off),
+                       at<int32_t>(ws, l.rows), at<float>(ws, l.roww), at<int32_t>(ws, l.tokrow),
+                       at<void>(ws, l.scratch), s),
+           "destination plan");
+  GemmArgs pg;
+  pg.fmt = act_dtype == SMOE_F32 ? SMOE_F32 : SMOE_BF16;
+  pg.epi = EPI_ROWSCALE;
+  pg.A = x;
+  pg.lda = H;
+  pg.a_rows = at<int32_t>(ws, l.rows);
+  pg.W = edge_value_w;
+  pg.Wt = act_dtype == SMOE_BF16 ? edge_value_w_tiles : nullptr;
+  pg.w_gstride = static_cast<int64_t>(H) * H;
+  pg.ldw = H;
+  pg.K = H;
+  pg.N_out = H;
+  pg.grp_off = at<int32_t>(ws, l.off);
+  pg.G = E;
+  pg.max_rows = N * S;
+  pg.out = at<void>(ws, l.proj);
+  pg.ldo = H;
+  pg.out_dtype = act_dtype;
+  pg.row_scale = at<float>(ws, l.roww);
+  SMOE_TRY(launch_grouped_gemm(pg, s), "edge GEMM");
+  SMOE_TRY(launch_msg_combine(at<void>(ws, l.proj), act_dtype, at<int32_t>(ws, l.tok_d),
+                              at<int32_t>(ws, l.tokrow), N, S, H, msg, msg_dtype, s),
+           "message combine");
+  return SMOE_OK;
+}
+
+SMOE_API int smoe_combine_epilogue(const void* h, const void* x0, int act_dtype, const void* delta,
+                                   int delta_dtype, int N, int H, float alpha, float beta,
+                                   const float* ln_w, const float* ln_b, float eps, void* out,
+                                   void* stream) {
+  int rc = check_act(act_dtype, H);
+  if (rc != SMOE_OK) return rc;
+  if (delta_dtype != SMOE_F32 && delta_dtype != SMOE_BF16)
+    return fail(SMOE_EUNSUPPORTED, "delta dtype");
+  if (N < 0) return fail(SMOE_EINVAL, "N");
+  if (N == 0) return SMOE_OK;
+  if (!h || !x0 || !delta || !out) return fail(SMOE_EINVAL, "null buffer");
+  SMOE_TRY(launch_epilogue(h, x0, act_dtype, delta, delta_dtype, nullptr, nullptr, nullptr, N, 1, H,
+                           alpha, beta, ln_w, ln_b, eps, out, static_cast<hipStream_t>(stream)),
+           "epilogue");
+  return SMOE_OK;
+}
+
 }  // extern "C"

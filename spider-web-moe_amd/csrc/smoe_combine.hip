@@ -158,12 +158,16 @@ __global__ __launch_bounds__(256) void k_epilogue(
   }
   // lane j (< K): the token's j-th expert row if its weight is > 0 (rows
   // with weight <= 0 are dropped from the FFN, sparse_experts.py:56); lanes
-  // past K read entry K-1 and drop it
-  const int64_t e = static_cast<int64_t>(t) * K + (lane < K ? lane : K - 1);
-  const int te = tok_e[e];
-  const float tw = tok_ew[e];
-  const int tr = e_tokrow[e];
-  const int my_row = (lane < K && te >= 0 && tw > 0.f) ? tr : -1;
+  // past K read entry K-1 and drop it.  Without routing (tok_e null) y is
+  // the dense delta [N, H] and lane 0 takes row t.
+  int my_row = lane == 0 ? t : -1;
+  if (tok_e) {
+    const int64_t e = static_cast<int64_t>(t) * K + (lane < K ? lane : K - 1);
+    const int te = tok_e[e];
+    const float tw = tok_ew[e];
+    const int tr = e_tokrow[e];
+    my_row = (lane < K && te >= 0 && tw > 0.f) ? tr : -1;
+  }
   gather_add<CPL, YDT>(y, H, my_row, __ballot(my_row >= 0), d);  // ascending expert order
   float s = 0.f;
 #pragma unroll

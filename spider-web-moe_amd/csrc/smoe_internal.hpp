@@ -85,6 +85,13 @@ int launch_merge_slots(const int32_t* idx, const float* w, int N, int K, int E, 
 int launch_edge_topm(const float* edge_logit, const int32_t* tok_e, const int32_t* e_tokrow,
                      int N, int E, int K, int M, int S, int32_t* edge_idx, float* edge_w,
                      int32_t* tok_d, float* tok_dc, hipStream_t s);
+// per-source top-m rows of the expert plan -> [N,K,M] in the caller's slot order
+int launch_gather_topm(const int32_t* src_idx, const int32_t* tok_e, const int32_t* e_tokrow,
+                       const int32_t* edge_idx, const float* edge_w, int N, int K, int M,
+                       int32_t* out_idx, float* out_w, hipStream_t s);
+// given edges [N,K,M] -> per-token destination coefficients (S per token)
+int launch_dest_coeffs(const int32_t* src_idx, const int32_t* eidx, const float* ew, int N, int K,
+                       int M, int E, int S, int32_t* tok_d, float* tok_dc, hipStream_t s);
 size_t plan_scratch_bytes(int N, int G);
 int launch_plan(const int32_t* tok_g, const float* tok_w, int N, int S, int G, int drop_nonpos,
                 int32_t* cnt, int32_t* acnt, int32_t* off, int32_t* rows, float* roww,

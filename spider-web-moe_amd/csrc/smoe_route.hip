@@ -118,7 +118,8 @@ int launch_route_topk(const float* logits, int N, int E, int K, int32_t* top_idx
 // (sum over the token's slots of that group, in slot order, from 0 — the
 // accumulation of sparse_experts.py:52-55).  Ids outside [0, E) never match
 // an expert and are dropped, as in the reference; drop_nonpos also drops
-// merged weights <= 0 (sparse_experts.py:56).
+// merged weights <= 0 (sparse_experts.py:56).  w == nullptr: every slot
+// weighs 1 (a binary source mask, model.py:277-279).
 __global__ __launch_bounds__(256) void k_merge_slots(const int32_t* __restrict__ idx,
                                                      const float* __restrict__ w, int N, int K,
                                                      int E, int drop_nonpos,
@@ -127,7 +128,7 @@ __global__ __launch_bounds__(256) void k_merge_slots(const int32_t* __restrict__
   const int t = blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= N) return;
   const int32_t* ti = idx + static_cast<int64_t>(t) * K;
-  const float* tw = w + static_cast<int64_t>(t) * K;
+  const float* tw = w ? w + static_cast<int64_t>(t) * K : nullptr;
   int out = 0;
   int last = -1;
   // emit groups in ascending order: repeatedly take the smallest id > last
@@ -140,7 +141,7 @@ __global__ __launch_bounds__(256) void k_merge_slots(const int32_t* __restrict__
     if (best == kBig) break;
     float acc = 0.f;
     for (int s = 0; s < K; ++s)
-      if (ti[s] == best) acc = acc + tw[s];
+      if (ti[s] == best) acc = acc + (tw ? tw[s] : 1.f);
     last = best;
     if (drop_nonpos && !(acc > 0.f)) continue;
     tok_g[static_cast<int64_t>(t) * K + out] = best;
@@ -293,6 +294,101 @@ int launch_edge_topm(const float* edge_logit, const int32_t* tok_e, const int32_
   else SMOE_EDGE_TOPM_K(64);
 #undef SMOE_EDGE_TOPM_K
 #undef SMOE_EDGE_TOPM
+  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
+// Per-source top-m in the caller's slot order: slot j of token t takes the
+// row of its source in the expert plan (the token's merged, ascending
+// sources tok_e and their plan rows e_tokrow) and copies that row's m
+// destinations and weights; slots without a valid source get -1 / 0.
+__global__ __launch_bounds__(256) void k_gather_topm(const int32_t* __restrict__ src_idx,
+                                                     const int32_t* __restrict__ tok_e,
+                                                     const int32_t* __restrict__ e_tokrow,
+                                                     const int32_t* __restrict__ edge_idx,
+                                                     const float* __restrict__ edge_w, int N,
+                                                     int K, int M, int32_t* __restrict__ out_idx,
+                                                     float* __restrict__ out_w) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= static_cast<int64_t>(N) * K) return;
+  const int64_t t = i / K;
+  const int s = src_idx[i];
+  int row = -1;
+  for (int q = 0; q < K; ++q)
+    if (s >= 0 && tok_e[t * K + q] == s) {
+      row = e_tokrow[t * K + q];
+      break;
+    }
+  for (int j = 0; j < M; ++j) {
+    out_idx[i * M + j] = row >= 0 ? edge_idx[static_cast<int64_t>(row) * M + j] : -1;
+    out_w[i * M + j] = row >= 0 ? edge_w[static_cast<int64_t>(row) * M + j] : 0.f;
+  }
+}
+
+int launch_gather_topm(const int32_t* src_idx, const int32_t* tok_e, const int32_t* e_tokrow,
+                       const int32_t* edge_idx, const float* edge_w, int N, int K, int M,
+                       int32_t* out_idx, float* out_w, hipStream_t s) {
+  const int64_t n = static_cast<int64_t>(N) * K;
+  if (n <= 0) return SMOE_OK;
+  hipLaunchKernelGGL(k_gather_topm, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
+                     src_idx, tok_e, e_tokrow, edge_idx, edge_w, N, K, M, out_idx, out_w);
+  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
+// Destination coefficients of given edges (model.py:277-288): one wave per
+// token, lane d = destination d.  The token's distinct valid sources are
+// taken in ascending order (a binary mask: a source listed twice counts
+// once) and each adds the weights of its edges into d, as the fused top-m
+// does; the nonzero destinations, ascending, fill tok_d / tok_dc (S
+// entries per token, -1 / 0 past them).
+__global__ __launch_bounds__(256) void k_dest_coeffs(const int32_t* __restrict__ src_idx,
+                                                     const int32_t* __restrict__ eidx,
+                                                     const float* __restrict__ ew, int N, int K,
+                                                     int M, int E, int S,
+                                                     int32_t* __restrict__ tok_d,
+                                                     float* __restrict__ tok_dc) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= N) return;  // wave-uniform
+  const int32_t* ts = src_idx + static_cast<int64_t>(t) * K;
+  float c = 0.f;
+  int last = -1;
+  for (int it = 0; it < K; ++it) {  // uniform: every lane scans the same slots
+    int best = kBig, bj = 0;
+    for (int j = 0; j < K; ++j) {
+      const int e = ts[j];
+      if (e > last && e >= 0 && e < E && e < best) {
+        best = e;
+        bj = j;
+      }
+    }
+    if (best == kBig) break;
+    last = best;
+    const int64_t b = (static_cast<int64_t>(t) * K + bj) * M;
+    for (int j = 0; j < M; ++j)
+      if (eidx[b + j] == lane) c += ew[b + j];
+  }
+  const bool nz = lane < E && c != 0.f;
+  const uint64_t m = __ballot(nz);
+  const int cnt = __popcll(m);
+  if (nz) {
+    const int rank = __popcll(m & ((1ull << lane) - 1));
+    if (rank < S) {
+      tok_d[static_cast<int64_t>(t) * S + rank] = lane;
+      tok_dc[static_cast<int64_t>(t) * S + rank] = c;
+    }
+  }
+  if (lane >= cnt && lane < S) {
+    tok_d[static_cast<int64_t>(t) * S + lane] = -1;
+    tok_dc[static_cast<int64_t>(t) * S + lane] = 0.f;
+  }
+}
+
+int launch_dest_coeffs(const int32_t* src_idx, const int32_t* eidx, const float* ew, int N, int K,
+                       int M, int E, int S, int32_t* tok_d, float* tok_dc, hipStream_t s) {
+  if (E < 1 || E > 64 || S < 1 || S > 64 || K < 1 || M < 1) return SMOE_EINVAL;
+  if (N <= 0) return SMOE_OK;
+  hipLaunchKernelGGL(k_dest_coeffs, dim3((N + 3) / 4), dim3(256), 0, s, src_idx, eidx, ew, N, K, M,
+                     E, S, tok_d, tok_dc);
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 

@@ -72,6 +72,14 @@ SIGNATURES = {
     "smoe_expert_delta": (_c_int, [ctypes.POINTER(SmoeExperts), _vp, _vp, _vp, _c_int, _c_int,
                                    _vp, _c_int, _vp, _sz, _vp]),
     "smoe_pack_weight_tiles": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp]),
+    "smoe_edge_topm_workspace_bytes": (_sz, [_c_int, _c_int, _c_int, _c_int]),
+    "smoe_edge_topm": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _c_int, _vp, _c_int, _c_int,
+                                _c_int, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "smoe_edge_message_workspace_bytes": (_sz, [_c_int, _c_int, _c_int, _c_int, _c_int, _c_int]),
+    "smoe_edge_message": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int, _c_int, _c_int,
+                                   _vp, _vp, _vp, _vp, _c_int, _vp, _sz, _vp]),
+    "smoe_combine_epilogue": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_float,
+                                       _c_float, _vp, _vp, _c_float, _vp, _vp]),
     "smoe_profile_stages": (_c_int, [ctypes.c_uint32, ctypes.POINTER(_vp), _c_int]),
     "smoe_profile_count": (_c_int, [ctypes.POINTER(ctypes.c_int32), _c_int]),
     "smoe_events_create": (_c_int, [_c_int, ctypes.POINTER(_vp)]),
@@ -84,7 +92,7 @@ STAGES = ["router_gemm", "route_topk", "expert_plan", "edge_logits", "edge_topm"
           # bf16 steps of N <= 64: stages 0-5 as one GEMM and one routing workgroup
           "front_gemm", "front_route"]
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 _LIB = None
 
 

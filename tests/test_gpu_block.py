@@ -217,3 +217,86 @@ def test_cpu_tensors_are_rejected():
     wl = make_block("c2")
     with pytest.raises(RuntimeError):
         wl.layer(wl.h.cpu(), wl.x0.cpu(), 0)
+
+
+STAGE_SPECS = [
+    dict(dtype="bf16", act="swiglu", experts="bf16"),
+    dict(dtype="bf16", act="gelu", experts="fp8"),
+    dict(dtype="bf16", act="gelu", experts="int4"),
+    dict(dtype="f32", act="gelu", experts="bf16"),
+]
+
+
+@pytest.mark.parametrize("spec", STAGE_SPECS, ids=lambda s: f"{s['dtype']}-{s['act']}-{s['experts']}")
+def test_stage_entries_compose_block_forward(spec):
+    """The stage entry points chained the way model.py:240-317 chains the
+    stages (smoe_router_topk -> smoe_edge_topm -> smoe_edge_message ->
+    smoe_expert_delta -> smoe_combine_epilogue) give smoe_block_forward's
+    loop output bit for bit (the same kernels on the same rows).  Their
+    intermediate results are also checked against the oracle: top-k
+    indices, and per token the destination set of the selected edges."""
+    import ctypes
+    from spider_moe_amd import _native as nat
+    from spider_moe_amd.workloads import make_block
+    say("stage entries", spec)
+    wl = make_block("c1", tokens=300, hidden_size=128, num_experts=8, top_k=2, edges_per_expert=3,
+                    expert_ffn_size=256, num_loops=2, expert_activation=spec["act"],
+                    experts=spec["experts"], dtype=spec["dtype"], group_size=64)
+    layer, r = wl.layer, 1
+    n, hid = wl.h.shape[0], wl.h.shape[-1]
+    e, k, m = layer.num_experts, layer.top_k, layer.edges_per_expert
+    with torch.no_grad():
+        want = layer(wl.h, wl.x0, r).reshape(n, hid)
+    torch.cuda.synchronize()
+    d = layer._pack().desc
+    lib, st = nat.lib(), nat.stream_of(torch.device(dev))
+    x, x0 = wl.h.reshape(n, hid).contiguous(), wl.x0.reshape(n, hid).contiguous()
+    act = d.act_dtype
+    fdt = torch.float32 if d.experts.format == nat.F32 else torch.bfloat16
+
+    def ws(nbytes):
+        assert nbytes > 0
+        return torch.empty(nbytes, dtype=torch.uint8, device=dev)
+
+    top_w = torch.empty(n, k, device=dev)
+    top_i = torch.empty(n, k, dtype=torch.int32, device=dev)
+    w0 = ws(lib.smoe_router_workspace_bytes(n, e))
+    nat.check(lib.smoe_router_topk(x.data_ptr(), act, n, hid, d.router_w, d.loop_bias + 4 * r * e, e,
+                                   k, None, top_w.data_ptr(), top_i.data_ptr(), w0.data_ptr(),
+                                   w0.numel(), st), "router_topk")
+    eidx = torch.empty(n, k, m, dtype=torch.int32, device=dev)
+    ew = torch.empty(n, k, m, device=dev)
+    w1 = ws(lib.smoe_edge_topm_workspace_bytes(n, k, e, m))
+    nat.check(lib.smoe_edge_topm(x.data_ptr(), act, n, hid, d.edge_gen_w, hid + d.L,
+                                 d.edge_loop_bias + 4 * r * e * e, e, k, m, top_i.data_ptr(),
+                                 eidx.data_ptr(), ew.data_ptr(), w1.data_ptr(), w1.numel(), st),
+              "edge_topm")
+    msg = torch.empty(n, hid, dtype=fdt, device=dev)
+    w2 = ws(lib.smoe_edge_message_workspace_bytes(n, hid, e, k, m, act))
+    nat.check(lib.smoe_edge_message(x.data_ptr(), act, n, hid, d.edge_value_w, d.edge_value_w_tiles,
+                                    e, k, m, top_i.data_ptr(), eidx.data_ptr(), ew.data_ptr(),
+                                    msg.data_ptr(), nat.dtype_code(fdt), w2.data_ptr(), w2.numel(),
+                                    st), "edge_message")
+    delta = torch.empty(n, hid, device=dev)
+    w3 = ws(lib.smoe_expert_delta_workspace_bytes(ctypes.byref(d.experts), n, k))
+    nat.check(lib.smoe_expert_delta(ctypes.byref(d.experts), msg.data_ptr(), top_i.data_ptr(),
+                                    top_w.data_ptr(), n, k, delta.data_ptr(), nat.F32, w3.data_ptr(),
+                                    w3.numel(), st), "expert_delta")
+    out = torch.empty_like(x)
+    nat.check(lib.smoe_combine_epilogue(x.data_ptr(), x0.data_ptr(), act, delta.data_ptr(), nat.F32,
+                                        n, hid, d.alpha, d.beta, d.ln_w, d.ln_b, d.eps,
+                                        out.data_ptr(), st), "combine_epilogue")
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
+    # against the oracle: top-k and each token's destination set
+    ref, aux = B.block_forward(x.float().cpu(), x0.float().cpu(), oracle_weights(layer), r,
+                               out_bf16=(x.dtype == torch.bfloat16))
+    ties = (aux.router_gap < TIE_GAP) | (aux.edge_gap < TIE_GAP)
+    ti, ei, eww = top_i.long().cpu(), eidx.long().cpu(), ew.cpu()
+    for t in range(n):
+        if bool(ties[t]):
+            continue
+        assert ti[t].tolist() == aux.top_i[t].tolist(), t
+        dst = {int(x_) for x_ in ei[t].flatten().tolist() if x_ >= 0}
+        assert dst == set(torch.nonzero(aux.coef[t] != 0).flatten().tolist()), t
+        assert torch.allclose(eww[t].sum(-1), torch.ones(k), atol=1e-5)  # softmax rows

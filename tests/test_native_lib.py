@@ -38,7 +38,7 @@ def test_exports_every_declared_symbol(nat):
 
 def test_identity(nat):
     lib = nat.lib()
-    assert lib.smoe_abi_version() == 4
+    assert lib.smoe_abi_version() == 5
     assert lib.smoe_backend_name() == b"hip-gfx950"
     assert lib.smoe_backend_caps() == 0b1111
 
@@ -117,3 +117,55 @@ def test_capacity_and_range_errors(nat):
     assert rc == 1  # loop range past num_loops
     # N == 0 is a no-op
     assert lib.smoe_block_forward(ctypes.byref(b), None, None, None, 0, 0, 1, None, 0, None) == 0
+
+
+def test_stage_entries_reject_bad_arguments(nat):
+    """Shape, dtype, null-buffer and workspace checks of the stage entry
+    points run before any launch (no device needed)."""
+    lib = nat.lib()
+    p = 0x1000  # never dereferenced: every call below fails its checks first
+    # edge top-m: E, K, M ranges; ldw; null buffers; workspace size
+    assert lib.smoe_edge_topm_workspace_bytes(10, 2, 0, 2) == 0
+    assert lib.smoe_edge_topm_workspace_bytes(10, 2, 16, 2) > 0
+    args = lambda **o: dict(dict(x=p, adt=nat.BF16, n=10, h=128, w=p, ldw=160, b=p, e=16, k=2, m=2,
+                                  src=p, oi=p, ow=p, ws=p, wsb=1 << 30), **o)
+    def topm(a):
+        return lib.smoe_edge_topm(a["x"], a["adt"], a["n"], a["h"], a["w"], a["ldw"], a["b"],
+                                  a["e"], a["k"], a["m"], a["src"], a["oi"], a["ow"], a["ws"],
+                                  a["wsb"], None)
+    assert topm(args(e=0)) == 1
+    assert topm(args(k=17)) == 1
+    assert topm(args(m=3, e=2)) == 1
+    assert topm(args(h=100)) == 1
+    assert topm(args(ldw=100)) == 1
+    assert topm(args(ldw=161)) == 1
+    assert topm(args(adt=nat.INT4)) == -2
+    assert topm(args(src=None)) == 1
+    assert topm(args(wsb=16)) == 3
+    # edge message
+    assert lib.smoe_edge_message_workspace_bytes(10, 128, 16, 2, 2, nat.INT4) == 0
+    assert lib.smoe_edge_message_workspace_bytes(10, 128, 16, 2, 2, nat.BF16) > 0
+    def msg(**o):
+        a = dict(dict(x=p, adt=nat.BF16, n=10, h=128, w=p, t=None, e=16, k=2, m=2, src=p, ei=p,
+                      ew=p, out=p, odt=nat.BF16, ws=p, wsb=1 << 30), **o)
+        return lib.smoe_edge_message(a["x"], a["adt"], a["n"], a["h"], a["w"], a["t"], a["e"],
+                                     a["k"], a["m"], a["src"], a["ei"], a["ew"], a["out"], a["odt"],
+                                     a["ws"], a["wsb"], None)
+    assert msg(e=65) == 1
+    assert msg(odt=nat.INT4) == -2
+    assert msg(ei=None) == 1
+    assert msg(wsb=16) == 3
+    assert msg(n=-1) == 1
+    # epilogue
+    def epi(**o):
+        a = dict(dict(h=p, x0=p, adt=nat.BF16, d=p, ddt=nat.F32, n=10, hid=128), **o)
+        return lib.smoe_combine_epilogue(a["h"], a["x0"], a["adt"], a["d"], a["ddt"], a["n"],
+                                         a["hid"], 0.5, 0.1, None, None, 1e-5, p, None)
+    assert epi(hid=100) == 1
+    assert epi(ddt=nat.INT4) == -2
+    assert epi(d=None) == 1
+    assert epi(adt=nat.FP8_E4M3) == -2
+    # N == 0 is a no-op
+    assert epi(n=0) == 0
+    assert topm(args(n=0)) == 0
+    assert msg(n=0) == 0
