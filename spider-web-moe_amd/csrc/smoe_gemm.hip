@@ -1251,8 +1251,19 @@ __global__ __launch_bounds__(256, WGS) void k_gemm_stream(const GemmArgs p) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int q = lane >> 4, l16 = lane & 15;
-  const int g = blockIdx.y;
-  const int nb = blockIdx.x * 256;
+  // (group, strip) of this workgroup: workgroup ids are dealt to the 8 XCDs
+  // round robin, so the linear id is split into 8 contiguous ranges of
+  // (group, strip) pairs, one per XCD, and a group's strips share one L2
+  // (its activation rows come from HBM once instead of once per strip)
+  int g, nb;
+  {
+    const int S = gridDim.x, T = S * gridDim.y;
+    const int bid = blockIdx.x + S * blockIdx.y;
+    const int x = bid & 7, local = bid >> 3, base = T >> 3, rem = T & 7;
+    const int logical = x * base + min(x, rem) + local;
+    g = logical / S;
+    nb = (logical - g * S) * 256;
+  }
   int r_lo, r_hi;
   if (p.G == 0) {
     r_lo = 0;
