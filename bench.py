@@ -244,6 +244,49 @@ def cpu_baseline(name="c1", sample_tokens=8192, budget_s=30.0):
                       "oracle faithful fp32 (torch CPU)"}
 
 
+def run_decode_exit(steps, warmup):
+    """The c2 decode step (64 tokens, 6 loops) with the early-exit gate:
+    eager calls and HIP-graph replays (spider_moe_amd.graph), ungated and
+    gated.  Threshold 1.0 keeps every token in orbit (the gate's own cost);
+    a random exit head at threshold 0.5 makes tokens leave at mixed loops."""
+    import torch
+    from spider_moe_amd.graph import BlockDecodeGraph
+    from spider_moe_amd.workloads import make_block
+
+    log("decode exit: building")
+    wl = make_block("c2")
+    layer, h, x0 = wl.layer, wl.h, wl.x0
+    hid = layer.hidden_size
+
+    def timed(fn):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return round(e0.elapsed_time(e1) / steps, 4)
+
+    res = {"workload": "c2 decode with the exit gate", "steps": steps}
+    with torch.no_grad():
+        runner = BlockDecodeGraph(layer)
+        res["eager_ms"] = timed(lambda: layer.forward_loops(h, x0))
+        res["graph_ms"] = timed(lambda: runner.run(h, x0, early_exit=False))
+        res["eager_gate_ms"] = timed(lambda: layer.forward_loops_exit(h, x0, 1.0))
+        res["graph_gate_ms"] = timed(lambda: runner.run(h, x0, early_exit=True, threshold=1.0))
+        g = torch.Generator().manual_seed(31)
+        layer.exit_head.weight.copy_((torch.randn(1, hid, generator=g) / hid ** 0.5).to(layer.exit_head.weight))
+        layer.exit_head.bias.zero_()
+        res["graph_mixed_exit_ms"] = timed(lambda: runner.run(h, x0, early_exit=True, threshold=0.5))
+        _, loops = runner.run(h, x0, early_exit=True, threshold=0.5)
+        res["mixed_exit_loops_hist"] = torch.bincount(loops.long().cpu(), minlength=7).tolist()
+    log("decode exit:", res)
+    return res
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -293,6 +336,8 @@ def main():
         "stage_ms_per_step": head["stage_ms_per_step"],
         "workloads": {k: v for k, v in results.items() if v is not head},
     }
+    if "c2" in names:
+        line["decode_exit"] = run_decode_exit(a.steps, a.warmup)
     if not a.no_cpu:
         log("cpu baseline")
         line["cpu_baseline"] = cpu_baseline(head["workload"])

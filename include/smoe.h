@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define SMOE_ABI_VERSION 5
+#define SMOE_ABI_VERSION 6
 
 /* status codes (spider_kernels.h convention; see scalar.cpp:9,45,58) */
 #define SMOE_OK 0
@@ -178,6 +178,26 @@ SMOE_API int smoe_edge_loop_bias(const void* edge_gen_w, int act_dtype, const fl
 SMOE_API int smoe_block_forward(const smoe_block* blk, const void* h_in, const void* x0,
                                 void* h_out, int N, int loop_begin, int num_loops,
                                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* Early-exit decode (SpiderWebLM._run_recurrent_decode with early_exit,
+ * model.py:450-473, and the early_exit branch of SpiderWebLM.forward,
+ * model.py:683-698; the ActiveSet compaction of spider_moe/active_set.py:14-64
+ * kept on the device): smoe_block_forward over the tokens still in orbit.
+ * active i32 [N] in/out: nonzero = in orbit.  Per loop, tokens with
+ * active[t] == 0 get no routing (no expert or edge work) and keep their h;
+ * every other token gets h' and leaves the orbit (active[t] := 0) when
+ * sigmoid(exit_wb[0:H] . h' + exit_wb[H]) > threshold, computed in fp32 over
+ * h' as stored (exit_head, model.py:185,467).  loops i32 [N] in/out or NULL:
+ * incremented for each loop a token runs.  No host synchronization: a
+ * fixed-R decode step with early exit can be captured in one HIP graph.
+ * Replaces spider_early_exit_f32 (spider_kernels.h:109-111) and the exit
+ * mask of spider_moe_loop_step_f32 (spider_kernels.h:113-121), fused into
+ * the block's epilogue. */
+SMOE_API int smoe_block_forward_exit(const smoe_block* blk, const void* h_in, const void* x0,
+                                     void* h_out, int N, int loop_begin, int num_loops,
+                                     const float* exit_wb, float threshold, int32_t* active,
+                                     int32_t* loops, void* workspace, size_t workspace_bytes,
+                                     void* stream);
 
 /* Router stage alone (model.py:255-258; spider_router_f32,
  * spider_kernels.h:26-28, with the logits GEMM of model.py:255 fused in):

@@ -321,3 +321,43 @@ def block_loops(h, x0, w: BlockWeights, num_loops: int, **kw):
     for r in range(num_loops):
         h, _ = block_forward(h, x0, w, r, **kw)
     return h
+
+
+def exit_logit(h, exit_w, exit_b):
+    """exit_head(h) (model.py:185,467): h . w + b in float32; the confidence
+    is its sigmoid."""
+    return h.float() @ exit_w.float().reshape(-1) + float(exit_b)
+
+
+def block_loops_exit(h, x0, w: BlockWeights, num_loops: int, exit_w, exit_b, threshold: float,
+                     *, loop_begin: int = 0, **kw):
+    """Early-exit decode: SpiderWebLM._run_recurrent_decode(early_exit=True)
+    (model.py:450-473) over the ActiveSet compaction of active_set.py:14-64.
+    Each loop gathers the rows still in orbit (compact_active: index_select),
+    runs the block on them, writes them back (scatter_active: index_copy_)
+    and drops the rows whose sigmoid(exit_head(h')) > threshold
+    (ActiveSet.drop); the loop stops when no row is left (model.py:461-462).
+
+    Returns (h [N, H], loops [N] = loops each row ran, margin [N] = the
+    smallest |exit logit - logit(threshold)| over the loops a row ran: rows
+    with a tiny margin are near-ties of the exit decision)."""
+    h = h.float().clone()
+    x0 = x0.float()
+    n = h.shape[0]
+    idx = torch.arange(n)
+    loops = torch.zeros(n, dtype=torch.long)
+    margin = torch.full((n,), float("inf"))
+    if 0.0 < threshold < 1.0:
+        z_thr = float(np.log(threshold / (1.0 - threshold)))
+    else:
+        z_thr = float("inf") if threshold >= 1.0 else float("-inf")
+    for r in range(loop_begin, loop_begin + num_loops):
+        if idx.numel() == 0:
+            break
+        h_new, _ = block_forward(h.index_select(0, idx), x0.index_select(0, idx), w, r, **kw)
+        h.index_copy_(0, idx, h_new)
+        z = exit_logit(h_new, exit_w, exit_b)
+        loops[idx] += 1
+        margin[idx] = torch.minimum(margin[idx], (z - z_thr).abs())
+        idx = idx[~(torch.sigmoid(z) > threshold)]
+    return h, loops, margin

@@ -327,9 +327,13 @@ SMOE_API int smoe_edge_loop_bias(const void* edge_gen_w, int act_dtype, const fl
   return SMOE_OK;
 }
 
-SMOE_API int smoe_block_forward(const smoe_block* b, const void* h_in, const void* x0,
-                                void* h_out, int N, int loop_begin, int num_loops, void* ws,
-                                size_t ws_bytes, void* stream) {
+namespace {
+// Loops [loop_begin, loop_begin + num_loops) of the block; gate (or null)
+// is the exit gate of the early-exit decode: routing skips tokens whose
+// gate->active entry is 0 and the epilogue passes their h through.
+int block_forward(const smoe_block* b, const void* h_in, const void* x0, void* h_out, int N,
+                  int loop_begin, int num_loops, const ExitGate* gate, void* ws, size_t ws_bytes,
+                  void* stream) {
   int rc = check_block(b);
   if (rc != SMOE_OK) return rc;
   if (N < 0 || loop_begin < 0 || num_loops < 0 || loop_begin + num_loops > b->R)
@@ -345,6 +349,7 @@ SMOE_API int smoe_block_forward(const smoe_block* b, const void* h_in, const voi
   const int gfmt = adt == SMOE_F32 ? SMOE_F32 : SMOE_BF16;  // router / edge weights
 
   const bool front = front_ok(b, N);
+  const int32_t* active = gate ? gate->active : nullptr;
   const void* cur = h_in;
   for (int i = 0; i < num_loops; ++i) {
     const int r = loop_begin + i;
@@ -383,7 +388,7 @@ SMOE_API int smoe_block_forward(const smoe_block* b, const void* h_in, const voi
                                at<float>(ws, l.tok_dc), at<int32_t>(ws, l.d_cnt),
                                at<int32_t>(ws, l.d_acnt), at<int32_t>(ws, l.d_off),
                                at<int32_t>(ws, l.d_rows), at<float>(ws, l.d_roww),
-                               at<int32_t>(ws, l.d_tokrow), s),
+                               at<int32_t>(ws, l.d_tokrow), active, s),
             "front routing");
     } else {
 
@@ -407,7 +412,7 @@ SMOE_API int smoe_block_forward(const smoe_block* b, const void* h_in, const voi
     // 2 top-k
     STAGE(SMOE_STAGE_ROUTE_TOPK, launch_route_topk(at<float>(ws, l.logits), N, E, K, at<int32_t>(ws, l.top_idx),
                                at<float>(ws, l.top_w), at<int32_t>(ws, l.tok_e),
-                               at<float>(ws, l.tok_ew), s),
+                               at<float>(ws, l.tok_ew), active, s),
              "route_topk");
     // 3 expert / source plan (keeps every selected source; the FFN combine
     //   skips weights <= 0)
@@ -484,11 +489,31 @@ SMOE_API int smoe_block_forward(const smoe_block* b, const void* h_in, const voi
     // 11 combine + residual + LayerNorm
     STAGE(SMOE_STAGE_EPILOGUE, launch_epilogue(cur, x0, adt, at<void>(ws, l.y), fdt, at<int32_t>(ws, l.tok_e),
                              at<float>(ws, l.tok_ew), at<int32_t>(ws, l.e_tokrow), N, K, H,
-                             b->alpha, b->beta, b->ln_w, b->ln_b, b->eps, dst, s),
+                             b->alpha, b->beta, b->ln_w, b->ln_b, b->eps, dst, gate, s),
              "epilogue");
     cur = dst;
   }
   return SMOE_OK;
+}
+}  // namespace
+
+SMOE_API int smoe_block_forward(const smoe_block* b, const void* h_in, const void* x0,
+                                void* h_out, int N, int loop_begin, int num_loops, void* ws,
+                                size_t ws_bytes, void* stream) {
+  return block_forward(b, h_in, x0, h_out, N, loop_begin, num_loops, nullptr, ws, ws_bytes,
+                       stream);
+}
+
+SMOE_API int smoe_block_forward_exit(const smoe_block* b, const void* h_in, const void* x0,
+                                     void* h_out, int N, int loop_begin, int num_loops,
+                                     const float* exit_wb, float threshold, int32_t* active,
+                                     int32_t* loops, void* ws, size_t ws_bytes, void* stream) {
+  if (!exit_wb || !active) return fail(SMOE_EINVAL, "exit gate buffers");
+  // NaN test on the bits: fast-math builds fold a self-comparison away
+  const uint32_t tb = __builtin_bit_cast(uint32_t, threshold);
+  if ((tb & 0x7fffffffu) > 0x7f800000u) return fail(SMOE_EINVAL, "threshold is NaN");
+  const ExitGate gate{exit_wb, threshold, active, loops};
+  return block_forward(b, h_in, x0, h_out, N, loop_begin, num_loops, &gate, ws, ws_bytes, stream);
 }
 
 SMOE_API int smoe_pack_weight_tiles(const void* w, int format, int G, int N, int K, void* out,
@@ -576,7 +601,7 @@ SMOE_API int smoe_router_topk(const void* x, int act_dtype, int N, int H, const 
   rg.ldo = E;
   rg.bias = loop_bias_row;
   SMOE_TRY(launch_grouped_gemm(rg, s), "router GEMM");
-  SMOE_TRY(launch_route_topk(lg, N, E, K, top_idx, top_w, te, tw, s), "route_topk");
+  SMOE_TRY(launch_route_topk(lg, N, E, K, top_idx, top_w, te, tw, nullptr, s), "route_topk");
   return SMOE_OK;
 }
 
@@ -851,7 +876,8 @@ SMOE_API int smoe_combine_epilogue(const void* h, const void* x0, int act_dtype,
   if (N == 0) return SMOE_OK;
   if (!h || !x0 || !delta || !out) return fail(SMOE_EINVAL, "null buffer");
   SMOE_TRY(launch_epilogue(h, x0, act_dtype, delta, delta_dtype, nullptr, nullptr, nullptr, N, 1, H,
-                           alpha, beta, ln_w, ln_b, eps, out, static_cast<hipStream_t>(stream)),
+                           alpha, beta, ln_w, ln_b, eps, out, nullptr,
+                           static_cast<hipStream_t>(stream)),
            "epilogue");
   return SMOE_OK;
 }

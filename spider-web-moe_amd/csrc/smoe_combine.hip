@@ -125,13 +125,20 @@ __global__ __launch_bounds__(256) void k_msg_combine(const void* __restrict__ pr
   }
 }
 
-template <int CPL, int ADT, int YDT>
+// GATE: the exit gate of the early-exit decode (model.py:450-473).  A token
+// whose active[t] is 0 left the orbit in an earlier loop: its h passes
+// through unchanged.  An active token gets h' and then
+// conf = sigmoid(exit_w . h' + exit_b) (fp32, over h' as stored); it leaves
+// the orbit (active[t] = 0) when conf > thr, and loops[t] (if not null)
+// counts the loops it ran.
+template <int CPL, int ADT, int YDT, bool GATE>
 __global__ __launch_bounds__(256) void k_epilogue(
     const void* __restrict__ h, const void* __restrict__ x0, const void* __restrict__ y,
     const int32_t* __restrict__ tok_e, const float* __restrict__ tok_ew,
     const int32_t* __restrict__ e_tokrow, int N, int K, int H, float alpha, float beta,
     const float* __restrict__ ln_w, const float* __restrict__ ln_b, float eps,
-    void* __restrict__ out) {
+    void* __restrict__ out, const float* __restrict__ exit_wb, float thr,
+    int32_t* __restrict__ active, int32_t* __restrict__ loops) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= N) return;
@@ -155,6 +162,15 @@ __global__ __launch_bounds__(256) void k_epilogue(
     else
 #pragma unroll
       for (int i = 0; i < 8; ++i) gb[c][i] = 0.f;
+  }
+  if (GATE && active[t] == 0) {  // wave-uniform: out of orbit, h passes through
+    if (out != h)
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const int col = (lane + 64 * c) * 8;
+        if (col < H) store8<ADT>(out, static_cast<int64_t>(t) * H + col, hv[c]);
+      }
+    return;
   }
   // lane j (< K): the token's j-th expert row if its weight is > 0 (rows
   // with weight <= 0 are dropped from the FFN, sparse_experts.py:56); lanes
@@ -180,6 +196,12 @@ __global__ __launch_bounds__(256) void k_epilogue(
         s += d[c][i];
       }
   }
+  if (GATE)  // x0 is consumed: its registers take the exit weights
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int col = (lane + 64 * c) * 8;
+      load8<SMOE_F32>(exit_wb, col < H ? col : 0, xv[c]);
+    }
   const float mean = wave_sum(s) / static_cast<float>(H);
   float q = 0.f;
 #pragma unroll
@@ -193,6 +215,7 @@ __global__ __launch_bounds__(256) void k_epilogue(
       }
   }
   const float rstd = 1.0f / sqrtf(wave_sum(q) / static_cast<float>(H) + eps);
+  float g = 0.f;  // exit-gate dot product (GATE)
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
     const int col = (lane + 64 * c) * 8;
@@ -201,6 +224,19 @@ __global__ __launch_bounds__(256) void k_epilogue(
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[i] = (d[c][i] - mean) * rstd * gw[c][i] + gb[c][i];
       store8<ADT>(out, static_cast<int64_t>(t) * H + col, o);
+      if (GATE)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const float stored = ADT == SMOE_BF16 ? bf2f(f2bf(o[i])) : o[i];
+          g += stored * xv[c][i];
+        }
+    }
+  }
+  if (GATE) {
+    const float z = wave_sum(g) + exit_wb[H];
+    if (lane == 0) {
+      if (1.0f / (1.0f + expf(-z)) > thr) active[t] = 0;
+      if (loops) loops[t] += 1;
     }
   }
 }
@@ -265,15 +301,22 @@ int launch_msg_combine(const void* proj, int pdt, const int32_t* tok_d, const in
 int launch_epilogue(const void* h, const void* x0, int adt, const void* y, int ydt,
                     const int32_t* tok_e, const float* tok_ew, const int32_t* e_tokrow, int N,
                     int K, int H, float alpha, float beta, const float* ln_w, const float* ln_b,
-                    float eps, void* out, hipStream_t s) {
+                    float eps, void* out, const ExitGate* gate, hipStream_t s) {
   if (K < 1 || K > 64) return SMOE_EINVAL;  // one lane per entry
   if (N <= 0) return SMOE_OK;
+  if (gate && (!gate->exit_wb || !gate->active)) return SMOE_EINVAL;
   return by_cpl(H, [&](auto cpl) {
     return by_dt(adt, [&](auto ad) {
       return by_dt(ydt, [&](auto yd) {
-        hipLaunchKernelGGL((k_epilogue<decltype(cpl)::value, decltype(ad)::value, decltype(yd)::value>),
-                           dim3((N + 3) / 4), dim3(256), 0, s, h, x0, y, tok_e, tok_ew, e_tokrow, N,
-                           K, H, alpha, beta, ln_w, ln_b, eps, out);
+        constexpr int C = decltype(cpl)::value, A = decltype(ad)::value, Y = decltype(yd)::value;
+        if (gate)
+          hipLaunchKernelGGL((k_epilogue<C, A, Y, true>), dim3((N + 3) / 4), dim3(256), 0, s, h, x0,
+                             y, tok_e, tok_ew, e_tokrow, N, K, H, alpha, beta, ln_w, ln_b, eps, out,
+                             gate->exit_wb, gate->threshold, gate->active, gate->loops);
+        else
+          hipLaunchKernelGGL((k_epilogue<C, A, Y, false>), dim3((N + 3) / 4), dim3(256), 0, s, h,
+                             x0, y, tok_e, tok_ew, e_tokrow, N, K, H, alpha, beta, ln_w, ln_b, eps,
+                             out, nullptr, 0.f, nullptr, nullptr);
         return last_rc();
       });
     });

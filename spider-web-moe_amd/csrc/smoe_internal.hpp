@@ -79,7 +79,7 @@ int launch_front_gemm(const GemmArgs& a, hipStream_t s);
 
 // ---- routing ----
 int launch_route_topk(const float* logits, int N, int E, int K, int32_t* top_idx, float* top_w,
-                      int32_t* tok_e, float* tok_ew, hipStream_t s);
+                      int32_t* tok_e, float* tok_ew, const int32_t* active, hipStream_t s);
 int launch_merge_slots(const int32_t* idx, const float* w, int N, int K, int E, int drop_nonpos,
                        int32_t* tok_g, float* tok_w, hipStream_t s);
 int launch_edge_topm(const float* edge_logit, const int32_t* tok_e, const int32_t* e_tokrow,
@@ -107,19 +107,29 @@ int launch_front_route(const float* front, int ldf, int N, int E, int K, int M, 
                        int32_t* e_rows, float* e_roww, int32_t* e_tokrow, float* edge_logit,
                        int32_t* edge_idx, float* edge_w, int32_t* tok_d, float* tok_dc,
                        int32_t* d_cnt, int32_t* d_acnt, int32_t* d_off, int32_t* d_rows,
-                       float* d_roww, int32_t* d_tokrow, hipStream_t s);
+                       float* d_roww, int32_t* d_tokrow, const int32_t* active,
+                       hipStream_t s);
 constexpr int kFrontMaxN = 64;
 int launch_edge_loop_bias(const void* wg, int act_dtype, const float* bg, const float* emb, int E,
                           int H, int L, int R, float* out, hipStream_t s);
 
 // ---- combine ----
+// Exit gate of the early-exit decode, fused into the epilogue: exit_wb f32
+// [H + 1] (exit_head weight, then bias), active i32 [N] in/out (nonzero = in
+// orbit), loops i32 [N] in/out or null (loops run per token).
+struct ExitGate {
+  const float* exit_wb;
+  float threshold;
+  int32_t* active;
+  int32_t* loops;
+};
 int launch_msg_combine(const void* proj, int proj_dtype, const int32_t* tok_d,
                        const int32_t* d_tokrow, int N, int S, int H, void* msg, int msg_dtype,
                        hipStream_t s);
 int launch_epilogue(const void* h, const void* x0, int act_dtype, const void* y, int y_dtype,
                     const int32_t* tok_e, const float* tok_ew, const int32_t* e_tokrow, int N,
                     int K, int H, float alpha, float beta, const float* ln_w, const float* ln_b,
-                    float eps, void* out, hipStream_t s);
+                    float eps, void* out, const ExitGate* gate, hipStream_t s);
 int launch_delta_combine(const void* y, int y_dtype, const int32_t* tok_row, int N, int K, int H,
                          void* out, int out_dtype, hipStream_t s);
 

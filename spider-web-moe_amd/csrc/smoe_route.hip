@@ -32,8 +32,11 @@ constexpr int kBig = 1 << 20;
 // the single-workgroup front, which runs each instruction a few times only.
 // p of the selected expert is recomputed from its logit (the same ops on the
 // same value as p itself).
+// live == false (a token that has left the orbit under an exit gate): the
+// token's tok_e / tok_ew slots are all -1 / 0, so every plan, the edge
+// stages and the expert GEMMs skip it; top_idx / top_w are still written.
 template <int SEG>
-__device__ __forceinline__ void topk_seg(float v, int t, bool ok, int E, int K,
+__device__ __forceinline__ void topk_seg(float v, int t, bool ok, bool live, int E, int K,
                                          int32_t* __restrict__ top_idx, float* __restrict__ top_w,
                                          int32_t* __restrict__ tok_e, float* __restrict__ tok_ew,
                                          int32_t* tok_e2, float* tok_ew2) {
@@ -67,13 +70,21 @@ __device__ __forceinline__ void topk_seg(float v, int t, bool ok, int E, int K,
   // distinct experts of the token in ascending order (lane order)
   const uint64_t segm = SEG == 64 ? ~0ull : ((1ull << SEG) - 1);
   const uint64_t m = (__ballot(sel) >> sbase) & segm;
-  if (ok && sel) {
+  if (ok && live && sel) {
     const int rank = __popcll(m & ((1ull << e) - 1));
     tok_e[static_cast<int64_t>(t) * K + rank] = e;
     tok_ew[static_cast<int64_t>(t) * K + rank] = p / denom;
     if (tok_e2) {
       tok_e2[t * K + rank] = e;
       tok_ew2[t * K + rank] = p / denom;
+    }
+  }
+  if (ok && !live && e < K) {
+    tok_e[static_cast<int64_t>(t) * K + e] = -1;
+    tok_ew[static_cast<int64_t>(t) * K + e] = 0.f;
+    if (tok_e2) {
+      tok_e2[t * K + e] = -1;
+      tok_ew2[t * K + e] = 0.f;
     }
   }
 }
@@ -83,7 +94,8 @@ __global__ __launch_bounds__(256) void k_route_topk(const float* __restrict__ lo
                                                     int K, int32_t* __restrict__ top_idx,
                                                     float* __restrict__ top_w,
                                                     int32_t* __restrict__ tok_e,
-                                                    float* __restrict__ tok_ew) {
+                                                    float* __restrict__ tok_ew,
+                                                    const int32_t* __restrict__ active) {
   constexpr int TPW = 64 / SEG;
   const int lane = threadIdx.x & 63;
   const int t0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * TPW;
@@ -92,24 +104,25 @@ __global__ __launch_bounds__(256) void k_route_topk(const float* __restrict__ lo
   const int t = t0 + lane / SEG;
   const bool ok = t < N;
   const float v = logits[static_cast<int64_t>(ok ? t : N - 1) * E + (e < E ? e : E - 1)];
-  topk_seg<SEG>(v, t, ok, E, K, top_idx, top_w, tok_e, tok_ew, nullptr, nullptr);
+  const bool live = !active || active[ok ? t : N - 1] != 0;
+  topk_seg<SEG>(v, t, ok, live, E, K, top_idx, top_w, tok_e, tok_ew, nullptr, nullptr);
 }
 
 // segment width for E entries per token (E <= 64)
 inline int seg_of(int E) { return E <= 16 ? 16 : (E <= 32 ? 32 : 64); }
 
 int launch_route_topk(const float* logits, int N, int E, int K, int32_t* top_idx, float* top_w,
-                      int32_t* tok_e, float* tok_ew, hipStream_t s) {
+                      int32_t* tok_e, float* tok_ew, const int32_t* active, hipStream_t s) {
   if (E < 1 || E > 64 || K < 1 || K > E || K > 16) return SMOE_EINVAL;
   if (N <= 0) return SMOE_OK;
   const int seg = seg_of(E), per_block = 4 * (64 / seg);
   const dim3 grid((N + per_block - 1) / per_block), block(256);
   if (seg == 16)
-    hipLaunchKernelGGL(k_route_topk<16>, grid, block, 0, s, logits, N, E, K, top_idx, top_w, tok_e, tok_ew);
+    hipLaunchKernelGGL(k_route_topk<16>, grid, block, 0, s, logits, N, E, K, top_idx, top_w, tok_e, tok_ew, active);
   else if (seg == 32)
-    hipLaunchKernelGGL(k_route_topk<32>, grid, block, 0, s, logits, N, E, K, top_idx, top_w, tok_e, tok_ew);
+    hipLaunchKernelGGL(k_route_topk<32>, grid, block, 0, s, logits, N, E, K, top_idx, top_w, tok_e, tok_ew, active);
   else
-    hipLaunchKernelGGL(k_route_topk<64>, grid, block, 0, s, logits, N, E, K, top_idx, top_w, tok_e, tok_ew);
+    hipLaunchKernelGGL(k_route_topk<64>, grid, block, 0, s, logits, N, E, K, top_idx, top_w, tok_e, tok_ew, active);
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 
@@ -765,7 +778,7 @@ __global__ __launch_bounds__(1024) void k_front_route(
     int32_t* __restrict__ edge_idx, float* __restrict__ edge_w, int32_t* __restrict__ tok_d,
     float* __restrict__ tok_dc, int32_t* __restrict__ d_cnt, int32_t* __restrict__ d_acnt,
     int32_t* __restrict__ d_off, int32_t* __restrict__ d_rows, float* __restrict__ d_roww,
-    int32_t* __restrict__ d_tokrow) {
+    int32_t* __restrict__ d_tokrow, const int32_t* __restrict__ active) {
   constexpr int PASS = 1024 / SEG;  // tokens per pass
   __shared__ int32_t s_e[kFrontMaxSrc], s_etr[kFrontMaxSrc], s_d[kFrontMaxDst], s_dtr[kFrontMaxDst];
   __shared__ float s_ew[kFrontMaxSrc], s_dc[kFrontMaxDst];
@@ -780,8 +793,9 @@ __global__ __launch_bounds__(1024) void k_front_route(
     const int t = t0 + tl;
     const bool ok = t < N;
     const float v = front[static_cast<int64_t>(ok ? t : N - 1) * ldf + le];
+    const bool live = !active || active[ok ? t : N - 1] != 0;
     if (ok && e < E) logits[static_cast<int64_t>(t) * E + e] = v;
-    topk_seg<SEG>(v, t, ok, E, K, top_idx, top_w, tok_e, tok_ew, s_e, s_ew);
+    topk_seg<SEG>(v, t, ok, live, E, K, top_idx, top_w, tok_e, tok_ew, s_e, s_ew);
   }
   lds_barrier();
   // 2 expert plan (wave 0)
@@ -827,7 +841,7 @@ int launch_front_route(const float* front, int ldf, int N, int E, int K, int M, 
                        int32_t* e_rows, float* e_roww, int32_t* e_tokrow, float* edge_logit,
                        int32_t* edge_idx, float* edge_w, int32_t* tok_d, float* tok_dc,
                        int32_t* d_cnt, int32_t* d_acnt, int32_t* d_off, int32_t* d_rows,
-                       float* d_roww, int32_t* d_tokrow, hipStream_t s) {
+                       float* d_roww, int32_t* d_tokrow, const int32_t* active, hipStream_t s) {
   if (N < 1 || N > kFrontMaxN || E < 1 || E > 64 || K < 1 || K > 16 || K > E || M < 1 || M > 16 ||
       M > E || S < 1 || S > 64 || ldf < E + E * E)
     return SMOE_EINVAL;
@@ -835,7 +849,7 @@ int launch_front_route(const float* front, int ldf, int N, int E, int K, int M, 
   hipLaunchKernelGGL((k_front_route<SG, KB>), dim3(1), dim3(1024), 0, s, front, ldf, N, E, K, M, S, \
                      logits, top_idx, top_w, tok_e, tok_ew, e_cnt, e_acnt, e_off, e_rows,          \
                      e_roww, e_tokrow, edge_logit, edge_idx, edge_w, tok_d, tok_dc, d_cnt, d_acnt, \
-                     d_off, d_rows, d_roww, d_tokrow)
+                     d_off, d_rows, d_roww, d_tokrow, active)
 #define SMOE_FRONT_K(SG)           \
   do {                             \
     if (K <= 1) SMOE_FRONT(SG, 1); \

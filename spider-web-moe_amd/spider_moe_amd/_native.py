@@ -62,6 +62,9 @@ SIGNATURES = {
                                      _vp]),
     "smoe_block_forward": (_c_int, [ctypes.POINTER(SmoeBlock), _vp, _vp, _vp, _c_int, _c_int,
                                     _c_int, _vp, _sz, _vp]),
+    "smoe_block_forward_exit": (_c_int, [ctypes.POINTER(SmoeBlock), _vp, _vp, _vp, _c_int,
+                                         _c_int, _c_int, _vp, ctypes.c_float, _vp, _vp, _vp, _sz,
+                                         _vp]),
     "smoe_router_workspace_bytes": (_sz, [_c_int, _c_int]),
     "smoe_router_topk": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int, _c_int, _vp,
                                   _vp, _vp, _vp, _sz, _vp]),
@@ -92,7 +95,7 @@ STAGES = ["router_gemm", "route_topk", "expert_plan", "edge_logits", "edge_topm"
           # bf16 steps of N <= 64: stages 0-5 as one GEMM and one routing workgroup
           "front_gemm", "front_route"]
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 _LIB = None
 
 

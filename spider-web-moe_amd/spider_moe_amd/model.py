@@ -258,6 +258,8 @@ class SpiderMoELayer(nn.Module):
         d.experts = ex
         d.ln_w, d.ln_b = f32(self.norm.weight).data_ptr(), f32(self.norm.bias).data_ptr()
         d.alpha, d.beta, d.eps = self.residual_scale, self.reinject_weight, self.norm.eps
+        # exit gate: exit_head weight [H] then bias, fp32
+        k.exit_wb = f32(torch.cat([self.exit_head.weight.reshape(-1), self.exit_head.bias.reshape(-1)]))
         self._packed, self._packed_key = k, key
         return k
 
@@ -273,7 +275,7 @@ class SpiderMoELayer(nn.Module):
         return self._ws
 
     # ----------------------------------------------------------- forward ----
-    def _run(self, h, x0, loop_begin: int, num_loops: int):
+    def _run(self, h, x0, loop_begin: int, num_loops: int, gate=None):
         if torch.is_grad_enabled() and self.training and any(p.requires_grad for p in self.parameters()):
             raise RuntimeError("spider_moe_amd's HIP block is forward-only: call it under "
                                "torch.no_grad() or in eval mode")
@@ -286,10 +288,18 @@ class SpiderMoELayer(nn.Module):
         out = torch.empty_like(h2)
         k = self._pack()
         ws = self._workspace(n, dev)
-        nat.check(nat.lib().smoe_block_forward(ctypes.byref(k.desc), h2.data_ptr(), x2.data_ptr(),
-                                               out.data_ptr(), n, loop_begin, num_loops,
-                                               ws.data_ptr(), ws.numel(), nat.stream_of(dev)),
-                  "smoe_block_forward")
+        if gate is None:
+            nat.check(nat.lib().smoe_block_forward(ctypes.byref(k.desc), h2.data_ptr(), x2.data_ptr(),
+                                                   out.data_ptr(), n, loop_begin, num_loops,
+                                                   ws.data_ptr(), ws.numel(), nat.stream_of(dev)),
+                      "smoe_block_forward")
+        else:
+            threshold, active, loops = gate
+            nat.check(nat.lib().smoe_block_forward_exit(
+                ctypes.byref(k.desc), h2.data_ptr(), x2.data_ptr(), out.data_ptr(), n, loop_begin,
+                num_loops, k.exit_wb.data_ptr(), float(threshold), active.data_ptr(),
+                loops.data_ptr(), ws.data_ptr(), ws.numel(), nat.stream_of(dev)),
+                "smoe_block_forward_exit")
         self._last_n = n
         return out.view(b, t, width)
 
@@ -310,6 +320,31 @@ class SpiderMoELayer(nn.Module):
         if loop_begin < 0 or num_loops < 0 or loop_begin + num_loops > self.num_loops:
             raise IndexError("loop range out of bounds")
         return self._run(h, x0, loop_begin, num_loops)
+
+    def forward_loops_exit(self, h, x0, threshold: float, loop_begin: int = 0,
+                           num_loops: int | None = None, active=None, loops=None):
+        """Early-exit decode over loops [loop_begin, loop_begin+num_loops)
+        in one native call, the active set kept on the device
+        (SpiderWebLM._run_recurrent_decode with early_exit, model.py:450-473;
+        ActiveSet, active_set.py:14-64).  A token leaves the orbit after the
+        loop where sigmoid(exit_head(h')) > threshold and keeps that h'.
+        active / loops (int32 [B*T], updated in place; default: all in
+        orbit / zeros) carry the set across calls.  Returns
+        (h_out, active, loops); loops[t] = loops token t ran."""
+        if num_loops is None:
+            num_loops = self.num_loops - loop_begin
+        if loop_begin < 0 or num_loops < 0 or loop_begin + num_loops > self.num_loops:
+            raise IndexError("loop range out of bounds")
+        n = h.shape[0] * h.shape[1]
+        if active is None:
+            active = torch.ones(n, dtype=torch.int32, device=h.device)
+        if loops is None:
+            loops = torch.zeros(n, dtype=torch.int32, device=h.device)
+        for name, t in (("active", active), ("loops", loops)):
+            if t.dtype != torch.int32 or t.numel() != n or not t.is_contiguous() or t.device != h.device:
+                raise ValueError(f"{name} must be a contiguous int32 tensor of {n} elements on {h.device}")
+        out = self._run(h, x0, loop_begin, num_loops, gate=(threshold, active, loops))
+        return out, active, loops
 
     # ------------------------------------------------------ diagnostics ----
     def last_routing(self) -> dict:
@@ -453,6 +488,18 @@ class SpiderWebLM(nn.Module):
             self.register_buffer("rope_cos", cos, persistent=False)
             self.register_buffer("rope_sin", sin, persistent=False)
 
+    def _run_recurrent_full(self, h, x0):
+        """model.py:445-448."""
+        return self.recurrent.forward_loops(h, x0, 0, self.cfg.num_loops)
+
+    def _run_recurrent_decode(self, h, x0, early_exit):
+        """model.py:450-473: with early_exit, rows whose exit_head confidence
+        passes the threshold stop consuming loops (device-side active set,
+        no host synchronization between loops)."""
+        if not early_exit:
+            return self._run_recurrent_full(h, x0)
+        return self.recurrent.forward_loops_exit(h, x0, self.cfg.early_exit_threshold)[0]
+
     def quantize_moe_experts(self, group_size: int = 64) -> None:
         self.recurrent.quantize_experts(group_size=group_size)
 
@@ -480,6 +527,11 @@ class SpiderWebLM(nn.Module):
         if not early_exit and not return_stats:
             h = self.recurrent.forward_loops(h, x0, 0, self.cfg.num_loops)
             loops_used = self.cfg.num_loops
+        elif not return_stats:
+            # the block is token-wise, so freezing exited tokens (model.py:694-696)
+            # is the device-side active set; loops run = the last token's count
+            h, _, loops = self.recurrent.forward_loops_exit(h, x0, self.cfg.early_exit_threshold)
+            loops_used = int(loops.max().item()) if loops.numel() else 0
         else:
             active = torch.ones(h.shape[:2], dtype=torch.bool, device=h.device)
             for loop_idx in range(self.cfg.num_loops):

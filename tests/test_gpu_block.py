@@ -300,3 +300,123 @@ def test_stage_entries_compose_block_forward(spec):
         dst = {int(x_) for x_ in ei[t].flatten().tolist() if x_ >= 0}
         assert dst == set(torch.nonzero(aux.coef[t] != 0).flatten().tolist()), t
         assert torch.allclose(eww[t].sum(-1), torch.ones(k), atol=1e-5)  # softmax rows
+
+
+# ------------------------------------------------ early-exit decode ----
+EXIT_CASES = [dict(kind="bf16", tokens=64), dict(kind="bf16", tokens=300), dict(kind="f32", tokens=0)]
+
+
+def _exit_layer(case):
+    """bf16 SwiGLU blocks at N = 64 (fused routing front) and N = 300
+    (separate routing stages), and the reference fp32 golden block."""
+    if case["kind"] == "f32":
+        z, layer = _layer_from_golden("block_small")
+        return layer, torch.from_numpy(z["loop0/in"]).to(dev), torch.from_numpy(z["x0"]).to(dev)
+    from spider_moe_amd.workloads import make_block
+    wl = make_block("c1", tokens=case["tokens"], hidden_size=128, num_experts=16, top_k=2,
+                    edges_per_expert=2, expert_ffn_size=256, num_loops=3,
+                    expert_activation="swiglu", experts="bf16")
+    return wl.layer, wl.h, wl.x0
+
+
+def _set_exit(layer, w, b):
+    with torch.no_grad():
+        layer.exit_head.weight.copy_(w.reshape(1, -1).to(layer.exit_head.weight))
+        layer.exit_head.bias.fill_(b)
+
+
+@pytest.mark.parametrize("case", EXIT_CASES, ids=lambda c: f"{c['kind']}-{c['tokens']}")
+def test_exit_gate_forced_and_never(case):
+    """exit bias +20: every token leaves after the first loop and keeps it
+    (tests/test_early_exit_compaction.py:51-70); bias -20: the full loop run
+    (:73-82).  Both bit for bit against smoe_block_forward."""
+    say("exit forced/never", case)
+    layer, h, x0 = _exit_layer(case)
+    r = layer.num_loops
+    zero = torch.zeros(layer.hidden_size)
+    with torch.no_grad():
+        _set_exit(layer, zero, 20.0)
+        one = layer(h, x0, 0)
+        out, active, loops = layer.forward_loops_exit(h, x0, 0.85)
+        torch.cuda.synchronize()
+        assert torch.equal(out, one)
+        assert int(active.abs().sum()) == 0 and bool((loops == 1).all())
+        _set_exit(layer, zero, -20.0)
+        full = layer.forward_loops(h, x0, 0, r)
+        out, active, loops = layer.forward_loops_exit(h, x0, 0.85)
+        torch.cuda.synchronize()
+        assert torch.equal(out, full)
+        assert bool((active == 1).all()) and bool((loops == r).all())
+
+
+@pytest.mark.parametrize("case", EXIT_CASES[:2], ids=lambda c: f"{c['kind']}-{c['tokens']}")
+def test_exit_gate_partial_teacher_forced(case):
+    """A random exit_head: tokens leave at different loops.  Teacher-forced
+    against the ungated block run loop by loop on every token: a token's
+    output is the ungated state after its exit loop (within 1e-2; the count
+    of bit-identical rows is printed), and each exit decision equals the
+    oracle's sigmoid(exit_head(h')) > threshold on that state, except where
+    the exit logit is within 1e-4 of the threshold's."""
+    say("exit partial", case)
+    layer, h, x0 = _exit_layer(case)
+    r, hid = layer.num_loops, layer.hidden_size
+    ew = torch.randn(hid, generator=torch.Generator().manual_seed(9)) / hid ** 0.5
+    thr = 0.6
+    _set_exit(layer, ew, 0.0)
+    ew_stored = layer.exit_head.weight.detach().float().cpu().reshape(-1)
+    with torch.no_grad():
+        out, active, loops = layer.forward_loops_exit(h, x0, thr)
+        states, cur = [], h
+        for li in range(r):
+            cur = layer(cur, x0, li)
+            states.append(cur.reshape(-1, hid).float().cpu())
+    torch.cuda.synchronize()
+    n = states[0].shape[0]
+    loops = loops.cpu().long()
+    z_thr = float(np.log(thr / (1 - thr)))
+    exp_loops = torch.full((n,), r, dtype=torch.long)
+    tie = torch.zeros(n, dtype=torch.bool)
+    done = torch.zeros(n, dtype=torch.bool)
+    for li in range(r):
+        z = B.exit_logit(states[li], ew_stored, 0.0)
+        tie |= ~done & ((z - z_thr).abs() < 1e-4)
+        ex = ~done & (torch.sigmoid(z) > thr)
+        exp_loops[ex] = li + 1
+        done |= ex
+    ok = ~tie
+    assert torch.equal(loops[ok], exp_loops[ok]), (loops[ok][:20], exp_loops[ok][:20])
+    assert len(set(loops.tolist())) >= 2, "no mix of exit loops"
+    assert torch.equal(active.cpu()[ok] != 0, ~done[ok])
+    pick = torch.stack([states[int(l) - 1][t] for t, l in enumerate(loops.tolist())])
+    g = out.reshape(-1, hid).float().cpu()
+    err = (g[ok] - pick[ok]).abs()
+    assert bool((err <= 1e-2 + 1e-2 * pick[ok].abs()).all()), float(err.max())
+    say("loops hist", torch.bincount(loops, minlength=r + 1).tolist(), "ties", int(tie.sum()),
+        "bit-identical rows", int((g[ok] == pick[ok]).all(-1).sum()), "of", int(ok.sum()))
+
+
+def test_decode_graph_replays_match_eager():
+    """The R-loop decode with the exit gate captured as one HIP graph
+    (spider_infer/cuda_graph.py:79-130): replays with new inputs, with eager
+    work in between, equal the eager call bit for bit; so does the ungated
+    graph against forward_loops."""
+    from spider_moe_amd.graph import BlockDecodeGraph
+    say("decode graph")
+    layer, h, x0 = _exit_layer(EXIT_CASES[0])
+    hid = layer.hidden_size
+    ew = torch.randn(hid, generator=torch.Generator().manual_seed(9)) / hid ** 0.5
+    _set_exit(layer, ew, 0.0)
+    runner = BlockDecodeGraph(layer)
+    gen = torch.Generator().manual_seed(21)
+    with torch.no_grad():
+        for i in range(3):
+            hi = torch.randn(h.shape, generator=gen).to(h)
+            xi = torch.randn(x0.shape, generator=gen).to(x0)
+            g_out, g_loops = runner.run(hi, xi, early_exit=True, threshold=0.6)
+            e_out, _, e_loops = layer.forward_loops_exit(hi, xi, 0.6)
+            torch.cuda.synchronize()
+            assert torch.equal(g_out, e_out) and torch.equal(g_loops, e_loops), i
+            g_full, _ = runner.run(hi, xi, early_exit=False)
+            torch.cuda.synchronize()
+            assert torch.equal(g_full, layer.forward_loops(hi, xi)), i
+    assert runner.stats()["hits"] == 4 and runner.stats()["misses"] == 2

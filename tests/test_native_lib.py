@@ -38,7 +38,7 @@ def test_exports_every_declared_symbol(nat):
 
 def test_identity(nat):
     lib = nat.lib()
-    assert lib.smoe_abi_version() == 5
+    assert lib.smoe_abi_version() == 6
     assert lib.smoe_backend_name() == b"hip-gfx950"
     assert lib.smoe_backend_caps() == 0b1111
 
@@ -117,6 +117,22 @@ def test_capacity_and_range_errors(nat):
     assert rc == 1  # loop range past num_loops
     # N == 0 is a no-op
     assert lib.smoe_block_forward(ctypes.byref(b), None, None, None, 0, 0, 1, None, 0, None) == 0
+
+
+def test_exit_gate_argument_errors(nat):
+    """smoe_block_forward_exit: missing gate buffers, a NaN threshold, a
+    short workspace and a bad loop range are rejected before any launch."""
+    lib = nat.lib()
+    b = _block(nat)
+    need = lib.smoe_block_workspace_bytes(ctypes.byref(b), 64)
+    p = 0x1000
+    f = lambda wb, thr, act, ws_bytes=need, lb=0: lib.smoe_block_forward_exit(
+        ctypes.byref(b), p, p, p, 64, lb, 1, wb, thr, act, None, p, ws_bytes, None)
+    assert f(None, 0.5, p) == 1
+    assert f(p, 0.5, None) == 1
+    assert f(p, float("nan"), p) == 1
+    assert f(p, 0.5, p, need - 1) == 3
+    assert f(p, 0.5, p, need, 6) == 1  # loop 6 of 6
 
 
 def test_stage_entries_reject_bad_arguments(nat):

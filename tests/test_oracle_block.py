@@ -322,3 +322,74 @@ def test_planted_message_mistake_is_caught():
             coef_bad[torch.arange(h.shape[0]), d] += tw[:, s] * ew[torch.arange(h.shape[0]), ti[:, s], j]
     bad = B.message_grouped(h, w, coef_bad)
     assert (bad - good).abs().max() > 1e-2
+
+
+# ------------------------------------------------------- early exit ----
+def _exit_case():
+    z, w, cfg = load_block("block_mid")
+    hid = cfg["hidden_size"]
+    h = torch.from_numpy(z["loop0/in"]).reshape(-1, hid)[:24]
+    x0 = torch.randn(h.shape, generator=torch.Generator().manual_seed(11))
+    return w, h, x0, cfg["num_loops"]
+
+
+def test_exit_oracle_forced_exit_is_one_loop():
+    """exit_head bias +20: every row leaves after loop 0 and keeps the
+    loop-0 state (tests/test_early_exit_compaction.py:51-70)."""
+    w, h, x0, r = _exit_case()
+    one, _ = B.block_forward(h, x0, w, 0)
+    out, loops, _ = B.block_loops_exit(h, x0, w, r, torch.zeros(h.shape[1]), 20.0, 0.85)
+    assert torch.equal(out, one)
+    assert (loops == 1).all()
+
+
+def test_exit_oracle_no_exit_runs_all_loops():
+    """exit_head bias -20: no row leaves; the result is the full loop run
+    (tests/test_early_exit_compaction.py:73-82)."""
+    w, h, x0, r = _exit_case()
+    full = B.block_loops(h, x0, w, r)
+    out, loops, _ = B.block_loops_exit(h, x0, w, r, torch.zeros(h.shape[1]), -20.0, 0.85)
+    assert torch.equal(out, full)
+    assert (loops == r).all()
+
+
+def _per_token_exit(h, x0, w, r, ew, eb, thr):
+    """Brute force: each row alone, loop by loop, until it exits."""
+    outs, loops = [], []
+    for t in range(h.shape[0]):
+        ht, n = h[t:t + 1].float(), 0
+        for li in range(r):
+            ht, _ = B.block_forward(ht, x0[t:t + 1], w, li)
+            n += 1
+            if bool(torch.sigmoid(B.exit_logit(ht, ew, eb)) > thr):
+                break
+        outs.append(ht)
+        loops.append(n)
+    return torch.cat(outs), torch.tensor(loops)
+
+
+def test_exit_oracle_matches_per_token_loop():
+    """Partial exits (a random exit_head): the compacted batch equals each
+    row run alone until its own exit (tests/test_early_exit_compaction.py:85-109
+    checks the exited row against a single loop)."""
+    w, h, x0, r = _exit_case()
+    ew = torch.randn(h.shape[1], generator=torch.Generator().manual_seed(3)) * 0.5
+    out, loops, margin = B.block_loops_exit(h, x0, w, r, ew, 0.0, 0.7)
+    ref, ref_loops = _per_token_exit(h, x0, w, r, ew, 0.0, 0.7)
+    assert len(set(loops.tolist())) >= 2, loops  # a mix of exit loops
+    ok = margin > 1e-4
+    assert torch.equal(loops[ok], ref_loops[ok])
+    torch.testing.assert_close(out[ok], ref[ok], rtol=1e-5, atol=1e-5)
+
+
+def test_planted_exit_mistake_is_caught():
+    """Updating rows after they exit (dropping the compaction) differs from
+    the per-row run."""
+    w, h, x0, r = _exit_case()
+    ew = torch.randn(h.shape[1], generator=torch.Generator().manual_seed(3)) * 0.5
+    _, loops, _ = B.block_loops_exit(h, x0, w, r, ew, 0.0, 0.7)
+    bad = B.block_loops(h, x0, w, r)  # every row runs every loop
+    ref, _ = _per_token_exit(h, x0, w, r, ew, 0.0, 0.7)
+    early = loops < r
+    assert bool(early.any())
+    assert (bad[early] - ref[early]).abs().max() > 1e-2
