@@ -163,6 +163,11 @@ __global__ __launch_bounds__(256) void k_epilogue(
 #pragma unroll
       for (int i = 0; i < 8; ++i) gb[c][i] = 0.f;
   }
+  // the loop count is read here, unconditionally (from active when loops is
+  // null, value unused), so its latency hides behind the row loads; a load
+  // under the final lane-0 branch would be waited for at the kernel's end
+  int loops_in = 0;
+  if (GATE) loops_in = (loops ? loops : active)[t];
   if (GATE && active[t] == 0) {  // wave-uniform: out of orbit, h passes through
     if (out != h)
 #pragma unroll
@@ -236,7 +241,7 @@ __global__ __launch_bounds__(256) void k_epilogue(
     const float z = wave_sum(g) + exit_wb[H];
     if (lane == 0) {
       if (1.0f / (1.0f + expf(-z)) > thr) active[t] = 0;
-      if (loops) loops[t] += 1;
+      if (loops) loops[t] = loops_in + 1;
     }
   }
 }
