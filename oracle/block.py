@@ -323,14 +323,16 @@ def block_loops(h, x0, w: BlockWeights, num_loops: int, **kw):
     return h
 
 
-def exit_logit(h, exit_w, exit_b):
+def exit_logit(h, exit_w, exit_b, bf16: bool = False):
     """exit_head(h) (model.py:185,467): h . w + b in float32; the confidence
-    is its sigmoid."""
-    return h.float() @ exit_w.float().reshape(-1) + float(exit_b)
+    is its sigmoid.  bf16: the exit head of a bf16 model is a bf16 Linear,
+    whose output is rounded to bf16 before `.float()` and the sigmoid."""
+    z = h.float() @ exit_w.float().reshape(-1) + float(exit_b)
+    return round_bf16(z) if bf16 else z
 
 
 def block_loops_exit(h, x0, w: BlockWeights, num_loops: int, exit_w, exit_b, threshold: float,
-                     *, loop_begin: int = 0, **kw):
+                     *, loop_begin: int = 0, logit_bf16: bool = False, **kw):
     """Early-exit decode: SpiderWebLM._run_recurrent_decode(early_exit=True)
     (model.py:450-473) over the ActiveSet compaction of active_set.py:14-64.
     Each loop gathers the rows still in orbit (compact_active: index_select),
@@ -356,7 +358,7 @@ def block_loops_exit(h, x0, w: BlockWeights, num_loops: int, exit_w, exit_b, thr
             break
         h_new, _ = block_forward(h.index_select(0, idx), x0.index_select(0, idx), w, r, **kw)
         h.index_copy_(0, idx, h_new)
-        z = exit_logit(h_new, exit_w, exit_b)
+        z = exit_logit(h_new, exit_w, exit_b, bf16=logit_bf16)
         loops[idx] += 1
         margin[idx] = torch.minimum(margin[idx], (z - z_thr).abs())
         idx = idx[~(torch.sigmoid(z) > threshold)]

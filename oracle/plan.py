@@ -18,8 +18,8 @@ Pins (tests/test_oracle_plan.py): the reference's known answer
 (tests/test_forge_04.py:18-27: experts {0,1,2}, expert 1 holds 2 tokens); the
 duplicate-slot case (tests/test_sparse_experts_parity.py:77-98); invariants
 (counts sum to the number of positive merged pairs; each expert's positions
-strictly ascending); a brute-force per-token enumeration; and golden plans
-written by the reference's own build_dispatch_plan (tests/golden/plan.npz).
+strictly ascending); and a brute-force per-token enumeration.  No golden
+plan file is committed: the known answer and the brute force pin it.
 """
 from __future__ import annotations
 

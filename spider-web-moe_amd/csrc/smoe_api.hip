@@ -338,12 +338,20 @@ int block_forward(const smoe_block* b, const void* h_in, const void* x0, void* h
   if (rc != SMOE_OK) return rc;
   if (N < 0 || loop_begin < 0 || num_loops < 0 || loop_begin + num_loops > b->R)
     return fail(SMOE_EINVAL, "N / loop range");
-  if (N == 0 || num_loops == 0) return SMOE_OK;
+  if (N == 0) return SMOE_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (num_loops == 0) {  // no loop: h_out = h_in (the reference returns h unchanged)
+    if (!h_in || !h_out) return fail(SMOE_EINVAL, "null buffer");
+    if (h_out != h_in &&
+        hipMemcpyAsync(h_out, h_in, static_cast<size_t>(N) * b->H * esize(b->act_dtype),
+                       hipMemcpyDeviceToDevice, s) != hipSuccess)
+      return fail(SMOE_EHIP, "hipMemcpyAsync");
+    return SMOE_OK;
+  }
   if (!h_in || !x0 || !h_out || !ws) return fail(SMOE_EINVAL, "null buffer");
   smoe_ws_layout l;
   make_layout(b, N, &l);
   if (ws_bytes < l.total) return fail(SMOE_ECAPACITY, "workspace too small");
-  hipStream_t s = static_cast<hipStream_t>(stream);
   const int H = b->H, E = b->E, K = b->K, M = b->M, L = b->L, S = l.S;
   const int adt = b->act_dtype, fdt = l.ffn_dtype;
   const int gfmt = adt == SMOE_F32 ? SMOE_F32 : SMOE_BF16;  // router / edge weights

@@ -238,7 +238,10 @@ __global__ __launch_bounds__(256) void k_epilogue(
     }
   }
   if (GATE) {
-    const float z = wave_sum(g) + exit_wb[H];
+    // a bf16 model's exit_head is a bf16 Linear: its output (the logit) is
+    // rounded to bf16 before the fp32 sigmoid (model.py:467)
+    float z = wave_sum(g) + exit_wb[H];
+    if (ADT == SMOE_BF16) z = bf2f(f2bf(z));
     if (lane == 0) {
       if (1.0f / (1.0f + expf(-z)) > thr) active[t] = 0;
       if (loops) loops[t] = loops_in + 1;

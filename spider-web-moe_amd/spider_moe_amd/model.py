@@ -88,6 +88,7 @@ class SpiderMoELayer(nn.Module):
         self.exit_head = nn.Linear(h, 1)
         self.residual_scale = cfg.residual_scale
         self.reinject_weight = cfg.re_inject_weight
+        self.early_exit_threshold = float(getattr(cfg, "early_exit_threshold", 0.85))
         self.expert_parallel = bool(getattr(cfg, "expert_parallel", True))
         self.offload_experts = False
         self._expert_store = None
@@ -107,6 +108,7 @@ class SpiderMoELayer(nn.Module):
         self._packed_key = None
         self._ws: torch.Tensor | None = None
         self._last_n = 0
+        self._last_ws: torch.Tensor | None = None
 
     # ------------------------------------------------------ quantization ----
     @torch.no_grad()
@@ -263,19 +265,27 @@ class SpiderMoELayer(nn.Module):
         self._packed, self._packed_key = k, key
         return k
 
-    def _workspace(self, n: int, dev) -> torch.Tensor:
+    def workspace_bytes(self, n: int) -> int:
+        """Bytes of the native workspace a call over n tokens needs."""
         k = self._pack()
         need = nat.lib().smoe_block_workspace_bytes(ctypes.byref(k.desc), n)
         if need == 0:
             nat.check(nat.lib().smoe_block_workspace_layout(ctypes.byref(k.desc), n,
                                                             ctypes.byref(nat.SmoeWsLayout())),
                       "smoe_block_workspace_layout")
+        return max(need, 256)
+
+    def _workspace(self, n: int, dev) -> torch.Tensor:
+        need = self.workspace_bytes(n)
         if self._ws is None or self._ws.numel() < need or self._ws.device != dev:
-            self._ws = torch.empty(max(need, 256), dtype=torch.uint8, device=dev)
+            self._ws = torch.empty(need, dtype=torch.uint8, device=dev)
         return self._ws
 
     # ----------------------------------------------------------- forward ----
-    def _run(self, h, x0, loop_begin: int, num_loops: int, gate=None):
+    def _run(self, h, x0, loop_begin: int, num_loops: int, gate=None, workspace=None):
+        """workspace: a caller-owned uint8 device tensor of at least
+        workspace_bytes(B*T) bytes (a captured graph keeps its own), or None
+        for the layer's shared one (reallocated when a call needs more)."""
         if torch.is_grad_enabled() and self.training and any(p.requires_grad for p in self.parameters()):
             raise RuntimeError("spider_moe_amd's HIP block is forward-only: call it under "
                                "torch.no_grad() or in eval mode")
@@ -285,9 +295,18 @@ class SpiderMoELayer(nn.Module):
         h2 = _aligned(h.reshape(b * t, width).to(act).contiguous())
         x2 = _aligned(x0.reshape(b * t, width).to(act).contiguous())
         n = b * t
+        if num_loops == 0:  # no loop to run: h unchanged (a copy, as for any call)
+            return h2.clone().view(b, t, width)
         out = torch.empty_like(h2)
         k = self._pack()
-        ws = self._workspace(n, dev)
+        if workspace is None:
+            ws = self._workspace(n, dev)
+        else:
+            if (workspace.dtype != torch.uint8 or workspace.device != dev
+                    or not workspace.is_contiguous() or workspace.numel() < self.workspace_bytes(n)):
+                raise ValueError("workspace must be a contiguous uint8 tensor on the input's GPU "
+                                 f"of at least {self.workspace_bytes(n)} bytes")
+            ws = workspace
         if gate is None:
             nat.check(nat.lib().smoe_block_forward(ctypes.byref(k.desc), h2.data_ptr(), x2.data_ptr(),
                                                    out.data_ptr(), n, loop_begin, num_loops,
@@ -301,6 +320,7 @@ class SpiderMoELayer(nn.Module):
                 loops.data_ptr(), ws.data_ptr(), ws.numel(), nat.stream_of(dev)),
                 "smoe_block_forward_exit")
         self._last_n = n
+        self._last_ws = ws
         return out.view(b, t, width)
 
     def forward(self, h, x0, loop_idx, return_stats=False):
@@ -312,25 +332,31 @@ class SpiderMoELayer(nn.Module):
             return updated
         return updated, self._stats(h, updated, int(loop_idx))
 
-    def forward_loops(self, h, x0, loop_begin: int = 0, num_loops: int | None = None):
+    def forward_loops(self, h, x0, loop_begin: int = 0, num_loops: int | None = None, *,
+                      workspace=None):
         """Loops [loop_begin, loop_begin+num_loops) in one native call — the
-        loop driver of SpiderWebLM._run_recurrent_full (model.py:445-448)."""
+        loop driver of SpiderWebLM._run_recurrent_full (model.py:445-448).
+        With num_loops == 0 the result is a copy of h."""
         if num_loops is None:
             num_loops = self.num_loops - loop_begin
         if loop_begin < 0 or num_loops < 0 or loop_begin + num_loops > self.num_loops:
             raise IndexError("loop range out of bounds")
-        return self._run(h, x0, loop_begin, num_loops)
+        return self._run(h, x0, loop_begin, num_loops, workspace=workspace)
 
-    def forward_loops_exit(self, h, x0, threshold: float, loop_begin: int = 0,
-                           num_loops: int | None = None, active=None, loops=None):
+    def forward_loops_exit(self, h, x0, threshold: float | None = None, loop_begin: int = 0,
+                           num_loops: int | None = None, active=None, loops=None, *,
+                           workspace=None):
         """Early-exit decode over loops [loop_begin, loop_begin+num_loops)
         in one native call, the active set kept on the device
         (SpiderWebLM._run_recurrent_decode with early_exit, model.py:450-473;
         ActiveSet, active_set.py:14-64).  A token leaves the orbit after the
         loop where sigmoid(exit_head(h')) > threshold and keeps that h'.
         active / loops (int32 [B*T], updated in place; default: all in
-        orbit / zeros) carry the set across calls.  Returns
-        (h_out, active, loops); loops[t] = loops token t ran."""
+        orbit / zeros) carry the set across calls.  threshold defaults to
+        the config's early_exit_threshold.  Returns (h_out, active, loops);
+        loops[t] = loops token t ran."""
+        if threshold is None:
+            threshold = self.early_exit_threshold
         if num_loops is None:
             num_loops = self.num_loops - loop_begin
         if loop_begin < 0 or num_loops < 0 or loop_begin + num_loops > self.num_loops:
@@ -343,7 +369,8 @@ class SpiderMoELayer(nn.Module):
         for name, t in (("active", active), ("loops", loops)):
             if t.dtype != torch.int32 or t.numel() != n or not t.is_contiguous() or t.device != h.device:
                 raise ValueError(f"{name} must be a contiguous int32 tensor of {n} elements on {h.device}")
-        out = self._run(h, x0, loop_begin, num_loops, gate=(threshold, active, loops))
+        out = self._run(h, x0, loop_begin, num_loops, gate=(threshold, active, loops),
+                        workspace=workspace)
         return out, active, loops
 
     # ------------------------------------------------------ diagnostics ----
@@ -354,14 +381,24 @@ class SpiderMoELayer(nn.Module):
         lay = nat.SmoeWsLayout()
         nat.check(nat.lib().smoe_block_workspace_layout(ctypes.byref(k.desc), n, ctypes.byref(lay)),
                   "smoe_block_workspace_layout")
-        ws = self._ws
+        ws = self._last_ws
         e, kk, m, s = self.num_experts, self.top_k, self.edges_per_expert, lay.S
+        h = self.hidden_size
+        fdt = torch.float32 if lay.ffn_dtype == nat.F32 else torch.bfloat16
 
         def view(off, count, dtype):
             esz = torch.tensor([], dtype=dtype).element_size()
             return ws[off:off + count * esz].view(dtype).clone()
 
         out = {
+            # the last loop's message [N, H] and weighted expert outputs
+            # y [N*K, H] (row = expert-plan row) in the FFN dtype
+            "msg": view(lay.msg, n * h, fdt).view(n, h),
+            "y": view(lay.y, n * kk * h, fdt).view(n * kk, h),
+            "e_tokrow": view(lay.e_tokrow, n * kk, torch.int32).view(n, kk),
+            "d_acnt": view(lay.d_acnt, e, torch.int32),
+            "d_roww": view(lay.d_roww, n * s, torch.float32),
+            "d_tokrow": view(lay.d_tokrow, n * s, torch.int32).view(n, s),
             "logits": view(lay.logits, n * e, torch.float32).view(n, e),
             "top_idx": view(lay.top_idx, n * kk, torch.int32).view(n, kk),
             "top_w": view(lay.top_w, n * kk, torch.float32).view(n, kk),
@@ -562,9 +599,14 @@ class SpiderWebLM(nn.Module):
         return out
 
 
-def init_normal_(module: nn.Module, generator: torch.Generator, std: float = 0.02) -> None:
+def init_normal_(module: nn.Module, generator: torch.Generator, std: float | str = 0.02) -> None:
     """Seeded re-draw of every parameter in named_parameters order: matrices
-    and embeddings N(0, std), biases 0, LayerNorm weights 1, loop_bias 0."""
+    and embeddings N(0, std), biases 0, LayerNorm weights 1, loop_bias 0.
+
+    std="fan_in" draws each matrix N(0, 1/fan_in) instead (fan_in = its last
+    dimension; embeddings N(0, 1)), so every projection of an N(0, 1) input
+    is O(1): the message, the expert delta and the residual all move the
+    block's output by O(1)."""
     with torch.no_grad():
         for name, p in module.named_parameters():
             if name.endswith("loop_bias"):
@@ -575,7 +617,10 @@ def init_normal_(module: nn.Module, generator: torch.Generator, std: float = 0.0
             elif name.endswith("bias"):
                 p.zero_()
             else:
-                p.copy_(torch.randn(p.shape, generator=generator) * std)
+                scale = std
+                if std == "fan_in":
+                    scale = 1.0 if "embedding" in name else p.shape[-1] ** -0.5
+                p.copy_(torch.randn(p.shape, generator=generator) * scale)
 
 
 __all__ = ["SpiderMoELayer", "SpiderWebLM", "TransformerLayer", "SwiGLUGate", "init_normal_"]

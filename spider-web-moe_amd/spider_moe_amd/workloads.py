@@ -79,13 +79,14 @@ def block_config(name: str, tokens: int | None = None, **over) -> tuple[ModelCon
 
 
 def make_block(name: str, device="cuda", tokens: int | None = None, seed: int | None = None,
-               **over) -> BlockWorkload:
-    """Build the block of workload `name` on `device` with its inputs."""
+               std: float | str = 0.02, **over) -> BlockWorkload:
+    """Build the block of workload `name` on `device` with its inputs.
+    std: the weights' init scale (init_normal_; "fan_in" = 1/sqrt(fan_in))."""
     c = int(name[1:])
     cfg, spec = block_config(name, tokens, **over)
     gen = torch.Generator().manual_seed(1000 + c if seed is None else seed)
     layer = SpiderMoELayer(cfg)
-    init_normal_(layer, gen)
+    init_normal_(layer, gen, std)
     if spec.get("zipf"):
         with torch.no_grad():
             layer.loop_bias.copy_(zipf_loop_bias(cfg.num_loops, cfg.num_experts, spec["zipf"],

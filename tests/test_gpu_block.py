@@ -13,10 +13,10 @@ import numpy as np
 import pytest
 import torch
 
-from _helpers import TIE_GAP, oracle_weights, routing_agrees
+from _helpers import (TIE_GAP, check_edges, check_plans, check_values, oracle_weights,
+                      routing_agrees)
 from conftest import GOLDEN
 from oracle import block as B
-from oracle import plan as P
 
 pytestmark = pytest.mark.gpu
 dev = "cuda"
@@ -42,7 +42,11 @@ def _layer_from_golden(name):
 
 
 def _check_loop(layer, h, x0, loop, out_tol, mode="faithful"):
-    """Run one loop on the GPU and the oracle (same input), compare."""
+    """Run one loop on the GPU and the oracle (same input: teacher-forced),
+    compare: top-k indices and destination sets (bit-exact off near-ties),
+    both in-block dispatch plans (bit-exact, from the device's own routing),
+    per-source top-m destinations and alpha, the message and the expert
+    delta (check_values), and the block output."""
     n, hid = h.shape[0] * h.shape[1], h.shape[-1]
     with torch.no_grad():
         got = layer(h, x0, loop)
@@ -53,17 +57,15 @@ def _check_loop(layer, h, x0, loop, out_tol, mode="faithful"):
                                loop, mode=mode, out_bf16=(h.dtype == torch.bfloat16))
     ok, rep = routing_agrees(gpu, aux, layer)
     assert rep["mismatch_non_tie"] == 0, rep
-    # dispatch counts / permutation, bit-exact over the tokens with exact routing
-    if bool(ok.all()):
-        _, ocnt, operm, opw, _ = P.dispatch_plan(aux.top_i.numpy(), aux.top_w.numpy(), layer.num_experts)
-        assert gpu["e_acnt"].cpu().numpy().tolist() == ocnt.tolist()
-        rows = gpu["e_rows"].cpu().numpy()[: int(gpu["e_off"][-1])]
-        roww = gpu["e_roww"].cpu().numpy()[: len(rows)]
-        assert rows[roww > 0].tolist() == operm.tolist()
+    check_plans(gpu, layer.num_experts)
+    rep["edge_rows"] = check_edges(gpu, aux, ok)
+    rep.update(check_values(gpu, aux, ok))
     g = got.reshape(n, hid).float().cpu()
     err = (g[ok] - ref[ok]).abs()
     bound = out_tol + out_tol * ref[ok].abs()
     assert bool((err <= bound).all()), (float(err.max()), rep)
+    rep["max_err"] = float(err.max())
+    say("loop", loop, rep)
     return got, rep
 
 
@@ -105,11 +107,14 @@ SMALL = [
 
 @pytest.mark.parametrize("spec", SMALL, ids=lambda s: f"{s['act']}-{s['experts']}")
 def test_block_small_bf16_per_loop(spec):
+    """Weights N(0, 1/fan_in), so the message and the expert delta move the
+    output by O(1) (a delta = 0 or msg = 0 block fails the 1e-2 bound:
+    tests/test_oracle_block.py::test_output_bound_sees_message_and_delta)."""
     from spider_moe_amd.workloads import make_block
     say("small block", spec)
     wl = make_block("c1", tokens=300, hidden_size=128, num_experts=8, top_k=2, edges_per_expert=3,
                     expert_ffn_size=256, num_loops=3, expert_activation=spec["act"],
-                    experts=spec["experts"], group_size=64)
+                    experts=spec["experts"], group_size=64, std="fan_in")
     h = wl.h
     for r in range(3):
         h, rep = _check_loop(wl.layer, h, wl.x0, r, 1e-2)
@@ -121,12 +126,13 @@ def test_block_small_steps_fused_front(n, e, k, m):
     """bf16 steps of N <= 64 tokens run stages 1-6 as one logits GEMM over
     the router and every edge-generator row plus one routing workgroup
     (top-k, expert plan, top-m, destination plan); N = 65 and 200 take the
-    separate stages.  Routing, plans and outputs against the oracle for two
-    loops, at E 16 / 32 / 64."""
+    separate stages.  Routing, plans, edges, message, delta and outputs
+    against the oracle for two loops, at E 16 / 32 / 64."""
     from spider_moe_amd.workloads import make_block
     say("fused front", n, e, k, m)
     wl = make_block("c1", tokens=n, hidden_size=128, num_experts=e, top_k=k, edges_per_expert=m,
-                    expert_ffn_size=256, num_loops=2, expert_activation="swiglu", experts="bf16")
+                    expert_ffn_size=256, num_loops=2, expert_activation="swiglu", experts="bf16",
+                    std="fan_in")
     h = wl.h
     for r in range(2):
         h, rep = _check_loop(wl.layer, h, wl.x0, r, 1e-2)
@@ -138,47 +144,60 @@ def test_block_small_steps_fused_front(n, e, k, m):
 def test_block_skewed_empty_experts():
     from spider_moe_amd.workloads import make_block
     say("skewed small")
-    wl = make_block("c3", tokens=2000, hidden_size=128, expert_ffn_size=128, num_loops=2)
-    _, rep = _check_loop(wl.layer, wl.h, wl.x0, 0, 1e-2)
+    wl = make_block("c3", tokens=2000, hidden_size=128, expert_ffn_size=128, num_loops=2,
+                    std="fan_in")
+    h = wl.h
+    for r in range(2):
+        h, rep = _check_loop(wl.layer, h, wl.x0, r, 1e-2)
     r = wl.layer.last_routing()
     assert (r["e_acnt"] == 0).sum() >= 4  # the forced-empty experts
 
 
 @pytest.mark.parametrize("name", ["c1", "c2", "c3", "c4"])
 def test_block_full_size_token_subset(name):
-    """Full-size workload on the GPU; the oracle checks a random token subset
-    (the block is token-wise, so any subset is an exact sub-problem) and the
-    whole-batch properties: plan counts, sources and determinism."""
+    """Full-size workload on the GPU, every loop, teacher-forced: loop r runs
+    on the GPU's own loop r-1 output, and the oracle (faithful form) runs
+    loop r on a random subset of those same states (the block is token-wise,
+    so any subset is an exact sub-problem).  Per loop: both dispatch plans
+    bit-exact over all N tokens; top-k, destination sets, per-source edges,
+    message, delta and outputs on the subset; loop 0 bit-reproducible."""
     from spider_moe_amd.workloads import make_block
     say("full size", name)
     wl = make_block(name)
     layer = wl.layer
     n = wl.h.shape[0]
-    with torch.no_grad():
-        out1 = layer(wl.h, wl.x0, 0)
-        gpu = layer.last_routing()
-        out2 = layer(wl.h, wl.x0, 0)
-    torch.cuda.synchronize()
-    assert torch.equal(out1, out2), "not bit-reproducible"
     k = layer.top_k
-    assert int(gpu["e_cnt"].sum()) == n * k                   # every selected source has a row
-    assert int(gpu["d_cnt"].sum()) == int((gpu["tok_d"] >= 0).sum())
-    assert torch.isfinite(out1.float()).all()
-    # oracle on a subset of tokens
-    sel = torch.randperm(n, generator=torch.Generator().manual_seed(5))[:96].sort().values
     w = oracle_weights(layer)
-    hs = wl.h.reshape(n, -1)[sel].float().cpu()
-    xs = wl.x0.reshape(n, -1)[sel].float().cpu()
-    ref, aux = B.block_forward(hs, xs, w, 0, mode="grouped", out_bf16=True)
-    sub = {kk: v for kk, v in gpu.items()}
-    sub["top_idx"] = gpu["top_idx"][sel.to(gpu["top_idx"].device)]
-    sub["tok_d"] = gpu["tok_d"][sel.to(gpu["tok_d"].device)]
-    ok, rep = routing_agrees(sub, aux, layer)
-    assert rep["mismatch_non_tie"] == 0, rep
-    g = out1.reshape(n, -1)[sel.to(dev)].float().cpu()
-    err = (g[ok] - ref[ok]).abs()
-    assert bool((err <= 1e-2 + 1e-2 * ref[ok].abs()).all()), float(err.max())
-    say(name, "ties", rep["ties"], "max err", float(err.max()))
+    sel = torch.randperm(n, generator=torch.Generator().manual_seed(5))[:96].sort().values
+    cur = wl.h
+    for r in range(layer.num_loops):
+        with torch.no_grad():
+            out = layer(cur, wl.x0, r)
+            gpu = layer.last_routing()
+            if r == 0:
+                again = layer(cur, wl.x0, r)
+        torch.cuda.synchronize()
+        if r == 0:
+            assert torch.equal(out, again), "not bit-reproducible"
+        assert int(gpu["e_cnt"].sum()) == n * k               # every selected source has a row
+        assert torch.isfinite(out.float()).all()
+        check_plans(gpu, layer.num_experts)
+        hs = cur.reshape(n, -1)[sel.to(dev)].float().cpu()
+        xs = wl.x0.reshape(n, -1)[sel.to(dev)].float().cpu()
+        ref, aux = B.block_forward(hs, xs, w, r, mode="faithful", out_bf16=True)
+        sub = dict(gpu)
+        sub["top_idx"] = gpu["top_idx"][sel.to(dev)]
+        sub["tok_d"] = gpu["tok_d"][sel.to(dev)]
+        ok, rep = routing_agrees(sub, aux, layer)
+        assert rep["mismatch_non_tie"] == 0, rep
+        rep["edge_rows"] = check_edges(gpu, aux, ok, sel=sel)
+        rep.update(check_values(gpu, aux, ok, sel=sel))
+        g = out.reshape(n, -1)[sel.to(dev)].float().cpu()
+        err = (g[ok] - ref[ok]).abs()
+        assert bool((err <= 1e-2 + 1e-2 * ref[ok].abs()).all()), (r, float(err.max()), rep)
+        rep["max_err"] = float(err.max())
+        say(name, "loop", r, rep)
+        cur = out
 
 
 def test_multi_loop_call_equals_per_loop_calls():
@@ -241,7 +260,7 @@ def test_stage_entries_compose_block_forward(spec):
     say("stage entries", spec)
     wl = make_block("c1", tokens=300, hidden_size=128, num_experts=8, top_k=2, edges_per_expert=3,
                     expert_ffn_size=256, num_loops=2, expert_activation=spec["act"],
-                    experts=spec["experts"], dtype=spec["dtype"], group_size=64)
+                    experts=spec["experts"], dtype=spec["dtype"], group_size=64, std="fan_in")
     layer, r = wl.layer, 1
     n, hid = wl.h.shape[0], wl.h.shape[-1]
     e, k, m = layer.num_experts, layer.top_k, layer.edges_per_expert
@@ -299,7 +318,15 @@ def test_stage_entries_compose_block_forward(spec):
         assert ti[t].tolist() == aux.top_i[t].tolist(), t
         dst = {int(x_) for x_ in ei[t].flatten().tolist() if x_ >= 0}
         assert dst == set(torch.nonzero(aux.coef[t] != 0).flatten().tolist()), t
-        assert torch.allclose(eww[t].sum(-1), torch.ones(k), atol=1e-5)  # softmax rows
+        for j in range(k):  # slot j's source: its top-m (descending logit) and alpha
+            src = int(aux.top_i[t, j])
+            assert ei[t, j].tolist() == aux.edge_idx[t, src].tolist(), (t, j)
+            assert torch.allclose(eww[t, j], aux.edge_w[t, src], rtol=0, atol=1e-5), (t, j)
+    # the message and delta of the stage entries, against the oracle's
+    ok = ~ties
+    from _helpers import DELTA_TOL, MSG_TOL, row_ratio
+    assert float(row_ratio(msg.float().cpu()[ok], aux.msg[ok]).max()) <= MSG_TOL
+    assert float(row_ratio(delta.float().cpu()[ok], aux.delta[ok]).max()) <= DELTA_TOL
 
 
 # ------------------------------------------------ early-exit decode ----
@@ -355,8 +382,9 @@ def test_exit_gate_partial_teacher_forced(case):
     against the ungated block run loop by loop on every token: a token's
     output is the ungated state after its exit loop (within 1e-2; the count
     of bit-identical rows is printed), and each exit decision equals the
-    oracle's sigmoid(exit_head(h')) > threshold on that state, except where
-    the exit logit is within 1e-4 of the threshold's."""
+    oracle's sigmoid(exit_head(h')) > threshold on that state, the logit
+    rounded to bf16 as a bf16 exit_head Linear gives it, except where the
+    fp32 logit is within two bf16 ulps of the threshold's."""
     say("exit partial", case)
     layer, h, x0 = _exit_layer(case)
     r, hid = layer.num_loops, layer.hidden_size
@@ -374,13 +402,14 @@ def test_exit_gate_partial_teacher_forced(case):
     n = states[0].shape[0]
     loops = loops.cpu().long()
     z_thr = float(np.log(thr / (1 - thr)))
+    band = 2.0 * 2.0 ** (np.floor(np.log2(abs(z_thr))) - 7)  # two bf16 ulps at the threshold
     exp_loops = torch.full((n,), r, dtype=torch.long)
     tie = torch.zeros(n, dtype=torch.bool)
     done = torch.zeros(n, dtype=torch.bool)
     for li in range(r):
         z = B.exit_logit(states[li], ew_stored, 0.0)
-        tie |= ~done & ((z - z_thr).abs() < 1e-4)
-        ex = ~done & (torch.sigmoid(z) > thr)
+        tie |= ~done & ((z - z_thr).abs() < band)
+        ex = ~done & (torch.sigmoid(B.exit_logit(states[li], ew_stored, 0.0, bf16=True)) > thr)
         exp_loops[ex] = li + 1
         done |= ex
     ok = ~tie
@@ -420,3 +449,74 @@ def test_decode_graph_replays_match_eager():
             torch.cuda.synchronize()
             assert torch.equal(g_full, layer.forward_loops(hi, xi)), i
     assert runner.stats()["hits"] == 4 and runner.stats()["misses"] == 2
+
+
+def test_decode_graph_survives_workspace_growth_and_weight_update():
+    """A captured graph owns its workspace and the packed weights it reads:
+    graphs at two token counts, an eager call over more tokens in between
+    (which grows the layer's shared workspace), interleaved replays, then a
+    weight update (a repack: the stale graphs are captured again).  Every
+    replay equals the eager call on the layer's current weights."""
+    from spider_moe_amd.graph import BlockDecodeGraph
+    from spider_moe_amd.workloads import make_block
+    say("decode graph: workspace growth + weight update")
+    wl = make_block("c1", tokens=300, hidden_size=128, num_experts=16, top_k=2,
+                    edges_per_expert=2, expert_ffn_size=256, num_loops=3,
+                    expert_activation="swiglu", experts="bf16", std="fan_in")
+    layer = wl.layer
+    hid = layer.hidden_size
+    ew = torch.randn(hid, generator=torch.Generator().manual_seed(9)) / hid ** 0.5
+    _set_exit(layer, ew, 0.0)
+    runner = BlockDecodeGraph(layer)
+    gen = torch.Generator().manual_seed(33)
+
+    def inputs(n):
+        return (torch.randn(n, 1, hid, generator=gen).to(wl.h),
+                torch.randn(n, 1, hid, generator=gen).to(wl.h))
+
+    def same_as_eager(n):
+        hi, xi = inputs(n)
+        g_out, g_loops = runner.run(hi, xi, early_exit=True, threshold=0.6)
+        e_out, _, e_loops = layer.forward_loops_exit(hi, xi, 0.6)
+        torch.cuda.synchronize()
+        assert torch.equal(g_out, e_out) and torch.equal(g_loops, e_loops), n
+
+    with torch.no_grad():
+        same_as_eager(16)
+        same_as_eager(64)
+        big = layer.forward_loops(wl.h, wl.x0)         # 300 tokens: a larger shared workspace
+        torch.cuda.synchronize()
+        assert layer._ws.numel() >= layer.workspace_bytes(300)
+        same_as_eager(16)
+        same_as_eager(64)
+        layer.experts[3][2].weight.mul_(-1.5)          # a weight update: repack
+        same_as_eager(64)
+        same_as_eager(16)
+        assert not torch.equal(layer.forward_loops(wl.h, wl.x0), big)
+    st = runner.stats()
+    assert st["misses"] == 4 and st["recaptures"] == 2 and st["hits"] == 2, st
+
+
+def test_zero_loops_return_h():
+    """num_loops == 0 runs no loop: the result is h (a copy), through the
+    layer and through smoe_block_forward (h_out = h_in)."""
+    import ctypes
+    from spider_moe_amd import _native as nat
+    from spider_moe_amd.workloads import make_block
+    say("zero loops")
+    wl = make_block("c1", tokens=40, hidden_size=128, num_experts=8, top_k=2, edges_per_expert=2,
+                    expert_ffn_size=256, num_loops=3, expert_activation="swiglu", experts="bf16")
+    layer = wl.layer
+    with torch.no_grad():
+        out = layer.forward_loops(wl.h, wl.x0, layer.num_loops)
+        out2, active, loops = layer.forward_loops_exit(wl.h, wl.x0, 0.5, 1, 0)
+        d = layer._pack().desc
+        h2 = wl.h.reshape(40, -1).contiguous()
+        dst = torch.zeros_like(h2)
+        nat.check(nat.lib().smoe_block_forward(ctypes.byref(d), h2.data_ptr(), wl.x0.data_ptr(),
+                                               dst.data_ptr(), 40, 2, 0, None, 0,
+                                               nat.stream_of(h2.device)), "smoe_block_forward")
+    torch.cuda.synchronize()
+    assert torch.equal(out, wl.h) and out.data_ptr() != wl.h.data_ptr()
+    assert torch.equal(out2, wl.h) and bool((active == 1).all()) and int(loops.sum()) == 0
+    assert torch.equal(dst, h2)

@@ -393,3 +393,94 @@ def test_planted_exit_mistake_is_caught():
     early = loops < r
     assert bool(early.any())
     assert (bad[early] - ref[early]).abs().max() > 1e-2
+
+
+# ------------------------------------- sensitivity of the GPU checks ----
+# The GPU parity tests compare the device's message and expert delta with the
+# oracle (tests/_helpers.py: check_values) and the block outputs with a
+# 1e-2 bound.  These CPU tests show, on the oracle, that (a) the bf16 storage
+# the device uses stays well inside the value tolerances and (b) a missing
+# message term, a missing expert, msg = 0 or delta = 0 fails them, at the
+# shapes and weight scales the GPU tests run.
+from _helpers import DELTA_TOL, MSG_TOL, oracle_weights, row_ratio  # noqa: E402
+
+GPU_SMALL = dict(tokens=300, hidden_size=128, num_experts=8, top_k=2, edges_per_expert=3,
+                 expert_ffn_size=256, num_loops=3, group_size=64, std="fan_in")
+
+
+def _cpu_block(act, experts, **over):
+    from spider_moe_amd.workloads import make_block
+    spec = dict(GPU_SMALL)
+    spec.update(over)
+    wl = make_block("c1", device="cpu", expert_activation=act, experts=experts, **spec)
+    n = wl.h.shape[0]
+    return (wl.h.reshape(n, -1).float(), wl.x0.reshape(n, -1).float(), oracle_weights(wl.layer))
+
+
+def _device_storage(h, w, aux):
+    """The block's message and delta with the device's bf16 storage: each
+    destination row c * W_edge[d] h rounded to bf16, their sum in ascending
+    destination rounded to bf16; the FFN hidden activation and each expert's
+    weighted output rounded to bf16, summed in ascending expert order."""
+    n, hid = h.shape
+    rb = B.round_bf16
+    msg = torch.zeros(n, hid)
+    for d in range(w.num_experts):
+        c = aux.coef[:, d]
+        rows = torch.nonzero(c != 0).flatten()
+        if rows.numel():
+            msg[rows] += rb(c[rows].unsqueeze(-1) * (h[rows] @ w.edge_value_w[d].t()))
+    msg = rb(msg)
+    delta = torch.zeros(n, hid)
+    for e in range(w.num_experts):
+        tw = (aux.top_w * (aux.top_i == e)).sum(-1)
+        rows = torch.nonzero(tw > 0).flatten()
+        if rows.numel():
+            hid_act = B._expert_ffn(msg[rows], w, e, hidden_bf16=True)
+            delta[rows] += rb(hid_act * tw[rows].unsqueeze(-1))
+    return msg, delta
+
+
+@pytest.mark.parametrize("act,experts", [("gelu", "bf16"), ("swiglu", "bf16"), ("swiglu", "fp8"),
+                                         ("gelu", "int4")])
+def test_value_tolerances_are_calibrated(act, experts):
+    h, x0, w = _cpu_block(act, experts)
+    _, aux = B.block_forward(h, x0, w, 0, out_bf16=True)
+    msg, delta = _device_storage(h, w, aux)
+    rm, rd = float(row_ratio(msg, aux.msg).max()), float(row_ratio(delta, aux.delta).max())
+    assert rm < MSG_TOL / 3 and rd < DELTA_TOL / 2, (rm, rd)
+    # planted mistakes: each token's last destination dropped from the message;
+    # each token's second expert dropped from delta
+    bad_msg = aux.msg.clone()
+    for t in range(h.shape[0]):
+        d = int(torch.nonzero(aux.coef[t]).flatten()[-1])
+        bad_msg[t] -= aux.coef[t, d] * (h[t] @ w.edge_value_w[d].t())
+    assert float(row_ratio(bad_msg, aux.msg).min()) > MSG_TOL
+    tw = aux.top_w.clone()
+    tw[:, 1] = 0.0
+    bad_delta = B.expert_delta(aux.msg, aux.top_i, tw, w)
+    assert float(row_ratio(bad_delta, aux.delta).min()) > DELTA_TOL
+    assert float(row_ratio(torch.zeros_like(msg), aux.msg).min()) == 1.0
+
+
+def _fails_bound(out, ref, tol=1e-2):
+    return bool(((out - ref).abs() > tol + tol * ref.abs()).any())
+
+
+@pytest.mark.parametrize("shape", ["gpu_small", "smoke"])
+def test_output_bound_sees_message_and_delta(shape):
+    """A block computed with delta = 0, or with msg = 0, fails the 1e-2
+    output bound of the GPU block tests (so the bound checks the FFN and
+    the message, not only the routing)."""
+    if shape == "gpu_small":
+        cases = [_cpu_block("gelu", "bf16"), _cpu_block("swiglu", "bf16")]
+    else:  # the smoke: the c1 block (H 1024, std 0.02 weights), 64 tokens
+        cases = [_cpu_block("swiglu", "bf16", tokens=64, hidden_size=1024, num_experts=16,
+                            top_k=2, edges_per_expert=2, expert_ffn_size=2816, std=0.02)]
+    for h, x0, w in cases:
+        ref, aux = B.block_forward(h, x0, w, 0, out_bf16=True)
+        no_delta = B.round_bf16(B.epilogue(h, torch.zeros_like(h), x0, w))
+        assert _fails_bound(no_delta, ref)
+        w0 = B.BlockWeights(**{**w.__dict__, "edge_value_w": torch.zeros_like(w.edge_value_w)})
+        no_msg, _ = B.block_forward(h, x0, w0, 0, out_bf16=True)
+        assert _fails_bound(no_msg, ref)
