@@ -199,6 +199,26 @@ SMOE_API int smoe_block_forward_exit(const smoe_block* blk, const void* h_in, co
                                      int32_t* loops, void* workspace, size_t workspace_bytes,
                                      void* stream);
 
+/* Allocation-free smoe_block_forward.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory or pass a workspace
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  The block workspace is a static device array of
+ * SMOE_SCRATCH_BYTES inside libsmoe.so, one per GPU, held until the process
+ * ends; a call whose workspace (smoe_block_workspace_bytes(blk, N)) exceeds
+ * it fails with SMOE_ECAPACITY and launches nothing.  The limit admits
+ * decode-size steps: 64 tokens of the H 1024, E 16, U 2816 block need about
+ * 2 MiB.  Every call on a GPU shares that GPU's array (the kernels write
+ * every workspace byte they read, so nothing is cleared between calls):
+ * calls that overlap in time on one GPU (two streams or two host threads)
+ * race and give wrong results, so serialize them.  The call runs on the
+ * current device and `stream` must belong to it.  Arguments and results as
+ * smoe_block_forward, bit for bit; no hipMalloc / hipFree or other
+ * allocating routine is called. */
+#define SMOE_SCRATCH_BYTES (8u << 20)
+SMOE_API int smoe_block_forward_scratch(const smoe_block* blk, const void* h_in, const void* x0,
+                                        void* h_out, int N, int loop_begin, int num_loops,
+                                        void* stream);
+
 /* Router stage alone (model.py:255-258; spider_router_f32,
  * spider_kernels.h:26-28, with the logits GEMM of model.py:255 fused in):
  * x [N,H] act_dtype, router_w [E,H] act_dtype, loop_bias_row f32 [E] or NULL

@@ -13,6 +13,7 @@
 //   10 down GEMM          w * (W_down act + b_down)           (sparse_experts.py:62-63)
 //   11 epilogue           LN(h + a*sum_e y + b*x0)            (model.py:317)
 // No step reads routing back to the host; grids are sized for the worst case.
+#include <mutex>
 #include <string>
 #include <type_traits>
 
@@ -522,6 +523,63 @@ SMOE_API int smoe_block_forward_exit(const smoe_block* b, const void* h_in, cons
   if ((tb & 0x7fffffffu) > 0x7f800000u) return fail(SMOE_EINVAL, "threshold is NaN");
   const ExitGate gate{exit_wb, threshold, active, loops};
   return block_forward(b, h_in, x0, h_out, N, loop_begin, num_loops, &gate, ws, ws_bytes, stream);
+}
+
+// ---- smoe_block_forward_scratch: the block workspace in a static device
+// array instead of a caller's buffer ----
+namespace {
+// `scratch` is a host-side stand-in for the device array: host code never
+// passes it (or takes its address) directly.  The device address is read
+// once per device with hipGetSymbolAddress, with that device current, and
+// every later use (the kernels' workspace argument) goes through it.
+__device__ __align__(256) unsigned char scratch[SMOE_SCRATCH_BYTES];
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of the current device's scratch array.
+int scratch_address(hipStream_t s, void** out) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(SMOE_EHIP, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(SMOE_EINVAL, "device id beyond 64");
+  if (s) {  // the stream must belong to the current device (its array is used)
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(s, &sdev) != hipSuccess) return fail(SMOE_EHIP, "hipStreamGetDevice");
+    if (sdev != dev) return fail(SMOE_EINVAL, "stream is not on the current device");
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(SMOE_EHIP, (std::string("hipGetSymbolAddress(scratch): ") +
+                              hipGetErrorString(e)).c_str());
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return SMOE_OK;
+}
+}  // namespace
+
+SMOE_API int smoe_block_forward_scratch(const smoe_block* b, const void* h_in, const void* x0,
+                                        void* h_out, int N, int loop_begin, int num_loops,
+                                        void* stream) {
+  const int rc = check_block(b);
+  if (rc != SMOE_OK) return rc;
+  if (N < 0) return fail(SMOE_EINVAL, "N");
+  smoe_ws_layout l;
+  make_layout(b, N, &l);
+  if (l.total > static_cast<size_t>(SMOE_SCRATCH_BYTES))
+    return fail(SMOE_ECAPACITY, ("workspace of " + std::to_string(l.total) +
+                                 " bytes exceeds the static scratch of " +
+                                 std::to_string(SMOE_SCRATCH_BYTES) + " bytes")
+                                    .c_str());
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  const int arc = scratch_address(s, &ws);
+  if (arc != SMOE_OK) return arc;
+  return block_forward(b, h_in, x0, h_out, N, loop_begin, num_loops, nullptr, ws,
+                       SMOE_SCRATCH_BYTES, stream);
 }
 
 SMOE_API int smoe_pack_weight_tiles(const void* w, int format, int G, int N, int K, void* out,

@@ -65,6 +65,8 @@ SIGNATURES = {
     "smoe_block_forward_exit": (_c_int, [ctypes.POINTER(SmoeBlock), _vp, _vp, _vp, _c_int,
                                          _c_int, _c_int, _vp, ctypes.c_float, _vp, _vp, _vp, _sz,
                                          _vp]),
+    "smoe_block_forward_scratch": (_c_int, [ctypes.POINTER(SmoeBlock), _vp, _vp, _vp, _c_int,
+                                            _c_int, _c_int, _vp]),
     "smoe_router_workspace_bytes": (_sz, [_c_int, _c_int]),
     "smoe_router_topk": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _c_int, _c_int, _vp,
                                   _vp, _vp, _vp, _sz, _vp]),
