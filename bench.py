@@ -41,26 +41,37 @@ DESC = {
     "c4": "int4 experts g128 fp16 scales: H2048 E64 k2 m4 U1408 GELU R4 N2176 (128 decode + 2048 prefill)",
 }
 BOUND = {"c1": "mfma", "c2": "hbm", "c3": "mfma", "c4": "hbm"}
-# the up / gate GEMM kernel the launcher picks for each workload's shapes
-# (rows per expert, N_out, format); rocprof summaries under profiles/ name it too
-UP_KERNEL = {
-    "c1": "k_gemm_pp<4,4,SwiGLU,320> (bf16 weight tiles, 8-wave ping-pong, LDS-DMA ring)",
-    "c2": "k_gemm_decode<fp8,SwiGLU,4,1,2,3> (weight streaming, K split over 2 waves, 3-step register ring per wave)",
-    "c3": "k_gemm_ring<128,3,4> (bf16 GELU, LDS-DMA ring, 2 workgroups/CU)",
-    "c4": "k_gemm_stream<int4,GELU,6,3,2> (weight streaming, both operands by LDS-DMA ring, 2 workgroups/CU)",
+# the GEMM stages of a loop; the roofline reports the one with the most time
+GEMM_STAGES = ("edge_gemm", "up_gemm", "down_gemm")
+# the kernel the launcher picks for each workload's GEMM shapes (rows per
+# group, N_out, format); rocprof summaries under profiles/ name them too
+GEMM_KERNEL = {
+    ("c1", "up_gemm"): "k_gemm_pp<4,4,SwiGLU,320> (bf16 weight tiles, 8-wave ping-pong, LDS-DMA ring)",
+    ("c1", "down_gemm"): "k_gemm_pp<4,4,down,320> (bf16 weight tiles, 8-wave ping-pong, LDS-DMA ring)",
+    ("c1", "edge_gemm"): "k_gemm_pp<4,4,rowscale,256> (bf16 weight tiles, 8-wave ping-pong, LDS-DMA ring)",
+    ("c2", "up_gemm"): "k_gemm_decode<fp8,SwiGLU,4,1,2,3> (weight streaming, K split over 2 waves, 3-step register ring per wave)",
+    ("c2", "down_gemm"): "k_gemm_decode<fp8,down,4,1,4,3> (weight streaming, K split over 4 waves)",
+    ("c2", "edge_gemm"): "k_gemm_decode<bf16,rowscale,4,2,4,3> (weight streaming, K split over 4 waves)",
+    ("c3", "up_gemm"): "k_gemm_ring<128,3,4> (bf16 GELU, LDS-DMA ring, 2 workgroups/CU)",
+    ("c3", "down_gemm"): "k_gemm_pp<4,4,down,320> (bf16 weight tiles, 8-wave ping-pong)",
+    ("c3", "edge_gemm"): "k_gemm_pp<4,4,rowscale,256> (bf16 weight tiles, 8-wave ping-pong)",
+    ("c4", "up_gemm"): "k_gemm_stream<int4,GELU,6,3,2> (weight streaming, both operands by LDS-DMA ring, 2 workgroups/CU)",
+    ("c4", "down_gemm"): "k_gemm_stream<int4,down,6,3,2> (weight streaming, 2 workgroups/CU)",
+    ("c4", "edge_gemm"): "k_gemm_pp<4,4,rowscale,320> (bf16 weight tiles, 320-row tiles: one per destination)",
 }
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.md")
 
 
-def measured_traffic(name):
-    """HBM bytes per launch of the workload's up GEMM from the committed pmc
-    summary: lines `traffic <workload> <bytes>` (None when not measured)."""
+def measured_traffic(name, stage):
+    """HBM bytes per launch of a workload's GEMM stage from the committed pmc
+    summary: lines `traffic <workload> <stage> <bytes>` (None when not
+    measured)."""
     try:
         with open(TRAFFIC_FILE) as f:
             for line in f:
                 parts = line.strip().strip("`").split()
-                if len(parts) == 3 and parts[0] == "traffic" and parts[1] == name:
-                    return float(parts[2])
+                if len(parts) == 4 and parts[0] == "traffic" and parts[1:3] == [name, stage]:
+                    return float(parts[3])
     except OSError:
         pass
     return None
@@ -103,6 +114,41 @@ def up_gemm_bytes(layer, rows: int, e_touched: int) -> float:
     if layer.expert_activation == "gelu":
         wb += 4 * u
     return wb * e_touched + rows * h * 2 + rows * u * 2
+
+
+def down_gemm_bytes(layer, rows: int, e_touched: int) -> float:
+    h, u = layer.hidden_size, layer.expert_ffn_size
+    fmt = layer.expert_format
+    wb = {"fp8": 1.0, "int4": 0.5, "bf16": 2.0, "f32": 4.0}[fmt] * h * u
+    if fmt == "fp8":
+        wb += 4 * h
+    elif fmt == "int4":
+        wb += layer._int4_w_down.scales.element_size() * h * u / layer._int4_w_down.group_size
+    if layer.expert_activation == "gelu":
+        wb += 4 * h
+    return wb * e_touched + rows * u * 2 + rows * h * 2
+
+
+def gemm_work(layer, stage, acc):
+    """Algorithmic (flops, bytes) of one launch of a GEMM stage, averaged
+    over the loops: flops 2 H^2 per destination row (edge), 4 H U (SwiGLU) /
+    2 H U (GELU) per expert row (up), 2 H U per expert row (down); bytes the
+    weights of the touched groups in storage format (+ scales, biases) and
+    the activation rows in and out (bf16)."""
+    h, u = layer.hidden_size, layer.expert_ffn_size
+    upc = 4 if layer.expert_activation == "swiglu" else 2
+    f = b = 0.0
+    for a in acc:
+        if stage == "edge_gemm":
+            f += 2 * h * h * a["d_rows"]
+            b += a["d_touched"] * 2 * h * h + a["d_rows"] * h * 2 * 2
+        elif stage == "up_gemm":
+            f += upc * h * u * a["s_rows"]
+            b += up_gemm_bytes(layer, a["s_rows"], a["e_touched"])
+        else:
+            f += 2 * h * u * a["s_rows"]
+            b += down_gemm_bytes(layer, a["s_rows"], a["e_touched"])
+    return f / len(acc), b / len(acc)
 
 
 def accounting(layer, h, x0):
@@ -150,12 +196,9 @@ def run_workload(name, steps, warmup):
             layer.forward_loops(h, x0, 0, r)
         torch.cuda.synchronize()
         log(name, "timing", steps, "steps")
+        # pass 1, the timed region: K plain steps between two events
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        # timed region: HIP events around the up GEMM launches only (on the
-        # block's stream), so the dominant kernel is timed in the same steps
-        up_timer = nat.StageTimer(stages=["up_gemm"], capacity=steps * r + 16)
         torch.cuda.synchronize()
-        up_timer.start()
         t0 = time.perf_counter()
         e0.record()
         for _ in range(steps):
@@ -164,38 +207,48 @@ def run_workload(name, steps, warmup):
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         ms = e0.elapsed_time(e1) / steps
-        up = up_timer.stop().get("up_gemm", [])
-        up_timer.close()
-        # second pass: HIP events around every stage launch (breakdown)
+        # pass 2: HIP events around every stage launch (breakdown), which
+        # names the dominant GEMM
         timer = nat.StageTimer(capacity=steps * r * len(nat.STAGES) + 16)
         timer.start()
         for _ in range(steps):
             layer.forward_loops(h, x0, 0, r)
         stages = timer.stop()
         timer.close()
+        dom = max(GEMM_STAGES, key=lambda s: sum(stages.get(s, [0.0])))
+        # pass 3: the dominant GEMM alone, its launches recording their own
+        # events (hipExtLaunchKernelGGL: the interval is the kernel's
+        # execution); those launches cost the host ~15 us each, so the step
+        # time comes from pass 1
+        dom_timer = nat.StageTimer(stages=[dom], capacity=steps * r + 16)
+        dom_timer.start()
+        for _ in range(steps):
+            layer.forward_loops(h, x0, 0, r)
+        dom_ms_list = dom_timer.stop().get(dom, [])
+        dom_timer.close()
     acc = accounting(layer, h, x0)
     flops, bytes_ = block_work(layer, n, acc)
-    up_ms = sum(up) / max(len(up), 1)
-    hidden, u = layer.hidden_size, layer.expert_ffn_size
-    upc = 4 if layer.expert_activation == "swiglu" else 2
-    up_flops = sum(upc * hidden * u * a["s_rows"] for a in acc) / len(acc)
-    up_bytes = sum(up_gemm_bytes(layer, a["s_rows"], a["e_touched"]) for a in acc) / len(acc)
-    bound = BOUND[name]
-    if bound == "mfma":
-        ach = up_flops / (up_ms * 1e-3) / 1e12
+    dom_ms = sum(dom_ms_list) / max(len(dom_ms_list), 1)
+    g_flops, g_bytes = gemm_work(layer, dom, acc)
+    # the GEMM's bound follows its arithmetic intensity against the ridge point
+    g_bound = "mfma" if g_flops / g_bytes > PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9) else "hbm"
+    if g_bound == "mfma":
+        ach = g_flops / (dom_ms * 1e-3) / 1e12
         roof = {"bound": "mfma", "achieved": round(ach, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                "frac": round(ach / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic(name),
-                "kernel": UP_KERNEL[name],
-                "work_per_launch": f"{up_flops:.4g} flop", "avg_launch_ms": round(up_ms, 4)}
+                "frac": round(ach / PEAK_BF16_TFLOPS, 4)}
+    else:
+        ach = g_bytes / (dom_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": round(ach / PEAK_HBM_GBS, 4)}
+    roof.update({"traffic": measured_traffic(name, dom), "stage": dom,
+                 "kernel": GEMM_KERNEL.get((name, dom), dom),
+                 "work_per_launch": f"{g_flops:.4g} flop, {g_bytes:.4g} B",
+                 "avg_launch_ms": round(dom_ms, 4)})
+    if BOUND[name] == "mfma":
         blk = flops / (ms * 1e-3) / 1e12
         block_roof = {"bound": "mfma", "achieved": round(blk, 1), "unit": "TFLOP/s",
                       "frac": round(blk / PEAK_BF16_TFLOPS, 4), "work_per_step": f"{flops:.4g} flop"}
     else:
-        ach = up_bytes / (up_ms * 1e-3) / 1e9
-        roof = {"bound": "hbm", "achieved": round(ach, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                "frac": round(ach / PEAK_HBM_GBS, 4), "traffic": measured_traffic(name),
-                "kernel": UP_KERNEL[name],
-                "work_per_launch": f"{up_bytes:.4g} B", "avg_launch_ms": round(up_ms, 4)}
         blk = bytes_ / (ms * 1e-3) / 1e9
         block_roof = {"bound": "hbm", "achieved": round(blk, 1), "unit": "GB/s",
                       "frac": round(blk / PEAK_HBM_GBS, 4), "work_per_step": f"{bytes_:.4g} B"}

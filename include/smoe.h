@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define SMOE_ABI_VERSION 6
+#define SMOE_ABI_VERSION 7
 
 /* status codes (spider_kernels.h convention; see scalar.cpp:9,45,58) */
 #define SMOE_OK 0
@@ -147,6 +147,9 @@ typedef struct smoe_ws_layout {
   size_t scratch;   /* plan scratch                                               */
   size_t front;     /* f32 [N,E+E*E]  router logits | edge logits of every source,  */
                     /*                bf16 steps of N <= 64 (else 0 bytes)          */
+  size_t sel_idx;   /* i32 [N,K,M]    decode loop: the top-m of each token's sources */
+  size_t sel_w;     /* f32 [N,K,M]    (ascending), their weights (else 0 bytes)     */
+  size_t h_tmp2;    /* act [N,H]      decode loop: second loop-input buffer         */
   int S;            /* destinations per token: min(E, K*M)                        */
   int ffn_dtype;    /* SMOE_F32 or SMOE_BF16                                      */
 } smoe_ws_layout;

@@ -183,6 +183,15 @@ bool front_ok(const smoe_block* b, int N) {
          b->M <= 16 && S <= 64 && b->H % 64 == 0 && (E + E * E) % 4 == 0 && E % 4 == 0 && (b->H + b->L) % 8 == 0;
 }
 
+// bf16 decode steps the two-launch decode loop takes (k_decode_front +
+// k_decode_plan in place of the front GEMM, the routing workgroup and the
+// previous loop's epilogue); the early-exit gate keeps the general loop.
+bool decode_ok(const smoe_block* b, int N) {
+  const int E = b->E, S = (E < b->K * b->M) ? E : b->K * b->M;
+  return b->act_dtype == SMOE_BF16 && b->experts.format != SMOE_F32 &&
+         decode_front_fits(N, b->H, E, b->K, b->M, S, b->H + b->L);
+}
+
 void make_layout(const smoe_block* b, int N, smoe_ws_layout* l) {
   const size_t n = N > 0 ? static_cast<size_t>(N) : 1;
   const int E = b->E, K = b->K, M = b->M, H = b->H;
@@ -219,6 +228,10 @@ void make_layout(const smoe_block* b, int N, smoe_ws_layout* l) {
   l->h_tmp = z.take(n * H * esize(b->act_dtype));
   l->scratch = z.take(plan_scratch_bytes(N, E));
   l->front = z.take(front_ok(b, N) ? n * (E + E * E) * 4 : 0);
+  const bool dec = decode_ok(b, N);
+  l->sel_idx = z.take(dec ? n * K * M * 4 : 0);
+  l->sel_w = z.take(dec ? n * K * M * 4 : 0);
+  l->h_tmp2 = z.take(dec ? n * H * esize(b->act_dtype) : 0);
   l->total = z.off;
   l->S = S;
   l->ffn_dtype = fdt;
@@ -357,13 +370,64 @@ int block_forward(const smoe_block* b, const void* h_in, const void* x0, void* h
   const int adt = b->act_dtype, fdt = l.ffn_dtype;
   const int gfmt = adt == SMOE_F32 ? SMOE_F32 : SMOE_BF16;  // router / edge weights
 
+  const bool dec = !gate && decode_ok(b, N);
   const bool front = front_ok(b, N);
   const int32_t* active = gate ? gate->active : nullptr;
   const void* cur = h_in;
   for (int i = 0; i < num_loops; ++i) {
     const int r = loop_begin + i;
     void* dst = ((num_loops - 1 - i) % 2 == 0) ? h_out : at<void>(ws, l.h_tmp);
-    if (front) {
+    if (dec) {
+      // the loop's input: h_in, or the previous loop's LayerNorm, computed by
+      // this loop's front and kept in h_tmp / h_tmp2 (never the buffer the
+      // previous input is read from)
+      void* in_r = i == 0 ? const_cast<void*>(h_in) : at<void>(ws, (i % 2) ? l.h_tmp : l.h_tmp2);
+      DecFront fa;
+      fa.h = cur;
+      fa.x0 = x0;
+      if (i > 0) {
+        fa.y = at<void>(ws, l.y);
+        fa.tok_e = at<int32_t>(ws, l.tok_e);
+        fa.tok_ew = at<float>(ws, l.tok_ew);
+        fa.e_tokrow = at<int32_t>(ws, l.e_tokrow);
+        fa.ln_w = b->ln_w;
+        fa.ln_b = b->ln_b;
+        fa.alpha = b->alpha;
+        fa.beta = b->beta;
+        fa.eps = b->eps;
+        fa.h_out = in_r;
+      }
+      fa.router_w = b->router_w;
+      fa.router_bias = b->loop_bias + static_cast<int64_t>(r) * E;
+      fa.edge_w = b->edge_gen_w;
+      fa.ldw = H + L;
+      fa.edge_bias = b->edge_loop_bias + static_cast<int64_t>(r) * E * E;
+      fa.N = N;
+      fa.H = H;
+      fa.E = E;
+      fa.K = K;
+      fa.M = M;
+      fa.logits = at<float>(ws, l.logits);
+      fa.top_idx = at<int32_t>(ws, l.top_idx);
+      fa.top_w = at<float>(ws, l.top_w);
+      fa.sel_idx = at<int32_t>(ws, l.sel_idx);
+      fa.sel_w = at<float>(ws, l.sel_w);
+      STAGE(SMOE_STAGE_FRONT_GEMM, launch_decode_front(fa, s), "decode front");
+      STAGE(SMOE_STAGE_FRONT_ROUTE,
+            launch_decode_plan(at<int32_t>(ws, l.top_idx), at<float>(ws, l.top_w),
+                               at<int32_t>(ws, l.sel_idx), at<float>(ws, l.sel_w), N, E, K, M, S,
+                               at<int32_t>(ws, l.tok_e), at<float>(ws, l.tok_ew),
+                               at<int32_t>(ws, l.e_cnt), at<int32_t>(ws, l.e_acnt),
+                               at<int32_t>(ws, l.e_off), at<int32_t>(ws, l.e_rows),
+                               at<float>(ws, l.e_roww), at<int32_t>(ws, l.e_tokrow),
+                               at<int32_t>(ws, l.edge_idx), at<float>(ws, l.edge_w),
+                               at<int32_t>(ws, l.tok_d), at<float>(ws, l.tok_dc),
+                               at<int32_t>(ws, l.d_cnt), at<int32_t>(ws, l.d_acnt),
+                               at<int32_t>(ws, l.d_off), at<int32_t>(ws, l.d_rows),
+                               at<float>(ws, l.d_roww), at<int32_t>(ws, l.d_tokrow), s),
+            "decode plans");
+      cur = in_r;
+    } else if (front) {
       // 1-6 fused: [router | all edge generator rows] logits, then routing
       const int ldf = E + E * E;
       GemmArgs fg;
@@ -495,12 +559,15 @@ int block_forward(const smoe_block* b, const void* h_in, const void* x0, void* h
                      at<int32_t>(ws, l.e_rows), at<float>(ws, l.e_roww), N * K,
                      at<void>(ws, l.act), at<void>(ws, l.y), s);
     if (rc != SMOE_OK) return rc;
-    // 11 combine + residual + LayerNorm
+    // 11 combine + residual + LayerNorm (the decode loop: in the next loop's
+    // front, and after the last loop)
+    if (dec && i + 1 < num_loops) continue;
+    void* out_r = dec ? h_out : dst;
     STAGE(SMOE_STAGE_EPILOGUE, launch_epilogue(cur, x0, adt, at<void>(ws, l.y), fdt, at<int32_t>(ws, l.tok_e),
                              at<float>(ws, l.tok_ew), at<int32_t>(ws, l.e_tokrow), N, K, H,
-                             b->alpha, b->beta, b->ln_w, b->ln_b, b->eps, dst, gate, s),
+                             b->alpha, b->beta, b->ln_w, b->ln_b, b->eps, out_r, gate, s),
              "epilogue");
-    cur = dst;
+    cur = out_r;
   }
   return SMOE_OK;
 }

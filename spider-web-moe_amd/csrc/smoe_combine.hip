@@ -12,89 +12,9 @@
 // a multiple of 8.
 #include "smoe_common.hpp"
 #include "smoe_internal.hpp"
+#include "smoe_rows.hpp"
 
 namespace smoe {
-
-// 8 consecutive elements of a bf16 or f32 array <-> 8 floats, as 16-byte
-// vectors.  The dtype is a template argument: a run-time dtype branch would
-// make each load wait before the branches join.
-template <int DT>
-__device__ __forceinline__ void load8(const void* base, int64_t off, float* v) {
-  if constexpr (DT == SMOE_F32) {
-    const f32x4 a = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(base) + off);
-    const f32x4 b = *reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(base) + off + 4);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[i] = a[i];
-      v[4 + i] = b[i];
-    }
-  } else {
-    const u32x4 a = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(base) + off);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      v[2 * i] = __uint_as_float(a[i] << 16);
-      v[2 * i + 1] = __uint_as_float(a[i] & 0xFFFF0000u);
-    }
-  }
-}
-
-template <int DT>
-__device__ __forceinline__ void store8(void* base, int64_t off, const float* v) {
-  if constexpr (DT == SMOE_F32) {
-    float* p = reinterpret_cast<float*>(base) + off;
-    *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
-    *reinterpret_cast<f32x4*>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
-  } else {
-    u32x4 a;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) a[i] = pack_bf2(v[2 * i], v[2 * i + 1]);
-    *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(base) + off) = a;
-  }
-}
-
-// Keeps a loaded value live here, so the compiler issues the loads of a
-// batch together instead of sinking each into the branch that consumes it.
-__device__ __forceinline__ void pin(float x) { asm volatile("" : : "v"(x)); }
-
-// acc += the rows named by the set bits of `live` (lane j of my_row holds a
-// row index when bit j is set), in ascending bit order.  Loads of a batch of
-// rows are issued together; a batch slot past the last row loads row 0 and
-// is not added.
-template <int CPL, int DT>
-__device__ __forceinline__ void gather_add(const void* __restrict__ base, int H,
-                                           int my_row, uint64_t live, float (&acc)[CPL][8]) {
-  constexpr int B = CPL >= 8 ? 1 : 8 / CPL;  // rows per batch (<= 8 x 16 B loads per lane)
-  const int lane = threadIdx.x & 63;
-  while (live) {
-    float v[B][CPL][8];
-    bool use[B];
-#pragma unroll
-    for (int b = 0; b < B; ++b) {
-      use[b] = live != 0;
-      const int src = use[b] ? __ffsll(static_cast<unsigned long long>(live)) - 1 : 0;
-      live &= live - 1;
-      const int r = __shfl(my_row, src);
-      const int64_t row = use[b] ? r : 0;
-#pragma unroll
-      for (int c = 0; c < CPL; ++c) {  // columns past H load column 0 (not stored)
-        const int col = (lane + 64 * c) * 8;
-        load8<DT>(base, row * H + (col < H ? col : 0), v[b][c]);
-      }
-    }
-#pragma unroll
-    for (int b = 0; b < B; ++b)
-#pragma unroll
-      for (int c = 0; c < CPL; ++c)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) pin(v[b][c][i]);
-#pragma unroll
-    for (int b = 0; b < B; ++b)
-#pragma unroll
-      for (int c = 0; c < CPL; ++c)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[c][i] += use[b] ? v[b][c][i] : 0.f;
-  }
-}
 
 // CPL = 8-element chunks per lane (H <= 512 * CPL)
 // Lane j (< S) holds the token's j-th (destination, row) entry.
@@ -144,25 +64,12 @@ __global__ __launch_bounds__(256) void k_epilogue(
   if (t >= N) return;
   // the token's own rows and the LayerNorm parameters do not depend on the
   // routing: their loads go out first, with the routing metadata
-  float hv[CPL][8], xv[CPL][8], d[CPL][8], gw[CPL][8], gb[CPL][8];
+  float hv[CPL][8], xv[CPL][8], d[CPL][8], gw[CPL][8], gb[CPL][8], ew[CPL][8];
+  ln_load<CPL, ADT>(h, x0, ln_w, ln_b, t, H, hv, xv, gw, gb);
 #pragma unroll
-  for (int c = 0; c < CPL; ++c) {  // columns past H load column 0 (not stored)
-    const int col = (lane + 64 * c) * 8;
-    const int cc = col < H ? col : 0;
-    const int64_t o = static_cast<int64_t>(t) * H + cc;
+  for (int c = 0; c < CPL; ++c)
 #pragma unroll
     for (int i = 0; i < 8; ++i) d[c][i] = 0.f;
-    load8<ADT>(h, o, hv[c]);
-    load8<ADT>(x0, o, xv[c]);
-    if (ln_w) load8<SMOE_F32>(ln_w, cc, gw[c]);
-    else
-#pragma unroll
-      for (int i = 0; i < 8; ++i) gw[c][i] = 1.f;
-    if (ln_b) load8<SMOE_F32>(ln_b, cc, gb[c]);
-    else
-#pragma unroll
-      for (int i = 0; i < 8; ++i) gb[c][i] = 0.f;
-  }
   // the loop count is read here, unconditionally (from active when loops is
   // null, value unused), so its latency hides behind the row loads; a load
   // under the final lane-0 branch would be waited for at the kernel's end
@@ -190,50 +97,25 @@ __global__ __launch_bounds__(256) void k_epilogue(
     my_row = (lane < K && te >= 0 && tw > 0.f) ? tr : -1;
   }
   gather_add<CPL, YDT>(y, H, my_row, __ballot(my_row >= 0), d);  // ascending expert order
-  float s = 0.f;
-#pragma unroll
-  for (int c = 0; c < CPL; ++c) {
-    const int col = (lane + 64 * c) * 8;
-    if (col < H)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        d[c][i] = (hv[c][i] + alpha * d[c][i]) + beta * xv[c][i];
-        s += d[c][i];
-      }
-  }
-  if (GATE)  // x0 is consumed: its registers take the exit weights
+  if (GATE)  // x0 is read by ln_row before it returns: the exit weights go elsewhere
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
       const int col = (lane + 64 * c) * 8;
-      load8<SMOE_F32>(exit_wb, col < H ? col : 0, xv[c]);
+      load8<SMOE_F32>(exit_wb, col < H ? col : 0, ew[c]);
     }
-  const float mean = wave_sum(s) / static_cast<float>(H);
-  float q = 0.f;
-#pragma unroll
-  for (int c = 0; c < CPL; ++c) {
-    const int col = (lane + 64 * c) * 8;
-    if (col < H)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float z = d[c][i] - mean;
-        q += z * z;
-      }
-  }
-  const float rstd = 1.0f / sqrtf(wave_sum(q) / static_cast<float>(H) + eps);
+  float o[CPL][8];
+  ln_row<CPL>(hv, xv, gw, gb, d, H, alpha, beta, eps, o);
   float g = 0.f;  // exit-gate dot product (GATE)
 #pragma unroll
   for (int c = 0; c < CPL; ++c) {
     const int col = (lane + 64 * c) * 8;
     if (col < H) {
-      float o[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = (d[c][i] - mean) * rstd * gw[c][i] + gb[c][i];
-      store8<ADT>(out, static_cast<int64_t>(t) * H + col, o);
+      store8<ADT>(out, static_cast<int64_t>(t) * H + col, o[c]);
       if (GATE)
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const float stored = ADT == SMOE_BF16 ? bf2f(f2bf(o[i])) : o[i];
-          g += stored * xv[c][i];
+          const float stored = ADT == SMOE_BF16 ? bf2f(f2bf(o[c][i])) : o[c][i];
+          g += stored * ew[c][i];
         }
     }
   }
@@ -272,22 +154,6 @@ __global__ __launch_bounds__(256) void k_delta_combine(const void* __restrict__ 
 }
 
 namespace {
-template <typename F>
-int by_cpl(int H, F&& f) {
-  if (H <= 0 || H % 8) return SMOE_EINVAL;
-  if (H <= 512) return f(std::integral_constant<int, 1>{});
-  if (H <= 1024) return f(std::integral_constant<int, 2>{});
-  if (H <= 2048) return f(std::integral_constant<int, 4>{});
-  if (H <= 4096) return f(std::integral_constant<int, 8>{});
-  return SMOE_EINVAL;
-}
-// dtype code (SMOE_F32 / SMOE_BF16) -> compile-time constant
-template <typename F>
-int by_dt(int dt, F&& f) {
-  if (dt == SMOE_F32) return f(std::integral_constant<int, SMOE_F32>{});
-  if (dt == SMOE_BF16) return f(std::integral_constant<int, SMOE_BF16>{});
-  return SMOE_EUNSUPPORTED;
-}
 int last_rc() { return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP; }
 }  // namespace
 

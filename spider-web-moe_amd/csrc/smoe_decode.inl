@@ -1,0 +1,407 @@
+// Decode loop kernels (bf16, N <= 64 tokens).  Included by smoe_route.hip,
+// inside namespace smoe, after the routing device functions it uses
+// (topk_seg, plan64_wave, seg_argmax).
+//
+// Decode steps spend most of a loop's time outside the weight streams when
+// every routing stage is its own launch.  Here a loop takes two launches
+// before its edge GEMM:
+//
+//  k_decode_front (strip, 16-token tile; 16 waves): the tile's input rows go
+//   to LDS as bf16 — for loops after the first, as the previous loop's
+//   LayerNorm (ln_row over h_{r-1}, x0 and the previous loop's expert rows,
+//   the operations of k_epilogue in its order, so the rows are the bits that
+//   kernel writes; the router strip stores them as the loop's input).  Wave
+//   w normalises token w, so the 16 latency chains overlap.  The router
+//   rows and the strip's own weights are requested first, so their latency
+//   hides behind that.  One 16 x 16 x 32 MFMA per 32-k step and 16-channel
+//   tile, K split over the waves and added in wave order, + bias.  Every
+//   strip then runs the router top-k of its tokens (topk_seg; the same bits
+//   in every strip, since the logits are computed the same way); strip 0
+//   writes it, strip s + 1 runs top-m over source s's logits (topm_row, the
+//   operations of topm_seg) and, for each token that selected s, writes its
+//   destinations and softmax weights at s's rank among the token's sources.
+//
+//  k_decode_plan (one workgroup, two waves that share no data): wave 0 sorts
+//   each token's top-k by expert (tok_e / tok_ew), builds the expert plan
+//   (plan64_wave) and puts each source's edges at its plan row; wave 1 sums
+//   each token's destination coefficients over its sources in ascending
+//   order (the order topm_seg adds them), lists them ascending (tok_d /
+//   tok_dc) and builds the destination plan.
+//
+// The previous loop's epilogue is folded into the next front, so a call
+// ends with one k_epilogue after its last loop.
+
+// Top-m of one source row over the E lanes of a segment (lane d: the logit
+// of the edge to destination d): the operations of topm_seg for one live
+// source; written, when `sel`, to sel_idx / sel_w [N, K, M] at (t, rank).
+template <int SEG>
+__device__ __forceinline__ void topm_row(float v, int t, bool ok, bool sel_src, int rank, int E,
+                                         int K, int M, int32_t* __restrict__ sel_idx,
+                                         float* __restrict__ sel_w) {
+  const int lane = threadIdx.x & 63;
+  const int d = lane & (SEG - 1);
+  const bool in = d < E;
+  const float vj = in ? v : -INFINITY;
+  bool sel = false;
+  float vmax = 0.f, den = 0.f, rec_v = 0.f;
+  int rec_i = 0;
+#pragma unroll 1
+  for (int i = 0; i < M; ++i) {
+    float cv = (in && !sel) ? vj : -INFINITY;
+    int ci = (in && !sel) ? d : kBig;
+    seg_argmax<SEG>(cv, ci);
+    sel = sel || d == ci;
+    vmax = i == 0 ? cv : vmax;
+    rec_v = d == i ? cv : rec_v;
+    rec_i = d == i ? ci : rec_i;
+    den += expf(cv - vmax);
+  }
+  if (ok && sel_src && d < M) {
+    const int64_t o = (static_cast<int64_t>(t) * K + rank) * M + d;
+    sel_idx[o] = rec_i;
+    sel_w[o] = expf(rec_v - vmax) / den;
+  }
+}
+
+// CPL: row chunks per lane (H); SEG: lanes per token (E); ET: 16-channel
+// tiles of E; NS: H / 128; PRO: the input rows are the previous loop's
+// LayerNorm.
+template <int CPL, int SEG, int ET, int NS, bool PRO>
+__global__ __launch_bounds__(1024) void k_decode_front(const DecFront a) {
+  constexpr int TT = 16;                    // tokens per tile (one per wave)
+  constexpr int NW = 16;                    // waves
+  constexpr int H = NS * 128;
+  constexpr int KST = H / 32;               // 32-k steps
+  constexpr int NSW = (KST + NW - 1) / NW;  // steps per wave (the last may be short)
+  constexpr int LDX = H + 8;                // LDS row pitch (bf16): 16-byte reads conflict-free
+  constexpr int LTW = ET * 16 + 1;
+  constexpr int XA_BYTES = TT * LDX * 2, RED_BYTES = NW * 2 * ET * 64 * 16;
+  // the input rows, then (once every wave's MFMAs are done) the waves' partials
+  __shared__ __attribute__((aligned(16))) uint8_t smem[XA_BYTES > RED_BYTES ? XA_BYTES : RED_BYTES];
+  __shared__ float lt[2][TT][LTW];          // [router | the strip's source] logits
+  uint16_t* xa = reinterpret_cast<uint16_t*>(smem);
+  f32x4* red = reinterpret_cast<f32x4*>(smem);  // [NW][2 ET][64]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q = lane >> 4, l16 = lane & 15;
+  const int strip = blockIdx.x, t0 = blockIdx.y * TT;
+  const bool src = strip > 0;
+  const int E = a.E, N = a.N;
+  // 1 weight fragments (lane: row l16 of tile ct, k 8q.. of step wave +
+  // 16 st): the router's, and (strips > 0) the source's E edge rows; rows
+  // past E read row E - 1 (never stored), steps past the last read step 0
+  // (not multiplied)
+  const uint16_t* rw = reinterpret_cast<const uint16_t*>(a.router_w);
+  const uint16_t* sw = reinterpret_cast<const uint16_t*>(a.edge_w) +
+                       static_cast<int64_t>(src ? strip - 1 : 0) * E * a.ldw;
+  u32x4 wr[NSW][ET], ws[NSW][ET];
+#pragma unroll
+  for (int ct = 0; ct < ET; ++ct) {
+    const int row = min(16 * ct + l16, E - 1);
+#pragma unroll
+    for (int st = 0; st < NSW; ++st) {
+      const int k = wave + NW * st;
+      const int kk = 32 * (k < KST ? k : 0) + 8 * q;
+      wr[st][ct] = *reinterpret_cast<const u32x4*>(rw + static_cast<int64_t>(row) * H + kk);
+      if (src)
+        ws[st][ct] = *reinterpret_cast<const u32x4*>(sw + static_cast<int64_t>(row) * a.ldw + kk);
+      else
+        ws[st][ct] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+  // 2 token `wave` of the tile -> LDS (bf16); rows past N are zeros
+  {
+    const int j = wave;
+    const int t = t0 + j;
+    float o[CPL][8];
+    if (t < N) {  // wave-uniform
+      if constexpr (PRO) {
+        float hv[CPL][8], xv[CPL][8], gw[CPL][8], gb[CPL][8];
+        ln_load<CPL, SMOE_BF16>(a.h, a.x0, a.ln_w, a.ln_b, t, H, hv, xv, gw, gb);
+#pragma unroll
+        for (int c = 0; c < CPL; ++c)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[c][i] = 0.f;
+        const int64_t e = static_cast<int64_t>(t) * a.K + (lane < a.K ? lane : a.K - 1);
+        const int te = a.tok_e[e];
+        const float tw = a.tok_ew[e];
+        const int tr = a.e_tokrow[e];
+        const int my_row = (lane < a.K && te >= 0 && tw > 0.f) ? tr : -1;
+        gather_add<CPL, SMOE_BF16>(a.y, H, my_row, __ballot(my_row >= 0), o);
+        ln_row<CPL>(hv, xv, gw, gb, o, H, a.alpha, a.beta, a.eps, o);  // in place
+      } else {
+#pragma unroll
+        for (int c = 0; c < CPL; ++c) {
+          const int col = (lane + 64 * c) * 8;
+          load8<SMOE_BF16>(a.h, static_cast<int64_t>(t) * H + (col < H ? col : 0), o[c]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < CPL; ++c)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[c][i] = 0.f;
+    }
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {
+      const int col = (lane + 64 * c) * 8;
+      if (col < H) {
+        u32x4 pk;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pk[i] = pack_bf2(o[c][2 * i], o[c][2 * i + 1]);
+        *reinterpret_cast<u32x4*>(xa + j * LDX + col) = pk;
+        if (PRO && strip == 0 && t < N)
+          *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(a.h_out) +
+                                    static_cast<int64_t>(t) * H + col) = pk;
+      }
+    }
+  }
+  lds_barrier();
+  // 3 logits: this wave's k steps, then the waves' partials in wave order
+  f32x4 acc[2 * ET];
+#pragma unroll
+  for (int c = 0; c < 2 * ET; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int st = 0; st < NSW; ++st) {
+    const int k = wave + NW * st;
+    if (k < KST) {  // wave-uniform
+      const u32x4 b = *reinterpret_cast<const u32x4*>(xa + l16 * LDX + 32 * k + 8 * q);
+#pragma unroll
+      for (int ct = 0; ct < ET; ++ct) {
+        acc[ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, wr[st][ct]),
+                                                          __builtin_bit_cast(bf16x8, b), acc[ct],
+                                                          0, 0, 0);
+        if (src)
+          acc[ET + ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8, ws[st][ct]), __builtin_bit_cast(bf16x8, b), acc[ET + ct],
+              0, 0, 0);
+      }
+    }
+  }
+  lds_barrier();  // every wave's reads of the rows are done: `red` reuses them
+#pragma unroll
+  for (int c = 0; c < 2 * ET; ++c) red[(wave * 2 * ET + c) * 64 + lane] = acc[c];
+  lds_barrier();
+  if (wave < 2 * ET && (src || wave < ET)) {  // tile `wave`: channels 4q.. of token l16
+    const int seg = wave / ET, ct = wave % ET;  // seg 0 router, 1 the source
+    f32x4 s = red[wave * 64 + lane];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) s += red[(w * 2 * ET + wave) * 64 + lane];
+    const float* bias = seg == 0 ? a.router_bias : a.edge_bias + (strip - 1) * E;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ch = 16 * ct + 4 * q + i;
+      if (ch < E) lt[seg][l16][ch] = s[i] + bias[ch];
+    }
+  }
+  lds_barrier();
+  // 4 per token: a segment of SEG lanes, lane e = channel e
+  constexpr int TPW = 64 / SEG;
+  const int e = lane & (SEG - 1);
+  if (wave * TPW < TT) {  // wave-uniform: waves past the tile's tokens are done
+    const int j = wave * TPW + lane / SEG;
+    const int t = t0 + j;
+    const bool ok = t < N;
+    const int ec = e < E ? e : 0;
+    const float v = lt[0][j][ec];
+    const uint64_t m = topk_seg<SEG>(v, t, ok && !src, true, E, a.K, a.top_idx, a.top_w, nullptr,
+                                     nullptr, nullptr, nullptr);
+    if (!src) {
+      if (ok && e < E) a.logits[static_cast<int64_t>(t) * E + e] = v;
+    } else {
+      const int s = strip - 1;
+      const bool sel_src = (m >> s) & 1ull;
+      const int rank = __popcll(m & ((1ull << s) - 1ull));
+      topm_row<SEG>(lt[1][j][ec], t, ok, sel_src, rank, E, a.K, a.M, a.sel_idx, a.sel_w);
+    }
+  }
+}
+
+bool decode_front_fits(int N, int H, int E, int K, int M, int S, int ldw) {
+  return N >= 1 && N <= kFrontMaxN && E >= 1 && E <= 64 && K >= 1 && K <= 16 && K <= E &&
+         M >= 1 && M <= 16 && M <= E && K * M <= 64 && S >= 1 && S <= 16 && H >= 128 &&
+         H <= 1024 && H % 128 == 0 && ldw >= H && ldw % 8 == 0;  // H > 1024: the rows spill
+}
+
+namespace {
+template <int CPL, int NS, bool PRO>
+int decode_front_e(const DecFront& a, hipStream_t s) {
+  const dim3 grid(a.E + 1, (a.N + 15) / 16), block(1024);
+  const int et = (a.E + 15) / 16;
+#define SMOE_DFRONT(SG, ET_)                                                              \
+  do {                                                                                    \
+    SMOE_LAUNCH((k_decode_front<CPL, SG, ET_, NS, PRO>), grid, block, 0, s, a);           \
+    return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;                         \
+  } while (0)
+  switch (et) {
+    case 1: SMOE_DFRONT(16, 1);
+    case 2: SMOE_DFRONT(32, 2);
+    case 3: SMOE_DFRONT(64, 3);
+    case 4: SMOE_DFRONT(64, 4);
+    default: return SMOE_EINVAL;
+  }
+#undef SMOE_DFRONT
+}
+template <bool PRO>
+int decode_front_h(const DecFront& a, hipStream_t s) {
+  switch (a.H) {
+    case 128: return decode_front_e<1, 1, PRO>(a, s);
+    case 256: return decode_front_e<1, 2, PRO>(a, s);
+    case 384: return decode_front_e<1, 3, PRO>(a, s);
+    case 512: return decode_front_e<1, 4, PRO>(a, s);
+    case 640: return decode_front_e<2, 5, PRO>(a, s);
+    case 768: return decode_front_e<2, 6, PRO>(a, s);
+    case 896: return decode_front_e<2, 7, PRO>(a, s);
+    case 1024: return decode_front_e<2, 8, PRO>(a, s);
+    default: return SMOE_EINVAL;
+  }
+}
+}  // namespace
+
+int launch_decode_front(const DecFront& a, hipStream_t s) {
+  const int S = a.E < a.K * a.M ? a.E : a.K * a.M;
+  if (!decode_front_fits(a.N, a.H, a.E, a.K, a.M, S, a.ldw)) return SMOE_EINVAL;
+  if (!a.h || !a.router_w || !a.edge_w || !a.router_bias || !a.edge_bias || !a.logits ||
+      !a.top_idx || !a.top_w || !a.sel_idx || !a.sel_w)
+    return SMOE_EINVAL;
+  if (a.y) {
+    if (!a.x0 || !a.tok_e || !a.tok_ew || !a.e_tokrow || !a.h_out) return SMOE_EINVAL;
+    return decode_front_h<true>(a, s);
+  }
+  return decode_front_h<false>(a, s);
+}
+
+// Plans of a decode loop (N <= 64 tokens, S <= 16 destinations per token);
+// KB >= K and KMB >= K * M (compile-time buckets).  Lane t = token t.
+constexpr int kDecMaxS = 16;
+template <int KB, int KMB>
+__global__ __launch_bounds__(128) void k_decode_plan(
+    const int32_t* __restrict__ top_idx, const float* __restrict__ top_w,
+    const int32_t* __restrict__ sel_idx, const float* __restrict__ sel_w, int N, int E, int K,
+    int M, int S, int32_t* __restrict__ tok_e, float* __restrict__ tok_ew,
+    int32_t* __restrict__ e_cnt, int32_t* __restrict__ e_acnt, int32_t* __restrict__ e_off,
+    int32_t* __restrict__ e_rows, float* __restrict__ e_roww, int32_t* __restrict__ e_tokrow,
+    int32_t* __restrict__ edge_idx, float* __restrict__ edge_w, int32_t* __restrict__ tok_d,
+    float* __restrict__ tok_dc, int32_t* __restrict__ d_cnt, int32_t* __restrict__ d_acnt,
+    int32_t* __restrict__ d_off, int32_t* __restrict__ d_rows, float* __restrict__ d_roww,
+    int32_t* __restrict__ d_tokrow) {
+  __shared__ int32_t s_te[kFrontMaxN * KB], s_etr[kFrontMaxN * KB];
+  __shared__ float s_tw[kFrontMaxN * KB];
+  __shared__ float s_c[kFrontMaxN * 65];
+  __shared__ int32_t s_td[kFrontMaxN * kDecMaxS], s_dtr[kFrontMaxN * kDecMaxS];
+  __shared__ float s_tc[kFrontMaxN * kDecMaxS];
+  __shared__ uint64_t s_km[2][64], s_am[2][64];
+  __shared__ int s_off[2][64];
+  const int t = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const bool tv = t < N;
+  const int tc = tv ? t : 0;
+  const int km = K * M;
+  if (wave == 0) {
+    // the token's top-k sorted by expert (ids are distinct: rank = # smaller),
+    // its sources' edges (in that order already) loaded alongside
+    int ti[KB], ei[KMB];
+    float tw[KB], ew[KMB];
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {
+      const int jj = j < K ? j : K - 1;
+      ti[j] = top_idx[tc * K + jj];
+      tw[j] = top_w[tc * K + jj];
+    }
+#pragma unroll
+    for (int u = 0; u < KMB; ++u) {
+      const int uu = u < km ? u : km - 1;
+      ei[u] = sel_idx[tc * km + uu];
+      ew[u] = sel_w[tc * km + uu];
+    }
+    if (tv)
+#pragma unroll
+      for (int j = 0; j < KB; ++j) {
+        if (j >= K) break;
+        int rank = 0;
+#pragma unroll
+        for (int i = 0; i < KB; ++i) rank += (i < K && ti[i] < ti[j]) ? 1 : 0;
+        s_te[t * K + rank] = ti[j];
+        s_tw[t * K + rank] = tw[j];
+        tok_e[t * K + rank] = ti[j];
+        tok_ew[t * K + rank] = tw[j];
+      }
+    plan64_wave(s_te, s_tw, N, K, E, 0, e_cnt, e_acnt, e_off, e_rows, e_roww, s_etr, s_km[0],
+                s_am[0], s_off[0]);
+    if (tv)
+#pragma unroll
+      for (int u = 0; u < KMB; ++u) {
+        if (u >= km) break;
+        const int j = u / M, i = u - j * M;
+        const int row = s_etr[t * K + j];
+        if (i == 0) e_tokrow[t * K + j] = row;
+        if (row >= 0) {
+          edge_idx[static_cast<int64_t>(row) * M + i] = ei[u];
+          edge_w[static_cast<int64_t>(row) * M + i] = ew[u];
+        }
+      }
+  } else {
+    // destination coefficients: sum over the sources in ascending order
+    int ei[KMB];
+    float ew[KMB];
+#pragma unroll
+    for (int u = 0; u < KMB; ++u) {
+      const int uu = u < km ? u : km - 1;
+      ei[u] = sel_idx[tc * km + uu];
+      ew[u] = sel_w[tc * km + uu];
+    }
+    float* crow = s_c + tc * 65;
+    if (tv) {
+      for (int d = 0; d < E; ++d) crow[d] = 0.f;
+#pragma unroll
+      for (int u = 0; u < KMB; ++u)
+        if (u < km) crow[ei[u]] += ew[u];
+      int cnt = 0;
+      for (int d = 0; d < E; ++d) {
+        const float c = crow[d];
+        if (c != 0.f) {
+          s_td[t * S + cnt] = d;
+          s_tc[t * S + cnt] = c;
+          ++cnt;
+        }
+      }
+      for (int j = cnt; j < S; ++j) {
+        s_td[t * S + j] = -1;
+        s_tc[t * S + j] = 0.f;
+      }
+      for (int j = 0; j < S; ++j) {
+        tok_d[t * S + j] = s_td[t * S + j];
+        tok_dc[t * S + j] = s_tc[t * S + j];
+      }
+    }
+    plan64_wave(s_td, s_tc, N, S, E, 1, d_cnt, d_acnt, d_off, d_rows, d_roww, s_dtr, s_km[1],
+                s_am[1], s_off[1]);
+    if (tv)
+      for (int j = 0; j < S; ++j) d_tokrow[t * S + j] = s_dtr[t * S + j];
+  }
+}
+
+int launch_decode_plan(const int32_t* top_idx, const float* top_w, const int32_t* sel_idx,
+                       const float* sel_w, int N, int E, int K, int M, int S, int32_t* tok_e,
+                       float* tok_ew, int32_t* e_cnt, int32_t* e_acnt, int32_t* e_off,
+                       int32_t* e_rows, float* e_roww, int32_t* e_tokrow, int32_t* edge_idx,
+                       float* edge_w, int32_t* tok_d, float* tok_dc, int32_t* d_cnt,
+                       int32_t* d_acnt, int32_t* d_off, int32_t* d_rows, float* d_roww,
+                       int32_t* d_tokrow, hipStream_t s) {
+  if (N < 1 || N > kFrontMaxN || E < 1 || E > 64 || K < 1 || K > 16 || K > E || M < 1 ||
+      M > E || M > 16 || S < 1 || S > kDecMaxS || S != (E < K * M ? E : K * M))
+    return SMOE_EINVAL;
+  const int km = K * M;
+#define SMOE_DPLAN(KB_, KMB_)                                                                  \
+  hipLaunchKernelGGL((k_decode_plan<KB_, KMB_>), dim3(1), dim3(128), 0, s, top_idx, top_w,      \
+                     sel_idx, sel_w, N, E, K, M, S, tok_e, tok_ew, e_cnt, e_acnt, e_off, e_rows, \
+                     e_roww, e_tokrow, edge_idx, edge_w, tok_d, tok_dc, d_cnt, d_acnt, d_off,    \
+                     d_rows, d_roww, d_tokrow)
+  if (K <= 2 && km <= 4) SMOE_DPLAN(2, 4);
+  else if (K <= 2 && km <= 8) SMOE_DPLAN(2, 8);
+  else if (K <= 4 && km <= 8) SMOE_DPLAN(4, 8);
+  else if (K <= 4 && km <= 16) SMOE_DPLAN(4, 16);
+  else if (K <= 8 && km <= 32) SMOE_DPLAN(8, 32);
+  else if (km <= 64) SMOE_DPLAN(16, 64);
+  else return SMOE_EINVAL;
+#undef SMOE_DPLAN
+  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}

@@ -110,6 +110,52 @@ int launch_front_route(const float* front, int ldf, int N, int E, int K, int M, 
                        float* d_roww, int32_t* d_tokrow, const int32_t* active,
                        hipStream_t s);
 constexpr int kFrontMaxN = 64;
+
+// ---- decode loop (bf16, N <= 64): two launches in place of the front GEMM,
+// the routing workgroup and the previous loop's epilogue ----
+// k_decode_front: per (strip, 16-token tile); every strip computes the
+// router logits and top-k of its tokens; strip 0 writes them, strip s + 1
+// computes source s's E edge logits, and for each token that selected s its
+// top-m and softmax weights, written at the source's rank among the token's
+// sources (ascending).  With `y` set it first computes the tile's input rows
+// as the previous loop's LayerNorm (h_{r-1}, its expert rows y and routing
+// tok_e / tok_ew / e_tokrow, x0), and strip 0 writes them to h_out.
+struct DecFront {
+  const void* h = nullptr;  // the loop's input (no y) or the previous loop's input (y set)
+  const void* x0 = nullptr;
+  const void* y = nullptr;  // previous loop's expert rows (bf16), or null
+  const int32_t* tok_e = nullptr;
+  const float* tok_ew = nullptr;
+  const int32_t* e_tokrow = nullptr;
+  const float* ln_w = nullptr;
+  const float* ln_b = nullptr;
+  float alpha = 0.f, beta = 0.f, eps = 0.f;
+  void* h_out = nullptr;  // y set: the LayerNorm rows (this loop's input)
+  const void* router_w = nullptr;  // bf16 [E, H]
+  const float* router_bias = nullptr;  // [E]
+  const void* edge_w = nullptr;  // bf16 [E * E, ldw]
+  int ldw = 0;
+  const float* edge_bias = nullptr;  // [E * E]
+  int N = 0, H = 0, E = 0, K = 0, M = 0;
+  float* logits = nullptr;   // [N, E]
+  int32_t* top_idx = nullptr;  // [N, K]
+  float* top_w = nullptr;
+  int32_t* sel_idx = nullptr;  // [N, K, M] top-m destinations of each selected source
+  float* sel_w = nullptr;      // their softmax weights
+};
+// shapes the decode loop takes (else the general stages run)
+bool decode_front_fits(int N, int H, int E, int K, int M, int S, int ldw);
+int launch_decode_front(const DecFront& a, hipStream_t s);
+// k_decode_plan: one workgroup: the tokens' sources ascending (tok_e /
+// tok_ew), the expert plan and each source row's edges at its plan row; the
+// destination coefficients (tok_d / tok_dc) and the destination plan.
+int launch_decode_plan(const int32_t* top_idx, const float* top_w, const int32_t* sel_idx,
+                       const float* sel_w, int N, int E, int K, int M, int S, int32_t* tok_e,
+                       float* tok_ew, int32_t* e_cnt, int32_t* e_acnt, int32_t* e_off,
+                       int32_t* e_rows, float* e_roww, int32_t* e_tokrow, int32_t* edge_idx,
+                       float* edge_w, int32_t* tok_d, float* tok_dc, int32_t* d_cnt,
+                       int32_t* d_acnt, int32_t* d_off, int32_t* d_rows, float* d_roww,
+                       int32_t* d_tokrow, hipStream_t s);
 int launch_edge_loop_bias(const void* wg, int act_dtype, const float* bg, const float* emb, int E,
                           int H, int L, int R, float* out, hipStream_t s);
 

@@ -19,6 +19,7 @@
 // from wave ballots (deterministic, no atomics on the output order).
 #include "smoe_common.hpp"
 #include "smoe_internal.hpp"
+#include "smoe_rows.hpp"
 
 namespace smoe {
 
@@ -35,8 +36,9 @@ constexpr int kBig = 1 << 20;
 // live == false (a token that has left the orbit under an exit gate): the
 // token's tok_e / tok_ew slots are all -1 / 0, so every plan, the edge
 // stages and the expert GEMMs skip it; top_idx / top_w are still written.
+// Returns the segment's mask of selected experts (bit e = expert e).
 template <int SEG>
-__device__ __forceinline__ void topk_seg(float v, int t, bool ok, bool live, int E, int K,
+__device__ __forceinline__ uint64_t topk_seg(float v, int t, bool ok, bool live, int E, int K,
                                          int32_t* __restrict__ top_idx, float* __restrict__ top_w,
                                          int32_t* __restrict__ tok_e, float* __restrict__ tok_ew,
                                          int32_t* tok_e2, float* tok_ew2) {
@@ -70,6 +72,7 @@ __device__ __forceinline__ void topk_seg(float v, int t, bool ok, bool live, int
   // distinct experts of the token in ascending order (lane order)
   const uint64_t segm = SEG == 64 ? ~0ull : ((1ull << SEG) - 1);
   const uint64_t m = (__ballot(sel) >> sbase) & segm;
+  if (!tok_e) return m;  // top-k only (the decode front: its plan kernel sorts the sources)
   if (ok && live && sel) {
     const int rank = __popcll(m & ((1ull << e) - 1));
     tok_e[static_cast<int64_t>(t) * K + rank] = e;
@@ -87,6 +90,7 @@ __device__ __forceinline__ void topk_seg(float v, int t, bool ok, bool live, int
       tok_ew2[t * K + e] = 0.f;
     }
   }
+  return m;
 }
 
 template <int SEG>
@@ -866,6 +870,9 @@ int launch_front_route(const float* front, int ldf, int N, int E, int K, int M, 
 #undef SMOE_FRONT
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
+
+// ------------------------------------------------------- decode loop ----
+#include "smoe_decode.inl"
 
 size_t plan_scratch_bytes(int N, int G) {
   const size_t C = (static_cast<size_t>(N > 0 ? N : 1) + 63) / 64;

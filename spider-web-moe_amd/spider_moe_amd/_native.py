@@ -42,7 +42,7 @@ class SmoeBlock(ctypes.Structure):
 _LAYOUT_FIELDS = ["total", "logits", "top_idx", "top_w", "tok_e", "tok_ew", "e_cnt", "e_acnt",
                   "e_off", "e_rows", "e_roww", "e_tokrow", "edge_logit", "edge_idx", "edge_w",
                   "tok_d", "tok_dc", "d_cnt", "d_acnt", "d_off", "d_rows", "d_roww", "d_tokrow",
-                  "proj", "msg", "act", "y", "h_tmp", "scratch", "front"]
+                  "proj", "msg", "act", "y", "h_tmp", "scratch", "front", "sel_idx", "sel_w", "h_tmp2"]
 
 
 class SmoeWsLayout(ctypes.Structure):
@@ -97,7 +97,7 @@ STAGES = ["router_gemm", "route_topk", "expert_plan", "edge_logits", "edge_topm"
           # bf16 steps of N <= 64: stages 0-5 as one GEMM and one routing workgroup
           "front_gemm", "front_route"]
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 _LIB = None
 
 

@@ -50,6 +50,7 @@ class _Packed:
     def __init__(self):
         self.keep = []
         self.desc = nat.SmoeBlock()
+        self.ws_need = {}  # tokens -> workspace bytes
 
 
 class SpiderMoELayer(nn.Module):
@@ -106,6 +107,7 @@ class SpiderMoELayer(nn.Module):
         self.weight_tiles = True
         self._packed: _Packed | None = None
         self._packed_key = None
+        self._plist = None
         self._ws: torch.Tensor | None = None
         self._last_n = 0
         self._last_ws: torch.Tensor | None = None
@@ -149,14 +151,20 @@ class SpiderMoELayer(nn.Module):
 
     # ----------------------------------------------------------- packing ----
     def _state_key(self):
+        # the parameter objects are listed once per pack (walking the module
+        # tree costs more than the key); a parameter that is modified in
+        # place, moved (.to) or re-typed changes its version, address or dtype
+        plist = self._plist if self._plist is not None else list(self.parameters())
         return (self.expert_format, id(self._int4_w_up), id(self._fp8), self.weight_tiles,
-                tuple((p.data_ptr(), p._version, p.dtype) for p in self.parameters()))
+                len(plist), tuple([(p.data_ptr(), p._version, p.dtype) for p in plist]))
 
     @torch.no_grad()
     def _pack(self) -> _Packed:
         key = self._state_key()
         if self._packed is not None and self._packed_key == key:
             return self._packed
+        self._plist = list(self.parameters())
+        key = self._state_key()
         dev = nat.require_gpu(*self.parameters())
         act = self.router.weight.dtype
         adt = nat.dtype_code(act)
@@ -265,18 +273,21 @@ class SpiderMoELayer(nn.Module):
         self._packed, self._packed_key = k, key
         return k
 
-    def workspace_bytes(self, n: int) -> int:
+    def workspace_bytes(self, n: int, packed: _Packed | None = None) -> int:
         """Bytes of the native workspace a call over n tokens needs."""
-        k = self._pack()
-        need = nat.lib().smoe_block_workspace_bytes(ctypes.byref(k.desc), n)
-        if need == 0:
-            nat.check(nat.lib().smoe_block_workspace_layout(ctypes.byref(k.desc), n,
-                                                            ctypes.byref(nat.SmoeWsLayout())),
-                      "smoe_block_workspace_layout")
-        return max(need, 256)
+        k = packed if packed is not None else self._pack()
+        need = k.ws_need.get(n)
+        if need is None:
+            need = nat.lib().smoe_block_workspace_bytes(ctypes.byref(k.desc), n)
+            if need == 0:
+                nat.check(nat.lib().smoe_block_workspace_layout(ctypes.byref(k.desc), n,
+                                                                ctypes.byref(nat.SmoeWsLayout())),
+                          "smoe_block_workspace_layout")
+            need = k.ws_need[n] = max(need, 256)
+        return need
 
-    def _workspace(self, n: int, dev) -> torch.Tensor:
-        need = self.workspace_bytes(n)
+    def _workspace(self, n: int, dev, packed: _Packed) -> torch.Tensor:
+        need = self.workspace_bytes(n, packed)
         if self._ws is None or self._ws.numel() < need or self._ws.device != dev:
             self._ws = torch.empty(need, dtype=torch.uint8, device=dev)
         return self._ws
@@ -300,12 +311,13 @@ class SpiderMoELayer(nn.Module):
         out = torch.empty_like(h2)
         k = self._pack()
         if workspace is None:
-            ws = self._workspace(n, dev)
+            ws = self._workspace(n, dev, k)
         else:
+            need = self.workspace_bytes(n, k)
             if (workspace.dtype != torch.uint8 or workspace.device != dev
-                    or not workspace.is_contiguous() or workspace.numel() < self.workspace_bytes(n)):
+                    or not workspace.is_contiguous() or workspace.numel() < need):
                 raise ValueError("workspace must be a contiguous uint8 tensor on the input's GPU "
-                                 f"of at least {self.workspace_bytes(n)} bytes")
+                                 f"of at least {need} bytes")
             ws = workspace
         if gate is None:
             nat.check(nat.lib().smoe_block_forward(ctypes.byref(k.desc), h2.data_ptr(), x2.data_ptr(),

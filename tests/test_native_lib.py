@@ -38,7 +38,7 @@ def test_exports_every_declared_symbol(nat):
 
 def test_identity(nat):
     lib = nat.lib()
-    assert lib.smoe_abi_version() == 6
+    assert lib.smoe_abi_version() == 7
     assert lib.smoe_backend_name() == b"hip-gfx950"
     assert lib.smoe_backend_caps() == 0b1111
 
@@ -69,8 +69,10 @@ def test_workspace_layout_is_consistent(nat):
     assert lay.total == lib.smoe_block_workspace_bytes(ctypes.byref(b), n)
     offs = sorted((getattr(lay, f), f) for f in nat._LAYOUT_FIELDS if f != "total")
     assert all(o % 256 == 0 for o, _ in offs)
-    assert lay.front == lay.total  # the fused small-step front is off at this N: empty region
-    assert max(o for o, f in offs if f != "front") < lay.total
+    # the small-step regions are empty at this N (they sit at the end)
+    small_only = ("front", "sel_idx", "sel_w", "h_tmp2")
+    assert all(getattr(lay, f) == lay.total for f in small_only)
+    assert max(o for o, f in offs if f not in small_only) < lay.total
     assert lay.S == 4 and lay.ffn_dtype == nat.BF16
     # regions do not overlap: each is at least its size from the next
     assert lay.top_idx - lay.logits >= n * 16 * 4
@@ -80,6 +82,10 @@ def test_workspace_layout_is_consistent(nat):
     small = nat.SmoeWsLayout()
     assert lib.smoe_block_workspace_layout(ctypes.byref(b), 64, ctypes.byref(small)) == 0
     assert small.total - small.front >= 64 * (16 + 16 * 16) * 4
+    # and the decode loop's regions: per-token source edges [N, K, M], a second input buffer
+    assert small.sel_w - small.sel_idx >= 64 * 2 * 2 * 4
+    assert small.h_tmp2 - small.sel_w >= 64 * 2 * 2 * 4
+    assert small.total - small.h_tmp2 >= 64 * 1024 * 2
 
 
 @pytest.mark.parametrize("bad", [dict(K=0), dict(K=17), dict(E=65), dict(M=0), dict(H=1000),
