@@ -298,6 +298,43 @@ SMOE_API int smoe_combine_epilogue(const void* h, const void* x0, int act_dtype,
                                    float beta, const float* ln_w, const float* ln_b, float eps,
                                    void* out, void* stream);
 
+/* ---- Forge surfaces (spider_infer/forge) on the same kernels ---- */
+
+/* Top-k selection over f32 logits [N,E] (1 <= K <= E <= 64) -> top_w f32
+ * [N,K], top_idx i32 [N,K], descending.
+ *   SMOE_SELECT_ROUTER: the block's router (model.py:256-258): softmax over
+ *     the E logits, top-k, weights renormalised by max(sum, 1e-9);
+ *   SMOE_SELECT_TOPK_SOFTMAX: ForgeSelect.route (forge/select/api.py:28-40):
+ *     top-k on the logits, softmax over the k values.
+ * Ties go to the lower index.  No workspace. */
+#define SMOE_SELECT_ROUTER 0
+#define SMOE_SELECT_TOPK_SOFTMAX 1
+SMOE_API int smoe_select_topk(const float* logits, int N, int E, int K, int mode, float* top_w,
+                              int32_t* top_idx, void* stream);
+
+/* out [N, N_out] = act(x [N,K] . W^T * scale + bias): ForgeGEMM.linear /
+ * linear_fp8 / the two halves of expert_ffn (forge/gemm/api.py:34-58,
+ * fp8.py:22-78, triton_kernels.py:65-123) on the block's GEMM kernels.
+ * x: f32 (w_format SMOE_F32) or bf16 (SMOE_BF16, SMOE_FP8_E4M3); W
+ * [N_out, K] row-major (e4m3 codes for SMOE_FP8_E4M3, whose scale f32
+ * [N_out] is required: a per-tensor scale is that value in every entry);
+ * bias f32 [N_out] or NULL; act SMOE_LINEAR_NONE (out f32) or
+ * SMOE_LINEAR_GELU (erf GELU; out f32 or bf16).  K % 32 == 0 (f32: % 16). */
+#define SMOE_LINEAR_NONE 0
+#define SMOE_LINEAR_GELU 1
+SMOE_API int smoe_linear(const void* x, int N, int K, const void* w, int w_format,
+                         const float* w_scale, const float* bias, int N_out, int act, void* out,
+                         int out_dtype, void* stream);
+
+/* out [N,H] = per token, the sum over its rows tok_row [N,K] (-1: none, in
+ * slot order) of y [R,H] times row_w [R] (NULL: 1), each product rounded to
+ * y's dtype and each partial sum to out's (SMOE_F32 / SMOE_BF16): the
+ * combine of dispatch_expert_ffn (forge/ep/dispatch.py:127-134, 176-180),
+ * a scatter-add of weighted expert outputs in ascending expert order. */
+SMOE_API int smoe_combine_rows(const void* y, int y_dtype, const float* row_w,
+                               const int32_t* tok_row, int N, int K, int H, void* out,
+                               int out_dtype, void* stream);
+
 /* ---- diagnostics (no counterpart in the reference; used by bench.py) ----
  * Stage ids of smoe_block_forward, in launch order within a loop. */
 #define SMOE_STAGE_ROUTER_GEMM 0

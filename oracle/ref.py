@@ -128,3 +128,66 @@ def loop_epilogue_f32(h, delta, x0, alpha, beta, ln_w, ln_b, eps):
     rc = lib().spider_loop_epilogue_f32(_fp(h), _fp(d), _fp(x), b, hid, alpha, beta,
                                         _fp(g), _fp(lb), eps, _fp(out))
     return rc, out
+
+
+def graph_message_passing_f32(hidden, row_ptr, col_idx, edge_w, assign, route, loop_idx=0):
+    """spider_graph_message_passing_f32 (scalar.cpp:36-53): the static CSR
+    graph with route weights (v1)."""
+    h = _f32(hidden)
+    rp = np.ascontiguousarray(row_ptr, np.int32)
+    ci = np.ascontiguousarray(col_idx, np.int32)
+    ew = _f32(edge_w)
+    asg = np.ascontiguousarray(assign, np.int32)
+    rw = _f32(route)
+    b, hid = h.shape
+    e = len(rp) - 1
+    out = np.zeros_like(h)
+    rc = lib().spider_graph_message_passing_f32(_fp(h), b, hid, e, asg.shape[1], _ip(rp), _ip(ci),
+                                                _fp(ew), len(ci), loop_idx, _ip(asg), _fp(rw),
+                                                _fp(out))
+    return rc, out
+
+
+def early_exit_f32(h, proj, threshold):
+    """spider_early_exit_f32 (scalar.cpp:94-104)."""
+    h = _f32(h)
+    p = _f32(proj)
+    b, hid = h.shape
+    mask = np.zeros(b, np.uint8)
+    lib().spider_early_exit_f32.argtypes = [_f32p, _f32p, ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_float, ctypes.POINTER(ctypes.c_uint8)]
+    rc = lib().spider_early_exit_f32(_fp(h), _fp(p), b, hid, threshold,
+                                     mask.ctypes.data_as(ctypes.POINTER(ctypes.c_uint8)))
+    return rc, mask
+
+
+def moe_loop_step_f32(h, x0, k, loop_idx, router_w, loop_bias, w_up, w_down, ln_w, ln_b, alpha,
+                      beta, eps, exit_proj=None, threshold=0.85):
+    """spider_moe_loop_step_f32 (scalar_phase1_1.cpp:62-121) without the
+    edge-value graph (W_edge and the CSR NULL: messages = h)."""
+    h = _f32(h)
+    x = _f32(x0)
+    rw = _f32(router_w)
+    lb = _f32(loop_bias)
+    wu = _f32(w_up)
+    wd = _f32(w_down)
+    g = _f32(ln_w)
+    gb = _f32(ln_b)
+    b, hid = h.shape
+    e = rw.shape[1]
+    u = wu.shape[2]
+    out = np.zeros_like(h)
+    mask = np.zeros(b, np.uint8)
+    asg = np.zeros((b, k), np.int32)
+    route = np.zeros((b, k), np.float32)
+    msgs = np.zeros_like(h)
+    ep = None if exit_proj is None else _f32(exit_proj)
+    c_i, c_f, vp = ctypes.c_int, ctypes.c_float, ctypes.c_void_p
+    fn = lib().spider_moe_loop_step_f32
+    fn.argtypes = [vp, vp, c_i, c_i, c_i, c_i, c_i, c_i, vp, vp, vp, vp, vp, c_i, vp, vp, vp,
+                   vp, vp, c_f, c_f, c_f, vp, c_f, vp, vp, vp, vp, vp]
+    ptr = lambda a: None if a is None else a.ctypes.data  # noqa: E731
+    rc = fn(ptr(h), ptr(x), b, hid, e, k, u, loop_idx, ptr(rw), ptr(lb), None, None, None, 0,
+            None, ptr(wu), ptr(wd), ptr(g), ptr(gb), alpha, beta, eps, ptr(ep), threshold,
+            ptr(out), ptr(mask), ptr(asg), ptr(route), ptr(msgs))
+    return rc, out, mask, asg, route

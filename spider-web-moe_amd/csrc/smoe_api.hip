@@ -997,6 +997,70 @@ SMOE_API int smoe_edge_message(const void* x, int act_dtype, int N, int H,
   return SMOE_OK;
 }
 
+SMOE_API int smoe_select_topk(const float* logits, int N, int E, int K, int mode, float* top_w,
+                              int32_t* top_idx, void* stream) {
+  if (N < 0 || E < 1 || E > 64 || K < 1 || K > E) return fail(SMOE_EINVAL, "select shape");
+  if (mode != SMOE_SELECT_ROUTER && mode != SMOE_SELECT_TOPK_SOFTMAX)
+    return fail(SMOE_EINVAL, "select mode");
+  if (N == 0) return SMOE_OK;
+  if (!logits || !top_w || !top_idx) return fail(SMOE_EINVAL, "null buffer");
+  SMOE_TRY(launch_select_topk(logits, N, E, K, mode, top_w, top_idx,
+                              static_cast<hipStream_t>(stream)),
+           "select top-k");
+  return SMOE_OK;
+}
+
+SMOE_API int smoe_linear(const void* x, int N, int K, const void* w, int w_format,
+                         const float* w_scale, const float* bias, int N_out, int act, void* out,
+                         int out_dtype, void* stream) {
+  if (N < 0 || K <= 0 || N_out <= 0) return fail(SMOE_EINVAL, "linear shape");
+  if (w_format != SMOE_F32 && w_format != SMOE_BF16 && w_format != SMOE_FP8_E4M3)
+    return fail(SMOE_EUNSUPPORTED, "linear weight format");
+  if (act != SMOE_LINEAR_NONE && act != SMOE_LINEAR_GELU) return fail(SMOE_EINVAL, "act");
+  if (out_dtype != SMOE_F32 && out_dtype != SMOE_BF16) return fail(SMOE_EUNSUPPORTED, "out dtype");
+  if (act == SMOE_LINEAR_NONE && out_dtype != SMOE_F32)
+    return fail(SMOE_EUNSUPPORTED, "a linear without activation writes f32");
+  if (w_format == SMOE_F32 && (K % 16 || out_dtype != SMOE_F32))
+    return fail(SMOE_EINVAL, "f32 linear: K % 16 == 0, f32 out");
+  if (w_format != SMOE_F32 && K % 32) return fail(SMOE_EINVAL, "linear: K % 32 == 0");
+  if (w_format == SMOE_FP8_E4M3 && !w_scale) return fail(SMOE_EINVAL, "fp8 weights need a scale");
+  if (N == 0) return SMOE_OK;
+  if (!x || !w || !out) return fail(SMOE_EINVAL, "null buffer");
+  GemmArgs g;
+  g.fmt = w_format;
+  g.epi = act == SMOE_LINEAR_GELU ? EPI_GELU : EPI_F32_BIAS;
+  g.A = x;
+  g.lda = K;
+  g.W = w;
+  g.ldw = K;
+  g.S = w_scale;
+  g.K = K;
+  g.N_out = N_out;
+  g.G = 0;
+  g.single_rows = N;
+  g.out = out;
+  g.ldo = N_out;
+  g.out_dtype = out_dtype;
+  g.bias = bias;
+  SMOE_TRY(launch_grouped_gemm(g, static_cast<hipStream_t>(stream)), "linear GEMM");
+  return SMOE_OK;
+}
+
+SMOE_API int smoe_combine_rows(const void* y, int y_dtype, const float* row_w,
+                               const int32_t* tok_row, int N, int K, int H, void* out,
+                               int out_dtype, void* stream) {
+  if (N < 0 || K < 1 || K > 64 || H <= 0 || H % 8 || H > 4096)
+    return fail(SMOE_EINVAL, "combine shape (1 <= K <= 64, H % 8 == 0, H <= 4096)");
+  if ((y_dtype != SMOE_F32 && y_dtype != SMOE_BF16) || (out_dtype != SMOE_F32 && out_dtype != SMOE_BF16))
+    return fail(SMOE_EUNSUPPORTED, "combine dtype");
+  if (N == 0) return SMOE_OK;
+  if (!y || !tok_row || !out) return fail(SMOE_EINVAL, "null buffer");
+  SMOE_TRY(launch_combine_rows(y, y_dtype, row_w, tok_row, N, K, H, out, out_dtype,
+                               static_cast<hipStream_t>(stream)),
+           "combine rows");
+  return SMOE_OK;
+}
+
 SMOE_API int smoe_combine_epilogue(const void* h, const void* x0, int act_dtype, const void* delta,
                                    int delta_dtype, int N, int H, float alpha, float beta,
                                    const float* ln_w, const float* ln_b, float eps, void* out,

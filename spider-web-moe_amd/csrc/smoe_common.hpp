@@ -15,6 +15,28 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 constexpr int kWave = 64;
 
+// ------------------------------------------------- separately rounded ----
+// A product and a sum each rounded on its own, as a CPU computes a * b + c
+// without fma.  HIP's __fmul_rn / __fadd_rn are the plain operators, which
+// -ffp-contract=fast fuses into one fma; operations written under
+// contract(off) carry no contraction flag, so they stay apart after inlining.
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+__device__ __forceinline__ double mul_rn(double a, double b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ double add_rn(double a, double b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+
 // ---------------------------------------------------------------- bf16 ----
 __device__ __forceinline__ float bf2f(uint16_t b) {
   return __uint_as_float(static_cast<uint32_t>(b) << 16);

@@ -111,6 +111,15 @@ int launch_front_route(const float* front, int ldf, int N, int E, int K, int M, 
                        hipStream_t s);
 constexpr int kFrontMaxN = 64;
 
+// ---- Forge surfaces (smoe_forge.hip) ----
+// top-k of f32 logits [N, E] (E <= 64): mode 0 the router's softmax / top-k
+// / renorm, mode 1 top-k on the logits then softmax over the k values
+int launch_select_topk(const float* logits, int N, int E, int K, int mode, float* top_w,
+                       int32_t* top_idx, hipStream_t s);
+// out[t] = sum over the token's rows tok_row [N, K] of y[row] * row_w[row]
+int launch_combine_rows(const void* y, int ydt, const float* row_w, const int32_t* tok_row,
+                        int N, int K, int H, void* out, int odt, hipStream_t s);
+
 // ---- decode loop (bf16, N <= 64): two launches in place of the front GEMM,
 // the routing workgroup and the previous loop's epilogue ----
 // k_decode_front: per (strip, 16-token tile); every strip computes the

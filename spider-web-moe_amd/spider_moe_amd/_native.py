@@ -17,6 +17,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libs
 # formats / activations / status codes (include/smoe.h)
 F32, BF16, FP8_E4M3, INT4, F16 = 0, 1, 2, 3, 4
 ACT_GELU, ACT_SWIGLU = 0, 1
+SMOE_SELECT_ROUTER, SMOE_SELECT_TOPK_SOFTMAX = 0, 1
 STATUS = {0: "ok", 1: "invalid argument", 2: "index out of range", 3: "capacity",
           -2: "unsupported dtype/format", 4: "HIP runtime error"}
 
@@ -85,11 +86,38 @@ SIGNATURES = {
                                    _vp, _vp, _vp, _vp, _c_int, _vp, _sz, _vp]),
     "smoe_combine_epilogue": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_float,
                                        _c_float, _vp, _vp, _c_float, _vp, _vp]),
+    "smoe_select_topk": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp]),
+    "smoe_linear": (_c_int, [_vp, _c_int, _c_int, _vp, _c_int, _vp, _vp, _c_int, _c_int, _vp,
+                             _c_int, _vp]),
+    "smoe_combine_rows": (_c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_int,
+                                   _vp]),
     "smoe_profile_stages": (_c_int, [ctypes.c_uint32, ctypes.POINTER(_vp), _c_int]),
     "smoe_profile_count": (_c_int, [ctypes.POINTER(ctypes.c_int32), _c_int]),
     "smoe_events_create": (_c_int, [_c_int, ctypes.POINTER(_vp)]),
     "smoe_events_destroy": (_c_int, [_c_int, ctypes.POINTER(_vp)]),
     "smoe_events_elapsed": (_c_int, [_c_int, ctypes.POINTER(_vp), ctypes.POINTER(ctypes.c_float)]),
+}
+
+# the reference's device ABI (include/spider_cuda.h), exported by the same library
+_f = ctypes.c_float
+SPIDER_CUDA_SIGNATURES = {
+    "spider_cuda_router_f32": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp]),
+    "spider_cuda_graph_message_passing_f32": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _vp,
+                                                       _vp, _vp, _c_int, _c_int, _vp, _vp, _vp,
+                                                       _vp]),
+    "spider_cuda_expert_grouped_gemm_f32": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                                     _vp, _vp, _vp, _vp, _vp, _vp]),
+    "spider_cuda_expert_workspace_bytes": (_sz, [_c_int, _c_int, _c_int]),
+    "spider_cuda_expert_grouped_gemm_v2_f32": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int,
+                                                        _c_int, _vp, _vp, _vp, _vp, _vp, _vp,
+                                                        _vp]),
+    "spider_cuda_loop_epilogue_f32": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _f, _f, _vp, _vp,
+                                               _f, _vp, _vp]),
+    "spider_cuda_early_exit_f32": (_c_int, [_vp, _vp, _c_int, _c_int, _f, _vp, _vp]),
+    "spider_cuda_moe_loop_step_f32": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                               _c_int, _vp, _vp, _vp, _vp, _vp, _c_int, _vp, _vp,
+                                               _vp, _vp, _f, _f, _f, _vp, _f, _vp, _vp, _vp, _vp,
+                                               _vp, _vp]),
 }
 
 STAGES = ["router_gemm", "route_topk", "expert_plan", "edge_logits", "edge_topm", "dest_plan",
@@ -110,7 +138,7 @@ def lib():
                 f"{LIB_PATH} is missing: build it with `python spider-web-moe_amd/build.py` "
                 "(spider_moe_amd has no CPU fallback)")
         handle = ctypes.CDLL(LIB_PATH)
-        for name, (res, args) in SIGNATURES.items():
+        for name, (res, args) in {**SIGNATURES, **SPIDER_CUDA_SIGNATURES}.items():
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args

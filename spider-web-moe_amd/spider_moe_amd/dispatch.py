@@ -92,10 +92,51 @@ def build_dispatch_plan(top_indices, top_weights, *, num_experts: int, local_onl
                         token_rows=tokrow)
 
 
+@torch.no_grad()
 def dispatch_expert_ffn(messages, top_indices, top_weights, *, w_up, b_up, w_down, b_down,
                         num_experts, expert_fn=None):
-    """dispatch.py:145-185 (the expert_fn callback form is not provided)."""
-    if expert_fn is not None:
-        raise NotImplementedError("expert_fn callbacks are not supported; the FFN runs in HIP")
-    return sparse_expert_delta(messages, top_indices, top_weights, w_up, b_up, w_down, b_down,
-                               num_experts=num_experts, top_k=top_indices.shape[-1])
+    """dispatch.py:145-185: dispatch -> local expert FFN -> combine.
+
+    Without expert_fn the FFN (Linear + bias, erf GELU, Linear + bias) is
+    sparse_expert_delta on the grouped GEMM kernels.  With expert_fn, the
+    plan comes from the GPU plan kernels and, for each non-empty expert in
+    ascending order, expert_fn(expert_id, tokens) runs on that expert's
+    packed token rows (dispatch_tokens, :118-124); its outputs are stacked
+    in plan order and the weighted combine (combine_tokens, :127-134: each
+    output times its routing weight, added per token in ascending expert
+    order) runs as one kernel (smoe_combine_rows).  messages [B,T,H] or
+    [N,H]; returns delta in messages' shape and dtype."""
+    if expert_fn is None:
+        m3 = messages if messages.ndim == 3 else messages.unsqueeze(1)
+        k = top_indices.shape[-1]
+        d = sparse_expert_delta(m3, top_indices.reshape(m3.shape[0], m3.shape[1], k),
+                                top_weights.reshape(m3.shape[0], m3.shape[1], k), w_up, b_up,
+                                w_down, b_down, num_experts=num_experts, top_k=k)
+        return d.view_as(messages)
+    dev = nat.require_gpu(messages, top_indices, top_weights)
+    if messages.dtype not in (torch.float32, torch.bfloat16):
+        raise TypeError("messages must be float32 or bfloat16")
+    h = messages.shape[-1]
+    flat = messages.reshape(-1, h)
+    plan = build_dispatch_plan(top_indices.reshape(flat.shape[0], -1),
+                               top_weights.reshape(flat.shape[0], -1), num_experts=num_experts)
+    rows = plan.rows.numel()
+    y = torch.empty(max(rows, 1), h, dtype=messages.dtype, device=dev)
+    off = 0
+    for asg in plan.assignments:
+        out = expert_fn(asg.expert_id, flat.index_select(0, asg.token_index))
+        n = asg.token_index.numel()
+        if out.shape != (n, h):
+            raise ValueError(f"expert_fn returned {tuple(out.shape)} for {n} tokens; "
+                             f"expected ({n}, {h})")
+        y[off:off + n] = out.to(messages.dtype)
+        off += n
+    dt = nat.dtype_code(messages.dtype)
+    delta = torch.empty(flat.shape[0], h, dtype=messages.dtype, device=dev)
+    k = plan.token_rows.shape[-1]
+    nat.check(nat.lib().smoe_combine_rows(y.data_ptr(), dt, plan.row_weights.data_ptr(),
+                                          plan.token_rows.data_ptr(), flat.shape[0], k, h,
+                                          delta.data_ptr(), dt, nat.stream_of(dev)),
+              "smoe_combine_rows")
+    plan.hidden = h
+    return delta.view_as(messages)

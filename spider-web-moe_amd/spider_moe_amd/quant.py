@@ -88,6 +88,16 @@ def dequantize_fp8_per_channel(codes: torch.Tensor, scale: torch.Tensor,
     return (codes.float() * scale.float().unsqueeze(-1)).to(dtype)
 
 
+def quantize_fp8_per_tensor(weight: torch.Tensor):
+    """One scale for the whole tensor, the format of the reference's
+    quantize_fp8 / compute_fp8_scale (quant.py:30-56): scale = max(amax / 448,
+    1e-12) (fp32, a 0-dim tensor), codes = (w.float() / scale) cast to
+    float8_e4m3fn (round to nearest even)."""
+    w = weight.detach().float()
+    scale = (w.abs().amax() / FP8_E4M3_MAX).clamp_min(1e-12)
+    return (w / scale).to(torch.float8_e4m3fn).contiguous(), scale
+
+
 # ------------------------------------------------------ SwiGLU layout ----
 SWIGLU_BLOCK = 32
 

@@ -1,0 +1,323 @@
+"""GPU parity of the reference's device ABI (spider_cuda_* through
+HipKernels / NativeLoop) against oracle/native.py, and of the Forge
+surfaces (ForgeSelect, ForgeGEMM, dispatch_expert_ffn with an expert_fn)
+against oracle/forge.py.
+
+Tolerances: the device ABI follows the scalar library's operation order;
+what remains are libm differences (expf in the router, tanhf in the GELU)
+and the router's sum order (a wave reduction against index order), so
+router weights compare at rtol 1e-5, expert outputs at rtol 1e-4 and the
+epilogue (a two-pass double variance against Welford) at 1e-5; the graph
+pass, indices, masks and the dispatch combine (fp32 and bf16) are exact."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import forge as OF
+from oracle import native as ON
+
+pytestmark = pytest.mark.gpu
+
+dev = "cuda"
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+
+
+def _kern():
+    from spider_moe_amd.native_compat import HipKernels
+    return HipKernels(dev)
+
+
+def _rng(seed):
+    return np.random.default_rng(seed)
+
+
+# ----------------------------------------------------- device ABI ----
+@pytest.mark.parametrize("b,e,k", [(2, 4, 2), (300, 16, 2), (77, 64, 8), (5, 33, 3)])
+def test_spider_cuda_router(b, e, k):
+    say("spider_cuda_router", b, e, k)
+    kern = _kern()
+    r = _rng(e + k)
+    logits = r.standard_normal((b, e)).astype(np.float32)
+    bias = (0.1 * r.standard_normal((3, e))).astype(np.float32)
+    for loop in (0, 2):
+        w, i = kern.router(logits, bias, k, loop)
+        wo, io = ON.router(logits, bias[loop], k)
+        assert np.array_equal(i, io)
+        assert np.allclose(w, wo, rtol=1e-5, atol=1e-7)
+    if b == 2:  # kernels/tests/test_kernels.cpp:7-18
+        w, i = kern.router(np.array([[1, 2, 3, 4], [4, 3, 2, 1]], np.float32),
+                           np.zeros((1, 4), np.float32), 2)
+        assert i.tolist() == [[3, 2], [0, 1]]
+        assert np.allclose(w.sum(-1), 1.0, atol=1e-6)
+
+
+def test_spider_cuda_argument_errors():
+    kern = _kern()
+    with pytest.raises(RuntimeError, match="spider_cuda_router_f32 failed"):
+        kern.router(np.zeros((2, 4), np.float32), np.zeros((1, 4), np.float32), 5)
+    with pytest.raises(RuntimeError, match="spider_cuda_router_f32 failed"):
+        kern.router(np.zeros((2, 80), np.float32), np.zeros((1, 80), np.float32), 2)
+
+
+def _csr(e, r, fanout=3):
+    rp = [0]
+    ci = []
+    for s in range(e):
+        n = int(r.integers(0, fanout + 1))
+        ci += [int(x) for x in r.integers(0, e, n)]
+        rp.append(len(ci))
+    return np.array(rp, np.int32), np.array(ci, np.int32)
+
+
+@pytest.mark.parametrize("b,h,e,k", [(5, 16, 6, 2), (200, 256, 16, 2), (33, 1000, 32, 4)])
+def test_spider_cuda_graph_v1(b, h, e, k):
+    say("spider_cuda_graph", b, h, e, k)
+    kern = _kern()
+    r = _rng(h)
+    x = r.standard_normal((b, h)).astype(np.float32)
+    rp, ci = _csr(e, r)
+    nnz = len(ci)
+    ew = r.random(2 * nnz).astype(np.float32)
+    asg = r.integers(0, e, (b, k)).astype(np.int32)
+    asg[0, -1] = -1  # an empty slot is skipped
+    rw = r.random((b, k)).astype(np.float32)
+    for loop in (0, 1):
+        got = kern.graph(x, rp, ci, ew, asg, rw, e, loop)
+        want = ON.graph_v1(x, rp, ew, asg, rw, nnz=nnz, loop_idx=loop)
+        assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("workspace", [False, True])
+@pytest.mark.parametrize("b,h,u,e,k", [(5, 32, 24, 4, 2), (64, 256, 512, 8, 2), (9, 200, 72, 5, 3)])
+def test_spider_cuda_expert_ffn(workspace, b, h, u, e, k):
+    say("spider_cuda_expert", workspace, b, h, u, e, k)
+    kern = _kern()
+    r = _rng(h + u)
+    x = r.standard_normal((b, h)).astype(np.float32)
+    wu = (r.standard_normal((e, h, u)) / np.sqrt(h)).astype(np.float32)
+    wd = (r.standard_normal((e, u, h)) / np.sqrt(u)).astype(np.float32)
+    asg = r.integers(0, e, (b, k)).astype(np.int32)
+    asg[1, 0] = -1
+    rw = r.random((b, k)).astype(np.float32)
+    got = kern.expert_ffn(x, asg, rw, wu, wd, e, workspace=workspace)
+    want = ON.experts(x, asg, rw, wu, wd)
+    assert np.allclose(got, want, rtol=1e-4, atol=1e-5)
+    assert np.abs(want).max() > 0.1
+
+
+@pytest.mark.parametrize("b,h", [(8, 48), (300, 1024), (3, 4000)])
+def test_spider_cuda_epilogue_and_exit(b, h):
+    say("spider_cuda_epilogue", b, h)
+    kern = _kern()
+    r = _rng(h)
+    hh, d, x0 = (r.standard_normal((b, h)).astype(np.float32) for _ in range(3))
+    g = (1 + 0.1 * r.standard_normal(h)).astype(np.float32)
+    lb = (0.1 * r.standard_normal(h)).astype(np.float32)
+    got = kern.epilogue(hh, d, x0, g, lb, 0.5, 0.1, 1e-5)
+    want = ON.epilogue(hh, d, x0, 0.5, 0.1, g, lb, 1e-5)
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-5)
+    proj = (r.standard_normal(h) / np.sqrt(h)).astype(np.float32)
+    for thr in (0.3, 0.5, 0.8):
+        mask = kern.early_exit(want, proj, thr)
+        mo, conf = ON.exit_mask(want, proj, thr)
+        far = np.abs(conf - thr) > 1e-5
+        assert np.array_equal(mask[far], mo[far])
+
+
+@pytest.mark.parametrize("graph", [False, True])
+@pytest.mark.parametrize("b,h,u,e,k", [(7, 32, 24, 8, 2), (128, 512, 256, 16, 2)])
+def test_spider_cuda_moe_loop_step(graph, b, h, u, e, k):
+    say("spider_cuda_loop_step", graph, b, h, u, e, k)
+    kern = _kern()
+    r = _rng(b + h)
+    hh, x0 = (r.standard_normal((b, h)).astype(np.float32) for _ in range(2))
+    rw = (r.standard_normal((h, e)) / np.sqrt(h)).astype(np.float32)
+    bias = (0.1 * r.standard_normal((1, e))).astype(np.float32)
+    wu = (r.standard_normal((e, h, u)) / np.sqrt(h)).astype(np.float32)
+    wd = (r.standard_normal((e, u, h)) / np.sqrt(u)).astype(np.float32)
+    g = (1 + 0.1 * r.standard_normal(h)).astype(np.float32)
+    lb = (0.1 * r.standard_normal(h)).astype(np.float32)
+    proj = (r.standard_normal(h) / np.sqrt(h)).astype(np.float32)
+    csr = None
+    if graph:
+        rp, ci = _csr(e, r)
+        csr = (rp, ci, r.random(len(ci)).astype(np.float32))
+    hn, mask, asg, route = kern.moe_loop_step(hh, x0, 0, router_w=rw, loop_bias=bias, W_up=wu,
+                                              W_down=wd, ln_weight=g, ln_bias=lb, top_k=k,
+                                              alpha=0.5, beta=0.1, csr=csr, exit_proj=proj,
+                                              exit_threshold=0.5)
+    wn, wm, wa, wr, _ = ON.loop_step(hh, x0, k, rw, bias[0], wu, wd, g, lb, 0.5, 0.1, 1e-5,
+                                     csr=csr, exit_proj=proj, threshold=0.5)
+    assert np.array_equal(asg, wa)
+    assert np.allclose(route, wr, rtol=1e-5, atol=1e-7)
+    assert np.allclose(hn, wn, rtol=1e-4, atol=1e-4)
+    _, conf = ON.exit_mask(wn, proj, 0.5)
+    far = np.abs(conf - 0.5) > 1e-4
+    assert np.array_equal(mask[far], wm[far])
+
+
+def test_native_loop_runs_a_spiderw_bundle(tmp_path):
+    """NativeLoop over a bundle written to disk: every loop equals the
+    oracle's loop step (static CSR graph with per-loop edge weights, exit
+    head present but early exit off)."""
+    from spider_moe_amd.native_compat import NativeLoop
+    from spider_moe_amd.spiderw import SpiderWMeta, write_spiderw
+    say("native_loop bundle")
+    r = _rng(11)
+    h, e, k, u, loops, b = 64, 8, 2, 96, 3, 20
+    rp, ci = _csr(e, r)
+    t = {"router": (r.standard_normal((h, e)) / np.sqrt(h)).astype(np.float32),
+         "loop_bias": (0.1 * r.standard_normal((loops, e))).astype(np.float32),
+         "expert_up": (r.standard_normal((e, h, u)) / np.sqrt(h)).astype(np.float32),
+         "expert_down": (r.standard_normal((e, u, h)) / np.sqrt(u)).astype(np.float32),
+         "moe_norm": np.stack([1 + 0.1 * r.standard_normal(h),
+                               0.1 * r.standard_normal(h)]).astype(np.float32),
+         "exit_head": (r.standard_normal(h) / np.sqrt(h)).astype(np.float32),
+         "csr_row_ptr": rp, "csr_col_idx": ci,
+         "csr_edge_w": r.random(loops * len(ci)).astype(np.float32)}
+    meta = SpiderWMeta(flags=2, hidden_size=h, num_experts=e, top_k=k, num_loops=loops,
+                       expert_ffn_size=u)
+    p = tmp_path / "block.spiderw"
+    write_spiderw(p, meta, t)
+    nl = NativeLoop(str(p))
+    x = r.standard_normal((b, h)).astype(np.float32)
+    got = nl.run_loops(torch.from_numpy(x).to(dev)).cpu().numpy()
+    want = x
+    nnz = len(ci)
+    for loop in range(loops):
+        ew = t["csr_edge_w"][loop * nnz:(loop + 1) * nnz]
+        want = ON.loop_step(want, x, k, t["router"], t["loop_bias"][loop], t["expert_up"],
+                            t["expert_down"], t["moe_norm"][0], t["moe_norm"][1], 0.5, 0.1, 1e-5,
+                            csr=(rp, ci, ew))[0]
+    assert np.allclose(got, want, rtol=1e-3, atol=1e-3)
+
+
+# ---------------------------------------------------------- forge ----
+@pytest.mark.parametrize("n,e,k", [(1, 4, 2), (500, 16, 2), (1000, 64, 6), (37, 40, 40)])
+def test_forge_select_route(n, e, k):
+    from spider_moe_amd.forge import ForgeConfig, ForgeSelect
+    say("forge_select", n, e, k)
+    g = torch.Generator().manual_seed(n + e)
+    logits = torch.randn(2, n, e, generator=g)
+    sel = ForgeSelect(ForgeConfig(select_top_k=k))
+    w, i = sel.route(logits.to(dev))
+    wo, io = OF.select_route(logits, k)
+    assert w.shape == (2, n, k) and i.dtype == torch.int64
+    assert torch.equal(i.cpu(), io)
+    assert torch.allclose(w.cpu(), wo, rtol=1e-5, atol=1e-7)
+    # bf16 logits: weights come back in bf16
+    wb, ib = sel.route(logits.to(dev, torch.bfloat16), top_k=1)
+    assert wb.dtype == torch.bfloat16 and torch.all(wb == 1)
+
+
+def test_select_router_mode_matches_block_router():
+    """smoe_select_topk mode 0 is the block's router selection
+    (model.py:255-258): top-k of the fp32 softmax, renormalised."""
+    from spider_moe_amd import _native as nat
+    from spider_moe_amd.forge import select_topk
+    say("select router mode")
+    g = torch.Generator().manual_seed(5)
+    logits = torch.randn(700, 32, generator=g)
+    w, i = select_topk(logits.to(dev), 4, nat.SMOE_SELECT_ROUTER)
+    p = logits.softmax(-1)
+    wo, io = p.topk(4, dim=-1)
+    wo = wo / wo.sum(-1, keepdim=True).clamp_min(1e-9)
+    assert torch.equal(i.cpu(), io)
+    assert torch.allclose(w.cpu(), wo, rtol=1e-5, atol=1e-7)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n,kd,no", [(3, 64, 40), (300, 256, 512), (1024, 512, 1000)])
+def test_forge_gemm_linear(dtype, n, kd, no):
+    from spider_moe_amd.forge import ForgeGEMM
+    say("forge_linear", dtype, n, kd, no)
+    g = torch.Generator().manual_seed(n + kd)
+    x = torch.randn(n, kd, generator=g).to(dtype)
+    w = (torch.randn(no, kd, generator=g) / kd ** 0.5).to(dtype)
+    b = torch.randn(no, generator=g).to(dtype)
+    got = ForgeGEMM().linear(x.to(dev), w.to(dev), b.to(dev)).cpu()
+    want = OF.linear(x, w, b)
+    assert got.dtype == dtype
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    assert torch.allclose(got.float(), want.float(), rtol=tol, atol=tol)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n,kd,no", [(5, 64, 128), (600, 512, 256)])
+def test_forge_gemm_fp8_linear(dtype, n, kd, no):
+    """Per-tensor fp8 weights (quantize_fp8): the codes and scale are the
+    oracle's exactly; the product within the bf16 rounding of the
+    activations (the reference rounds them to fp16)."""
+    from spider_moe_amd.forge import ForgeGEMM
+    from spider_moe_amd.quant import quantize_fp8_per_tensor
+    say("forge_fp8_linear", dtype, n, kd, no)
+    g = torch.Generator().manual_seed(n)
+    x = torch.randn(n, kd, generator=g).to(dtype)
+    w = (torch.randn(no, kd, generator=g) / kd ** 0.5)
+    b = torch.randn(no, generator=g)
+    codes, scale = quantize_fp8_per_tensor(w.to(dev))
+    oc, osc = OF.fp8_quantize_per_tensor(w)
+    assert torch.equal(codes.view(torch.uint8).cpu(), oc.view(torch.uint8))
+    assert float(scale) == pytest.approx(float(osc), rel=2e-7)  # torch's division on the GPU
+    gemm = ForgeGEMM()
+    got = gemm.linear_fp8(x.to(dev), w.to(dev), b.to(dev)).cpu().float()
+    want = OF.fp8_linear(x, w, b).float()
+    ref = (x.float() @ w.t() + b)
+    err = (got - want).abs().max() / want.abs().max()
+    assert err < 1.5e-2, err
+    # the fp8 result stays near the unquantized product (a sanity bound)
+    assert (got - ref).abs().max() / ref.abs().max() < 0.1
+    with pytest.raises(NotImplementedError):
+        gemm.linear_fp8(x.to(dev), w.to(dev), quantize_input=True)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_forge_gemm_expert_ffn(fp8):
+    from spider_moe_amd.forge import ForgeConfig, ForgeGEMM
+    say("forge_expert_ffn", fp8)
+    g = torch.Generator().manual_seed(9)
+    h, u, n = 256, 512, 200
+    bf = torch.bfloat16
+    x = torch.randn(n, h, generator=g).to(bf)
+    wu = (torch.randn(u, h, generator=g) / h ** 0.5).to(bf)
+    bu = (torch.randn(u, generator=g) * 0.1).to(bf)
+    wd = (torch.randn(h, u, generator=g) / u ** 0.5).to(bf)
+    bd = (torch.randn(h, generator=g) * 0.1).to(bf)
+    got = ForgeGEMM(ForgeConfig(gemm_fp8=fp8)).expert_ffn(
+        x.to(dev), wu.to(dev), bu.to(dev), wd.to(dev), bd.to(dev))
+    assert got.dtype == bf
+    got = got.cpu().float()
+    want = OF.expert_ffn(x, wu, bu, wd, bd, fp8).float()
+    err = (got - want).abs().max() / want.abs().max()
+    assert err < (3e-2 if fp8 else 2e-2), err
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n,h,e,k", [(10, 8, 5, 3), (513, 256, 16, 4), (64, 1000, 8, 2)])
+def test_dispatch_expert_fn_combine_is_exact(dtype, n, h, e, k):
+    """dispatch_expert_ffn with an expert_fn: the callback sees each
+    expert's packed rows and the weighted combine matches the reference's
+    per-expert index_add (ascending expert order, weight cast to the
+    output dtype) bit for bit."""
+    from spider_moe_amd.dispatch import dispatch_expert_ffn
+    say("dispatch_expert_fn", dtype, n, h, e, k)
+    g = torch.Generator().manual_seed(n + h)
+    msg = torch.randn(2, n, h, generator=g).to(dtype)
+    ti = torch.randint(0, e, (2, n, k), generator=g)
+    ti[0, 0] = torch.tensor([2] * (k - 1) + [1])  # duplicate slots merge
+    tw = torch.rand(2, n, k, generator=g)
+    tw[0, 1, 0] = 0.0
+    seen = []
+
+    def fn(eid, x):
+        seen.append(eid)
+        return x * float(eid + 1) + 0.25
+
+    got = dispatch_expert_ffn(msg.to(dev), ti.to(dev), tw.to(dev), w_up=None, b_up=None,
+                              w_down=None, b_down=None, num_experts=e, expert_fn=fn).cpu()
+    assert seen == sorted(set(seen)) and len(seen) >= 2
+    want = OF.dispatch_ffn(msg, ti, tw, e, fn)
+    assert got.dtype == dtype and torch.equal(got, want)

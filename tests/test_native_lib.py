@@ -36,6 +36,30 @@ def test_exports_every_declared_symbol(nat):
     assert set(nat.SIGNATURES) == set(syms)
 
 
+def test_exports_the_reference_device_abi(nat):
+    """include/spider_cuda.h: the reference's device ABI names
+    (kernels/include/spider_cuda.h:8-44), exported by libsmoe.so."""
+    text = open(os.path.join(ROOT, "include", "spider_cuda.h")).read()
+    syms = sorted(set(re.findall(r"SPIDER_CUDA_API\s+[\w\s\*]+?\b(spider_cuda_\w+)\s*\(", text)))
+    assert syms == sorted(["spider_cuda_router_f32", "spider_cuda_graph_message_passing_f32",
+                           "spider_cuda_expert_grouped_gemm_f32",
+                           "spider_cuda_expert_workspace_bytes",
+                           "spider_cuda_expert_grouped_gemm_v2_f32",
+                           "spider_cuda_loop_epilogue_f32", "spider_cuda_early_exit_f32",
+                           "spider_cuda_moe_loop_step_f32"])
+    handle = ctypes.CDLL(nat.LIB_PATH)
+    for s in syms:
+        assert hasattr(handle, s), s
+    assert set(nat.SPIDER_CUDA_SIGNATURES) == set(syms)
+    lib = nat.lib()
+    assert lib.spider_cuda_expert_workspace_bytes(4, 2, 8) == 4 * 2 * 8 * 4
+    assert lib.spider_cuda_expert_workspace_bytes(0, 2, 8) == 0
+    # argument checks return 1 before any launch
+    assert lib.spider_cuda_router_f32(None, None, 1, 4, 2, 0, None, None, None) == 1
+    assert lib.spider_cuda_router_f32(1, 1, 1, 65, 2, 0, 1, 1, None) == 1  # E > 64
+    assert lib.spider_cuda_early_exit_f32(None, None, 1, 4, 0.5, None, None) == 1
+
+
 def test_identity(nat):
     lib = nat.lib()
     assert lib.smoe_abi_version() == 7
