@@ -23,8 +23,9 @@
  * hipStream_t passed as void*) and returns 0, 1 for invalid arguments, or
  * the HIP error code.  Results are deterministic: every sum runs in a fixed
  * order (no atomics), unlike the reference's atomicAdd down projection.
- * Limits of this build: E <= 64 for the router; H <= 8192 and U <= 16384
- * for the expert FFN.  The workspace of spider_cuda_expert_grouped_gemm_v2_f32
+ * Limits of this build: E <= 256 for the router (E <= 64 in the loop
+ * step); H <= 8192 and U <= 16384 for the expert FFN (H + U <= 16384
+ * without a workspace).  The workspace of spider_cuda_expert_grouped_gemm_v2_f32
  * holds the hidden activations [B, K, U] as in the reference.
  */
 #pragma once
@@ -103,6 +104,46 @@ SPIDER_CUDA_API int spider_cuda_moe_loop_step_f32(
     const float* W_down, const float* ln_weight, const float* ln_bias, float alpha, float beta,
     float eps, const float* exit_proj, float exit_threshold, float* h_next, uint8_t* exit_mask,
     int32_t* tmp_assign, float* tmp_route, float* tmp_messages, void* stream);
+
+/* ---- Device-pointer forms of the reference's dynamic-edge host functions
+ * (kernels/include/spider_kernels.h:48-86).  The reference's CUDA header
+ * has no counterpart; these carry the scalar library's semantics
+ * (scalar_phase1_1.cpp:17-60, scalar_phase1_2.cpp:11-72,
+ * scalar_phase1_3.cpp:14-42) for the host entry points of spider_kernels.h
+ * and for GPU callers.  Sources or destinations outside [0, E) are skipped
+ * here; the host entry points reject them first. */
+
+/* out_proj [B,E,H]: out_proj[b,e,j] = sum_i h[b,i] W_edge[e][j][i], double
+ * sums in i order (W_edge [E,H,H]) */
+SPIDER_CUDA_API int spider_cuda_edge_project_f32(const float* h, int B, int H, int E,
+                                                 const float* W_edge, float* out_proj,
+                                                 void* stream);
+
+/* messages [B,H] = sum over selected sources (assign [B,K]) and their CSR
+ * edges of edge_w[loop_idx * nnz + edge] * projected[b, col_idx[edge], :] */
+SPIDER_CUDA_API int spider_cuda_graph_message_passing_v2_f32(
+    const float* projected, int B, int H, int E, int K, const int32_t* row_ptr,
+    const int32_t* col_idx, const float* edge_w, int nnz, int loop_idx, const int32_t* assign,
+    float* messages, void* stream);
+
+/* edge_logits [B,E,E] -> per (b, src) row the M largest (first index on
+ * ties; no candidate left: index -1) and a softmax over them:
+ * edge_idx [B,E,M], edge_w [B,E,M]; E <= 256 */
+SPIDER_CUDA_API int spider_cuda_edge_topk_f32(const float* edge_logits, int B, int E, int M,
+                                              int32_t* edge_idx, float* edge_w, void* stream);
+
+/* messages [B,H] = sum over selected sources and their M picks of
+ * edge_w[b,src,m] * projected[b, edge_idx[b,src,m], :] */
+SPIDER_CUDA_API int spider_cuda_graph_message_passing_dynamic_f32(
+    const float* projected, int B, int H, int E, int K, int M, const int32_t* edge_idx,
+    const float* edge_w, const int32_t* assign, float* messages, void* stream);
+
+/* out_logits [B,E*E] = [h, loop_emb] . W_gen^T (W_gen [E*E, H + D]),
+ * double sums in input order, no bias */
+SPIDER_CUDA_API int spider_cuda_edge_generator_f32(const float* h, int B, int H, int E,
+                                                   const float* loop_emb, int loop_emb_dim,
+                                                   const float* W_gen, float* out_logits,
+                                                   void* stream);
 
 #ifdef __cplusplus
 }

@@ -161,10 +161,51 @@ def early_exit_f32(h, proj, threshold):
     return rc, mask
 
 
+def edge_project_f32(hidden, w_edge):
+    """spider_edge_project_f32 (scalar_phase1_1.cpp:17-32): W_edge [E,H,H]."""
+    h = _f32(hidden)
+    we = _f32(w_edge)
+    b, hid = h.shape
+    e = we.shape[0]
+    out = np.zeros((b, e, hid), np.float32)
+    rc = lib().spider_edge_project_f32(_fp(h), b, hid, e, _fp(we), _fp(out))
+    return rc, out
+
+
+def graph_v2_f32(projected, row_ptr, col_idx, edge_w, assign, loop_idx=0):
+    """spider_graph_message_passing_v2_f32 (scalar_phase1_1.cpp:34-60)."""
+    p = _f32(projected)
+    rp = np.ascontiguousarray(row_ptr, np.int32)
+    ci = np.ascontiguousarray(col_idx, np.int32)
+    ew = _f32(edge_w)
+    asg = np.ascontiguousarray(assign, np.int32)
+    b, e, hid = p.shape
+    out = np.zeros((b, hid), np.float32)
+    rc = lib().spider_graph_message_passing_v2_f32(_fp(p), b, hid, e, asg.shape[1], _ip(rp),
+                                                   _ip(ci), _fp(ew), len(ci), loop_idx, _ip(asg),
+                                                   _fp(out))
+    return rc, out
+
+
+def graph_dynamic_f32(projected, edge_idx, edge_w, assign):
+    """spider_graph_message_passing_dynamic_f32 (scalar_phase1_2.cpp:49-72)."""
+    p = _f32(projected)
+    ei = np.ascontiguousarray(edge_idx, np.int32)
+    ew = _f32(edge_w)
+    asg = np.ascontiguousarray(assign, np.int32)
+    b, e, hid = p.shape
+    out = np.zeros((b, hid), np.float32)
+    rc = lib().spider_graph_message_passing_dynamic_f32(_fp(p), b, hid, e, asg.shape[1],
+                                                        ei.shape[2], _ip(ei), _fp(ew), _ip(asg),
+                                                        _fp(out))
+    return rc, out
+
+
 def moe_loop_step_f32(h, x0, k, loop_idx, router_w, loop_bias, w_up, w_down, ln_w, ln_b, alpha,
-                      beta, eps, exit_proj=None, threshold=0.85):
-    """spider_moe_loop_step_f32 (scalar_phase1_1.cpp:62-121) without the
-    edge-value graph (W_edge and the CSR NULL: messages = h)."""
+                      beta, eps, exit_proj=None, threshold=0.85, csr=None, w_edge=None):
+    """spider_moe_loop_step_f32 (scalar_phase1_1.cpp:62-121); csr =
+    (row_ptr, col_idx, edge_w [R*nnz]) with w_edge [E,H,H] selects the
+    edge-value graph, otherwise messages = h."""
     h = _f32(h)
     x = _f32(x0)
     rw = _f32(router_w)
@@ -187,7 +228,16 @@ def moe_loop_step_f32(h, x0, k, loop_idx, router_w, loop_bias, w_up, w_down, ln_
     fn.argtypes = [vp, vp, c_i, c_i, c_i, c_i, c_i, c_i, vp, vp, vp, vp, vp, c_i, vp, vp, vp,
                    vp, vp, c_f, c_f, c_f, vp, c_f, vp, vp, vp, vp, vp]
     ptr = lambda a: None if a is None else a.ctypes.data  # noqa: E731
-    rc = fn(ptr(h), ptr(x), b, hid, e, k, u, loop_idx, ptr(rw), ptr(lb), None, None, None, 0,
-            None, ptr(wu), ptr(wd), ptr(g), ptr(gb), alpha, beta, eps, ptr(ep), threshold,
-            ptr(out), ptr(mask), ptr(asg), ptr(route), ptr(msgs))
+    rp = ci = ew = we = None
+    nnz = 0
+    if csr is not None:
+        rp = np.ascontiguousarray(csr[0], np.int32)
+        ci = np.ascontiguousarray(csr[1], np.int32)
+        ew = _f32(csr[2])
+        nnz = len(ci)
+    if w_edge is not None:
+        we = _f32(w_edge)
+    rc = fn(ptr(h), ptr(x), b, hid, e, k, u, loop_idx, ptr(rw), ptr(lb), ptr(rp), ptr(ci),
+            ptr(ew), nnz, ptr(we), ptr(wu), ptr(wd), ptr(g), ptr(gb), alpha, beta, eps, ptr(ep),
+            threshold, ptr(out), ptr(mask), ptr(asg), ptr(route), ptr(msgs))
     return rc, out, mask, asg, route

@@ -58,6 +58,13 @@ def build(jobs: int = 4, verbose: bool = True) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
     os.replace(tmp, LIB)
+    # the file name the reference's ctypes binding looks for
+    # (kernels/python/spider_native.py:51-62): the host entry points of
+    # include/spider_kernels.h live in the same library
+    alias = os.path.join(LIB_DIR, "libspider_kernels.so")
+    if os.path.lexists(alias):
+        os.remove(alias)
+    os.symlink(os.path.basename(LIB), alias)
     if verbose:
         print(f"built {LIB}")
     return LIB

@@ -7,6 +7,7 @@
 // outputs follow the scalar library to the last bit or two.
 #include <math.h>
 
+#include <climits>
 #include <type_traits>
 
 #include "smoe_common.hpp"
@@ -112,9 +113,9 @@ __global__ __launch_bounds__(256) void k_ref_graph(const float* __restrict__ h, 
     const int src = assign[b * K + k];
     if (src < 0 || src >= E) continue;
     const float r = rw[b * K + k];
-    const int e1 = rp[src + 1];
-    for (int e = rp[src]; e < e1; ++e)
-      if (e < nnz) acc = fadd(acc, fmul(fmul(ew[static_cast<int64_t>(loop) * nnz + e], r), hv));
+    const int e1 = min(rp[src + 1], nnz);  // a malformed CSR never reads past its arrays
+    for (int e = max(rp[src], 0); e < e1; ++e)
+      acc = fadd(acc, fmul(fmul(ew[static_cast<int64_t>(loop) * nnz + e], r), hv));
   }
   out[static_cast<int64_t>(b) * H + j] = acc;
 }
@@ -265,6 +266,205 @@ __global__ void k_ref_copy_f32(const float* __restrict__ src, float* __restrict_
   if (i < n) dst[i] = src[i];
 }
 
+// ------------------------------------------------------ wide arg-max ----
+// LDS written by some lanes of a wave, then read by others of the same wave.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// The scalar library's iterative arg-max (scalar.cpp:18-27,
+// scalar_phase1_2.cpp:19-30) over one row of up to 64 * VPL values, one
+// wave per row: lane l holds index l + 64 c in v[c].  Pick m is the first
+// (lowest-index) largest value above `floor` among the indices not picked
+// yet — the scalar loop's strict "greater than the best so far" started at
+// floor (-1 for router probabilities, -inf for edge logits).  A pick with
+// no candidate left is (-1, floor), as there.  Lane 0 writes the picks.
+template <int VPL>
+__device__ __forceinline__ void wave_pick(const float (&v)[VPL], int n, int picks, float floor,
+                                          int32_t* __restrict__ out_i,
+                                          float* __restrict__ out_v) {
+  const int lane = threadIdx.x & 63;
+  unsigned used = 0;
+#pragma unroll 1
+  for (int m = 0; m < picks; ++m) {
+    float bv = -INFINITY;
+    int bi = kRefBig;
+#pragma unroll
+    for (int c = 0; c < VPL; ++c) {
+      const int e = lane + 64 * c;
+      if (e < n && !((used >> c) & 1u) && v[c] > floor && v[c] > bv) {
+        bv = v[c];
+        bi = e;
+      }
+    }
+    seg_argmax<64>(bv, bi);
+    if (bi != kRefBig && (bi & 63) == lane) used |= 1u << (bi >> 6);
+    if (lane == 0) {
+      out_i[m] = bi == kRefBig ? -1 : bi;
+      out_v[m] = bi == kRefBig ? floor : bv;
+    }
+  }
+}
+
+// Router rows of 64 < E <= 64 * VPL experts (the <= 64 form is
+// k_ref_router): p = exp(l + b - max) / sum, K picks of p, weights
+// renormalised by max(sum of picks in pick order, 1e-20).  One wave per
+// row; the picks go through LDS.
+template <int VPL>
+__global__ __launch_bounds__(256) void k_ref_router_wide(const float* __restrict__ logits,
+                                                         const float* __restrict__ bias, int B,
+                                                         int E, int K, float* __restrict__ w,
+                                                         int32_t* __restrict__ idx) {
+  __shared__ float sv[4][64 * VPL];
+  __shared__ int32_t si[4][64 * VPL];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int b = blockIdx.x * 4 + wave;
+  if (b >= B) return;  // wave-uniform; no block barrier below
+  float v[VPL];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int c = 0; c < VPL; ++c) {
+    const int e = lane + 64 * c;
+    v[c] = e < E ? fadd(logits[static_cast<int64_t>(b) * E + e], bias[e]) : -INFINITY;
+    mx = fmaxf(mx, v[c]);
+  }
+  mx = seg_max<64>(mx);
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < VPL; ++c) s += lane + 64 * c < E ? expf(v[c] - mx) : 0.f;
+  s = seg_sum<64>(s);
+#pragma unroll
+  for (int c = 0; c < VPL; ++c) v[c] = lane + 64 * c < E ? expf(v[c] - mx) / s : -INFINITY;
+  wave_pick<VPL>(v, E, K, -1.f, si[wave], sv[wave]);
+  wave_lds_sync();
+  float tot = 0.f;
+  for (int m = 0; m < K; ++m) tot = fadd(tot, sv[wave][m]);
+  const float d = fmaxf(tot, 1e-20f);
+  for (int m = lane; m < K; m += 64) {
+    w[static_cast<int64_t>(b) * K + m] = sv[wave][m] / d;
+    idx[static_cast<int64_t>(b) * K + m] = si[wave][m];
+  }
+}
+
+// --------------------------------------------------------- edge top-m ----
+// spider_edge_topk_f32 (scalar_phase1_2.cpp:11-47): for each (b, src) row
+// of E edge logits, M picks of the iterative arg-max, then a softmax over
+// the picked values (max, exp, sum in pick order, / max(sum, 1e-20)).  One
+// wave per row.
+template <int VPL>
+__global__ __launch_bounds__(256) void k_ref_edge_topk(const float* __restrict__ logits, int rows,
+                                                       int E, int M, int32_t* __restrict__ eidx,
+                                                       float* __restrict__ ew) {
+  __shared__ float sv[4][64 * VPL];
+  __shared__ int32_t si[4][64 * VPL];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = blockIdx.x * 4 + wave;
+  if (r >= rows) return;  // wave-uniform
+  float v[VPL];
+#pragma unroll
+  for (int c = 0; c < VPL; ++c) {
+    const int e = lane + 64 * c;
+    v[c] = e < E ? logits[static_cast<int64_t>(r) * E + e] : -INFINITY;
+  }
+  wave_pick<VPL>(v, E, M, -INFINITY, si[wave], sv[wave]);
+  wave_lds_sync();
+  float mx = -INFINITY;
+  for (int m = 0; m < M; ++m) mx = fmaxf(mx, sv[wave][m]);
+  for (int m = lane; m < M; m += 64) sv[wave][m] = expf(sv[wave][m] - mx);
+  wave_lds_sync();
+  float sum = 0.f;
+  for (int m = 0; m < M; ++m) sum = fadd(sum, sv[wave][m]);
+  const float d = fmaxf(sum, 1e-20f);
+  for (int m = lane; m < M; m += 64) {
+    eidx[static_cast<int64_t>(r) * M + m] = si[wave][m];
+    ew[static_cast<int64_t>(r) * M + m] = sv[wave][m] / d;
+  }
+}
+
+// ------------------------------------------------ graph v2 / dynamic ----
+// messages[b, j] = sum over the row's valid sources (slot order) and their
+// edges (CSR order, or the M picks of the (b, src) row) of scale *
+// projected[b, dst, j] — scalar_phase1_1.cpp:34-60 (scale = the loop's
+// edge weight) and scalar_phase1_2.cpp:49-72 (scale = the picked edge
+// weight).  Sources or destinations outside [0, E) are skipped (the host
+// entry points reject them first, as the scalar library does).
+__global__ __launch_bounds__(256) void k_ref_graph_proj(
+    const float* __restrict__ proj, int B, int H, int E, int K, const int32_t* __restrict__ rp,
+    const int32_t* __restrict__ ci, int nnz, const float* __restrict__ ew, int M,
+    const int32_t* __restrict__ eidx, const int32_t* __restrict__ assign,
+    float* __restrict__ out) {
+  const int b = blockIdx.y;
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= H) return;
+  float acc = 0.f;
+  for (int k = 0; k < K; ++k) {
+    const int src = assign[b * K + k];
+    if (src < 0 || src >= E) continue;
+    // static CSR (rp != nullptr) or the row's dynamic picks
+    // (a malformed CSR never reads past its arrays)
+    const int64_t e0 = rp ? max(rp[src], 0) : (static_cast<int64_t>(b) * E + src) * M;
+    const int64_t e1 = rp ? min(rp[src + 1], nnz) : e0 + M;
+    for (int64_t e = e0; e < e1; ++e) {
+      const int dst = rp ? ci[e] : eidx[e];
+      if (dst < 0 || dst >= E) continue;
+      acc = fadd(acc, fmul(ew[e], proj[(static_cast<int64_t>(b) * E + dst) * H + j]));
+    }
+  }
+  out[static_cast<int64_t>(b) * H + j] = acc;
+}
+
+// -------------------------------------------- double-accumulated GEMM ----
+// out[b, o] = float(sum over i ascending of double(A[b, i]) * double(W[o, i]))
+// with A[b] = [x[b, 0:H], x2[0:n_in - H]] and W row-major [O, n_in]: the
+// edge projection (W_edge [E, H, H] as [E*H, H], scalar_phase1_1.cpp:17-32)
+// and the edge generator (W_gen [E*E, H + D] over [h; loop_emb],
+// scalar_phase1_3.cpp:14-42).  Products of two floats are exact in double,
+// so each step rounds only the sum, in the scalar loop's order.  Tiles of
+// 64 outputs x 16 rows, 32-wide k steps through LDS; thread: one output of
+// 4 rows.
+__global__ __launch_bounds__(256) void k_ref_gemm_f64(const float* __restrict__ x, int H,
+                                                      const float* __restrict__ x2, int n_in,
+                                                      const float* __restrict__ W, int O, int B,
+                                                      float* __restrict__ out) {
+  __shared__ float sW[32][65];
+  __shared__ float sA[16][33];
+  const int tid = threadIdx.x, ol = tid & 63, bq = tid >> 6;
+  const int o0 = blockIdx.x * 64, b0 = blockIdx.y * 16;
+  double acc[4] = {0.0, 0.0, 0.0, 0.0};
+  for (int i0 = 0; i0 < n_in; i0 += 32) {
+#pragma unroll
+    for (int r = 0; r < 8; ++r) {
+      const int id = tid + 256 * r, row = id >> 5, col = id & 31;
+      const int o = o0 + row, i = i0 + col;
+      sW[col][row] = (o < O && i < n_in) ? W[static_cast<int64_t>(o) * n_in + i] : 0.f;
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int id = tid + 256 * r, row = id >> 5, col = id & 31;
+      const int b = b0 + row, i = i0 + col;
+      float a = 0.f;
+      if (b < B && i < n_in) a = i < H ? x[static_cast<int64_t>(b) * H + i] : x2[i - H];
+      sA[row][col] = a;
+    }
+    __syncthreads();
+    const int iend = min(32, n_in - i0);
+    for (int ii = 0; ii < iend; ++ii) {
+      const double wv = static_cast<double>(sW[ii][ol]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        acc[r] = add_rn(acc[r], mul_rn(static_cast<double>(sA[bq * 4 + r][ii]), wv));
+    }
+    __syncthreads();
+  }
+  const int o = o0 + ol;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int b = b0 + bq * 4 + r;
+    if (b < B && o < O) out[static_cast<int64_t>(b) * O + o] = static_cast<float>(acc[r]);
+  }
+}
+
 // ---------------------------------------------------------------- launch ----
 int rc_last() {
   const hipError_t e = hipGetLastError();
@@ -275,6 +475,12 @@ int seg_for(int E) { return E <= 16 ? 16 : (E <= 32 ? 32 : 64); }
 
 int launch_router(const float* logits, const float* bias, int B, int E, int K, float* w,
                   int32_t* idx, hipStream_t s) {
+  if (E > 64) {  // one wave per row, up to 4 experts per lane
+    const dim3 grid((B + 3) / 4), block(256);
+    if (E <= 128) hipLaunchKernelGGL(k_ref_router_wide<2>, grid, block, 0, s, logits, bias, B, E, K, w, idx);
+    else hipLaunchKernelGGL(k_ref_router_wide<4>, grid, block, 0, s, logits, bias, B, E, K, w, idx);
+    return rc_last();
+  }
   const int seg = seg_for(E), per = 4 * (64 / seg);
   const dim3 grid((B + per - 1) / per), block(256);
   if (seg == 16) hipLaunchKernelGGL(k_ref_router<16>, grid, block, 0, s, logits, bias, B, E, K, w, idx);
@@ -316,7 +522,40 @@ int launch_epilogue_ref(const float* h, const float* d, const float* x0, int B, 
   });
 }
 
+int launch_edge_topk(const float* logits, int rows, int E, int M, int32_t* eidx, float* ew,
+                     hipStream_t s) {
+  const dim3 grid((rows + 3) / 4), block(256);
+  if (E <= 64) hipLaunchKernelGGL(k_ref_edge_topk<1>, grid, block, 0, s, logits, rows, E, M, eidx, ew);
+  else if (E <= 128) hipLaunchKernelGGL(k_ref_edge_topk<2>, grid, block, 0, s, logits, rows, E, M, eidx, ew);
+  else hipLaunchKernelGGL(k_ref_edge_topk<4>, grid, block, 0, s, logits, rows, E, M, eidx, ew);
+  return rc_last();
+}
+
+int launch_gemm_f64(const float* x, int H, const float* x2, int n_in, const float* W, int O, int B,
+                    float* out, hipStream_t s) {
+  hipLaunchKernelGGL(k_ref_gemm_f64, dim3((O + 63) / 64, (B + 15) / 16), dim3(256), 0, s, x, H, x2,
+                     n_in, W, O, B, out);
+  return rc_last();
+}
+
 }  // namespace
+
+// The loop step's pieces for the host entry points (smoe_host_abi.hip).
+int ref_logits_router(const float* h, const float* router_w, const float* bias_row, int B, int H,
+                      int E, int K, float* w, int32_t* idx, hipStream_t s) {
+  if (E > 64) return 1;
+  hipLaunchKernelGGL(k_ref_logits_router, dim3(B), dim3(64), 0, s, h, router_w, bias_row, B, H, E,
+                     K, w, idx);
+  return rc_last();
+}
+
+int ref_copy_f32(const float* src, float* dst, int64_t n, hipStream_t s) {
+  if (n <= 0) return 0;
+  hipLaunchKernelGGL(k_ref_copy_f32, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s,
+                     src, dst, n);
+  return rc_last();
+}
+
 }  // namespace smoe
 
 using namespace smoe;
@@ -326,7 +565,7 @@ extern "C" {
 SPIDER_CUDA_API int spider_cuda_router_f32(const float* logits, const float* loop_bias, int B,
                                            int E, int K, int loop_idx, float* out_w,
                                            int32_t* out_idx, void* stream) {
-  if (!logits || !loop_bias || !out_w || !out_idx || B <= 0 || E <= 0 || E > 64 || K <= 0 ||
+  if (!logits || !loop_bias || !out_w || !out_idx || B <= 0 || E <= 0 || E > 256 || K <= 0 ||
       K > E || loop_idx < 0)
     return 1;
   return launch_router(logits, loop_bias + static_cast<int64_t>(loop_idx) * E, B, E, K, out_w,
@@ -435,6 +674,62 @@ SPIDER_CUDA_API int spider_cuda_moe_loop_step_f32(
     hipLaunchKernelGGL(k_ref_zero_u8, dim3((B + 255) / 256), dim3(256), 0, s, exit_mask, B);
   }
   return rc_last();
+}
+
+SPIDER_CUDA_API int spider_cuda_edge_project_f32(const float* h, int B, int H, int E,
+                                                 const float* W_edge, float* out_proj,
+                                                 void* stream) {
+  if (!h || !W_edge || !out_proj || B <= 0 || H <= 0 || E <= 0 ||
+      static_cast<int64_t>(E) * H > INT32_MAX)
+    return 1;
+  return launch_gemm_f64(h, H, nullptr, H, W_edge, E * H, B, out_proj,
+                         static_cast<hipStream_t>(stream));
+}
+
+SPIDER_CUDA_API int spider_cuda_graph_message_passing_v2_f32(
+    const float* projected, int B, int H, int E, int K, const int32_t* row_ptr,
+    const int32_t* col_idx, const float* edge_w, int nnz, int loop_idx, const int32_t* assign,
+    float* messages, void* stream) {
+  if (!projected || !row_ptr || !col_idx || !edge_w || !assign || !messages || B <= 0 || H <= 0 ||
+      E <= 0 || K <= 0 || nnz < 0 || loop_idx < 0)
+    return 1;
+  hipLaunchKernelGGL(k_ref_graph_proj, dim3((H + 255) / 256, B), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), projected, B, H, E, K, row_ptr, col_idx,
+                     nnz, edge_w + static_cast<int64_t>(loop_idx) * nnz, 0, nullptr, assign,
+                     messages);
+  return rc_last();
+}
+
+SPIDER_CUDA_API int spider_cuda_edge_topk_f32(const float* edge_logits, int B, int E, int M,
+                                              int32_t* edge_idx, float* edge_w, void* stream) {
+  if (!edge_logits || !edge_idx || !edge_w || B <= 0 || E <= 0 || E > 256 || M <= 0 || M > E ||
+      static_cast<int64_t>(B) * E > INT32_MAX)
+    return 1;
+  return launch_edge_topk(edge_logits, B * E, E, M, edge_idx, edge_w,
+                          static_cast<hipStream_t>(stream));
+}
+
+SPIDER_CUDA_API int spider_cuda_graph_message_passing_dynamic_f32(
+    const float* projected, int B, int H, int E, int K, int M, const int32_t* edge_idx,
+    const float* edge_w, const int32_t* assign, float* messages, void* stream) {
+  if (!projected || !edge_idx || !edge_w || !assign || !messages || B <= 0 || H <= 0 || E <= 0 ||
+      K <= 0 || M <= 0)
+    return 1;
+  hipLaunchKernelGGL(k_ref_graph_proj, dim3((H + 255) / 256, B), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), projected, B, H, E, K, nullptr, nullptr, 0,
+                     edge_w, M, edge_idx, assign, messages);
+  return rc_last();
+}
+
+SPIDER_CUDA_API int spider_cuda_edge_generator_f32(const float* h, int B, int H, int E,
+                                                   const float* loop_emb, int loop_emb_dim,
+                                                   const float* W_gen, float* out_logits,
+                                                   void* stream) {
+  if (!h || !loop_emb || !W_gen || !out_logits || B <= 0 || H <= 0 || E <= 0 ||
+      loop_emb_dim < 0 || static_cast<int64_t>(E) * E > INT32_MAX)
+    return 1;
+  return launch_gemm_f64(h, H, loop_emb, H + loop_emb_dim, W_gen, E * E, B, out_logits,
+                         static_cast<hipStream_t>(stream));
 }
 
 }  // extern "C"

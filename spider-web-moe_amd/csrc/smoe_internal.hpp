@@ -120,6 +120,14 @@ int launch_select_topk(const float* logits, int N, int E, int K, int mode, float
 int launch_combine_rows(const void* y, int ydt, const float* row_w, const int32_t* tok_row,
                         int N, int K, int H, void* out, int odt, hipStream_t s);
 
+// ---- the reference's native loop (smoe_compat.hip), for the host entry
+// points of smoe_host_abi.hip ----
+// logits = h . router_w ([H, E], double sums), then the router on
+// logits + bias_row (E <= 64)
+int ref_logits_router(const float* h, const float* router_w, const float* bias_row, int B, int H,
+                      int E, int K, float* w, int32_t* idx, hipStream_t s);
+int ref_copy_f32(const float* src, float* dst, int64_t n, hipStream_t s);
+
 // ---- decode loop (bf16, N <= 64): two launches in place of the front GEMM,
 // the routing workgroup and the previous loop's epilogue ----
 // k_decode_front: per (strip, 16-token tile); every strip computes the

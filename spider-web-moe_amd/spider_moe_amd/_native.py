@@ -120,6 +120,57 @@ SPIDER_CUDA_SIGNATURES = {
                                                _vp, _vp]),
 }
 
+# this build's device-pointer forms of the reference's dynamic-edge functions
+SPIDER_CUDA_SIGNATURES.update({
+    "spider_cuda_edge_project_f32": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp]),
+    "spider_cuda_graph_message_passing_v2_f32": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int,
+                                                          _vp, _vp, _vp, _c_int, _c_int, _vp, _vp,
+                                                          _vp]),
+    "spider_cuda_edge_topk_f32": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp, _vp]),
+    "spider_cuda_graph_message_passing_dynamic_f32": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int,
+                                                               _c_int, _vp, _vp, _vp, _vp, _vp]),
+    "spider_cuda_edge_generator_f32": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _c_int, _vp, _vp,
+                                                _vp]),
+})
+
+# the reference's host ABI (include/spider_kernels.h): host pointers
+SPIDER_HOST_SIGNATURES = {
+    "spider_router_f32": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp]),
+    "spider_router_f16": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp]),
+    "spider_graph_message_passing_f32": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
+                                                  _vp, _c_int, _c_int, _vp, _vp, _vp]),
+    "spider_graph_message_passing_f16": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
+                                                  _vp, _c_int, _c_int, _vp, _vp, _vp]),
+    "spider_edge_project_f32": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp]),
+    "spider_graph_message_passing_v2_f32": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
+                                                     _vp, _c_int, _c_int, _vp, _vp]),
+    "spider_edge_topk_f32": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp]),
+    "spider_graph_message_passing_dynamic_f32": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int,
+                                                          _c_int, _vp, _vp, _vp, _vp]),
+    "spider_graph_dynamic_with_edge_value_f32": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int,
+                                                          _c_int, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "spider_edge_generator_f32": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _c_int, _vp, _vp]),
+    "spider_edge_generator_topk_f32": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _c_int,
+                                                _vp, _vp, _vp, _vp]),
+    "spider_graph_from_generator_f32": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp,
+                                                 _c_int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "spider_expert_grouped_gemm_f32": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp,
+                                                _vp, _vp, _vp, _vp]),
+    "spider_expert_grouped_gemm_f16": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp,
+                                                _vp, _vp, _vp, _vp]),
+    "spider_loop_epilogue_f32": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _f, _f, _vp, _vp, _f,
+                                          _vp]),
+    "spider_loop_epilogue_f16": (_c_int, [_vp, _vp, _vp, _c_int, _c_int, _f, _f, _vp, _vp, _f,
+                                          _vp]),
+    "spider_early_exit_f32": (_c_int, [_vp, _vp, _c_int, _c_int, _f, _vp]),
+    "spider_moe_loop_step_f32": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int,
+                                          _c_int, _vp, _vp, _vp, _vp, _vp, _c_int, _vp, _vp, _vp,
+                                          _vp, _vp, _f, _f, _f, _vp, _f, _vp, _vp, _vp, _vp,
+                                          _vp]),
+    "spider_backend_name": (ctypes.c_char_p, []),
+    "spider_backend_caps": (ctypes.c_uint32, []),
+}
+
 STAGES = ["router_gemm", "route_topk", "expert_plan", "edge_logits", "edge_topm", "dest_plan",
           "edge_gemm", "msg_combine", "up_gemm", "down_gemm", "epilogue",
           # bf16 steps of N <= 64: stages 0-5 as one GEMM and one routing workgroup
@@ -138,7 +189,8 @@ def lib():
                 f"{LIB_PATH} is missing: build it with `python spider-web-moe_amd/build.py` "
                 "(spider_moe_amd has no CPU fallback)")
         handle = ctypes.CDLL(LIB_PATH)
-        for name, (res, args) in {**SIGNATURES, **SPIDER_CUDA_SIGNATURES}.items():
+        for name, (res, args) in {**SIGNATURES, **SPIDER_CUDA_SIGNATURES,
+                                  **SPIDER_HOST_SIGNATURES}.items():
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args

@@ -184,6 +184,251 @@ class HipKernels:
                 self._back(route, h))
 
 
+    # ------------------------------------------- dynamic-edge functions ----
+    def edge_project(self, hidden, W_edge):
+        """[B,E,H] = hidden . W_edge[e]^T per expert (double sums)."""
+        h = self._dev(hidden, torch.float32)
+        w = self._dev(W_edge, torch.float32)
+        b, hd = h.shape
+        e = w.shape[0]
+        out = torch.empty(b, e, hd, dtype=torch.float32, device=self.device)
+        _rc(self.lib.spider_cuda_edge_project_f32(h.data_ptr(), b, hd, e, w.data_ptr(),
+                                                  out.data_ptr(), self._stream()),
+            "spider_cuda_edge_project_f32")
+        return self._back(out, hidden)
+
+    def graph_v2(self, projected, row_ptr, col_idx, edge_w, assign, E: int, loop_idx: int = 0):
+        p = self._dev(projected, torch.float32)
+        rp = self._dev(row_ptr, torch.int32)
+        ci = self._dev(col_idx, torch.int32)
+        ew = self._dev(edge_w, torch.float32)
+        asg = self._dev(assign, torch.int32)
+        b, _, hd = p.shape
+        out = torch.empty(b, hd, dtype=torch.float32, device=self.device)
+        _rc(self.lib.spider_cuda_graph_message_passing_v2_f32(
+            p.data_ptr(), b, hd, E, asg.shape[1], rp.data_ptr(), ci.data_ptr(), ew.data_ptr(),
+            int(ci.shape[0]), loop_idx, asg.data_ptr(), out.data_ptr(), self._stream()),
+            "spider_cuda_graph_message_passing_v2_f32")
+        return self._back(out, projected)
+
+    def edge_topk(self, edge_logits, M: int):
+        g = self._dev(edge_logits, torch.float32)
+        if g.ndim == 2:
+            g = g.unsqueeze(0)
+        b, e, _ = g.shape
+        idx = torch.empty(b, e, M, dtype=torch.int32, device=self.device)
+        w = torch.empty(b, e, M, dtype=torch.float32, device=self.device)
+        _rc(self.lib.spider_cuda_edge_topk_f32(g.data_ptr(), b, e, M, idx.data_ptr(), w.data_ptr(),
+                                               self._stream()), "spider_cuda_edge_topk_f32")
+        return self._back(idx, edge_logits), self._back(w, edge_logits)
+
+    def edge_generator(self, hidden, loop_emb, W_gen, E: int):
+        h = self._dev(hidden, torch.float32)
+        emb = self._dev(loop_emb, torch.float32).reshape(-1)
+        w = self._dev(W_gen, torch.float32)
+        b, hd = h.shape
+        out = torch.empty(b, E, E, dtype=torch.float32, device=self.device)
+        _rc(self.lib.spider_cuda_edge_generator_f32(h.data_ptr(), b, hd, E, emb.data_ptr(),
+                                                    int(emb.numel()), w.data_ptr(),
+                                                    out.data_ptr(), self._stream()),
+            "spider_cuda_edge_generator_f32")
+        return self._back(out, hidden)
+
+    def graph_dynamic(self, projected, edge_indices, edge_weights, assign, E: int, M: int):
+        p = self._dev(projected, torch.float32)
+        ei = self._dev(edge_indices, torch.int32)
+        ew = self._dev(edge_weights, torch.float32)
+        asg = self._dev(assign, torch.int32)
+        b, _, hd = p.shape
+        out = torch.empty(b, hd, dtype=torch.float32, device=self.device)
+        _rc(self.lib.spider_cuda_graph_message_passing_dynamic_f32(
+            p.data_ptr(), b, hd, E, asg.shape[1], M, ei.data_ptr(), ew.data_ptr(), asg.data_ptr(),
+            out.data_ptr(), self._stream()), "spider_cuda_graph_message_passing_dynamic_f32")
+        return self._back(out, projected)
+
+    def graph_from_generator(self, hidden, loop_emb, W_gen, W_edge, assign, E: int, M: int):
+        logits = self.edge_generator(hidden, loop_emb, W_gen, E)
+        edge_idx, edge_w = self.edge_topk(logits, M)
+        projected = self.edge_project(hidden, W_edge)
+        return self.graph_dynamic(projected, edge_idx, edge_w, assign, E, M)
+
+
+def _host_f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _host_i32(a):
+    return np.ascontiguousarray(a, dtype=np.int32)
+
+
+class HostKernels:
+    """The reference's numpy binding (kernels/python/spider_native.py:196-480,
+    NativeKernels) over the host entry points of include/spider_kernels.h:
+    numpy arrays in and out, the compute on the GPU (libsmoe.so copies the
+    inputs to the current device and the results back).  Errors raise
+    RuntimeError("<fn> failed: rc") as there."""
+
+    def __init__(self):
+        self.lib = nat.lib()
+
+    @property
+    def backend(self) -> str:
+        return self.lib.spider_backend_name().decode()
+
+    @property
+    def caps(self) -> int:
+        return int(self.lib.spider_backend_caps())
+
+    @property
+    def has_cuda(self) -> bool:
+        return True
+
+    def _call(self, name: str, *args):
+        rc = getattr(self.lib, name)(*[a.ctypes.data if isinstance(a, np.ndarray) else a
+                                       for a in args])
+        if rc != 0:
+            raise RuntimeError(f"{name} failed: {rc}")
+
+    def router(self, logits, loop_bias, k: int, loop_idx: int = 0):
+        lg, bias = _host_f32(logits), _host_f32(loop_bias)
+        b, e = lg.shape
+        w = np.zeros((b, k), np.float32)
+        idx = np.zeros((b, k), np.int32)
+        self._call("spider_router_f32", lg, bias, b, e, k, loop_idx, w, idx)
+        return w, idx
+
+    def graph(self, hidden, row_ptr, col_idx, edge_w, assign, route, E: int, loop_idx: int = 0):
+        h = _host_f32(hidden)
+        b, hd = h.shape
+        asg = _host_i32(assign)
+        ci = _host_i32(col_idx)
+        out = np.zeros_like(h)
+        self._call("spider_graph_message_passing_f32", h, b, hd, E, asg.shape[1],
+                   _host_i32(row_ptr), ci, _host_f32(edge_w), int(ci.shape[0]), loop_idx, asg,
+                   _host_f32(route), out)
+        return out
+
+    def edge_project(self, hidden, W_edge):
+        h, w = _host_f32(hidden), _host_f32(W_edge)
+        b, hd = h.shape
+        out = np.zeros((b, w.shape[0], hd), np.float32)
+        self._call("spider_edge_project_f32", h, b, hd, w.shape[0], w, out)
+        return out
+
+    def graph_v2(self, projected, row_ptr, col_idx, edge_w, assign, E: int, loop_idx: int = 0):
+        p = _host_f32(projected)
+        b, _, hd = p.shape
+        asg = _host_i32(assign)
+        ci = _host_i32(col_idx)
+        out = np.zeros((b, hd), np.float32)
+        self._call("spider_graph_message_passing_v2_f32", p, b, hd, E, asg.shape[1],
+                   _host_i32(row_ptr), ci, _host_f32(edge_w), int(ci.shape[0]), loop_idx, asg,
+                   out)
+        return out
+
+    def edge_topk(self, edge_logits, M: int):
+        g = _host_f32(edge_logits)
+        if g.ndim == 2:
+            g = g.reshape(1, *g.shape)
+        b, e, _ = g.shape
+        idx = np.zeros((b, e, M), np.int32)
+        w = np.zeros((b, e, M), np.float32)
+        self._call("spider_edge_topk_f32", g, b, e, M, idx, w)
+        return idx, w
+
+    def edge_generator(self, hidden, loop_emb, W_gen, E: int):
+        h = _host_f32(hidden)
+        emb = _host_f32(loop_emb).reshape(-1)
+        b, hd = h.shape
+        out = np.zeros((b, E * E), np.float32)
+        self._call("spider_edge_generator_f32", h, b, hd, E, emb, int(emb.shape[0]),
+                   _host_f32(W_gen), out)
+        return out.reshape(b, E, E)
+
+    def graph_dynamic(self, projected, edge_indices, edge_weights, assign, E: int, M: int):
+        p = _host_f32(projected)
+        b, _, hd = p.shape
+        asg = _host_i32(assign)
+        out = np.zeros((b, hd), np.float32)
+        self._call("spider_graph_message_passing_dynamic_f32", p, b, hd, E, asg.shape[1], M,
+                   _host_i32(edge_indices), _host_f32(edge_weights), asg, out)
+        return out
+
+    def graph_from_generator(self, hidden, loop_emb, W_gen, W_edge, assign, E: int, M: int):
+        """spider_graph_from_generator_f32 in one call (the reference's
+        binding composes the four steps; the result is the same)."""
+        h = _host_f32(hidden)
+        emb = _host_f32(loop_emb).reshape(-1)
+        b, hd = h.shape
+        asg = _host_i32(assign)
+        msg = np.zeros((b, hd), np.float32)
+        logits = np.zeros((b, E * E), np.float32)
+        eidx = np.zeros((b, E, M), np.int32)
+        ew = np.zeros((b, E, M), np.float32)
+        proj = np.zeros((b, E, hd), np.float32)
+        self._call("spider_graph_from_generator_f32", h, b, hd, E, asg.shape[1], M, emb,
+                   int(emb.shape[0]), _host_f32(W_gen), _host_f32(W_edge), asg, msg, logits,
+                   eidx, ew, proj)
+        return msg
+
+    def expert_ffn(self, tokens, assign, route, W_up, W_down, E: int):
+        x = _host_f32(tokens)
+        b, hd = x.shape
+        wu = _host_f32(W_up)
+        asg = _host_i32(assign)
+        out = np.zeros_like(x)
+        self._call("spider_expert_grouped_gemm_f32", x, b, hd, wu.shape[-1], E, asg.shape[1], asg,
+                   _host_f32(route), wu, _host_f32(W_down), out)
+        return out
+
+    def epilogue(self, h, delta, x0, gamma, bias, alpha: float = 1.0, beta: float = 0.0,
+                 eps: float = 1e-5):
+        hh = _host_f32(h)
+        b, hd = hh.shape
+        out = np.zeros_like(hh)
+        self._call("spider_loop_epilogue_f32", hh, _host_f32(delta), _host_f32(x0), b, hd,
+                   float(alpha), float(beta), _host_f32(gamma), _host_f32(bias), float(eps), out)
+        return out
+
+    def early_exit(self, h, proj, threshold: float = 0.85):
+        hh = _host_f32(h)
+        b, hd = hh.shape
+        mask = np.zeros(b, np.uint8)
+        self._call("spider_early_exit_f32", hh, _host_f32(proj).reshape(-1), b, hd,
+                   float(threshold), mask)
+        return mask
+
+    def moe_loop_step(self, h, x0, loop_idx: int, *, router_w, loop_bias, W_up, W_down,
+                      ln_weight, ln_bias, top_k: int, alpha: float, beta: float,
+                      eps: float = 1e-5, csr=None, W_edge=None, exit_proj=None,
+                      exit_threshold: float = 0.85):
+        """spider_moe_loop_step_f32: (h_next, exit_mask, assign, route,
+        messages); the projected CSR pass when both csr = (row_ptr, col_idx,
+        edge_w [R*nnz]) and W_edge [E,H,H] are given, else messages = h."""
+        hh = _host_f32(h)
+        b, hd = hh.shape
+        rw = _host_f32(router_w)
+        e = rw.shape[1]
+        wu = _host_f32(W_up)
+        out = np.zeros_like(hh)
+        mask = np.zeros(b, np.uint8)
+        asg = np.zeros((b, top_k), np.int32)
+        route = np.zeros((b, top_k), np.float32)
+        msgs = np.zeros_like(hh)
+        rp = ci = ew = None
+        nnz = 0
+        if csr is not None:
+            rp, ci, ew = _host_i32(csr[0]), _host_i32(csr[1]), _host_f32(csr[2])
+            nnz = int(ci.shape[0])
+        we = None if W_edge is None else _host_f32(W_edge)
+        ep = None if exit_proj is None else _host_f32(exit_proj).reshape(-1)
+        self._call("spider_moe_loop_step_f32", hh, _host_f32(x0), b, hd, e, top_k, wu.shape[-1],
+                   loop_idx, rw, _host_f32(loop_bias), rp, ci, ew, nnz, we, wu, _host_f32(W_down),
+                   _host_f32(ln_weight), _host_f32(ln_bias), float(alpha), float(beta),
+                   float(eps), ep, float(exit_threshold), out, mask, asg, route, msgs)
+        return out, mask, asg, route, msgs
+
+
 class NativeLoop:
     """The block loops of a .spiderw bundle on the GPU (the loop body of
     native_backend.py:309-388 with the device ABI's static graph)."""
@@ -246,4 +491,4 @@ class NativeLoop:
         return h
 
 
-__all__ = ["HipKernels", "NativeLoop"]
+__all__ = ["HipKernels", "HostKernels", "NativeLoop"]

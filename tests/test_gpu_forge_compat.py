@@ -35,7 +35,8 @@ def _rng(seed):
 
 
 # ----------------------------------------------------- device ABI ----
-@pytest.mark.parametrize("b,e,k", [(2, 4, 2), (300, 16, 2), (77, 64, 8), (5, 33, 3)])
+@pytest.mark.parametrize("b,e,k", [(2, 4, 2), (300, 16, 2), (77, 64, 8), (5, 33, 3), (50, 100, 4),
+                                   (9, 256, 8)])
 def test_spider_cuda_router(b, e, k):
     say("spider_cuda_router", b, e, k)
     kern = _kern()
@@ -59,7 +60,7 @@ def test_spider_cuda_argument_errors():
     with pytest.raises(RuntimeError, match="spider_cuda_router_f32 failed"):
         kern.router(np.zeros((2, 4), np.float32), np.zeros((1, 4), np.float32), 5)
     with pytest.raises(RuntimeError, match="spider_cuda_router_f32 failed"):
-        kern.router(np.zeros((2, 80), np.float32), np.zeros((1, 80), np.float32), 2)
+        kern.router(np.zeros((2, 300), np.float32), np.zeros((1, 300), np.float32), 2)
 
 
 def _csr(e, r, fanout=3):
@@ -321,3 +322,164 @@ def test_dispatch_expert_fn_combine_is_exact(dtype, n, h, e, k):
     assert seen == sorted(set(seen)) and len(seen) >= 2
     want = OF.dispatch_ffn(msg, ti, tw, e, fn)
     assert got.dtype == dtype and torch.equal(got, want)
+
+
+# ------------------------------------------- host ABI (spider_kernels.h) ----
+def _host():
+    from spider_moe_amd.native_compat import HostKernels
+    return HostKernels()
+
+
+def test_host_abi_known_answers():
+    """The reference's own C++ checks (kernels/tests/test_kernels.cpp:7-18,
+    test_phase1_1.cpp:8-57, test_phase1_2.cpp:7-45, test_phase1_3.cpp:7-52)
+    through the host entry points on the GPU."""
+    say("host abi known answers")
+    hk = _host()
+    assert hk.backend == "hip-gfx950"
+    w, i = hk.router(np.array([[1, 2, 3, 4], [4, 3, 2, 1]], np.float32), np.zeros((1, 4), np.float32), 2)
+    assert i.tolist() == [[3, 2], [0, 1]] and np.allclose(w.sum(-1), 1, atol=1e-6)
+    h = (0.1 * np.arange(1, 9, dtype=np.float32)).reshape(2, 4)
+    we = np.stack([np.eye(4, dtype=np.float32)] * 3)
+    assert np.allclose(hk.edge_project(h, we), np.repeat(h[:, None], 3, axis=1), atol=1e-5)
+    m = hk.graph_v2(np.array([[[1, 0], [0, 2]]], np.float32), np.array([0, 1, 1]), np.array([1]),
+                    np.array([0.5], np.float32), np.array([[0]]), 2)
+    assert np.allclose(m, [[0, 1]], atol=1e-6)
+    idx, wt = hk.edge_topk(np.array([[[0, 1, 2], [3, 0, 1], [0, 0, 1]]], np.float32), 2)
+    assert idx[0, 0].tolist() == [2, 1] and abs(wt[0, 0].sum() - 1) < 1e-5
+    m = hk.graph_dynamic(np.array([[[1, 0], [0, 4]]], np.float32), np.array([[[1], [0]]]),
+                         np.array([[[0.5], [1.0]]], np.float32), np.array([[0]]), 2, 1)
+    assert np.allclose(m, [[0, 2]], atol=1e-5)
+    wg = np.zeros((4, 3), np.float32)
+    wg[1, 0] = wg[2, 0] = 5
+    lg = hk.edge_generator(np.array([[1, 0]], np.float32), np.zeros(1, np.float32), wg, 2)
+    assert lg.reshape(-1)[1] > lg.reshape(-1)[0]
+    wg = np.zeros((4, 2), np.float32)
+    wg[1, 0] = wg[2, 0] = 3
+    idx, wt = hk.edge_topk(hk.edge_generator(np.array([[1, 0]], np.float32),
+                                             np.zeros(0, np.float32), wg, 2), 1)
+    assert idx[0, 0, 0] == 1 and abs(wt[0, 0, 0] - 1) < 1e-5
+    wg = np.zeros((4, 2), np.float32)
+    wg[1, 0] = 2
+    m = hk.graph_from_generator(np.array([[1, 0]], np.float32), np.zeros(0, np.float32), wg,
+                                np.stack([np.eye(2, dtype=np.float32)] * 2), np.array([[0]]), 2, 1)
+    assert np.isfinite(m).all()
+    out, mask, *_ = hk.moe_loop_step(
+        np.full((1, 4), 0.05, np.float32), np.full((1, 4), 0.01, np.float32), 0,
+        router_w=np.full((4, 2), 0.02, np.float32), loop_bias=np.zeros(2, np.float32),
+        W_up=np.full((2, 4, 4), 0.01, np.float32), W_down=np.full((2, 4, 4), 0.01, np.float32),
+        ln_weight=np.ones(4, np.float32), ln_bias=np.zeros(4, np.float32), top_k=1, alpha=1.0,
+        beta=0.0, csr=(np.array([0, 1, 1]), np.array([0]), np.ones(1, np.float32)),
+        W_edge=np.stack([np.eye(4, dtype=np.float32)] * 2), exit_proj=np.full(4, 0.1, np.float32),
+        exit_threshold=0.99)
+    assert np.isfinite(out).all()
+    with pytest.raises(RuntimeError, match="spider_expert_grouped_gemm_f32 failed: 2"):
+        hk.expert_ffn(np.zeros((1, 4), np.float32), np.array([[3]]), np.ones((1, 1), np.float32),
+                      np.zeros((2, 4, 4), np.float32), np.zeros((2, 4, 4), np.float32), 2)
+
+
+@pytest.mark.parametrize("b,h,e,m,k", [(6, 24, 8, 3, 2), (4, 64, 100, 5, 4), (3, 32, 256, 4, 8)])
+def test_host_abi_dynamic_edges_match_oracle(b, h, e, m, k):
+    """Edge projection, generator, graph v2 and the dynamic pass are the
+    scalar library's float / double operations in its order: exact.  Edge
+    top-m indices exact, weights within expf's ulps; E up to 256."""
+    say("host abi dynamic", b, h, e, m, k)
+    hk = _host()
+    r = _rng(e + h)
+    x = r.standard_normal((b, h)).astype(np.float32)
+    we = (r.standard_normal((e, h, h)) / np.sqrt(h)).astype(np.float32)
+    proj = hk.edge_project(x, we)
+    assert np.array_equal(proj, ON.edge_project(x, we))
+    d = 3
+    wg = (r.standard_normal((e * e, h + d)) / np.sqrt(h)).astype(np.float32)
+    emb = r.standard_normal(d).astype(np.float32)
+    lg = hk.edge_generator(x, emb, wg, e)
+    assert np.array_equal(lg, ON.edge_generator(x, emb, wg))
+    lg[0, 1, :4] = lg[0, 1, 5]  # ties: first index
+    lg[0, 2, :] = -np.inf
+    lg[0, 2, 3] = 1.0  # one candidate, then none
+    idx, wt = hk.edge_topk(lg, m)
+    io, wo = ON.edge_topk(lg, m)
+    assert np.array_equal(idx, io)
+    fin = np.isfinite(wo)
+    assert np.allclose(wt[fin], wo[fin], rtol=1e-5, atol=1e-7)
+    asg = r.integers(-1, e, (b, k)).astype(np.int32)
+    asg[0, 0] = 1
+    ok = (idx >= 0).all(-1)  # sources whose picks are all valid
+    asg_ok = np.where(np.take_along_axis(ok, np.maximum(asg, 0), 1) | (asg < 0), asg, -1)
+    got = hk.graph_dynamic(proj, idx, wt, asg_ok, e, m)
+    assert np.array_equal(got, ON.graph_dynamic(proj, idx, wt, asg_ok))
+    rp = np.concatenate([[0], np.cumsum(r.integers(0, 3, e))]).astype(np.int32)
+    nnz = int(rp[-1])
+    ci = r.integers(0, e, nnz).astype(np.int32)
+    ew = r.random(2 * nnz).astype(np.float32)
+    for loop in (0, 1):
+        got = hk.graph_v2(proj, rp, ci, ew, asg, e, loop)
+        assert np.array_equal(got, ON.graph_v2(proj, rp, ci, ew, asg, nnz=nnz, loop_idx=loop))
+    lgr = r.standard_normal((b * 7, e)).astype(np.float32)
+    bias = (0.1 * r.standard_normal((2, e))).astype(np.float32)
+    w, i = hk.router(lgr, bias, k, 1)
+    wo, io = ON.router(lgr, bias[1], k)
+    assert np.array_equal(i, io) and np.allclose(w, wo, rtol=1e-5, atol=1e-7)
+
+
+def test_host_abi_loop_step_matches_oracle():
+    say("host abi loop step")
+    hk = _host()
+    r = _rng(31)
+    b, h, e, k, u = 64, 128, 16, 2, 96
+    x, x0 = (r.standard_normal((b, h)).astype(np.float32) for _ in range(2))
+    rw = (r.standard_normal((h, e)) / np.sqrt(h)).astype(np.float32)
+    bias = (0.1 * r.standard_normal((3, e))).astype(np.float32)
+    wu = (r.standard_normal((e, h, u)) / np.sqrt(h)).astype(np.float32)
+    wd = (r.standard_normal((e, u, h)) / np.sqrt(u)).astype(np.float32)
+    we = (r.standard_normal((e, h, h)) / np.sqrt(h)).astype(np.float32)
+    g = (1 + 0.1 * r.standard_normal(h)).astype(np.float32)
+    gb = (0.1 * r.standard_normal(h)).astype(np.float32)
+    proj = (r.standard_normal(h) / np.sqrt(h)).astype(np.float32)
+    rp, ci = _csr(e, r)
+    ew = r.random(3 * len(ci)).astype(np.float32)
+    for csr, wedge in (((rp, ci, ew), we), (None, None)):
+        hn, mask, asg, route, msgs = hk.moe_loop_step(
+            x, x0, 2, router_w=rw, loop_bias=bias, W_up=wu, W_down=wd, ln_weight=g, ln_bias=gb,
+            top_k=k, alpha=0.5, beta=0.1, csr=csr, W_edge=wedge, exit_proj=proj,
+            exit_threshold=0.5)
+        wn, _, wa, wr, wm = ON.loop_step(x, x0, k, rw, bias[2], wu, wd, g, gb, 0.5, 0.1, 1e-5,
+                                         csr=csr, w_edge=wedge, loop_idx=2)
+        assert np.array_equal(asg, wa) and np.allclose(route, wr, rtol=1e-5, atol=1e-7)
+        assert np.allclose(msgs, wm, rtol=1e-5, atol=1e-5)
+        assert np.allclose(hn, wn, rtol=1e-4, atol=1e-4)
+        _, conf = ON.exit_mask(wn, proj, 0.5)
+        far = np.abs(conf - 0.5) > 1e-4
+        assert np.array_equal(mask[far], (conf[far] > 0.5).astype(np.uint8))
+
+
+def test_host_abi_matches_the_compiled_scalar_library():
+    """Where oracle/_ref (the reference's scalar library compiled from its
+    sources) is present, the same calls on both libraries agree."""
+    from oracle import ref as R
+    if not R.available():
+        pytest.skip("oracle/_ref not built")
+    say("host abi vs scalar library")
+    hk = _host()
+    r = _rng(41)
+    b, h, e, m, k, u = 5, 32, 8, 3, 2, 40
+    x = r.standard_normal((b, h)).astype(np.float32)
+    we = (0.3 * r.standard_normal((e, h, h))).astype(np.float32)
+    rc, pr = R.edge_project_f32(x, we)
+    assert rc == 0 and np.array_equal(hk.edge_project(x, we), pr)
+    wg = (0.3 * r.standard_normal((e * e, h + 2))).astype(np.float32)
+    emb = r.standard_normal(2).astype(np.float32)
+    rc, lr = R.edge_generator_f32(x, emb, wg)
+    assert rc == 0 and np.array_equal(hk.edge_generator(x, emb, wg, e), lr)
+    rc, ir, wr = R.edge_topk_f32(lr, m)
+    idx, wt = hk.edge_topk(lr, m)
+    assert np.array_equal(idx, ir) and np.allclose(wt, wr, rtol=1e-5)
+    asg = r.integers(-1, e, (b, k)).astype(np.int32)
+    rc, gr = R.graph_dynamic_f32(pr, ir, wr, asg)
+    assert rc == 0 and np.array_equal(hk.graph_dynamic(pr, ir, wr, asg, e, m), gr)
+    wu = (0.2 * r.standard_normal((e, h, u))).astype(np.float32)
+    wd = (0.2 * r.standard_normal((e, u, h))).astype(np.float32)
+    rw = r.random((b, k)).astype(np.float32)
+    rc, er = R.expert_grouped_gemm_f32(x, asg, rw, wu, wd)
+    assert rc == 0 and np.allclose(hk.expert_ffn(x, asg, rw, wu, wd, e), er, rtol=1e-4, atol=1e-5)

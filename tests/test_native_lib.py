@@ -46,7 +46,13 @@ def test_exports_the_reference_device_abi(nat):
                            "spider_cuda_expert_workspace_bytes",
                            "spider_cuda_expert_grouped_gemm_v2_f32",
                            "spider_cuda_loop_epilogue_f32", "spider_cuda_early_exit_f32",
-                           "spider_cuda_moe_loop_step_f32"])
+                           "spider_cuda_moe_loop_step_f32",
+                           # device forms of the dynamic-edge host functions
+                           "spider_cuda_edge_project_f32",
+                           "spider_cuda_graph_message_passing_v2_f32",
+                           "spider_cuda_edge_topk_f32",
+                           "spider_cuda_graph_message_passing_dynamic_f32",
+                           "spider_cuda_edge_generator_f32"])
     handle = ctypes.CDLL(nat.LIB_PATH)
     for s in syms:
         assert hasattr(handle, s), s
@@ -56,8 +62,61 @@ def test_exports_the_reference_device_abi(nat):
     assert lib.spider_cuda_expert_workspace_bytes(0, 2, 8) == 0
     # argument checks return 1 before any launch
     assert lib.spider_cuda_router_f32(None, None, 1, 4, 2, 0, None, None, None) == 1
-    assert lib.spider_cuda_router_f32(1, 1, 1, 65, 2, 0, 1, 1, None) == 1  # E > 64
+    assert lib.spider_cuda_router_f32(1, 1, 1, 257, 2, 0, 1, 1, None) == 1  # E > 256
     assert lib.spider_cuda_early_exit_f32(None, None, 1, 4, 0.5, None, None) == 1
+    assert lib.spider_cuda_edge_topk_f32(1, 1, 4, 5, 1, 1, None) == 1  # M > E
+
+
+def test_exports_the_reference_host_abi(nat):
+    """include/spider_kernels.h: the reference's host ABI names of the MoE
+    loop (kernels/include/spider_kernels.h:26-121, 148-149); the argument
+    and index checks run on the host before any device work, so they are
+    exercised here without a GPU; the f16 entries return -2 like the
+    reference's stubs."""
+    import numpy as np
+    text = open(os.path.join(ROOT, "include", "spider_kernels.h")).read()
+    syms = sorted(set(re.findall(r"SPIDER_API\s+[\w\s\*]+?\b(spider_\w+)\s*\(", text)))
+    assert set(nat.SPIDER_HOST_SIGNATURES) == set(syms)
+    assert {"spider_router_f32", "spider_edge_topk_f32", "spider_graph_message_passing_dynamic_f32",
+            "spider_expert_grouped_gemm_f32", "spider_loop_epilogue_f32", "spider_early_exit_f32",
+            "spider_moe_loop_step_f32"} <= set(syms)
+    alias = os.path.join(os.path.dirname(nat.LIB_PATH), "libspider_kernels.so")
+    assert os.path.realpath(alias) == os.path.realpath(nat.LIB_PATH)
+    handle = ctypes.CDLL(alias)
+    for s in syms:
+        assert hasattr(handle, s), s
+    lib = nat.lib()
+    assert lib.spider_backend_name() == b"hip-gfx950" and lib.spider_backend_caps() & 1
+    for f16 in ("spider_router_f16", "spider_graph_message_passing_f16",
+                "spider_expert_grouped_gemm_f16", "spider_loop_epilogue_f16"):
+        args = [None if t is ctypes.c_void_p else t(0)
+                for t in nat.SPIDER_HOST_SIGNATURES[f16][1]]
+        assert getattr(lib, f16)(*args) == -2
+    z = np.zeros(64, np.float32)
+    zi = np.zeros(64, np.int32)
+    p = lambda a: a.ctypes.data  # noqa: E731
+    assert lib.spider_router_f32(p(z), p(z), 2, 4, 5, 0, p(z), p(zi)) == 1  # K > E
+    assert lib.spider_router_f32(None, p(z), 2, 4, 2, 0, p(z), p(zi)) == 1
+    assert lib.spider_loop_epilogue_f32(p(z), p(z), p(z), 1, 4, 1.0, 0.0, p(z), p(z), 0.0,
+                                        p(z)) == 1  # eps <= 0
+    assert lib.spider_edge_topk_f32(p(z), 1, 2, 3, p(zi), p(z)) == 1  # M > E
+    # a CSR that does not end at nnz, then a selected source >= E
+    rp = np.array([0, 1, 1], np.int32)
+    ci = np.array([1], np.int32)
+    asg = np.array([0, 2], np.int32)
+    assert lib.spider_graph_message_passing_f32(p(z), 2, 4, 2, 1, p(rp), p(ci), p(z), 2, 0,
+                                                p(asg), p(z), p(z)) == 1
+    assert lib.spider_graph_message_passing_f32(p(z), 2, 4, 2, 1, p(rp), p(ci), p(z), 1, 0,
+                                                p(asg), p(z), p(z)) == 2
+    ci_bad = np.array([5], np.int32)  # destination outside [0, E) of a selected source
+    asg0 = np.array([0, -1], np.int32)
+    assert lib.spider_graph_message_passing_v2_f32(p(z), 2, 4, 2, 1, p(rp), p(ci_bad), p(z), 1,
+                                                   0, p(asg0), p(z)) == 2
+    eidx = np.array([0, 7, 0, 0], np.int32)  # [B=1, E=2, M=2]: source 0 points at 7
+    assert lib.spider_graph_message_passing_dynamic_f32(p(z), 1, 4, 2, 1, 2, p(eidx), p(z),
+                                                        p(asg0), p(z)) == 2
+    assert lib.spider_expert_grouped_gemm_f32(p(z), 1, 4, 4, 2, 2, p(asg), p(z), p(z), p(z),
+                                              p(z)) == 2  # expert 2 >= E
 
 
 def test_identity(nat):

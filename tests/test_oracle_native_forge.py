@@ -213,3 +213,108 @@ def test_spiderw_roundtrip(tmp_path):
         load_spiderw_bytes = tmp_path / "bad.spiderw"
         load_spiderw_bytes.write_bytes(b"NOTSPIDR" + raw[8:])
         load_spiderw(load_spiderw_bytes)
+
+
+# ---------------------------------------------- dynamic-edge functions ----
+def test_dynamic_edge_known_answers():
+    """kernels/tests/test_phase1_1.cpp:8-33, test_phase1_2.cpp:7-31,
+    test_phase1_3.cpp:7-33."""
+    h = (0.1 * np.arange(1, 9, dtype=np.float32)).reshape(2, 4)
+    w = np.zeros((3, 4, 4), np.float32)
+    for e in range(3):
+        w[e] = np.eye(4, dtype=np.float32)
+    p = ON.edge_project(h, w)
+    assert np.allclose(p, np.repeat(h[:, None, :], 3, axis=1), atol=1e-7)
+    m = ON.graph_v2(np.array([[[1, 0], [0, 2]]], np.float32), np.array([0, 1, 1]), np.array([1]),
+                    np.array([0.5], np.float32), np.array([[0]]))
+    assert np.allclose(m, [[0, 1]])
+    idx, wt = ON.edge_topk(np.array([[[0, 1, 2], [3, 0, 1], [0, 0, 1]]], np.float32), 2)
+    assert idx[0, 0].tolist() == [2, 1] and abs(wt[0, 0].sum() - 1) < 1e-6
+    assert idx[0, 2].tolist() == [2, 0]  # ties go to the lower index
+    m = ON.graph_dynamic(np.array([[[1, 0], [0, 4]]], np.float32), np.array([[[1], [0]]]),
+                         np.array([[[0.5], [1.0]]], np.float32), np.array([[0]]))
+    assert np.allclose(m, [[0, 2]])
+    wg = np.zeros((4, 3), np.float32)
+    wg[1, 0] = wg[2, 0] = 5
+    lg = ON.edge_generator(np.array([[1, 0]], np.float32), np.zeros(1, np.float32), wg)
+    assert lg.reshape(-1)[1] > lg.reshape(-1)[0]
+    wg = np.zeros((4, 2), np.float32)
+    wg[1, 0] = wg[2, 0] = 3
+    idx, wt = ON.edge_topk(ON.edge_generator(np.array([[1, 0]], np.float32),
+                                             np.zeros(0, np.float32), wg), 1)
+    assert idx[0, 0, 0] == 1 and abs(wt[0, 0, 0] - 1) < 1e-6
+
+
+def test_edge_topk_without_candidates():
+    """All remaining logits -inf (or NaN): the pick is (-1, -inf), as the
+    scalar loop leaves it."""
+    g = np.full((1, 2, 2), -np.inf, np.float32)
+    g[0, 0, 1] = 0.5
+    g[0, 1, 0] = np.nan
+    idx, _ = ON.edge_topk(g, 2)
+    assert idx[0, 0].tolist() == [1, -1] and idx[0, 1].tolist() == [-1, -1]
+
+
+@needs_ref
+def test_dynamic_edge_functions_match_scalar_library():
+    r = np.random.default_rng(21)
+    b, h, e, m, k, d = 6, 24, 8, 3, 2, 5
+    x = r.standard_normal((b, h)).astype(np.float32)
+    we = (0.3 * r.standard_normal((e, h, h))).astype(np.float32)
+    rc, pr = R.edge_project_f32(x, we)
+    assert rc == 0 and np.array_equal(ON.edge_project(x, we), pr)
+    wg = (0.3 * r.standard_normal((e * e, h + d))).astype(np.float32)
+    emb = r.standard_normal(d).astype(np.float32)
+    rc, lr = R.edge_generator_f32(x, emb, wg)
+    lo = ON.edge_generator(x, emb, wg)
+    assert rc == 0 and np.array_equal(lo, lr)
+    lo[0, 1, :3] = lo[0, 1, 3]  # ties
+    rc, ir, wr = R.edge_topk_f32(lo, m)
+    io, wo = ON.edge_topk(lo, m)
+    assert rc == 0 and np.array_equal(io, ir) and np.allclose(wo, wr, rtol=2e-6)
+    asg = r.integers(-1, e, (b, k)).astype(np.int32)
+    rc, gr = R.graph_dynamic_f32(pr, ir, wr, asg)
+    assert rc == 0 and np.array_equal(ON.graph_dynamic(pr, ir, wr, asg), gr)
+    rp = np.array([0, 2, 3, 3, 5, 6, 8, 9, 10], np.int32)
+    ci = r.integers(0, e, 10).astype(np.int32)
+    ew = r.random(20).astype(np.float32)
+    for loop in (0, 1):
+        rc, vr = R.graph_v2_f32(pr, rp, ci, ew, asg, loop)
+        assert rc == 0
+        assert np.array_equal(ON.graph_v2(pr, rp, ci, ew, asg, nnz=10, loop_idx=loop), vr)
+
+
+@needs_ref
+def test_loop_step_with_edge_values_matches_scalar_library():
+    r = np.random.default_rng(22)
+    b, h, e, k, u = 5, 16, 6, 2, 24
+    x, x0 = (r.standard_normal((b, h)).astype(np.float32) for _ in range(2))
+    rw = (0.3 * r.standard_normal((h, e))).astype(np.float32)
+    bias = (0.1 * r.standard_normal((2, e))).astype(np.float32)
+    wu = (0.2 * r.standard_normal((e, h, u))).astype(np.float32)
+    wd = (0.2 * r.standard_normal((e, u, h))).astype(np.float32)
+    we = (0.3 * r.standard_normal((e, h, h))).astype(np.float32)
+    g = (1 + 0.1 * r.standard_normal(h)).astype(np.float32)
+    gb = (0.1 * r.standard_normal(h)).astype(np.float32)
+    rp = np.array([0, 1, 3, 3, 4, 6, 7], np.int32)
+    ci = r.integers(0, e, 7).astype(np.int32)
+    ew = r.random(14).astype(np.float32)
+    rc, hn, mk, asg, route = R.moe_loop_step_f32(x, x0, k, 1, rw, bias, wu, wd, g, gb, 0.5, 0.1,
+                                                 1e-5, None, 0.5, csr=(rp, ci, ew), w_edge=we)
+    assert rc == 0
+    got, mg, ag, rg, _ = ON.loop_step(x, x0, k, rw, bias[1], wu, wd, g, gb, 0.5, 0.1, 1e-5,
+                                      csr=(rp, ci, ew), w_edge=we, loop_idx=1)
+    assert np.array_equal(ag, asg) and np.allclose(rg, route, rtol=2e-6)
+    assert np.allclose(got, hn, rtol=1e-5, atol=1e-5) and not mg.any() and not mk.any()
+
+
+def test_planted_dynamic_edge_mistakes_are_caught():
+    """A projection with W_edge transposed, or a top-m without the
+    softmax, differs from the oracle."""
+    r = np.random.default_rng(23)
+    x = r.standard_normal((2, 8)).astype(np.float32)
+    we = r.standard_normal((3, 8, 8)).astype(np.float32)
+    assert not np.allclose(ON.edge_project(x, we), ON.edge_project(x, we.transpose(0, 2, 1)))
+    g = r.standard_normal((1, 4, 4)).astype(np.float32)
+    _, w = ON.edge_topk(g, 2)
+    assert np.allclose(w.sum(-1), 1, atol=1e-6) and not np.allclose(w, np.sort(g, -1)[..., ::-1][..., :2])
