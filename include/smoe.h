@@ -326,14 +326,24 @@ SMOE_API int smoe_linear(const void* x, int N, int K, const void* w, int w_forma
                          const float* w_scale, const float* bias, int N_out, int act, void* out,
                          int out_dtype, void* stream);
 
-/* out [N,H] = per token, the sum over its rows tok_row [N,K] (-1: none, in
- * slot order) of y [R,H] times row_w [R] (NULL: 1), each product rounded to
- * y's dtype and each partial sum to out's (SMOE_F32 / SMOE_BF16): the
- * combine of dispatch_expert_ffn (forge/ep/dispatch.py:127-134, 176-180),
- * a scatter-add of weighted expert outputs in ascending expert order. */
+/* out [N,H] = per token, the sum over its rows tok_row [N,K] (-1: none;
+ * distinct rows, added in ascending row order) of y [R,H] times row_w [R]
+ * (NULL: 1; cast to y's dtype first), each product rounded to y's dtype and
+ * each partial sum to out's (SMOE_F32 / SMOE_BF16): the combine of
+ * dispatch_expert_ffn (forge/ep/dispatch.py:127-134, 176-180), a
+ * scatter-add of weighted expert outputs in ascending expert order (plan
+ * rows are grouped by ascending expert). */
 SMOE_API int smoe_combine_rows(const void* y, int y_dtype, const float* row_w,
                                const int32_t* tok_row, int N, int K, int H, void* out,
                                int out_dtype, void* stream);
+
+/* ---- Dobu expert residency (spider_moe/expert_store.py:121-166) ----
+ * out[i] = map[ids[i]] for ids in [0, E), else -1: routed expert ids ->
+ * slots of the device-resident expert slab (map[e] = -1 for experts not in
+ * the slab), so smoe_expert_delta runs over the slab as E' = slot count
+ * experts.  n >= 0; no workspace. */
+SMOE_API int smoe_remap_ids(const int32_t* ids, int64_t n, const int32_t* map, int E,
+                            int32_t* out, void* stream);
 
 /* ---- diagnostics (no counterpart in the reference; used by bench.py) ----
  * Stage ids of smoe_block_forward, in launch order within a loop. */

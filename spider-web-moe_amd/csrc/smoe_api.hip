@@ -1061,6 +1061,15 @@ SMOE_API int smoe_combine_rows(const void* y, int y_dtype, const float* row_w,
   return SMOE_OK;
 }
 
+SMOE_API int smoe_remap_ids(const int32_t* ids, int64_t n, const int32_t* map, int E,
+                            int32_t* out, void* stream) {
+  if (n < 0 || E < 0) return fail(SMOE_EINVAL, "remap shape");
+  if (n == 0) return SMOE_OK;
+  if (!ids || !out || (E > 0 && !map)) return fail(SMOE_EINVAL, "null buffer");
+  SMOE_TRY(launch_remap_ids(ids, n, map, E, out, static_cast<hipStream_t>(stream)), "remap ids");
+  return SMOE_OK;
+}
+
 SMOE_API int smoe_combine_epilogue(const void* h, const void* x0, int act_dtype, const void* delta,
                                    int delta_dtype, int N, int H, float alpha, float beta,
                                    const float* ln_w, const float* ln_b, float eps, void* out,

@@ -111,6 +111,21 @@ __global__ __launch_bounds__(256) void k_combine_rows(const void* __restrict__ y
   }
 }
 
+// Routed expert ids -> slab slots (Dobu residency); 4 ids per thread.
+__global__ __launch_bounds__(256) void k_remap_ids(const int32_t* __restrict__ ids, int64_t n,
+                                                   const int32_t* __restrict__ map, int E,
+                                                   int32_t* __restrict__ out) {
+  const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int64_t i = i0 + u;
+    if (i < n) {
+      const int e = ids[i];
+      out[i] = (e >= 0 && e < E) ? map[e] : -1;
+    }
+  }
+}
+
 int rc() { return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP; }
 
 }  // namespace
@@ -132,6 +147,15 @@ int launch_select_topk(const float* logits, int N, int E, int K, int mode, float
   else if (seg == 32) SMOE_SEL(32);
   else SMOE_SEL(64);
 #undef SMOE_SEL
+  return rc();
+}
+
+int launch_remap_ids(const int32_t* ids, int64_t n, const int32_t* map, int E, int32_t* out,
+                     hipStream_t s) {
+  if (n <= 0) return SMOE_OK;
+  const int64_t blocks = (n + 1023) / 1024;
+  hipLaunchKernelGGL(k_remap_ids, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, s, ids, n, map,
+                     E, out);
   return rc();
 }
 

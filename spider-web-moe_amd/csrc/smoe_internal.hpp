@@ -119,6 +119,9 @@ int launch_select_topk(const float* logits, int N, int E, int K, int mode, float
 // out[t] = sum over the token's rows tok_row [N, K] of y[row] * row_w[row]
 int launch_combine_rows(const void* y, int ydt, const float* row_w, const int32_t* tok_row,
                         int N, int K, int H, void* out, int odt, hipStream_t s);
+// out[i] = map[ids[i]] for ids in [0, E), else -1
+int launch_remap_ids(const int32_t* ids, int64_t n, const int32_t* map, int E, int32_t* out,
+                     hipStream_t s);
 
 // ---- the reference's native loop (smoe_compat.hip), for the host entry
 // points of smoe_host_abi.hip ----

@@ -91,6 +91,7 @@ SIGNATURES = {
                              _c_int, _vp]),
     "smoe_combine_rows": (_c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_int,
                                    _vp]),
+    "smoe_remap_ids": (_c_int, [_vp, ctypes.c_int64, _vp, _c_int, _vp, _vp]),
     "smoe_profile_stages": (_c_int, [ctypes.c_uint32, ctypes.POINTER(_vp), _c_int]),
     "smoe_profile_count": (_c_int, [ctypes.POINTER(ctypes.c_int32), _c_int]),
     "smoe_events_create": (_c_int, [_c_int, ctypes.POINTER(_vp)]),

@@ -13,8 +13,9 @@ model.py:271,305-308).
 
 Scope: inference (no autograd through the HIP block), one GPU.  The
 ``return_stats`` diagnostics (model.py:327-349) are computed with torch from
-the kernels' routing outputs.  Expert offload (Dobu) and Lumen are outside
-this module and rejected at construction.
+the kernels' routing outputs.  With offload_experts (Orbit Dobu) the expert
+FFN weights stay in host memory behind an HBM working set (dobu.py).  Lumen
+is outside this module and rejected at construction.
 """
 from __future__ import annotations
 
@@ -58,8 +59,6 @@ class SpiderMoELayer(nn.Module):
 
     def __init__(self, cfg: ModelConfig):
         super().__init__()
-        if getattr(cfg, "offload_experts", False):
-            raise NotImplementedError("offload_experts (Dobu) is not part of spider_moe_amd")
         if getattr(cfg, "use_lumen", False):
             raise NotImplementedError("use_lumen is not part of spider_moe_amd")
         h, e = cfg.hidden_size, cfg.num_experts
@@ -111,6 +110,52 @@ class SpiderMoELayer(nn.Module):
         self._ws: torch.Tensor | None = None
         self._last_n = 0
         self._last_ws: torch.Tensor | None = None
+        self._expert_key = None
+        if getattr(cfg, "offload_experts", False):
+            self.enable_offload(self.top_dobu)
+
+    # ------------------------------------------------------ Dobu offload ----
+    def enable_offload(self, top_dobu: int = 4, *, pin_memory: bool = True,
+                       storage_device: str = "cpu"):
+        """Expert weights to a pinned host catalogue with an HBM working set
+        of top_dobu experts (model.py:189-201, orbit/dobu.py:82-101); the
+        expert modules leave the GPU.  Forward then runs the block's stages
+        with the FFN fed from the store.  Returns the store."""
+        from .dobu import ExpertChunkStore, offload_module_list_to_cpu
+        if self.expert_activation != "gelu":
+            raise ValueError("Dobu offload holds Linear + GELU + Linear experts")
+        self.top_dobu = int(top_dobu)
+        self._expert_store = ExpertChunkStore(self.experts, storage_device=storage_device,
+                                              max_gpu_experts=self.top_dobu,
+                                              pin_memory=pin_memory)
+        self._expert_key = self._experts_key()
+        offload_module_list_to_cpu(self.experts)
+        self._expert_key = self._experts_key()
+        self.offload_experts = True
+        self._packed = None
+        return self._expert_store
+
+    def _apply(self, fn, *args, **kwargs):
+        """.to() / .cuda() / .bfloat16(): offloaded experts are converted,
+        copied into the catalogue and moved back to the host."""
+        super()._apply(fn, *args, **kwargs)
+        if self.offload_experts and self._expert_store is not None:
+            self._sync_offloaded_experts()
+        return self
+
+    def _experts_key(self):
+        return tuple((p.data_ptr(), p._version, p.device.type) for p in self.experts.parameters())
+
+    def _sync_offloaded_experts(self):
+        """A weight of the (offloaded) expert modules changed, or the modules
+        were moved back to the GPU: refresh the catalogue, offload again."""
+        from .dobu import offload_module_list_to_cpu
+        key = self._experts_key()
+        if key == self._expert_key:
+            return
+        self._expert_store.load_catalogue(self.experts)
+        offload_module_list_to_cpu(self.experts)
+        self._expert_key = self._experts_key()
 
     # ------------------------------------------------------ quantization ----
     @torch.no_grad()
@@ -165,7 +210,8 @@ class SpiderMoELayer(nn.Module):
             return self._packed
         self._plist = list(self.parameters())
         key = self._state_key()
-        dev = nat.require_gpu(*self.parameters())
+        expert_ids = {id(p) for p in self.experts.parameters()} if self.offload_experts else set()
+        dev = nat.require_gpu(*[p for p in self.parameters() if id(p) not in expert_ids])
         act = self.router.weight.dtype
         adt = nat.dtype_code(act)
         e, h, u = self.num_experts, self.hidden_size, self.expert_ffn_size
@@ -202,7 +248,10 @@ class SpiderMoELayer(nn.Module):
         def gate_up(t):  # [E, 2U, X] stacked [gate; up] -> block interleave
             return interleave_gate_up(t[:, :u], t[:, u:]) if swiglu else t
 
-        if fmt == "int4":
+        if self.offload_experts:  # the FFN weights come from the Dobu store
+            ex.format = adt
+            w_up = w_down = s_up = s_down = b_up = b_down = None
+        elif fmt == "int4":
             qu, qd = self._int4_w_up, self._int4_w_down
             ex.format = nat.INT4
             ex.group_size = qu.group_size
@@ -236,12 +285,12 @@ class SpiderMoELayer(nn.Module):
             if not swiglu:
                 b_up = f32(torch.stack([m[0].bias for m in self.experts]))
                 b_down = f32(torch.stack([m[2].bias for m in self.experts]))
-        ex.w_up, ex.w_down = w_up.data_ptr(), w_down.data_ptr()
+        ex.w_up, ex.w_down = nat.ptr(w_up), nat.ptr(w_down)
         ex.s_up, ex.s_down = nat.ptr(s_up), nat.ptr(s_down)
         ex.b_up, ex.b_down = nat.ptr(b_up), nat.ptr(b_down)
 
         def tiles(w, code=nat.BF16):  # copy in the weight tile layout (smoe_pack_weight_tiles)
-            if not self.weight_tiles or w.shape[1] % 16 or w.shape[2] % 64:
+            if w is None or not self.weight_tiles or w.shape[1] % 16 or w.shape[2] % 64:
                 return None
             if w.dtype != (torch.bfloat16 if code == nat.BF16 else torch.uint8):
                 return None
@@ -308,6 +357,8 @@ class SpiderMoELayer(nn.Module):
         n = b * t
         if num_loops == 0:  # no loop to run: h unchanged (a copy, as for any call)
             return h2.clone().view(b, t, width)
+        if self.offload_experts:
+            return self._run_offload(h2, x2, loop_begin, num_loops, gate).view(b, t, width)
         out = torch.empty_like(h2)
         k = self._pack()
         if workspace is None:
@@ -334,6 +385,72 @@ class SpiderMoELayer(nn.Module):
         self._last_n = n
         self._last_ws = ws
         return out.view(b, t, width)
+
+    def _run_offload(self, x, x0, loop_begin: int, num_loops: int, gate=None):
+        """Loops with the expert FFN from the Dobu store (model.py:294-297):
+        router top-k, edge top-m and messages, the store's sparse delta, the
+        residual / LayerNorm epilogue — the block's stage entry points,
+        which smoe_block_forward chains inside one call.  The early-exit
+        gate is applied between loops as model.py:450-473 does."""
+        self._sync_offloaded_experts()
+        k = self._pack()
+        d = k.desc
+        dev = x.device
+        lib, st = nat.lib(), nat.stream_of(dev)
+        n, hid = x.shape
+        e, kk, m = self.num_experts, self.top_k, self.edges_per_expert
+        act = d.act_dtype
+        store = self._expert_store
+        fdt = store.dtype
+        logits = torch.empty(n, e, device=dev)
+        top_w = torch.empty(n, kk, device=dev)
+        top_i = torch.empty(n, kk, dtype=torch.int32, device=dev)
+        eidx = torch.empty(n, kk, m, dtype=torch.int32, device=dev)
+        ew = torch.empty(n, kk, m, device=dev)
+        msg = torch.empty(n, hid, dtype=fdt, device=dev)
+
+        def ws(nbytes):
+            return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
+
+        w0 = ws(lib.smoe_router_workspace_bytes(n, e))
+        w1 = ws(lib.smoe_edge_topm_workspace_bytes(n, kk, e, m))
+        w2 = ws(lib.smoe_edge_message_workspace_bytes(n, hid, e, kk, m, act))
+        if gate is not None:
+            threshold, active, loops = gate
+            exit_w = self.exit_head.weight.detach()
+            exit_b = self.exit_head.bias.detach()
+        for r in range(loop_begin, loop_begin + num_loops):
+            nat.check(lib.smoe_router_topk(x.data_ptr(), act, n, hid, d.router_w,
+                                           d.loop_bias + 4 * r * e, e, kk, logits.data_ptr(),
+                                           top_w.data_ptr(), top_i.data_ptr(), w0.data_ptr(),
+                                           w0.numel(), st),
+                      "smoe_router_topk")
+            nat.check(lib.smoe_edge_topm(x.data_ptr(), act, n, hid, d.edge_gen_w, hid + d.L,
+                                         d.edge_loop_bias + 4 * r * e * e, e, kk, m,
+                                         top_i.data_ptr(), eidx.data_ptr(), ew.data_ptr(),
+                                         w1.data_ptr(), w1.numel(), st), "smoe_edge_topm")
+            nat.check(lib.smoe_edge_message(x.data_ptr(), act, n, hid, d.edge_value_w,
+                                            d.edge_value_w_tiles, e, kk, m, top_i.data_ptr(),
+                                            eidx.data_ptr(), ew.data_ptr(), msg.data_ptr(),
+                                            nat.dtype_code(fdt), w2.data_ptr(), w2.numel(), st),
+                      "smoe_edge_message")
+            delta = store.sparse_delta(msg, top_i, top_w, kk, out_dtype=torch.float32)
+            out = torch.empty_like(x)
+            nat.check(lib.smoe_combine_epilogue(x.data_ptr(), x0.data_ptr(), act,
+                                                delta.data_ptr(), nat.F32, n, hid, d.alpha,
+                                                d.beta, d.ln_w, d.ln_b, d.eps, out.data_ptr(),
+                                                st), "smoe_combine_epilogue")
+            if gate is not None:  # frozen rows keep h; a row leaves after the loop it passes
+                on = active.bool()
+                loops += on.to(torch.int32)
+                out = torch.where(on.unsqueeze(-1), out, x)
+                conf = torch.sigmoid(torch.nn.functional.linear(out, exit_w, exit_b).float())
+                active.mul_((~(conf.squeeze(-1) > threshold)).to(torch.int32))
+            x = out
+        self._last_n = n
+        self._offload_last = {"msg": msg, "logits": logits, "top_idx": top_i, "top_w": top_w,
+                              "edge_idx": eidx.view(n * kk, m), "edge_w": ew.view(n * kk, m)}
+        return x
 
     def forward(self, h, x0, loop_idx, return_stats=False):
         """One loop of the block (model.py:240-349)."""
@@ -387,7 +504,11 @@ class SpiderMoELayer(nn.Module):
 
     # ------------------------------------------------------ diagnostics ----
     def last_routing(self) -> dict:
-        """Routing of the last loop computed (copies out of the workspace)."""
+        """Routing of the last loop computed (copies out of the workspace).
+        With Dobu offload: the staged path's message, logits, top-k and
+        edges (edge rows slot for slot with top_idx)."""
+        if self.offload_experts:
+            return {name: t.clone() for name, t in self._offload_last.items()}
         k = self._pack()
         n = self._last_n
         lay = nat.SmoeWsLayout()

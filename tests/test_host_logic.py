@@ -90,7 +90,9 @@ def test_config_validation_and_unsupported_features():
     with pytest.raises(ValueError):
         ModelConfig(expert_activation="relu").validate()
     with pytest.raises(NotImplementedError):
-        SpiderMoELayer(ModelConfig(offload_experts=True))
+        SpiderMoELayer(ModelConfig(use_lumen=True))
+    with pytest.raises(ValueError):  # Dobu holds Linear + GELU + Linear experts
+        SpiderMoELayer(ModelConfig(offload_experts=True, expert_activation="swiglu"))
 
 
 def test_zipf_bias_forces_empty_experts():
