@@ -3,27 +3,28 @@ spider_infer/orbit/dobu.py:1-127) on MI355X.
 
 The expert FFN weights live in one pinned host catalogue (up [E,U,H],
 down [E,H,U] in the experts' dtype, biases fp32).  HBM holds a slab of
-S = max(top_dobu, 1) expert slots in the same layout as the resident
-block's stacked weights, so the FFN runs on the same grouped-GEMM kernels
-(smoe_expert_delta) with the slab as an S-expert weight set: routed expert
-ids are mapped to slots on the device (smoe_remap_ids), ids of experts not
-in the slab to -1.
+2 S expert slots (S = max(top_dobu, 1): the LRU's S plus S staging slots)
+in the same layout as the resident block's stacked weights, so the FFN runs
+on the same grouped-GEMM kernels (smoe_expert_delta) with the slab as a
+2S-expert weight set: routed expert ids are mapped to slots on the device
+(smoe_remap_ids), ids of experts not in the slab to -1.
 
 One step (ExpertChunkStore.sparse_delta):
   1. the experts with at least one token of positive merged weight, from
      the dispatch plan's counts (one small device->host copy, where the
      reference calls .unique().tolist());
-  2. in ascending expert order, chunks of S experts: each expert of the
-     chunk is made resident exactly as the reference's _materialise does
-     (hit: move to the LRU end; miss: load, insert at the end, evict the
-     least recently used beyond top_dobu; with top_dobu 0 every use streams
-     through a transient slot and nothing stays), a load being one
-     asynchronous pinned-host -> HBM copy per weight on the compute stream
-     into the slot its evicted predecessor held;
-  3. the chunk's FFN delta over the slab (fp32), summed over chunks.
-Stream order keeps each copy after the previous chunk's reads of its slot
-and before the current chunk's.  top_k (router width) and top_dobu
-(residency) stay independent, as there.
+  2. in ascending expert order, chunks of S experts; each expert is made
+     resident exactly as the reference's _materialise does (hit: move to
+     the LRU end; miss: load, insert at the end, evict the least recently
+     used beyond top_dobu; with top_dobu 0 every use streams and nothing
+     stays).  A miss takes the free slot freed longest ago, an eviction
+     frees its slot; with S staging slots a chunk's loads never target a
+     slot of the chunk before it;
+  3. per chunk, the loads (asynchronous pinned-host -> HBM copies on a copy
+     stream, each after the last read of its slot) overlap the previous
+     chunk's FFN; the compute stream waits for them, runs the chunk's FFN
+     delta over the slab (fp32) and adds it up.
+top_k (router width) and top_dobu (residency) stay independent, as there.
 
 The catalogue is a snapshot of the experts' weights; the layer refreshes
 it when a weight changes (the reference keeps its construction-time copy).
@@ -122,7 +123,14 @@ class ExpertChunkStore:
 
     @property
     def slots(self) -> int:
+        """Experts of one chunk (and LRU slots): max(top_dobu, 1)."""
         return max(self.max_gpu_experts, 1)
+
+    @property
+    def physical_slots(self) -> int:
+        """Slab slots: the LRU's plus as many staging slots, so a chunk's
+        loads never wait for the chunk before it (double buffering)."""
+        return 2 * self.slots
 
     def _chunk_bytes(self) -> int:
         esz = torch.tensor([], dtype=self.dtype).element_size()
@@ -133,12 +141,16 @@ class ExpertChunkStore:
         s = self._slab
         if s is not None and s["dev"] == dev:
             return s
-        n, u, h = self.slots, self.ffn, self.hidden
+        n, u, h = self.physical_slots, self.ffn, self.hidden
         s = {"dev": dev,
              "up": torch.empty(n, u, h, dtype=self.dtype, device=dev),
              "down": torch.empty(n, h, u, dtype=self.dtype, device=dev),
              "b_up": torch.empty(n, u, dtype=torch.float32, device=dev),
-             "b_down": torch.empty(n, h, dtype=torch.float32, device=dev)}
+             "b_down": torch.empty(n, h, dtype=torch.float32, device=dev),
+             # copies run on a stream of their own (default priority), so
+             # one chunk's loads overlap the previous chunk's GEMMs
+             "copy": torch.cuda.Stream(dev),
+             "read_done": [None] * n}  # per slot: event after its last read
         ex = nat.SmoeExperts()
         ex.format = nat.dtype_code(self.dtype)
         ex.act = nat.ACT_GELU
@@ -147,33 +159,30 @@ class ExpertChunkStore:
         ex.b_up, ex.b_down = s["b_up"].data_ptr(), s["b_down"].data_ptr()
         s["desc"] = ex
         self._gpu_lru.clear()  # a new slab holds nothing yet
+        self._free = list(range(n))  # slots without a hot expert, oldest freed first
         self._slab = s
         return s
 
-    def _load(self, expert_id: int, slot: int) -> None:
-        s = self._slab
-        for name in ("up", "down", "b_up", "b_down"):
-            s[name][slot].copy_(self._cat[name][expert_id], non_blocking=True)
-        self.loads += 1
-
-    def _materialise(self, expert_id: int) -> int:
-        """expert_store.py:98-112 on slab slots: returns the expert's slot."""
+    def _materialise(self, expert_id: int):
+        """expert_store.py:98-112 on slab slots: (slot, load needed).  A
+        miss takes the free slot freed longest ago; the evicted expert's
+        slot joins the free list (it may still be read by the chunk in
+        flight, which the slot's event orders)."""
         if expert_id in self._gpu_lru:
             self.hits += 1
             self._gpu_lru.move_to_end(expert_id)
-            return self._gpu_lru[expert_id]
+            return self._gpu_lru[expert_id], False
         self.misses += 1
-        if self.max_gpu_experts == 0:  # always stream: one transient slot
-            self._load(expert_id, 0)
-            return 0
-        if len(self._gpu_lru) < self.max_gpu_experts:
-            used = set(self._gpu_lru.values())
-            slot = next(i for i in range(self.slots) if i not in used)
-        else:  # the least recently used leaves; its slot takes the new expert
-            _, slot = self._gpu_lru.popitem(last=False)
-        self._load(expert_id, slot)
+        self.loads += 1
+        slot = self._free.pop(0)
+        if self.max_gpu_experts == 0:  # always stream: nothing stays hot
+            self._free.append(slot)
+            return slot, True
         self._gpu_lru[expert_id] = slot
-        return slot
+        if len(self._gpu_lru) > self.max_gpu_experts:
+            _, old = self._gpu_lru.popitem(last=False)
+            self._free.append(old)
+        return slot, True
 
     def release_gpu(self) -> None:
         """expert_store.py:114-118: drop the HBM working set."""
@@ -185,23 +194,44 @@ class ExpertChunkStore:
             torch.cuda.empty_cache()
 
     # ------------------------------------------------------------ compute ----
-    def _used_experts(self, idx: torch.Tensor, w: torch.Tensor, dev) -> list[int]:
+    def _buffers(self, n: int, k: int, width: int, dev):
+        """Per-shape device buffers (plan, ids, partial delta, workspace)."""
+        key = (n, k, width, dev)
+        b = getattr(self, "_bufs", None)
+        if b is not None and b["key"] == key:
+            return b
+        lib = nat.lib()
+        e = self.num_experts
+        need = lib.smoe_dispatch_workspace_bytes(n, k, e)
+        dneed = lib.smoe_expert_delta_workspace_bytes(ctypes.byref(self._slab["desc"]), n, k)
+        if dneed == 0:
+            raise RuntimeError("smoe_expert_delta: unsupported expert shapes "
+                               f"({lib.smoe_last_error().decode()})")
+        i32, f32 = torch.int32, torch.float32
+        nk = max(n * k, 1)
+        b = {"key": key,
+             "counts": torch.empty(e, dtype=i32, device=dev),
+             "offsets": torch.empty(e + 1, dtype=i32, device=dev),
+             "rows": torch.empty(nk, dtype=i32, device=dev),
+             "roww": torch.empty(nk, dtype=f32, device=dev),
+             "tokrow": torch.empty(nk, dtype=i32, device=dev),
+             "plan_ws": torch.empty(max(need, 1), dtype=torch.uint8, device=dev),
+             "plan_need": need,
+             "slot_ids": torch.empty(nk, dtype=i32, device=dev),
+             "part": torch.empty(n, width, dtype=f32, device=dev),
+             "ws": torch.empty(dneed, dtype=torch.uint8, device=dev), "need": dneed}
+        self._bufs = b
+        return b
+
+    def _used_experts(self, idx, w, b, dev) -> list[int]:
         """Experts with a token of positive merged weight (dispatch plan counts)."""
         n, k = idx.shape
-        e = self.num_experts
-        lib = nat.lib()
-        counts = torch.empty(e, dtype=torch.int32, device=dev)
-        offsets = torch.empty(e + 1, dtype=torch.int32, device=dev)
-        rows = torch.empty(max(n * k, 1), dtype=torch.int32, device=dev)
-        roww = torch.empty(max(n * k, 1), dtype=torch.float32, device=dev)
-        tokrow = torch.empty(max(n * k, 1), dtype=torch.int32, device=dev)
-        need = lib.smoe_dispatch_workspace_bytes(n, k, e)
-        ws = torch.empty(max(need, 1), dtype=torch.uint8, device=dev)
-        nat.check(lib.smoe_dispatch_plan(idx.data_ptr(), w.data_ptr(), n, k, e, counts.data_ptr(),
-                                         offsets.data_ptr(), rows.data_ptr(), roww.data_ptr(),
-                                         tokrow.data_ptr(), ws.data_ptr(), need,
-                                         nat.stream_of(dev)), "smoe_dispatch_plan")
-        return torch.nonzero(counts.cpu() > 0).flatten().tolist()
+        nat.check(nat.lib().smoe_dispatch_plan(
+            idx.data_ptr(), w.data_ptr(), n, k, self.num_experts, b["counts"].data_ptr(),
+            b["offsets"].data_ptr(), b["rows"].data_ptr(), b["roww"].data_ptr(),
+            b["tokrow"].data_ptr(), b["plan_ws"].data_ptr(), b["plan_need"], nat.stream_of(dev)),
+            "smoe_dispatch_plan")
+        return torch.nonzero(b["counts"].cpu() > 0).flatten().tolist()
 
     @torch.no_grad()
     def sparse_delta(self, messages: torch.Tensor, top_indices: torch.Tensor,
@@ -209,44 +239,68 @@ class ExpertChunkStore:
         """expert_store.py:121-166: delta [B,T,H] (or [N,H]) of the routed
         experts' FFNs (Linear + bias, erf GELU, Linear + bias) times their
         merged routing weights, the weights coming from the catalogue
-        through the HBM working set.  out_dtype: default messages' dtype."""
+        through the HBM working set.  out_dtype: default messages' dtype.
+
+        The host decides every chunk's slots first (the LRU bookkeeping),
+        uploads the chunks' expert -> slot maps at once, then enqueues: per
+        chunk, its loads on the copy stream (each after the last read of
+        its slot), and on the compute stream a wait for them, the id remap,
+        the grouped FFN over the slab and the add into the delta."""
         dev = nat.require_gpu(messages, top_indices, top_weights)
         self.compute_device = dev
         width = messages.shape[-1]
         if width != self.hidden:
             raise ValueError(f"messages width {width} != expert hidden size {self.hidden}")
         n = messages.numel() // width
+        total = torch.empty(n, width, dtype=torch.float32, device=dev)
+        if n == 0:
+            return total.to(out_dtype or messages.dtype).view(messages.shape)
         idx = top_indices.reshape(n, top_k).to(torch.int32).contiguous()
         w = top_weights.reshape(n, top_k).to(torch.float32).contiguous()
         msg = messages.reshape(n, width).to(self.dtype).contiguous()
-        total = torch.zeros(n, width, dtype=torch.float32, device=dev)
-        if n == 0:
-            return total.to(out_dtype or messages.dtype).view(messages.shape)
-        used = self._used_experts(idx, w, dev)
         slab = self._ensure_slab(dev)
-        lib = nat.lib()
-        stream = nat.stream_of(dev)
-        ex = slab["desc"]
-        need = lib.smoe_expert_delta_workspace_bytes(ctypes.byref(ex), n, top_k)
-        if need == 0:
-            raise RuntimeError("smoe_expert_delta: unsupported expert shapes "
-                               f"({lib.smoe_last_error().decode()})")
-        ws = torch.empty(need, dtype=torch.uint8, device=dev)
-        slot_ids = torch.empty_like(idx)
-        part = torch.empty(n, width, dtype=torch.float32, device=dev)
+        b = self._buffers(n, top_k, width, dev)
+        used = self._used_experts(idx, w, b, dev)
+        chunks = []
         for start in range(0, len(used), self.slots):
-            chunk = used[start:start + self.slots]
-            smap = [-1] * self.num_experts
-            for e in chunk:
-                smap[e] = self._materialise(e)
-            smap_d = torch.tensor(smap, dtype=torch.int32).to(dev)
-            nat.check(lib.smoe_remap_ids(idx.data_ptr(), idx.numel(), smap_d.data_ptr(),
-                                         self.num_experts, slot_ids.data_ptr(), stream),
+            chunks.append([(e, *self._materialise(e)) for e in used[start:start + self.slots]])
+        if not chunks:
+            return total.zero_().to(out_dtype or messages.dtype).view(messages.shape)
+        smap = torch.full((len(chunks), self.num_experts), -1, dtype=torch.int32)
+        for c, chunk in enumerate(chunks):
+            for e, slot, _ in chunk:
+                smap[c, e] = slot
+        smap = smap.to(dev)
+        lib = nat.lib()
+        comp = torch.cuda.current_stream(dev)
+        copy = slab["copy"]
+        st = comp.cuda_stream
+        ex = slab["desc"]
+        for c, chunk in enumerate(chunks):
+            loads = [(e, slot) for e, slot, load in chunk if load]
+            if loads:
+                with torch.cuda.stream(copy):
+                    for e, slot in loads:
+                        ev = slab["read_done"][slot]
+                        if ev is not None:
+                            copy.wait_event(ev)
+                        for name in ("up", "down", "b_up", "b_down"):
+                            slab[name][slot].copy_(self._cat[name][e], non_blocking=True)
+                comp.wait_stream(copy)
+            nat.check(lib.smoe_remap_ids(idx.data_ptr(), idx.numel(), smap[c].data_ptr(),
+                                         self.num_experts, b["slot_ids"].data_ptr(), st),
                       "smoe_remap_ids")
-            nat.check(lib.smoe_expert_delta(ctypes.byref(ex), msg.data_ptr(), slot_ids.data_ptr(),
-                                            w.data_ptr(), n, top_k, part.data_ptr(), nat.F32,
-                                            ws.data_ptr(), need, stream), "smoe_expert_delta")
-            total.add_(part)
+            out = total if c == 0 else b["part"]
+            nat.check(lib.smoe_expert_delta(ctypes.byref(ex), msg.data_ptr(),
+                                            b["slot_ids"].data_ptr(), w.data_ptr(), n, top_k,
+                                            out.data_ptr(), nat.F32, b["ws"].data_ptr(), b["need"],
+                                            st), "smoe_expert_delta")
+            if c > 0:
+                total.add_(out)
+            done = torch.cuda.Event()
+            done.record(comp)
+            for _, slot, _ in chunk:
+                slab["read_done"][slot] = done
         return total.to(out_dtype or messages.dtype).view(messages.shape)
 
     def stats(self) -> dict:
@@ -265,6 +319,8 @@ class ExpertChunkStore:
             "loads": self.loads,
             "top_dobu_lru": self.max_gpu_experts,
             "policy": "dobu_residency",
+            "slab_slots": self.physical_slots,
+            "slab_bytes": per * self.physical_slots if self._slab is not None else 0,
         }
 
 
