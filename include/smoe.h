@@ -68,7 +68,12 @@ extern "C" {
  *               [32j, 32j+32) and rows [64j+32, 64j+64) are up rows
  *               [32j, 32j+32) — so w_up is [E,2U,H] (and s_up [E,2U(,..)]).
  *               w_gate must be NULL.
- *   b_up [E,U] and b_down [E,H] are fp32 or NULL. */
+ *   b_up [E,U] and b_down [E,H] are fp32 or NULL.
+ * Shapes: 1 <= E <= 256.  f32 experts and bf16 GELU experts take any H
+ * and U (shapes off the MFMA kernels' grid run a SIMT kernel); SwiGLU,
+ * fp8 and int4 experts need H, U % 32 == 0 (SwiGLU U % 64, int4 the group
+ * size dividing both).  Within a block (smoe_block) H % 8 == 0, H <= 4096,
+ * E <= 64. */
 typedef struct smoe_experts {
   int format;      /* SMOE_F32 / SMOE_BF16 / SMOE_FP8_E4M3 / SMOE_INT4 */
   int act;         /* SMOE_ACT_GELU / SMOE_ACT_SWIGLU */
@@ -319,7 +324,7 @@ SMOE_API int smoe_select_topk(const float* logits, int N, int E, int K, int mode
  * [N_out, K] row-major (e4m3 codes for SMOE_FP8_E4M3, whose scale f32
  * [N_out] is required: a per-tensor scale is that value in every entry);
  * bias f32 [N_out] or NULL; act SMOE_LINEAR_NONE (out f32) or
- * SMOE_LINEAR_GELU (erf GELU; out f32 or bf16).  K % 32 == 0 (f32: % 16). */
+ * SMOE_LINEAR_GELU (erf GELU; out f32 or bf16).  Any K (fp8: K % 32 == 0). */
 #define SMOE_LINEAR_NONE 0
 #define SMOE_LINEAR_GELU 1
 SMOE_API int smoe_linear(const void* x, int N, int K, const void* w, int w_format,

@@ -122,14 +122,14 @@ struct Bump {
 int ffn_dtype_of(const smoe_experts& ex) { return ex.format == SMOE_F32 ? SMOE_F32 : SMOE_BF16; }
 
 int check_experts(const smoe_experts& ex, int H) {
-  if (ex.E < 1 || ex.E > 64 || ex.H != H || ex.U <= 0) return fail(SMOE_EINVAL, "expert shape");
+  if (ex.E < 1 || ex.E > 256 || ex.H != H || H <= 0 || ex.U <= 0)
+    return fail(SMOE_EINVAL, "expert shape (1 <= E <= 256)");
   if (!ex.w_up || !ex.w_down) return fail(SMOE_EINVAL, "expert weights missing");
   if (ex.w_gate) return fail(SMOE_EINVAL, "w_gate must be NULL (gate interleaved into w_up)");
   if (ex.act != SMOE_ACT_GELU && ex.act != SMOE_ACT_SWIGLU) return fail(SMOE_EINVAL, "act");
   switch (ex.format) {
     case SMOE_F32:
       if (ex.act == SMOE_ACT_SWIGLU) return fail(SMOE_EUNSUPPORTED, "SwiGLU with fp32 experts");
-      if (H % 16 || ex.U % 16) return fail(SMOE_EINVAL, "fp32 experts need H, U % 16 == 0");
       break;
     case SMOE_BF16:
       break;
@@ -146,8 +146,11 @@ int check_experts(const smoe_experts& ex, int H) {
     default:
       return fail(SMOE_EUNSUPPORTED, "expert format");
   }
-  if (ex.format != SMOE_F32) {
-    if (H % 32 || ex.U % 32) return fail(SMOE_EINVAL, "MFMA experts need H, U % 32 == 0");
+  // bf16 GELU experts take any H, U (the SIMT kernel for shapes off the
+  // MFMA grid); SwiGLU pairs and the fp8 / int4 streams need the grid
+  const bool any_shape = ex.format == SMOE_F32 || (ex.format == SMOE_BF16 && ex.act == SMOE_ACT_GELU);
+  if (!any_shape) {
+    if (H % 32 || ex.U % 32) return fail(SMOE_EINVAL, "fp8 / int4 / SwiGLU experts need H, U % 32 == 0");
     if (ex.act == SMOE_ACT_SWIGLU && ex.U % 64)
       return fail(SMOE_EINVAL, "SwiGLU needs U % 64 == 0");
   }
@@ -158,9 +161,9 @@ int check_block(const smoe_block* b) {
   if (!b) return fail(SMOE_EINVAL, "null block");
   if (b->act_dtype != SMOE_F32 && b->act_dtype != SMOE_BF16)
     return fail(SMOE_EUNSUPPORTED, "act_dtype");
-  if (b->H <= 0 || b->H % 8 || b->H > 4096) return fail(SMOE_EINVAL, "H");
-  if (b->act_dtype == SMOE_BF16 && b->H % 32) return fail(SMOE_EINVAL, "bf16 needs H % 32 == 0");
-  if (b->act_dtype == SMOE_F32 && b->H % 16) return fail(SMOE_EINVAL, "fp32 needs H % 16 == 0");
+  // H % 8: the row kernels' 8-wide vectors; GEMMs off the MFMA grid take
+  // the SIMT kernel
+  if (b->H <= 0 || b->H % 8 || b->H > 4096) return fail(SMOE_EINVAL, "H (H % 8 == 0, <= 4096)");
   if (b->E < 1 || b->E > 64) return fail(SMOE_EINVAL, "E must be in [1, 64]");
   if (b->K < 1 || b->K > b->E || b->K > 16) return fail(SMOE_EINVAL, "top_k");
   if (b->M < 1 || b->M > b->E || b->M > 16) return fail(SMOE_EINVAL, "edges_per_expert");
@@ -811,9 +814,7 @@ namespace {
 
 int check_act(int adt, int H) {
   if (adt != SMOE_F32 && adt != SMOE_BF16) return fail(SMOE_EUNSUPPORTED, "act_dtype");
-  if (H <= 0 || H % 8 || H > 4096) return fail(SMOE_EINVAL, "H");
-  if (adt == SMOE_BF16 && H % 32) return fail(SMOE_EINVAL, "bf16 needs H % 32 == 0");
-  if (adt == SMOE_F32 && H % 16) return fail(SMOE_EINVAL, "fp32 needs H % 16 == 0");
+  if (H <= 0 || H % 8 || H > 4096) return fail(SMOE_EINVAL, "H (H % 8 == 0, <= 4096)");
   return SMOE_OK;
 }
 
@@ -1020,9 +1021,8 @@ SMOE_API int smoe_linear(const void* x, int N, int K, const void* w, int w_forma
   if (out_dtype != SMOE_F32 && out_dtype != SMOE_BF16) return fail(SMOE_EUNSUPPORTED, "out dtype");
   if (act == SMOE_LINEAR_NONE && out_dtype != SMOE_F32)
     return fail(SMOE_EUNSUPPORTED, "a linear without activation writes f32");
-  if (w_format == SMOE_F32 && (K % 16 || out_dtype != SMOE_F32))
-    return fail(SMOE_EINVAL, "f32 linear: K % 16 == 0, f32 out");
-  if (w_format != SMOE_F32 && K % 32) return fail(SMOE_EINVAL, "linear: K % 32 == 0");
+  if (w_format == SMOE_F32 && out_dtype != SMOE_F32) return fail(SMOE_EINVAL, "f32 linear: f32 out");
+  if (w_format == SMOE_FP8_E4M3 && K % 32) return fail(SMOE_EINVAL, "fp8 linear: K % 32 == 0");
   if (w_format == SMOE_FP8_E4M3 && !w_scale) return fail(SMOE_EINVAL, "fp8 weights need a scale");
   if (N == 0) return SMOE_OK;
   if (!x || !w || !out) return fail(SMOE_EINVAL, "null buffer");

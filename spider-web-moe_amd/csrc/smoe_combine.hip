@@ -153,6 +153,29 @@ __global__ __launch_bounds__(256) void k_delta_combine(const void* __restrict__ 
   }
 }
 
+// The same sum for rows of any width (H not a multiple of 8, or > 4096):
+// one thread per (token, column), the token's rows in slot order.
+template <int YDT, int ODT>
+__global__ __launch_bounds__(256) void k_delta_combine_any(const void* __restrict__ y,
+                                                           const int32_t* __restrict__ tok_row,
+                                                           int N, int K, int H,
+                                                           void* __restrict__ out) {
+  const int t = blockIdx.y;
+  const int j = blockIdx.x * 256 + threadIdx.x;
+  if (j >= H) return;
+  float acc = 0.f;
+  for (int s = 0; s < K; ++s) {
+    const int r = tok_row[static_cast<int64_t>(t) * K + s];
+    if (r < 0) continue;
+    const int64_t o = static_cast<int64_t>(r) * H + j;
+    acc += YDT == SMOE_F32 ? reinterpret_cast<const float*>(y)[o]
+                           : bf2f(reinterpret_cast<const uint16_t*>(y)[o]);
+  }
+  const int64_t o = static_cast<int64_t>(t) * H + j;
+  if (ODT == SMOE_F32) reinterpret_cast<float*>(out)[o] = acc;
+  else reinterpret_cast<uint16_t*>(out)[o] = f2bf(acc);
+}
+
 namespace {
 int last_rc() { return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP; }
 }  // namespace
@@ -199,8 +222,18 @@ int launch_epilogue(const void* h, const void* x0, int adt, const void* y, int y
 
 int launch_delta_combine(const void* y, int ydt, const int32_t* tok_row, int N, int K, int H,
                          void* out, int odt, hipStream_t s) {
-  if (K < 1 || K > 64) return SMOE_EINVAL;  // one lane per entry
+  if (K < 1 || K > 64 || H < 1 || N > 65535 * 64) return SMOE_EINVAL;  // one lane per entry
   if (N <= 0) return SMOE_OK;
+  if (H % 8 || H > 4096) {
+    if (N > 65535) return SMOE_EINVAL;  // grid.y
+    return by_dt(ydt, [&](auto yd) {
+      return by_dt(odt, [&](auto od) {
+        hipLaunchKernelGGL((k_delta_combine_any<decltype(yd)::value, decltype(od)::value>),
+                           dim3((H + 255) / 256, N), dim3(256), 0, s, y, tok_row, N, K, H, out);
+        return last_rc();
+      });
+    });
+  }
   return by_cpl(H, [&](auto cpl) {
     return by_dt(ydt, [&](auto yd) {
       return by_dt(odt, [&](auto od) {

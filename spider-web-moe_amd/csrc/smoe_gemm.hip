@@ -1415,9 +1415,20 @@ __global__ __launch_bounds__(256, WGS) void k_gemm_stream(const GemmArgs p) {
   }
 }
 
-// ----------------------------------------------------------------- fp32 ----
-template <int BM, int BN, int EPI>
-__global__ __launch_bounds__(256) void k_gemm_f32(const GemmArgs p) {
+// ------------------------------------------------- fp32 / any shape ----
+// SIMT tile GEMM with fp32 FMAs: the fp32 models' path (FMT = SMOE_F32, A
+// and W fp32) and the fallback for bf16 shapes the MFMA kernels do not take
+// (K or a row pitch not a multiple of their vector width; FMT = SMOE_BF16,
+// A and W bf16).  Any K and N_out: k past K reads as 0, which leaves every
+// sum unchanged (fma(a, 0, acc) == acc).
+template <int FMT>
+__device__ __forceinline__ float elem(const void* base, int64_t i) {
+  if constexpr (FMT == SMOE_F32) return reinterpret_cast<const float*>(base)[i];
+  else return bf2f(reinterpret_cast<const uint16_t*>(base)[i]);
+}
+
+template <int BM, int BN, int EPI, int FMT>
+__global__ __launch_bounds__(256) void k_gemm_simt(const GemmArgs p) {
   constexpr int BK = 16;
   constexpr int TM = BM / 16, TN = BN / 16;
   __shared__ float sA[BK][BM + 4];
@@ -1426,8 +1437,7 @@ __global__ __launch_bounds__(256) void k_gemm_f32(const GemmArgs p) {
   if (!find_tile(p, BM, blockIdx.x, g, m0, mrows)) return;
   const int n0 = blockIdx.y * BN;
   const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
-  const float* A = reinterpret_cast<const float*>(p.A);
-  const float* W = reinterpret_cast<const float*>(p.W) + g * p.w_gstride;
+  const int64_t wbase = g * p.w_gstride;
   float acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -1437,15 +1447,17 @@ __global__ __launch_bounds__(256) void k_gemm_f32(const GemmArgs p) {
     for (int e = tid; e < BM * BK; e += 256) {
       const int r = e / BK, kk = e % BK;
       float v = 0.f;
-      if (r < mrows) {
+      if (r < mrows && k0 + kk < p.K) {
         const int ar = p.a_rows ? p.a_rows[m0 + r] : (m0 + r);
-        v = A[static_cast<int64_t>(ar) * p.lda + k0 + kk];
+        v = elem<FMT>(p.A, static_cast<int64_t>(ar) * p.lda + k0 + kk);
       }
       sA[kk][r] = v;
     }
     for (int e = tid; e < BN * BK; e += 256) {
       const int r = e / BK, kk = e % BK;
-      sB[kk][r] = (n0 + r < p.N_out) ? W[static_cast<int64_t>(n0 + r) * p.ldw + k0 + kk] : 0.f;
+      sB[kk][r] = (n0 + r < p.N_out && k0 + kk < p.K)
+                      ? elem<FMT>(p.W, wbase + static_cast<int64_t>(n0 + r) * p.ldw + k0 + kk)
+                      : 0.f;
     }
     __syncthreads();
 #pragma unroll
@@ -1468,7 +1480,7 @@ __global__ __launch_bounds__(256) void k_gemm_f32(const GemmArgs p) {
     if (lr >= mrows) continue;
 #pragma unroll
     for (int j = 0; j < TN; ++j)
-      if (n0 + tx + 16 * j < p.N_out) epi_one<EPI>(p, SMOE_F32, g, m0 + lr, n0 + tx + 16 * j, acc[i][j]);
+      if (n0 + tx + 16 * j < p.N_out) epi_one<EPI>(p, FMT, g, m0 + lr, n0 + tx + 16 * j, acc[i][j]);
   }
 }
 
@@ -1592,18 +1604,25 @@ int launch_pp(const GemmArgs& a, hipStream_t s) {
                                    : launch_pp_fmt<NS, GM, BM, false>(a, s);
 }
 
-template <int BM, int BN>
-int launch_f32_bn(const GemmArgs& a, hipStream_t s) {
+template <int BM, int BN, int FMT>
+int launch_simt_bn(const GemmArgs& a, hipStream_t s) {
   const dim3 grid(max_tiles(a, BM), (a.N_out + BN - 1) / BN);
   if (grid.x == 0) return SMOE_OK;
   switch (a.epi) {
-    case EPI_F32_BIAS: SMOE_LAUNCH((k_gemm_f32<BM, BN, EPI_F32_BIAS>), grid, dim3(256), 0, s, a); break;
-    case EPI_ROWSCALE: SMOE_LAUNCH((k_gemm_f32<BM, BN, EPI_ROWSCALE>), grid, dim3(256), 0, s, a); break;
-    case EPI_GELU: SMOE_LAUNCH((k_gemm_f32<BM, BN, EPI_GELU>), grid, dim3(256), 0, s, a); break;
-    case EPI_DOWN: SMOE_LAUNCH((k_gemm_f32<BM, BN, EPI_DOWN>), grid, dim3(256), 0, s, a); break;
-    default: return SMOE_EUNSUPPORTED;  // SwiGLU on fp32 experts is not provided
+    case EPI_F32_BIAS: SMOE_LAUNCH((k_gemm_simt<BM, BN, EPI_F32_BIAS, FMT>), grid, dim3(256), 0, s, a); break;
+    case EPI_ROWSCALE: SMOE_LAUNCH((k_gemm_simt<BM, BN, EPI_ROWSCALE, FMT>), grid, dim3(256), 0, s, a); break;
+    case EPI_GELU: SMOE_LAUNCH((k_gemm_simt<BM, BN, EPI_GELU, FMT>), grid, dim3(256), 0, s, a); break;
+    case EPI_DOWN: SMOE_LAUNCH((k_gemm_simt<BM, BN, EPI_DOWN, FMT>), grid, dim3(256), 0, s, a); break;
+    default: return SMOE_EUNSUPPORTED;  // SwiGLU pairs need the MFMA kernels' shapes
   }
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
+template <int FMT>
+int launch_simt(const GemmArgs& a, hipStream_t s) {
+  if (a.N_out <= 16) return launch_simt_bn<64, 16, FMT>(a, s);
+  if (a.N_out <= 32) return launch_simt_bn<64, 32, FMT>(a, s);
+  return launch_simt_bn<64, 64, FMT>(a, s);
 }
 
 template <int FMT, int RT, int KSPLIT, bool PK>
@@ -1829,14 +1848,17 @@ int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
   // BN: the whole N range when it is small (router / edge logits: N_out = E),
   // otherwise 128 (64 for fp32); a partial last N tile is masked.
   if (a.fmt == SMOE_F32) {
-    if (a.K % 16 || a.epi == EPI_SWIGLU) return a.epi == EPI_SWIGLU ? SMOE_EUNSUPPORTED : SMOE_EINVAL;
-    if (a.N_out <= 16) return launch_f32_bn<64, 16>(a, s);
-    if (a.N_out <= 32) return launch_f32_bn<64, 32>(a, s);
-    return launch_f32_bn<64, 64>(a, s);
+    if (a.epi == EPI_SWIGLU) return SMOE_EUNSUPPORTED;
+    return launch_simt<SMOE_F32>(a, s);
   }
   if (a.fmt == SMOE_INT4 && (a.group_size <= 0 || a.group_size % 8 || a.K % a.group_size))
     return SMOE_EINVAL;
   const int bk = (a.K % 64 == 0) ? 64 : (a.K % 32 == 0 ? 32 : 0);
+  // bf16 shapes off the MFMA kernels' grid (K not a multiple of 32, or
+  // operand rows / groups not 16-byte aligned): the SIMT kernel
+  if (a.fmt == SMOE_BF16 && a.epi != EPI_SWIGLU &&
+      (!bk || a.lda % 8 || a.ldw % 8 || a.w_gstride % 8))
+    return launch_simt<SMOE_BF16>(a, s);
   if (!bk) return SMOE_EINVAL;
   if (a.epi == EPI_SWIGLU && a.N_out % 128) return SMOE_EINVAL;
   // decode: a few rows per group, weight streaming; also narrow outputs

@@ -105,6 +105,21 @@ SMALL = [
 ]
 
 
+@pytest.mark.parametrize("dtype,hid,u", [("bf16", 40, 56), ("f32", 24, 40), ("bf16", 96, 200)])
+def test_block_off_grid_shapes(dtype, hid, u):
+    """H and U off the MFMA kernels' grid (H % 32 != 0, U % 32 != 0): the
+    GEMMs take the SIMT kernel, the row kernels their 8-wide vectors; every
+    loop teacher-forced against the oracle with the full value checks."""
+    from spider_moe_amd.workloads import make_block
+    say("off-grid block", dtype, hid, u)
+    wl = make_block("c1", tokens=200, hidden_size=hid, num_experts=6, top_k=2, edges_per_expert=2,
+                    expert_ffn_size=u, num_loops=2, expert_activation="gelu", experts=dtype,
+                    dtype=dtype, std="fan_in")
+    h = wl.h
+    for r in range(2):
+        h, _ = _check_loop(wl.layer, h, wl.x0, r, 1e-2 if dtype == "bf16" else 1e-4)
+
+
 @pytest.mark.parametrize("spec", SMALL, ids=lambda s: f"{s['act']}-{s['experts']}")
 def test_block_small_bf16_per_loop(spec):
     """Weights N(0, 1/fan_in), so the message and the expert delta move the

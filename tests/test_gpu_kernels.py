@@ -133,14 +133,39 @@ def test_sparse_expert_delta_golden_f32():
     z = np.load(os.path.join(GOLDEN, "sparse_delta.npz"))
     t = {k: torch.from_numpy(z[k]).to(dev) for k in z.files}
     e = t["w_up"].shape[0]
-    # the golden case has h=16, u=24: the fp32 path needs multiples of 16 -> pad U to 32
-    pad = 32 - t["w_up"].shape[1]
-    wu = torch.nn.functional.pad(t["w_up"], (0, 0, 0, pad))
-    bu = torch.nn.functional.pad(t["b_up"], (0, pad))
-    wd = torch.nn.functional.pad(t["w_down"], (0, pad))
-    d = sparse_expert_delta(t["msg"], t["idx"], t["w"], wu, bu, wd, t["b_down"],
-                            num_experts=e, top_k=t["idx"].shape[-1], expert_parallel=False)
+    # the reference's own case as given: H 16, U 24 (K tails of the GEMMs masked)
+    d = sparse_expert_delta(t["msg"], t["idx"], t["w"], t["w_up"], t["b_up"], t["w_down"],
+                            t["b_down"], num_experts=e, top_k=t["idx"].shape[-1],
+                            expert_parallel=False)
     torch.testing.assert_close(d.cpu(), t["delta"].cpu(), rtol=1e-5, atol=1e-5)
+    # bf16 at the same odd shape runs the SIMT GEMM (K = 16 and 24)
+    bf = torch.bfloat16
+    d16 = sparse_expert_delta(t["msg"].to(bf), t["idx"], t["w"], t["w_up"].to(bf), t["b_up"],
+                              t["w_down"].to(bf), t["b_down"], num_experts=e,
+                              top_k=t["idx"].shape[-1])
+    ref16 = _oracle_delta(t["msg"].to(bf).float().cpu().reshape(-1, 16),
+                          t["idx"].cpu().reshape(-1, 3), t["w"].cpu().reshape(-1, 3),
+                          t["w_up"].to(bf).float().cpu(), t["b_up"].cpu(),
+                          t["w_down"].to(bf).float().cpu(), t["b_down"].cpu())
+    torch.testing.assert_close(d16.float().cpu().reshape(-1, 16), ref16, rtol=2e-2, atol=2e-2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n,h,u,e,k", [(300, 40, 56, 6, 2), (77, 24, 100, 100, 3),
+                                       (500, 64, 96, 256, 4), (33, 200, 72, 13, 2)])
+def test_sparse_expert_delta_any_shape(dtype, n, h, u, e, k):
+    """H and U off the MFMA grid (K tails masked in the SIMT kernel, any
+    row width in the combine) and E up to 256, against the oracle."""
+    from spider_moe_amd import sparse_expert_delta
+    say("sparse delta any shape", dtype, n, h, u, e, k)
+    msg, idx, w, wu, bu, wd, bd = _delta_case(n, h, u, e, k, 17)
+    wu, wd = wu.to(dtype).float(), wd.to(dtype).float()
+    ref = _oracle_delta(msg.to(dtype).float(), idx, w, wu, bu, wd, bd)
+    got = sparse_expert_delta(msg.to(dev, dtype).view(1, n, h), idx.to(dev).view(1, n, k),
+                              w.to(dev).view(1, n, k), wu.to(dev, dtype), bu.to(dev),
+                              wd.to(dev, dtype), bd.to(dev), num_experts=e, top_k=k)
+    tol = 1e-5 if dtype == torch.float32 else 2e-2
+    torch.testing.assert_close(got.float().cpu().view(n, h), ref, rtol=tol, atol=tol)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
