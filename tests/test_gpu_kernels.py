@@ -416,7 +416,14 @@ def test_invalid_arguments_are_rejected():
     n8 = nat()
     say("invalid args")
     ex = n8.SmoeExperts()
-    ex.format, ex.E, ex.H, ex.U = n8.BF16, 4, 100, 64  # H not a multiple of 32
+    ex.w_up = ex.w_down = ex.s_up = ex.s_down = 256  # never dereferenced by the size query
+    ex.format, ex.E, ex.H, ex.U = n8.FP8_E4M3, 4, 100, 64  # fp8: H not a multiple of 32
+    assert n8.lib().smoe_expert_delta_workspace_bytes(ctypes.byref(ex), 10, 2) == 0
+    ex.format, ex.act = n8.BF16, n8.ACT_SWIGLU  # SwiGLU pairs need the MFMA grid too
+    assert n8.lib().smoe_expert_delta_workspace_bytes(ctypes.byref(ex), 10, 2) == 0
+    ex.act = n8.ACT_GELU  # bf16 GELU takes any H (the SIMT kernel)
+    assert n8.lib().smoe_expert_delta_workspace_bytes(ctypes.byref(ex), 10, 2) > 0
+    ex.E = 257  # E > 256
     assert n8.lib().smoe_expert_delta_workspace_bytes(ctypes.byref(ex), 10, 2) == 0
     rc = n8.lib().smoe_router_topk(None, n8.BF16, 4, 64, None, None, 4, 5, None, None, None, None,
                                    0, None)
