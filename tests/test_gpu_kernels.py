@@ -431,18 +431,19 @@ def test_invalid_arguments_are_rejected():
 
 
 @pytest.mark.parametrize("act,u,n", [("gelu", 768, 2304), ("swiglu", 768, 2304), ("gelu", 640, 2304),
+                                     ("gelu", 768, 4096), ("swiglu", 768, 4096),
                                      ("swiglu", 704, 2304), ("gelu", 768, 1536), ("swiglu", 768, 1536),
                                      ("gelu", 1024, 1100), ("gelu", 768, 1200), ("swiglu", 768, 1200)])
 def test_large_bf16_experts_ragged_groups(act, u, n):
     """Shapes that take the large-tile LDS-DMA paths (> 128 rows per expert
     on average) with skewed routing: empty experts, single-row experts and
-    experts spanning several tiles.  With n = 2304 (576 rows per expert on
-    average) up N_out 768 / 1536 and down N_out 512 (multiples of 256) take
-    the 8-wave ping-pong kernel with 256-row tiles, up N_out 640 / 1408 (odd
-    multiples of 128) the 256 x 128 ring kernel.  With n = 1536 / 1100 (384 /
-    275 rows per expert; groups of 0, 1, ~100-400 and ~1000 rows) the
-    ping-pong kernel takes 128-row tiles, with n = 1200 (300 rows per expert)
-    its 320-row tiles."""
+    experts spanning several tiles.  With n = 2304 / 4096 (576 / 1024 rows
+    per expert on average) up N_out 768 / 1536 and down N_out 512 (multiples
+    of 256) take the 8-wave ping-pong kernel with 256- / 320-row tiles, up
+    N_out 640 / 1408 (odd multiples of 128) the 256 x 128 ring kernel.  With
+    n = 1536 / 1100 (384 / 275 rows per expert; groups of 0, 1, ~100-400 and
+    ~1000 rows) the ping-pong kernel takes 128-row tiles, with n = 1200 (300
+    rows per expert) its 320-row tiles."""
     from spider_moe_amd.quant import interleave_gate_up
     n8 = nat()
     say("large bf16 experts", act, u, n)
