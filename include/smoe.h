@@ -146,7 +146,10 @@ typedef struct smoe_ws_layout {
   size_t d_tokrow;  /* i32 [N,S]                                                 */
   size_t proj;      /* act  [N*S,H]   c * W_edge[d] h per destination row         */
   size_t msg;       /* ffn  [N,H]     messages                                    */
-  size_t act;       /* ffn  [N*K,U]   expert hidden activations                   */
+  size_t act;       /* ffn  [N*K,U]   expert hidden activations (row-major, or in   */
+                    /* 16-row bands of 1 KB lane-ordered 16x32 blocks, the weight */
+                    /* tile layout, between the large-tile GEMMs; N*K rounded up  */
+                    /* to 16 rows)                                                */
   size_t y;         /* ffn  [N*K,H]   weighted expert outputs                     */
   size_t h_tmp;     /* act  [N,H]     loop ping-pong buffer                       */
   size_t scratch;   /* plan scratch                                               */

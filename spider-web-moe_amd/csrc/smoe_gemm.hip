@@ -289,10 +289,71 @@ __device__ __forceinline__ int count_m_tiles(const GemmArgs& p) {
   return count_tiles(p, BM);
 }
 
+// Row tiles on 16-row bands (an operand or the output in the row-tile
+// layout): group g's tiles start at its first row rounded down to a multiple
+// of 16, BM rows apart; a tile's live rows are the group's, [rlo, rhi) in
+// tile rows.  A band shared by two groups is computed by a tile of each, and
+// each stores only its own rows.
+__device__ __forceinline__ void band_chunk(const GemmArgs& p, int BM, int b, int& lo, int& hi,
+                                           int& t) {
+  const int i = b + static_cast<int>(threadIdx.x & 63);
+  const int ic = i < p.G ? i : p.G - 1;
+  lo = p.grp_off[ic];
+  hi = p.grp_off[ic + 1];
+  t = (i < p.G && hi > lo) ? (hi - (lo & ~15) + BM - 1) / BM : 0;
+}
+
+__device__ __forceinline__ int count_band_tiles(const GemmArgs& p, int BM) {
+  if (p.G == 0) return (p.single_rows + BM - 1) / BM;
+  int total = 0;
+  for (int b = 0; b < p.G; b += 64) {
+    int lo, hi, t;
+    band_chunk(p, BM, b, lo, hi, t);
+    total += __builtin_amdgcn_readlane(wave_incl_scan(t), 63);
+  }
+  return total;
+}
+
+__device__ __forceinline__ bool find_band_tile(const GemmArgs& p, int BM, int tile, int& g, int& m0,
+                                               int& rlo, int& rhi) {
+  if (p.G == 0) {
+    int mrows;
+    if (!find_tile(p, BM, tile, g, m0, mrows)) return false;
+    rlo = 0;
+    rhi = mrows;
+    return true;
+  }
+  int acc = 0;
+  for (int b = 0; b < p.G; b += 64) {
+    int lo, hi, t;
+    band_chunk(p, BM, b, lo, hi, t);
+    const int incl = wave_incl_scan(t) + acc;
+    const uint64_t m = __ballot(tile < incl);
+    if (m) {
+      const int f = __builtin_ctzll(m);
+      g = b + f;
+      const int excl = __builtin_amdgcn_readlane(incl - t, f);
+      const int glo = __builtin_amdgcn_readlane(lo, f), ghi = __builtin_amdgcn_readlane(hi, f);
+      m0 = (glo & ~15) + (tile - excl) * BM;
+      rlo = max(glo - m0, 0);
+      rhi = min(ghi - m0, BM);
+      return true;
+    }
+    acc = __builtin_amdgcn_readlane(incl, 63);
+  }
+  return false;
+}
+
+__device__ __forceinline__ bool row_tiles(const GemmArgs& p) { return p.At != nullptr || p.out_tiles; }
+
+// The tile of this workgroup: group, first row m0, live rows [rlo, rhi) in
+// tile rows (rlo > 0 only for band-aligned tiles), first output channel.
 template <int BM, int BN, int GM>
-__device__ __forceinline__ bool big_tile(const GemmArgs& p, int& g, int& m0, int& mrows, int& n0) {
+__device__ __forceinline__ bool big_tile(const GemmArgs& p, int& g, int& m0, int& rlo, int& rhi,
+                                         int& n0) {
+  const bool bands = row_tiles(p);
   const int tn_count = (p.N_out + BN - 1) / BN;
-  const int tm_count = count_m_tiles<BM>(p);
+  const int tm_count = bands ? count_band_tiles(p, BM) : count_m_tiles<BM>(p);
   const int T = tm_count * tn_count;
   const int bid = blockIdx.x;
   if (bid >= T) return false;
@@ -305,7 +366,12 @@ __device__ __forceinline__ bool big_tile(const GemmArgs& p, int& g, int& m0, int
   const int in = logical - grp * GM * tn_count;
   const int tm = first_m + in % gsize;
   n0 = (in / gsize) * BN;
-  return find_tile(p, BM, tm, g, m0, mrows);
+  if (bands) return find_band_tile(p, BM, tm, g, m0, rlo, rhi);
+  int mrows;
+  if (!find_tile(p, BM, tm, g, m0, mrows)) return false;
+  rlo = 0;
+  rhi = mrows;
+  return true;
 }
 
 template <int EPI>
@@ -335,13 +401,16 @@ __device__ __forceinline__ void store4(const GemmArgs& p, int fmt, int g, int ro
 // in the (idle) LDS ring, then coalesced 16-byte row stores.  Staging
 // layout: row r, 16-byte chunk c at chunk c ^ (r & 15) (rows of OW bf16, no
 // padding; r & 7 for 8-chunk rows).  The caller has synchronised the
-// workgroup after its last read of the ring.  16-row tiles past the last
-// row are skipped.  With PASSES = 2 (a tile larger than the ring) the wave
-// rows wm = 0, 1 stage and store their TM rows one after the other.
+// workgroup after its last read of the ring.  Only the live rows [rlo, rhi)
+// are stored, and 16-row strips without any are skipped.  With PASSES = 2
+// (a tile larger than the ring) the wave rows wm = 0, 1 stage and store
+// their TM rows one after the other.  With p.out_tiles the stores follow the
+// row-tile layout (m0 a multiple of 16): 64 consecutive threads write one
+// 1 KB block (16 rows x 32 columns).
 template <int BM, int BN, int TM, int TN, int NT, int EPI, int PASSES = 1>
 __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const f32x4 (&acc)[TN / 16][TM / 16],
-                                              int g, int m0, int mrows, int n0, int wm, int wn,
-                                              uint8_t* ring) {
+                                              int g, int m0, int rlo, int rhi, int n0, int wm,
+                                              int wn, uint8_t* ring) {
   static_assert(PASSES == 1 || PASSES == 2, "staging passes");
   constexpr int FM = TM / 16, FN = TN / 16;
   constexpr int OW = (EPI == EPI_SWIGLU) ? BN / 2 : BN;  // output columns of the tile
@@ -381,7 +450,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const f32x4 (&a
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
       const int lr = wm * TM + i * 16 + fr;
-      rsv[i] = lr < mrows ? p.row_scale[m0 + lr] : 0.f;
+      rsv[i] = lr >= rlo && lr < rhi ? p.row_scale[m0 + lr] : 0.f;
     }
   }
 #pragma unroll 1
@@ -391,7 +460,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const f32x4 (&a
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int tr0 = wm * TM + i * 16;
-    if (tr0 >= mrows) continue;  // wave-uniform
+    if (tr0 >= rhi || tr0 + 16 <= rlo) continue;  // wave-uniform
     const int sr = tr0 + fr - srow0;  // staging row
     float rs = 0.f;
     if constexpr (HAS_RS) rs = rsv[i];
@@ -421,6 +490,22 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const f32x4 (&a
   }
   }
   __syncthreads();
+  if (p.out_tiles) {
+    constexpr int KB = OW / 32;  // 32-column blocks per tile row band
+    const int ldb = p.ldo >> 5;  // blocks per band of the whole output
+    for (int q = tid; q < SROWS / 16 * KB * 64; q += NT) {
+      const int blk = q >> 6, l = q & 63;
+      const int sr = (blk / KB) * 16 + (l & 15), cc = (blk % KB) * 32 + (l >> 4) * 8;
+      const int r = srow0 + sr;
+      if (r >= rlo && r < rhi && ncol0 + cc < ncols)
+        __builtin_nontemporal_store(
+            *reinterpret_cast<const u32x4*>(stg_at(sr, cc)),
+            reinterpret_cast<u32x4*>(out + ((static_cast<int64_t>((m0 + r) >> 4) * ldb +
+                                             ((ncol0 + cc) >> 5)) << 9) + 8 * l));
+    }
+    if (ps + 1 < PASSES) __syncthreads();
+    continue;
+  }
   for (int q = tid; q < SROWS * CPR_OUT; q += NT) {
     const int sr = q / CPR_OUT, cc = (q % CPR_OUT) * 8;
     const int r = srow0 + sr;
@@ -428,7 +513,7 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const f32x4 (&a
     // the burst streams past the caches (the next kernel reads it once).
     // With the epilogue loads hoisted: C1's up GEMM 2.20 -> 2.15 ms per
     // step, C3's step 3.66 -> 3.49 ms.
-    if (r < mrows && ncol0 + cc < ncols)
+    if (r >= rlo && r < rhi && ncol0 + cc < ncols)
       __builtin_nontemporal_store(
           *reinterpret_cast<const u32x4*>(stg_at(sr, cc)),
           reinterpret_cast<u32x4*>(out + static_cast<int64_t>(m0 + r) * p.ldo + ncol0 + cc));
@@ -484,8 +569,8 @@ __global__ __launch_bounds__(256, NS <= 3 ? 2 : 1) void k_gemm_ring(const GemmAr
                 "output staging fits in the ring");
   __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE];
 
-  int g, m0, mrows, n0;
-  if (!big_tile<BM, BN, GM>(p, g, m0, mrows, n0)) return;
+  int g, m0, rlo, mrows, n0;  // never given row tiles: rlo = 0
+  if (!big_tile<BM, BN, GM>(p, g, m0, rlo, mrows, n0)) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
@@ -590,7 +675,7 @@ __global__ __launch_bounds__(256, NS <= 3 ? 2 : 1) void k_gemm_ring(const GemmAr
   }
 
   __syncthreads();  // every wave is done with the ring (no DMA is outstanding here)
-  tile_epilogue<BM, BN, TM, TN, 256, EPI>(p, acc, g, m0, mrows, n0, wm, wn, ring);
+  tile_epilogue<BM, BN, TM, TN, 256, EPI>(p, acc, g, m0, 0, mrows, n0, wm, wn, ring);
 }
 
 // --------------------------------------------- MFMA, ping-pong 8 waves ----
@@ -638,8 +723,8 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
   static_assert(OUT_BYTES <= 2 * NS * STAGE, "output staging fits in the ring in two passes");
   __shared__ __attribute__((aligned(1024))) uint8_t ring[RING];
 
-  int g, m0, mrows, n0;
-  if (!big_tile<BM, BN, GM>(p, g, m0, mrows, n0)) return;  // workgroup-uniform
+  int g, m0, rlo, rhi, n0;
+  if (!big_tile<BM, BN, GM>(p, g, m0, rlo, rhi, n0)) return;  // workgroup-uniform
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int grp = wave >> 2;
   const int wm = grp, wn = wave & 3;
@@ -655,8 +740,11 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
     }
   };
 
-  // DMA sources: instruction j of wave w covers rows 16 (8 j + w) ..
+  // DMA sources: instruction j of wave w covers rows 16 (8 j + w) ..; with
+  // At, the 1 KB row-tile block of that band (bands past the buffer's last
+  // read its last band: never stored), the next one each K step
   const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A);
+  const int a_step = p.At ? 512 : 32;  // elements per K step
   const uint16_t* W = reinterpret_cast<const uint16_t*>(p.W) + g * p.w_gstride;
   const uint16_t* asrc[A_LD];
   const uint16_t* bsrc[B_LD];
@@ -665,9 +753,15 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
 #pragma unroll
     for (int j = 0; j < A_LD; ++j) {
       const int r = min(8 * j + wave, A_INS - 1) * 16 + pr;  // past A_INS: never issued
-      const int rr = r < mrows ? r : 0;  // rows past the group end: valid data, never stored
-      const int ar = p.a_rows ? p.a_rows[m0 + rr] : (m0 + rr);
-      asrc[j] = A + static_cast<int64_t>(ar) * p.lda + ((pc ^ ((r >> 1) & 3)) << 3);
+      if (p.At) {
+        const int band = min((m0 >> 4) + min(8 * j + wave, A_INS - 1), ((p.max_rows + 15) >> 4) - 1);
+        asrc[j] = reinterpret_cast<const uint16_t*>(p.At) +
+                  (static_cast<int64_t>(band) * (p.K >> 5)) * 512 + 8 * lane;
+      } else {
+        const int rr = r < rhi ? r : rlo;  // rows past the group end: valid data, never stored
+        const int ar = p.a_rows ? p.a_rows[m0 + rr] : (m0 + rr);
+        asrc[j] = A + static_cast<int64_t>(ar) * p.lda + ((pc ^ ((r >> 1) & 3)) << 3);
+      }
     }
 #pragma unroll
     for (int j = 0; j < B_LD; ++j) {
@@ -688,7 +782,7 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
 #pragma unroll
     for (int j = 0; j < A_LD; ++j)
       if (j + 1 < A_LD || a_hi)  // wave-uniform
-        __builtin_amdgcn_global_load_lds((gbl_vptr)(asrc[j] + k0),
+        __builtin_amdgcn_global_load_lds((gbl_vptr)(asrc[j] + stage * a_step),
                                          (lds_vptr)(base + (8 * j + wave) * 1024), 16, 0, 0);
 #pragma unroll
     for (int j = 0; j < B_LD; ++j)  // tile layout: each stage's block is the next 1 KB (512 elements)
@@ -696,6 +790,9 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
                                        (lds_vptr)(base + A_BYTES + (8 * j + wave) * 1024), 16, 0, 0);
   };
   const int fr = lane & 15, fc = lane >> 4;
+  // the lane's A fragment of strip i at a_lds + 1024 i: the swizzled 64-byte
+  // rows, or the row-tile block's lane-ordered fragments
+  const int a_lds = p.At ? wm * TM * 64 + 16 * lane : swz32(wm * TM + fr, fc);
   bf16x8 wf[FN], af[FM];
   auto read_frags = [&](int stage) {
     const uint8_t* sa = ring + (stage % NS) * STAGE;
@@ -706,7 +803,7 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
           sb + (PK ? (wn * TN / 16 + j) * 1024 + 16 * lane : swz32(wn * TN + j * 16 + fr, fc)));
 #pragma unroll
     for (int i = 0; i < FM; ++i)
-      af[i] = *reinterpret_cast<const bf16x8*>(sa + swz32(wm * TM + i * 16 + fr, fc));
+      af[i] = *reinterpret_cast<const bf16x8*>(sa + a_lds + 1024 * i);
   };
 
   f32x4 acc[FN][FM];
@@ -743,7 +840,7 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
     if (grp == 0 || k + 1 < KT) __builtin_amdgcn_s_barrier();
   }
   __syncthreads();  // every wave is done with the ring (no DMA is outstanding here)
-  tile_epilogue<BM, BN, TM, TN, 512, EPI, PASSES>(p, acc, g, m0, mrows, n0, wm, wn, ring);
+  tile_epilogue<BM, BN, TM, TN, 512, EPI, PASSES>(p, acc, g, m0, rlo, rhi, n0, wm, wn, ring);
 }
 
 // --------------------------------------------------------------- skinny ----
@@ -1552,7 +1649,9 @@ namespace {
 
 int max_tiles(const GemmArgs& a, int BM) {
   if (a.G == 0) return (a.single_rows + BM - 1) / BM;
-  return (a.max_rows + BM - 1) / BM + a.G;
+  // band-aligned tiles start up to 15 rows before their group
+  const int pad = (a.At || a.out_tiles) ? 15 * a.G : 0;
+  return (a.max_rows + pad + BM - 1) / BM + a.G;
 }
 
 template <int BM, int BN, int BK, int WM, int WN, int FMT>
@@ -1866,11 +1965,20 @@ bool pp_rows_320(const GemmArgs& a, int rpg) {
   return 115 * rounds(320) < 100 * rounds(256);
 }
 
+bool gemm_takes_row_tiles(const GemmArgs& a) {
+  if (a.W2 || a.fmt != SMOE_BF16 || a.out_dtype != SMOE_BF16 || a.epi == EPI_F32_BIAS) return false;
+  if (a.K % 64 || a.ldw % 8 || a.lda % 8 || a.ldo % 32 || a.w_gstride % 8 || a.N_out % 256)
+    return false;
+  return (a.G == 0 ? a.single_rows : a.max_rows / a.G) >= 256;
+}
+
 int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
   if (a.N_out <= 0 || a.K <= 0) return SMOE_EINVAL;
   if (a.W2) return SMOE_EINVAL;  // two weight segments: launch_front_gemm
   // pointers every launched workgroup dereferences
-  if (!a.A || !a.W || !a.out || (a.G > 0 && !a.grp_off)) return SMOE_EINVAL;
+  if (!(a.A || a.At) || !a.W || !a.out || (a.G > 0 && !a.grp_off)) return SMOE_EINVAL;
+  // row-tile operands / outputs: only the ping-pong kernels below read them
+  if ((a.At || a.out_tiles) && !gemm_takes_row_tiles(a)) return SMOE_EINVAL;
   if ((a.epi == EPI_ROWSCALE || a.epi == EPI_DOWN) && !a.row_scale) return SMOE_EINVAL;
   if ((a.fmt == SMOE_FP8_E4M3 || a.fmt == SMOE_INT4) && !a.S) return SMOE_EINVAL;
   // BN: the whole N range when it is small (router / edge logits: N_out = E),

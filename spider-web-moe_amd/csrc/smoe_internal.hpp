@@ -55,6 +55,14 @@ struct GemmArgs {
   int G = 0;
   int single_rows = 0;
   int max_rows = 0;              // worst-case total rows (grid sizing)
+  // The row-tile layout over plan rows (that of the weight tiles: 16 rows x
+  // 32 k = 1 KB of lane-ordered MFMA fragments, blocks of one 16-row band
+  // consecutive in k; plan row p sits in band p / 16): At, when set, is A in
+  // it (K columns; rows = plan rows, a_rows / lda unused), and out_tiles = 1
+  // writes out in it (ldo columns).  Only the ping-pong kernels take these
+  // (gemm_takes_row_tiles); their row tiles then start on 16-row bands.
+  const void* At = nullptr;
+  int out_tiles = 0;
   void* out = nullptr;
   int ldo = 0;
   int out_dtype = SMOE_F32;      // SMOE_F32 / SMOE_BF16
@@ -70,6 +78,11 @@ struct GemmArgs {
 };
 
 int launch_grouped_gemm(const GemmArgs& a, hipStream_t s);
+// true when launch_grouped_gemm runs `a` on a ping-pong kernel, which reads
+// At and writes out_tiles (the fields themselves are ignored here)
+bool gemm_takes_row_tiles(const GemmArgs& a);
+// elements of a plan-row tile buffer of `rows` rows x `cols` columns
+inline int64_t row_tile_elems(int64_t rows, int64_t cols) { return (rows + 15) / 16 * 16 * cols; }
 // bf16 / fp8 w [G,N,K] -> the weight tile layout (smoe_pack_weight_tiles)
 int launch_pack_weight_tiles(const void* w, int fmt, int G, int N, int K, void* out, hipStream_t s);
 // One bf16 GEMM over a few rows (G == 0, single_rows <= 64) with f32 logits
