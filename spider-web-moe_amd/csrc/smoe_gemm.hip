@@ -346,16 +346,17 @@ __device__ __forceinline__ bool find_band_tile(const GemmArgs& p, int BM, int ti
 
 __device__ __forceinline__ bool row_tiles(const GemmArgs& p) { return p.At != nullptr || p.out_tiles; }
 
-// The tile of this workgroup: group, first row m0, live rows [rlo, rhi) in
-// tile rows (rlo > 0 only for band-aligned tiles), first output channel.
+// The tile of workgroup bid: group, first row m0, live rows
+// [rlo, rhi) in tile rows (rlo > 0 only for band-aligned tiles), first
+// output channel.  Workgroup ids are dealt to the 8 XCDs round robin
+// (bid & 7 is the XCD).
 template <int BM, int BN, int GM>
-__device__ __forceinline__ bool big_tile(const GemmArgs& p, int& g, int& m0, int& rlo, int& rhi,
-                                         int& n0) {
+__device__ __forceinline__ bool big_tile(const GemmArgs& p, int bid, int& g, int& m0, int& rlo,
+                                         int& rhi, int& n0) {
   const bool bands = row_tiles(p);
   const int tn_count = (p.N_out + BN - 1) / BN;
   const int tm_count = bands ? count_band_tiles(p, BM) : count_m_tiles<BM>(p);
   const int T = tm_count * tn_count;
-  const int bid = blockIdx.x;
   if (bid >= T) return false;
   const int x = bid & 7, local = bid >> 3;
   const int base = T >> 3, rem = T & 7;
@@ -398,127 +399,141 @@ __device__ __forceinline__ void store4(const GemmArgs& p, int fmt, int g, int ro
 }
 
 // Epilogue of an LDS-staged tile: math in registers, the bf16 tile staged
-// in the (idle) LDS ring, then coalesced 16-byte row stores.  Staging
-// layout: row r, 16-byte chunk c at chunk c ^ (r & 15) (rows of OW bf16, no
-// padding; r & 7 for 8-chunk rows).  The caller has synchronised the
-// workgroup after its last read of the ring.  Only the live rows [rlo, rhi)
-// are stored, and 16-row strips without any are skipped.  With PASSES = 2
-// (a tile larger than the ring) the wave rows wm = 0, 1 stage and store
-// their TM rows one after the other.  With p.out_tiles the stores follow the
-// row-tile layout (m0 a multiple of 16): 64 consecutive threads write one
-// 1 KB block (16 rows x 32 columns).
-template <int BM, int BN, int TM, int TN, int NT, int EPI, int PASSES = 1>
+// in the (idle) LDS ring, then coalesced 16-byte stores.  Staging layout:
+// row r, 16-byte chunk c at chunk c ^ (r & 15) (rows of OW bf16, no padding;
+// r & 7 for 8-chunk rows).  Only the live rows [rlo, rhi) are stored, and
+// 16-row strips without any are skipped.  With p.out_tiles the stores follow
+// the row-tile layout (m0 a multiple of 16): 64 consecutive threads write
+// one 1 KB block (16 rows x 32 columns).
+//
+// The lane's bias values (4 channels of each fragment column; SwiGLU: of its
+// up columns) and the row scales of its strips are loaded before any math
+// (one memory round trip for the whole epilogue).  The costly activations
+// (SwiGLU; GELU of small wave tiles) are computed into packed registers
+// before the workgroup barrier that frees the ring (the caller need not
+// synchronise), so one wave row's math overlaps the other's last MFMAs; the
+// others are computed as they are staged (a packed tile of 4 channels per
+// fragment column would not fit beside the accumulators).
+// Without a bias (the SwiGLU experts) its loads and adds are compiled out.
+template <int BM, int BN, int TM, int TN, int NT, int EPI>
 __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const f32x4 (&acc)[TN / 16][TM / 16],
                                               int g, int m0, int rlo, int rhi, int n0, int wm,
                                               int wn, uint8_t* ring) {
-  static_assert(PASSES == 1 || PASSES == 2, "staging passes");
   constexpr int FM = TM / 16, FN = TN / 16;
   constexpr int OW = (EPI == EPI_SWIGLU) ? BN / 2 : BN;  // output columns of the tile
   constexpr int SWM = (OW / 8 >= 16 ? 16 : OW / 8) - 1;  // chunk swizzle mask
-  constexpr int SROWS = PASSES == 1 ? BM : TM;            // rows staged per pass
+  constexpr bool HAS_BIAS = EPI != EPI_ROWSCALE;
+  constexpr bool HAS_RS = EPI == EPI_ROWSCALE || EPI == EPI_DOWN;
+  constexpr int NJ = (EPI == EPI_SWIGLU) ? FN / 2 : FN;  // output fragment columns
+  constexpr bool EARLY = EPI == EPI_SWIGLU || (EPI == EPI_GELU && FM * NJ <= 16);
   const int tid = threadIdx.x, lane = tid & 63;
   const int fr = lane & 15, fc = lane >> 4;
   uint16_t* stg = reinterpret_cast<uint16_t*>(ring);
   auto stg_at = [&](int r, int col) {  // staging row r, col: multiple of 4
     return stg + r * OW + ((((col >> 3) ^ (r & SWM)) << 3) | (col & 7));
   };
-  constexpr int CPR_OUT = OW / 8;  // 16-byte chunks per output row
   const int ncol0 = (EPI == EPI_SWIGLU) ? (n0 >> 1) : n0;
   const int ncols = (EPI == EPI_SWIGLU) ? (p.N_out >> 1) : p.N_out;  // a last tile may be partial
-  uint16_t* out = reinterpret_cast<uint16_t*>(p.out);
-  // The lane's bias values (4 channels of each fragment column; SwiGLU: of
-  // its up columns) and the row scales of its FM rows, all loaded before
-  // any math: one memory round trip for the whole epilogue, not one per
-  // 16-row strip.
-  constexpr bool HAS_BIAS = EPI != EPI_ROWSCALE;
-  constexpr bool HAS_RS = EPI == EPI_ROWSCALE || EPI == EPI_DOWN;
-  constexpr int NB = HAS_BIAS ? ((EPI == EPI_SWIGLU) ? FN / 2 : FN) : 1;
-  float bq[NB][4];
-  float rsv[HAS_RS ? FM : 1];
-  if constexpr (HAS_BIAS) {
+  auto live = [&](int i) {  // strip i holds a live row (wave-uniform)
+    const int tr0 = wm * TM + i * 16;
+    return tr0 < rhi && tr0 + 16 > rlo;
+  };
+  auto body = [&](auto with_bias) {
+    constexpr bool WB = HAS_BIAS && decltype(with_bias)::value;
+    float bq[WB ? NJ : 1][4];
+    float rsv[HAS_RS ? FM : 1];
+    if constexpr (WB) {
 #pragma unroll
-    for (int j = 0, b = 0; j < FN; ++j) {
-      if (EPI == EPI_SWIGLU && (j & 3) >= 2) continue;
-      const int cl = wn * TN + j * 16 + fc * 4;
-      const int c = (EPI == EPI_SWIGLU) ? (n0 >> 1) + (cl >> 6) * 32 + (cl & 31) : n0 + cl;
+      for (int j = 0, b = 0; j < FN; ++j) {
+        if (EPI == EPI_SWIGLU && (j & 3) >= 2) continue;
+        const int cl = wn * TN + j * 16 + fc * 4;
+        const int c = (EPI == EPI_SWIGLU) ? (n0 >> 1) + (cl >> 6) * 32 + (cl & 31) : n0 + cl;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) bq[b][q] = c + q < ncols ? bias_at(p, g, c + q) : 0.f;
-      ++b;
+        for (int q = 0; q < 4; ++q) bq[b][q] = c + q < ncols ? bias_at(p, g, c + q) : 0.f;
+        ++b;
+      }
     }
-  }
-  if constexpr (HAS_RS) {
+    if constexpr (HAS_RS) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int lr = wm * TM + i * 16 + fr;
+        rsv[i] = lr >= rlo && lr < rhi ? p.row_scale[m0 + lr] : 0.f;
+      }
+    }
+    // the packed outputs of strip i, fragment column j (bias slot b)
+    auto value = [&](int i, int j, int b) {
+      float r[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        if constexpr (EPI == EPI_SWIGLU) {
+          const float up = acc[j + 2][i][q];
+          r[q] = silu(acc[j][i][q]) * (WB ? up + bq[WB ? b : 0][q] : up);
+        } else {
+          const float a = WB ? acc[j][i][q] + bq[WB ? b : 0][q] : acc[j][i][q];
+          if constexpr (HAS_RS) r[q] = a * rsv[HAS_RS ? i : 0];
+          else if constexpr (EPI == EPI_GELU) r[q] = gelu_erf(a);
+          else r[q] = a;
+        }
+      }
+      return u32x2{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3])};
+    };
+    u32x2 pk[EARLY ? FM : 1][NJ];
+    if constexpr (EARLY) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        if (!live(i)) continue;
+#pragma unroll
+        for (int j = 0, b = 0; j < FN; ++j) {
+          if (EPI == EPI_SWIGLU && (j & 3) >= 2) continue;
+          pk[i][b] = value(i, j, b);
+          ++b;
+        }
+      }
+    }
+    __syncthreads();  // every wave is done with the ring: it becomes the staging buffer
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
-      const int lr = wm * TM + i * 16 + fr;
-      rsv[i] = lr >= rlo && lr < rhi ? p.row_scale[m0 + lr] : 0.f;
-    }
-  }
-#pragma unroll 1
-  for (int ps = 0; ps < PASSES; ++ps) {
-  const int srow0 = PASSES == 1 ? 0 : ps * TM;  // first tile row of this pass
-  if (PASSES == 1 || wm == ps) {
+      if (!live(i)) continue;
+      const int sr = wm * TM + i * 16 + fr;  // staging row = tile row
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int tr0 = wm * TM + i * 16;
-    if (tr0 >= rhi || tr0 + 16 <= rlo) continue;  // wave-uniform
-    const int sr = tr0 + fr - srow0;  // staging row
-    float rs = 0.f;
-    if constexpr (HAS_RS) rs = rsv[i];
-#pragma unroll
-    for (int j = 0, b = 0; j < FN; ++j) {
-      const int cl = wn * TN + j * 16 + fc * 4;  // channel within the tile
-      float r[4];
-      if constexpr (EPI == EPI_SWIGLU) {
-        if ((j & 3) >= 2) continue;
-        const int ul = (cl >> 6) * 32 + (cl & 31);
-#pragma unroll
-        for (int q = 0; q < 4; ++q) r[q] = silu(acc[j][i][q]) * (acc[j + 2][i][q] + bq[b][q]);
-        *reinterpret_cast<u32x2*>(stg_at(sr, ul)) = u32x2{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3])};
-      } else {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float a = acc[j][i][q];
-          if constexpr (EPI == EPI_ROWSCALE) r[q] = a * rs;
-          else if constexpr (EPI == EPI_GELU) r[q] = gelu_erf(a + bq[b][q]);
-          else if constexpr (EPI == EPI_DOWN) r[q] = (a + bq[b][q]) * rs;
-          else r[q] = a + bq[b][q];
-        }
-        *reinterpret_cast<u32x2*>(stg_at(sr, cl)) = u32x2{pack_bf2(r[0], r[1]), pack_bf2(r[2], r[3])};
+      for (int j = 0, b = 0; j < FN; ++j) {
+        if (EPI == EPI_SWIGLU && (j & 3) >= 2) continue;
+        const int cl = wn * TN + j * 16 + fc * 4;  // channel within the tile
+        const int col = (EPI == EPI_SWIGLU) ? (cl >> 6) * 32 + (cl & 31) : cl;
+        *reinterpret_cast<u32x2*>(stg_at(sr, col)) = EARLY ? pk[EARLY ? i : 0][b] : value(i, j, b);
+        ++b;
       }
-      ++b;
     }
-  }
-  }
+  };
+  if (!HAS_BIAS || p.bias) body(std::true_type{});
+  else body(std::false_type{});
   __syncthreads();
+  uint16_t* out = reinterpret_cast<uint16_t*>(p.out);
   if (p.out_tiles) {
     constexpr int KB = OW / 32;  // 32-column blocks per tile row band
     const int ldb = p.ldo >> 5;  // blocks per band of the whole output
-    for (int q = tid; q < SROWS / 16 * KB * 64; q += NT) {
+    for (int q = tid; q < BM / 16 * KB * 64; q += NT) {
       const int blk = q >> 6, l = q & 63;
-      const int sr = (blk / KB) * 16 + (l & 15), cc = (blk % KB) * 32 + (l >> 4) * 8;
-      const int r = srow0 + sr;
+      const int r = (blk / KB) * 16 + (l & 15), cc = (blk % KB) * 32 + (l >> 4) * 8;
       if (r >= rlo && r < rhi && ncol0 + cc < ncols)
         __builtin_nontemporal_store(
-            *reinterpret_cast<const u32x4*>(stg_at(sr, cc)),
+            *reinterpret_cast<const u32x4*>(stg_at(r, cc)),
             reinterpret_cast<u32x4*>(out + ((static_cast<int64_t>((m0 + r) >> 4) * ldb +
                                              ((ncol0 + cc) >> 5)) << 9) + 8 * l));
     }
-    if (ps + 1 < PASSES) __syncthreads();
-    continue;
+    return;
   }
-  for (int q = tid; q < SROWS * CPR_OUT; q += NT) {
-    const int sr = q / CPR_OUT, cc = (q % CPR_OUT) * 8;
-    const int r = srow0 + sr;
+  constexpr int CPR_OUT = OW / 8;  // 16-byte chunks per output row
+  for (int q = tid; q < BM * CPR_OUT; q += NT) {
+    const int r = q / CPR_OUT, cc = (q % CPR_OUT) * 8;
     // non-temporal: every CU stores its tile at about the same time, and
     // the burst streams past the caches (the next kernel reads it once).
     // With the epilogue loads hoisted: C1's up GEMM 2.20 -> 2.15 ms per
     // step, C3's step 3.66 -> 3.49 ms.
     if (r >= rlo && r < rhi && ncol0 + cc < ncols)
       __builtin_nontemporal_store(
-          *reinterpret_cast<const u32x4*>(stg_at(sr, cc)),
+          *reinterpret_cast<const u32x4*>(stg_at(r, cc)),
           reinterpret_cast<u32x4*>(out + static_cast<int64_t>(m0 + r) * p.ldo + ncol0 + cc));
-  }
-  if (ps + 1 < PASSES) __syncthreads();  // the next pass restages into the ring
   }
 }
 
@@ -570,7 +585,7 @@ __global__ __launch_bounds__(256, NS <= 3 ? 2 : 1) void k_gemm_ring(const GemmAr
   __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE];
 
   int g, m0, rlo, mrows, n0;  // never given row tiles: rlo = 0
-  if (!big_tile<BM, BN, GM>(p, g, m0, rlo, mrows, n0)) return;
+  if (!big_tile<BM, BN, GM>(p, blockIdx.x, g, m0, rlo, mrows, n0)) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
 
@@ -674,7 +689,7 @@ __global__ __launch_bounds__(256, NS <= 3 ? 2 : 1) void k_gemm_ring(const GemmAr
     step(s + 1, wf1, af1, wf0, af0);
   }
 
-  __syncthreads();  // every wave is done with the ring (no DMA is outstanding here)
+  // (no DMA is outstanding here; the epilogue synchronises before it reuses the ring)
   tile_epilogue<BM, BN, TM, TN, 256, EPI>(p, acc, g, m0, 0, mrows, n0, wm, wn, ring);
 }
 
@@ -712,19 +727,17 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
   constexpr int A_HI = A_INS % 8 == 0 ? 8 : A_INS % 8;   // waves issuing A_LD of them
   constexpr int LD = A_LD + B_LD, LD_LO = (A_INS / 8) + B_LD;
   constexpr int OUT_BYTES = BM * ((EPI == EPI_SWIGLU) ? BN / 2 : BN) * 2;
-  // the ring also stages the output tile: sized for one staging pass when the
-  // 160 KB of LDS allow it (320 x 256 bf16 is exactly 160 KB; two passes
+  // the ring also stages the output tile, in one pass: it grows to the tile
+  // when that is larger (320 x 256 bf16 is exactly 160 KB; two passes
   // through the 144 KB ring cost a barrier and a half-idle store phase)
   constexpr int RING = NS * STAGE > OUT_BYTES ? NS * STAGE : OUT_BYTES;
   static_assert(RING <= 163840, "LDS of one workgroup");
-  constexpr int PASSES = OUT_BYTES <= RING ? 1 : 2;
   static_assert(NS >= 2, "ring depth");
   static_assert(BM == 128 || BM == 256 || BM == 320, "block rows");
-  static_assert(OUT_BYTES <= 2 * NS * STAGE, "output staging fits in the ring in two passes");
   __shared__ __attribute__((aligned(1024))) uint8_t ring[RING];
 
   int g, m0, rlo, rhi, n0;
-  if (!big_tile<BM, BN, GM>(p, g, m0, rlo, rhi, n0)) return;  // workgroup-uniform
+  if (!big_tile<BM, BN, GM>(p, blockIdx.x, g, m0, rlo, rhi, n0)) return;  // workgroup-uniform
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int grp = wave >> 2;
   const int wm = grp, wn = wave & 3;
@@ -839,8 +852,8 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
         acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[j][i], 0, 0, 0);
     if (grp == 0 || k + 1 < KT) __builtin_amdgcn_s_barrier();
   }
-  __syncthreads();  // every wave is done with the ring (no DMA is outstanding here)
-  tile_epilogue<BM, BN, TM, TN, 512, EPI, PASSES>(p, acc, g, m0, rlo, rhi, n0, wm, wn, ring);
+  // (no DMA is outstanding here; the epilogue synchronises before it reuses the ring)
+  tile_epilogue<BM, BN, TM, TN, 512, EPI>(p, acc, g, m0, rlo, rhi, n0, wm, wn, ring);
 }
 
 // --------------------------------------------------------------- skinny ----
