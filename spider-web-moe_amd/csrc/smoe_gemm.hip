@@ -415,7 +415,8 @@ __device__ __forceinline__ void store4(const GemmArgs& p, int fmt, int g, int ro
 // others are computed as they are staged (a packed tile of 4 channels per
 // fragment column would not fit beside the accumulators).
 // Without a bias (the SwiGLU experts) its loads and adds are compiled out.
-template <int BM, int BN, int TM, int TN, int NT, int EPI>
+// fp8 weights (WF): each channel's scale multiplies its accumulator first.
+template <int BM, int BN, int TM, int TN, int NT, int EPI, int WF = SMOE_BF16>
 __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const f32x4 (&acc)[TN / 16][TM / 16],
                                               int g, int m0, int rlo, int rhi, int n0, int wm,
                                               int wn, uint8_t* ring) {
@@ -438,10 +439,24 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const f32x4 (&a
     const int tr0 = wm * TM + i * 16;
     return tr0 < rhi && tr0 + 16 > rlo;
   };
+  constexpr bool F8 = WF == SMOE_FP8_E4M3;
   auto body = [&](auto with_bias) {
     constexpr bool WB = HAS_BIAS && decltype(with_bias)::value;
     float bq[WB ? NJ : 1][4];
     float rsv[HAS_RS ? FM : 1];
+    // fp8 channel scales: [fragment column][channel] (SwiGLU: gate, then up 32 on)
+    float sc[F8 ? FN : 1][4];
+    if constexpr (F8) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int c = n0 + wn * TN + j * 16 + fc * 4;
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          sc[j][q] = c + q < p.N_out
+                         ? reinterpret_cast<const float*>(p.S)[g * p.s_gstride + c + q]
+                         : 0.f;
+      }
+    }
     if constexpr (WB) {
 #pragma unroll
       for (int j = 0, b = 0; j < FN; ++j) {
@@ -466,10 +481,12 @@ __device__ __forceinline__ void tile_epilogue(const GemmArgs& p, const f32x4 (&a
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         if constexpr (EPI == EPI_SWIGLU) {
-          const float up = acc[j + 2][i][q];
-          r[q] = silu(acc[j][i][q]) * (WB ? up + bq[WB ? b : 0][q] : up);
+          const float gate = F8 ? acc[j][i][q] * sc[F8 ? j : 0][q] : acc[j][i][q];
+          const float up = F8 ? acc[j + 2][i][q] * sc[F8 ? j + 2 : 0][q] : acc[j + 2][i][q];
+          r[q] = silu(gate) * (WB ? up + bq[WB ? b : 0][q] : up);
         } else {
-          const float a = WB ? acc[j][i][q] + bq[WB ? b : 0][q] : acc[j][i][q];
+          const float v = F8 ? acc[j][i][q] * sc[F8 ? j : 0][q] : acc[j][i][q];
+          const float a = WB ? v + bq[WB ? b : 0][q] : v;
           if constexpr (HAS_RS) r[q] = a * rsv[HAS_RS ? i : 0];
           else if constexpr (EPI == EPI_GELU) r[q] = gelu_erf(a);
           else r[q] = a;
@@ -713,16 +730,24 @@ __global__ __launch_bounds__(256, NS <= 3 ? 2 : 1) void k_gemm_ring(const GemmAr
 // BM = 256 (wave tile 128 x 64) for many rows per group; BM = 128 (wave tile
 // 64 x 64, two workgroups per CU) when groups hold a few hundred rows and a
 // 256-row tile would be mostly padding.
-template <int NS, int GM, int EPI, int BM, bool PK = false>
+template <int NS, int GM, int EPI, int BM, bool PK = false, int WF = SMOE_BF16>
 __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmArgs p) {
+  // WF: the weight format.  fp8-e4m3 weights come from their weight tile
+  // copy (16 rows x 64 k per 1 KB block): a 32-k stage of a 16-row tile is
+  // half a block, a DMA instruction moves the halves of two tiles, and the
+  // fragment reads widen the codes to bf16 (exact) in registers; the
+  // per-channel scale is applied in the epilogue.  Half the W bytes of bf16
+  // through the DMA and LDS.
+  static_assert(WF == SMOE_BF16 || (WF == SMOE_FP8_E4M3 && PK), "fp8 weights need the tile copy");
+  constexpr bool F8 = WF == SMOE_FP8_E4M3;
   constexpr int BN = 256, TM = BM / 2, TN = 64;
   constexpr int FM = TM / 16, FN = TN / 16;
-  constexpr int A_BYTES = BM * 64, B_BYTES = BN * 64, STAGE = A_BYTES + B_BYTES;
-  // DMA instructions (16 rows each) per stage: A_INS of A, B_LD per wave of
-  // W.  With BM = 320 the 20 A instructions do not split evenly over the 8
-  // waves: waves 0-3 issue 3, waves 4-7 issue 2, and each wave's vmcnt waits
-  // count its own.
-  constexpr int A_INS = BM / 16, B_LD = BN / 16 / 8;
+  constexpr int A_BYTES = BM * 64, B_BYTES = BN * (F8 ? 32 : 64), STAGE = A_BYTES + B_BYTES;
+  // DMA instructions (16 rows each; fp8 W: 32 rows) per stage: A_INS of A,
+  // B_LD per wave of W.  With BM = 320 the 20 A instructions do not split
+  // evenly over the 8 waves: waves 0-3 issue 3, waves 4-7 issue 2, and each
+  // wave's vmcnt waits count its own.
+  constexpr int A_INS = BM / 16, B_LD = BN / (F8 ? 32 : 16) / 8;
   constexpr int A_LD = (A_INS + 7) / 8;                  // most per wave
   constexpr int A_HI = A_INS % 8 == 0 ? 8 : A_INS % 8;   // waves issuing A_LD of them
   constexpr int LD = A_LD + B_LD, LD_LO = (A_INS / 8) + B_LD;
@@ -760,7 +785,7 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
   const int a_step = p.At ? 512 : 32;  // elements per K step
   const uint16_t* W = reinterpret_cast<const uint16_t*>(p.W) + g * p.w_gstride;
   const uint16_t* asrc[A_LD];
-  const uint16_t* bsrc[B_LD];
+  const uint8_t* bsrc[B_LD];  // bytes
   {
     const int pr = lane >> 2, pc = lane & 3;
 #pragma unroll
@@ -779,13 +804,21 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
 #pragma unroll
     for (int j = 0; j < B_LD; ++j) {
       const int r = (8 * j + wave) * 16 + pr;
-      if constexpr (PK) {  // weight tile layout: 16 rows x 32 k = 1 KB of lane-ordered fragments
+      if constexpr (F8) {  // lanes 0-31: tile 2 (8 j + w), 32-63: the next; 512 B of each per stage
+        const int t = n0 + (2 * (8 * j + wave) + (lane >> 5)) * 16;
+        const int tile = (t < p.N_out ? t : n0) >> 4;
+        bsrc[j] = reinterpret_cast<const uint8_t*>(p.Wt) +
+                  ((static_cast<int64_t>(g) * (p.N_out >> 4) + tile) * (p.K >> 6)) * 1024 +
+                  16 * (lane & 31);
+      } else if constexpr (PK) {  // weight tile layout: 16 rows x 32 k = 1 KB of lane-ordered fragments
         const int tile = (n0 + (8 * j + wave) * 16 < p.N_out ? n0 + (8 * j + wave) * 16 : n0) >> 4;
-        bsrc[j] = reinterpret_cast<const uint16_t*>(p.Wt) +
-                  ((static_cast<int64_t>(g) * (p.N_out >> 4) + tile) * (p.K >> 5)) * 512 + 8 * lane;
+        bsrc[j] = reinterpret_cast<const uint8_t*>(
+            reinterpret_cast<const uint16_t*>(p.Wt) +
+            ((static_cast<int64_t>(g) * (p.N_out >> 4) + tile) * (p.K >> 5)) * 512 + 8 * lane);
       } else {
         const int n = n0 + r < p.N_out ? n0 + r : n0;
-        bsrc[j] = W + static_cast<int64_t>(n) * p.ldw + ((pc ^ ((r >> 1) & 3)) << 3);
+        bsrc[j] = reinterpret_cast<const uint8_t*>(W + static_cast<int64_t>(n) * p.ldw +
+                                                   ((pc ^ ((r >> 1) & 3)) << 3));
       }
     }
   }
@@ -798,8 +831,8 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
         __builtin_amdgcn_global_load_lds((gbl_vptr)(asrc[j] + stage * a_step),
                                          (lds_vptr)(base + (8 * j + wave) * 1024), 16, 0, 0);
 #pragma unroll
-    for (int j = 0; j < B_LD; ++j)  // tile layout: each stage's block is the next 1 KB (512 elements)
-      __builtin_amdgcn_global_load_lds((gbl_vptr)(bsrc[j] + (PK ? stage * 512 : k0)),
+    for (int j = 0; j < B_LD; ++j)  // tile layout: each stage's (half) block is the next 1 KB (512 B)
+      __builtin_amdgcn_global_load_lds((gbl_vptr)(bsrc[j] + stage * (F8 ? 512 : PK ? 1024 : 64)),
                                        (lds_vptr)(base + A_BYTES + (8 * j + wave) * 1024), 16, 0, 0);
   };
   const int fr = lane & 15, fc = lane >> 4;
@@ -811,9 +844,18 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
     const uint8_t* sa = ring + (stage % NS) * STAGE;
     const uint8_t* sb = sa + A_BYTES;
 #pragma unroll
-    for (int j = 0; j < FN; ++j)  // tile layout: block (wn * TN + 16 j) / 16 holds lane l's fragment at 16 l
-      wf[j] = *reinterpret_cast<const bf16x8*>(
-          sb + (PK ? (wn * TN / 16 + j) * 1024 + 16 * lane : swz32(wn * TN + j * 16 + fr, fc)));
+    for (int j = 0; j < FN; ++j) {
+      if constexpr (F8) {  // tile tt's half block: row fr, k 8 fc.. at 16 fr + 256 (fc >> 1) + 8 (fc & 1)
+        const int tt = wn * TN / 16 + j;
+        const u32x2 c = *reinterpret_cast<const u32x2*>(
+            sb + (tt >> 1) * 1024 + (tt & 1) * 512 + 16 * fr + 256 * (fc >> 1) + 8 * (fc & 1));
+        const u32x2 lo = fp8x4_to_bf16x4(c.x), hi = fp8x4_to_bf16x4(c.y);
+        wf[j] = __builtin_bit_cast(bf16x8, u32x4{lo.x, lo.y, hi.x, hi.y});
+      } else {  // tile layout: block (wn * TN + 16 j) / 16 holds lane l's fragment at 16 l
+        wf[j] = *reinterpret_cast<const bf16x8*>(
+            sb + (PK ? (wn * TN / 16 + j) * 1024 + 16 * lane : swz32(wn * TN + j * 16 + fr, fc)));
+      }
+    }
 #pragma unroll
     for (int i = 0; i < FM; ++i)
       af[i] = *reinterpret_cast<const bf16x8*>(sa + a_lds + 1024 * i);
@@ -853,7 +895,7 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
     if (grp == 0 || k + 1 < KT) __builtin_amdgcn_s_barrier();
   }
   // (no DMA is outstanding here; the epilogue synchronises before it reuses the ring)
-  tile_epilogue<BM, BN, TM, TN, 512, EPI>(p, acc, g, m0, rlo, rhi, n0, wm, wn, ring);
+  tile_epilogue<BM, BN, TM, TN, 512, EPI, WF>(p, acc, g, m0, rlo, rhi, n0, wm, wn, ring);
 }
 
 // --------------------------------------------------------------- skinny ----
@@ -1736,10 +1778,28 @@ int launch_pp_fmt(const GemmArgs& a, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 
+// fp8-e4m3 weights (their tile copy; the expert FFN's epilogues)
+template <int NS, int GM, int BM>
+int launch_pp_fp8(const GemmArgs& a, hipStream_t s) {
+  const int tiles = max_tiles(a, BM) * ((a.N_out + 255) / 256);
+  if (tiles == 0) return SMOE_OK;
+  const dim3 grid(tiles), block(512);
+  constexpr int F8 = SMOE_FP8_E4M3;
+  switch (a.epi) {
+    case EPI_GELU: SMOE_LAUNCH((k_gemm_pp<NS, GM, EPI_GELU, BM, true, F8>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU: SMOE_LAUNCH((k_gemm_pp<NS, GM, EPI_SWIGLU, BM, true, F8>), grid, block, 0, s, a); break;
+    case EPI_DOWN: SMOE_LAUNCH((k_gemm_pp<NS, GM, EPI_DOWN, BM, true, F8>), grid, block, 0, s, a); break;
+    default: return SMOE_EINVAL;
+  }
+  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
 // bf16 weights with a weight tile copy: the W operand's DMA reads each
-// 16-row x 32-k block as one contiguous 1 KB of lane-ordered fragments
+// 16-row x 32-k block as one contiguous 1 KB of lane-ordered fragments;
+// fp8 weights always come from their tile copy
 template <int NS, int GM, int BM>
 int launch_pp(const GemmArgs& a, hipStream_t s) {
+  if (a.fmt == SMOE_FP8_E4M3) return launch_pp_fp8<NS, GM, BM>(a, s);
   return a.Wt && a.fmt == SMOE_BF16 && a.N_out % 16 == 0 ? launch_pp_fmt<NS, GM, BM, true>(a, s)
                                    : launch_pp_fmt<NS, GM, BM, false>(a, s);
 }
@@ -1978,8 +2038,15 @@ bool pp_rows_320(const GemmArgs& a, int rpg) {
   return 115 * rounds(320) < 100 * rounds(256);
 }
 
+// Weights the ping-pong kernels read: bf16, or fp8-e4m3 from its tile copy
+// (not for the edge projection's row-scale epilogue).
+bool pp_weights(const GemmArgs& a) {
+  return a.fmt == SMOE_BF16 ||
+         (a.fmt == SMOE_FP8_E4M3 && a.Wt && a.N_out % 16 == 0 && a.epi != EPI_ROWSCALE);
+}
+
 bool gemm_takes_row_tiles(const GemmArgs& a) {
-  if (a.W2 || a.fmt != SMOE_BF16 || a.out_dtype != SMOE_BF16 || a.epi == EPI_F32_BIAS) return false;
+  if (a.W2 || !pp_weights(a) || a.out_dtype != SMOE_BF16 || a.epi == EPI_F32_BIAS) return false;
   if (a.K % 64 || a.ldw % 8 || a.lda % 8 || a.ldo % 32 || a.w_gstride % 8 || a.N_out % 256)
     return false;
   return (a.G == 0 ? a.single_rows : a.max_rows / a.G) >= 256;
@@ -2037,14 +2104,14 @@ int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
                                 (a.group_size & (a.group_size - 1)) == 0)))
       return launch_stream(a, s);
   }
-  // large bf16 problems (K % 64): 256 x 256 tiles, 8 waves in two ping-pong
+  // large bf16 / fp8 (tile copy) problems (K % 64): 256 x 256 tiles, 8 waves in two ping-pong
   // groups when N_out % 256 == 0 (128-row tiles, two workgroups per CU, for
   // groups of a few hundred rows); otherwise 256 x 128 ring tiles, two
   // workgroups per CU (a half-empty 256-wide last tile costs more than the
   // ring's weaker main loop).  A 384 x 128 single-workgroup tile for groups
   // of ~260 rows (each weight strip fetched once, dead 16-row tiles skipped)
   // measured 27% slower than the 128-row tiles at that shape.
-  if (a.fmt == SMOE_BF16 && a.out_dtype == SMOE_BF16 && a.epi != EPI_F32_BIAS && a.K % 64 == 0 &&
+  if (pp_weights(a) && a.out_dtype == SMOE_BF16 && a.epi != EPI_F32_BIAS && a.K % 64 == 0 &&
       a.ldw % 8 == 0 && a.lda % 8 == 0 && a.ldo % 8 == 0 &&
       (a.G == 0 ? a.single_rows : a.max_rows / (a.G > 0 ? a.G : 1)) >= 256) {
     const int rpg = a.G == 0 ? a.single_rows : a.max_rows / a.G;
@@ -2056,7 +2123,7 @@ int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
       return a.epi != EPI_ROWSCALE && pp_rows_320(a, rpg) ? launch_pp<4, 4, 320>(a, s)
                                                 : launch_pp<4, 4, 256>(a, s);
     }
-    if (a.N_out % 128 == 0) return launch_ring<128, 3, 4>(a, s);
+    if (a.N_out % 128 == 0 && a.fmt == SMOE_BF16) return launch_ring<128, 3, 4>(a, s);
   }
   const bool b64 = bk == 64;
   // narrow outputs (router / edge logits, N_out = E): 64-row tiles, one

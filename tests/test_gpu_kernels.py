@@ -311,6 +311,58 @@ def test_fp8_experts_every_code(act):
     assert (got - ref).abs().max() <= 2e-2 * scale + 1e-6, float((got - ref).abs().max() / scale)
 
 
+@pytest.mark.parametrize("act,n", [("gelu", 2304), ("swiglu", 2304), ("swiglu", 4096),
+                                   ("gelu", 1100)])
+def test_large_fp8_experts_ragged_groups(act, n):
+    """fp8-e4m3 experts at prefill sizes (> 256 rows per expert on average,
+    skewed: empty, single-row and multi-tile experts) with their weight tile
+    copies: the ping-pong kernel reads the fp8 tiles, widens them to bf16 in
+    registers and scales each channel in its epilogue (at n = 1100, 275 rows
+    per expert, its 128-row tiles).  Against the oracle over the dequantized
+    weights, and against the general fp8 kernel (no tile copy) at the same
+    bound."""
+    from spider_moe_amd.quant import interleave_gate_up, interleave_gate_up_rows
+    n8 = nat()
+    say("large fp8 experts", act, n)
+    h, u, e, k = 512, 768, 8, 2
+    g = torch.Generator().manual_seed(23)
+    p = torch.tensor([0.45, 0.3, 0.12, 0.08, 0.05, 0.0, 0.0, 0.0])
+    idx = torch.multinomial(p.expand(n, e), k, replacement=False, generator=g)
+    idx[7, 1] = 5
+    w = torch.rand(n, k, generator=g)
+    msg = torch.randn(n, h, generator=g).to(torch.bfloat16)
+    nup = 2 * u if act == "swiglu" else u
+    wu = torch.randn(e, nup, h, generator=g) * 0.04
+    wd = torch.randn(e, h, u, generator=g) * 0.04
+    cu, su = Q.fp8_quantize_per_channel(wu.numpy())
+    cd, sd = Q.fp8_quantize_per_channel(wd.numpy())
+    wu_f = torch.from_numpy(Q.fp8_dequantize_per_channel(cu, su))
+    wd_f = torch.from_numpy(Q.fp8_dequantize_per_channel(cd, sd))
+    bu = torch.randn(e, u, generator=g) * 0.1
+    bd = torch.randn(e, h, generator=g) * 0.1
+    if act == "swiglu":
+        ref = _oracle_delta(msg.float(), idx, w, wu_f[:, u:], bu, wd_f, bd, w_gate=wu_f[:, :u])
+        cu_t = interleave_gate_up(torch.from_numpy(cu[:, :u]), torch.from_numpy(cu[:, u:]))
+        su_t = interleave_gate_up_rows(torch.from_numpy(su[:, :u]), torch.from_numpy(su[:, u:]))
+        actc = n8.ACT_SWIGLU
+    else:
+        ref = _oracle_delta(msg.float(), idx, w, wu_f, bu, wd_f, bd)
+        cu_t, su_t = torch.from_numpy(cu), torch.from_numpy(su)
+        actc = n8.ACT_GELU
+    t = [x.contiguous().to(dev) for x in (cu_t, torch.from_numpy(cd), su_t, torch.from_numpy(sd),
+                                          bu, bd)]
+    ex = _experts_struct(n8, n8.FP8_E4M3, actc, e, h, u, t[0], t[1], s_up=t[2], s_down=t[3],
+                         b_up=t[4], b_down=t[5], scale_dtype=n8.F32)
+    plain = _run_delta(n8, ex, msg.to(dev), idx.to(torch.int32).to(dev), w.to(dev))
+    tu, td = _tiles(n8, t[0], n8.FP8_E4M3), _tiles(n8, t[1], n8.FP8_E4M3)
+    ex.w_up_tiles, ex.w_down_tiles = tu.data_ptr(), td.data_ptr()
+    got = _run_delta(n8, ex, msg.to(dev), idx.to(torch.int32).to(dev), w.to(dev))
+    scale = ref.abs().max()
+    assert torch.isfinite(got).all()
+    for out in (got, plain):
+        assert (out - ref).abs().max() <= 2e-2 * scale + 1e-6, float((out - ref).abs().max() / scale)
+
+
 @pytest.mark.parametrize("group,sdt", [(32, torch.float32), (128, torch.float16)])
 def test_int4_experts_match_oracle(group, sdt):
     from spider_moe_amd.quant import quantize_int4
