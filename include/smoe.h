@@ -87,10 +87,13 @@ typedef struct smoe_experts {
   const void* s_down;
   const float* b_up;
   const float* b_down;
-  /* optional (bf16 and fp8, else ignored): w_up / w_down in the weight
-   * tile layout (smoe_pack_weight_tiles), read instead of them by the decode
-   * weight stream and (bf16) as the ping-pong GEMM's weight operand; NULL to
-   * read the row-major weights (same results, bit for bit) */
+  /* optional: w_up / w_down in the weight tile layout, NULL to read the
+   * row-major weights.  bf16 and fp8 (smoe_pack_weight_tiles): read instead
+   * of them by the decode weight stream and the ping-pong GEMM (bit-identical
+   * results for bf16).  int4 (smoe_pack_int4_tiles): the bf16 tiles of the
+   * dequantized weights, read by the ping-pong GEMM at prefill sizes (>= 256
+   * rows per expert) in place of the general int4 kernel; the decode and
+   * stream kernels keep reading the packed int4. */
   const void* w_up_tiles;
   const void* w_down_tiles;
 } smoe_experts;
@@ -393,6 +396,17 @@ SMOE_API int smoe_remap_ids(const int32_t* ids, int64_t n, const int32_t* map, i
  * other kernel reads.  Returns -2 for other formats. */
 SMOE_API int smoe_pack_weight_tiles(const void* w, int format, int G, int N, int K, void* out,
                                     void* stream);
+
+/* int4 weights (packed [G,N,K/2] as quant.py:119-143 packs them, scales
+ * [G,N,K/group_size] of scale_dtype SMOE_F32 / SMOE_F16) -> the bf16 weight
+ * tile layout of their dequantized values, out [G,N,K] bf16: q * s rounded
+ * once to bf16, the values the int4 GEMM kernels multiply.  For the
+ * smoe_experts w_up_tiles / w_down_tiles of int4 experts: prefill-size
+ * expert GEMMs then run on the bf16 ping-pong kernel, at 4x the int4 bytes
+ * of memory.  N % 16, K % 64,
+ * group_size % 8, K % group_size.  No counterpart in the reference. */
+SMOE_API int smoe_pack_int4_tiles(const void* packed, const void* scales, int scale_dtype,
+                                  int group_size, int G, int N, int K, void* out, void* stream);
 
 /* When `events` is not NULL, every later smoe_block_forward records
  * events[2*i] before and events[2*i+1] after the i-th launch of a stage in

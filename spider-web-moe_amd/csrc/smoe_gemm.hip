@@ -1699,6 +1699,42 @@ int launch_pack_weight_tiles(const void* w, int fmt, int G, int N, int K, void* 
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 
+// int4 weights -> the bf16 weight tile layout of their dequantized values:
+// one thread per 16-byte fragment (8 consecutive k of one row), from the 4
+// packed bytes holding those k and the row's group scale: q * s rounded once
+// to bf16 (int4x8_to_bf16x8), the values every int4 GEMM here multiplies.
+__global__ __launch_bounds__(256) void k_pack_int4_tiles(const uint8_t* __restrict__ q,
+                                                         const void* __restrict__ sc, int s_f16,
+                                                         int gs, int64_t frags, int N, int K,
+                                                         uint16_t* __restrict__ out) {
+  const int64_t f = blockIdx.x * static_cast<int64_t>(256) + threadIdx.x;
+  if (f >= frags) return;
+  const int l = static_cast<int>(f & 63);
+  const int64_t blk = f >> 6;  // (g*T + t)*C + c
+  const int C = K / 32, T = N / 16;
+  const int c = static_cast<int>(blk % C);
+  const int64_t gt = blk / C;  // g*T + t
+  const int64_t g = gt / T, t = gt % T;
+  const int64_t row = g * N + 16 * t + (l & 15);
+  const int k = 32 * c + 8 * (l >> 4);
+  const uint32_t w = *reinterpret_cast<const uint32_t*>(q + row * (K / 2) + k / 2);
+  const float s = load_scale(sc, row * (K / gs) + k / gs, s_f16);
+  *reinterpret_cast<u32x4*>(out + f * 8) = int4x8_to_bf16x8(w, s);
+}
+
+int launch_pack_int4_tiles(const void* q, const void* scales, int s_f16, int gs, int G, int N, int K,
+                           void* out, hipStream_t s) {
+  if (!q || !scales || !out || G < 1 || N < 16 || K < 64 || N % 16 || K % 64 || gs <= 0 || gs % 8 ||
+      K % gs)
+    return SMOE_EINVAL;
+  if (reinterpret_cast<uintptr_t>(q) % 4 || reinterpret_cast<uintptr_t>(out) % 16) return SMOE_EINVAL;
+  const int64_t frags = static_cast<int64_t>(G) * N * K / 8;
+  hipLaunchKernelGGL(k_pack_int4_tiles, dim3(static_cast<unsigned>((frags + 255) / 256)), dim3(256),
+                     0, s, reinterpret_cast<const uint8_t*>(q), scales, s_f16, gs, frags, N, K,
+                     reinterpret_cast<uint16_t*>(out));
+  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
 // --------------------------------------------------------------- launch ----
 namespace {
 
@@ -1800,6 +1836,7 @@ int launch_pp_fp8(const GemmArgs& a, hipStream_t s) {
 template <int NS, int GM, int BM>
 int launch_pp(const GemmArgs& a, hipStream_t s) {
   if (a.fmt == SMOE_FP8_E4M3) return launch_pp_fp8<NS, GM, BM>(a, s);
+  if (a.fmt == SMOE_INT4) return launch_pp_fmt<NS, GM, BM, true>(a, s);  // bf16 dequant tiles
   return a.Wt && a.fmt == SMOE_BF16 && a.N_out % 16 == 0 ? launch_pp_fmt<NS, GM, BM, true>(a, s)
                                    : launch_pp_fmt<NS, GM, BM, false>(a, s);
 }
@@ -2038,11 +2075,12 @@ bool pp_rows_320(const GemmArgs& a, int rpg) {
   return 115 * rounds(320) < 100 * rounds(256);
 }
 
-// Weights the ping-pong kernels read: bf16, or fp8-e4m3 from its tile copy
-// (not for the edge projection's row-scale epilogue).
+// Weights the ping-pong kernels read: bf16; fp8-e4m3 from its tile copy;
+// int4 from the bf16 tile copy of its dequantized values (neither for the
+// edge projection's row-scale epilogue).
 bool pp_weights(const GemmArgs& a) {
-  return a.fmt == SMOE_BF16 ||
-         (a.fmt == SMOE_FP8_E4M3 && a.Wt && a.N_out % 16 == 0 && a.epi != EPI_ROWSCALE);
+  return a.fmt == SMOE_BF16 || ((a.fmt == SMOE_FP8_E4M3 || a.fmt == SMOE_INT4) && a.Wt &&
+                                a.N_out % 16 == 0 && a.epi != EPI_ROWSCALE);
 }
 
 bool gemm_takes_row_tiles(const GemmArgs& a) {

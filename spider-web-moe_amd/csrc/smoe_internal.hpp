@@ -43,7 +43,8 @@ struct GemmArgs {
   int lda = 0;                   // elements
   const int32_t* a_rows = nullptr;  // plan row -> A row; nullptr = identity
   const void* W = nullptr;
-  const void* Wt = nullptr;      // bf16 / fp8: W in the weight tile layout (or nullptr)
+  const void* Wt = nullptr;      // bf16 / fp8: W in the weight tile layout (or nullptr);
+                                 // int4: bf16 tiles of the dequantized W (large-tile GEMMs)
   int64_t w_gstride = 0;         // elements between groups
   int ldw = 0;                   // elements between rows of W
   const void* S = nullptr;       // fp8: f32 [G, N_out]; int4: [G, N_out, K/gs]
@@ -85,6 +86,9 @@ bool gemm_takes_row_tiles(const GemmArgs& a);
 inline int64_t row_tile_elems(int64_t rows, int64_t cols) { return (rows + 15) / 16 * 16 * cols; }
 // bf16 / fp8 w [G,N,K] -> the weight tile layout (smoe_pack_weight_tiles)
 int launch_pack_weight_tiles(const void* w, int fmt, int G, int N, int K, void* out, hipStream_t s);
+// int4 [G,N,K/2] + group scales -> bf16 tiles of the dequantized weights
+int launch_pack_int4_tiles(const void* q, const void* scales, int s_f16, int gs, int G, int N, int K,
+                           void* out, hipStream_t s);
 // One bf16 GEMM over a few rows (G == 0, single_rows <= 64) with f32 logits
 // out (EPI_F32_BIAS) from two weight segments: the router and all edge
 // generator rows of a small decode step in one pass.

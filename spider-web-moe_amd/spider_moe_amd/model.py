@@ -52,6 +52,9 @@ class _Packed:
         self.keep = []
         self.desc = nat.SmoeBlock()
         self.ws_need = {}  # tokens -> workspace bytes
+        # int4 experts: the sources of their bf16 dequant tiles, made on the
+        # first call with prefill-size expert groups (None once made / unused)
+        self.int4_tiles_src = None
 
 
 class SpiderMoELayer(nn.Module):
@@ -303,6 +306,10 @@ class SpiderMoELayer(nn.Module):
         if ex.format == nat.FP8_E4M3:
             ex.w_up_tiles = nat.ptr(tiles(w_up, nat.FP8_E4M3))
             ex.w_down_tiles = nat.ptr(tiles(w_down, nat.FP8_E4M3))
+        elif ex.format == nat.INT4:
+            if self.weight_tiles and all(q.shape[1] % 16 == 0 and (2 * q.shape[2]) % 64 == 0
+                                         for q in (w_up, w_down)):
+                k.int4_tiles_src = (w_up, s_up, w_down, s_down)
         elif ex.format == nat.BF16:
             ex.w_up_tiles = nat.ptr(tiles(w_up))
             ex.w_down_tiles = nat.ptr(tiles(w_down))
@@ -321,6 +328,28 @@ class SpiderMoELayer(nn.Module):
         k.exit_wb = f32(torch.cat([self.exit_head.weight.reshape(-1), self.exit_head.bias.reshape(-1)]))
         self._packed, self._packed_key = k, key
         return k
+
+    def _int4_prefill_tiles(self, k: _Packed, n: int, dev) -> None:
+        """int4 experts with weight_tiles: on the first call whose expert
+        groups reach the large-tile GEMM's size (n * top_k >= 256 per expert),
+        the bf16 tiles of the dequantized weights (smoe_pack_int4_tiles), 4x
+        the int4 bytes; decode-size calls keep the packed int4 alone."""
+        if k.int4_tiles_src is None or n * self.top_k < 256 * self.num_experts:
+            return
+        w_up, s_up, w_down, s_down = k.int4_tiles_src
+        ex = k.desc.experts
+        lib = nat.lib()
+        ptrs = []
+        for q, sc in ((w_up, s_up), (w_down, s_down)):
+            g, rows, half = q.shape
+            out = torch.empty(g, rows, 2 * half, dtype=torch.bfloat16, device=dev)
+            nat.check(lib.smoe_pack_int4_tiles(q.data_ptr(), sc.data_ptr(), ex.scale_dtype,
+                                               ex.group_size, g, rows, 2 * half, out.data_ptr(),
+                                               nat.stream_of(dev)), "smoe_pack_int4_tiles")
+            k.keep.append(out)
+            ptrs.append(out.data_ptr())
+        ex.w_up_tiles, ex.w_down_tiles = ptrs
+        k.int4_tiles_src = None
 
     def workspace_bytes(self, n: int, packed: _Packed | None = None) -> int:
         """Bytes of the native workspace a call over n tokens needs."""
@@ -361,6 +390,7 @@ class SpiderMoELayer(nn.Module):
             return self._run_offload(h2, x2, loop_begin, num_loops, gate).view(b, t, width)
         out = torch.empty_like(h2)
         k = self._pack()
+        self._int4_prefill_tiles(k, n, dev)
         if workspace is None:
             ws = self._workspace(n, dev, k)
         else:

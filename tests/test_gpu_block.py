@@ -135,6 +135,26 @@ def test_block_small_bf16_per_loop(spec):
         h, rep = _check_loop(wl.layer, h, wl.x0, r, 1e-2)
 
 
+@pytest.mark.parametrize("experts,act", [("fp8", "swiglu"), ("int4", "gelu"), ("int4", "swiglu")])
+def test_block_prefill_quantized_experts(experts, act):
+    """Quantized experts at prefill size (2048 tokens over 8 experts: ~512
+    rows each), so the expert GEMMs run on the large-tile kernel: fp8 from
+    its weight tiles, int4 from the bf16 tiles of its dequantized weights,
+    which the layer makes on this first prefill-size call.  Per loop against
+    the oracle (routing, plans, edges, message, delta, output)."""
+    from spider_moe_amd.workloads import make_block
+    say("prefill quantized block", experts, act)
+    wl = make_block("c1", tokens=2048, hidden_size=256, num_experts=8, top_k=2, edges_per_expert=2,
+                    expert_ffn_size=512, num_loops=2, expert_activation=act, experts=experts,
+                    group_size=128, std="fan_in")
+    h = wl.h
+    for r in range(2):
+        h, _ = _check_loop(wl.layer, h, wl.x0, r, 1e-2)
+    if experts == "int4":
+        ex = wl.layer._pack().desc.experts
+        assert ex.w_up_tiles and ex.w_down_tiles  # the dequant tiles were made and read
+
+
 @pytest.mark.parametrize("n,e,k,m", [(1, 16, 2, 2), (37, 16, 2, 2), (64, 32, 4, 2), (48, 64, 2, 4),
                                      (64, 16, 3, 3), (65, 16, 2, 2), (200, 64, 2, 4)])
 def test_block_small_steps_fused_front(n, e, k, m):

@@ -364,6 +364,80 @@ def test_large_fp8_experts_ragged_groups(act, n):
 
 
 @pytest.mark.parametrize("group,sdt", [(32, torch.float32), (128, torch.float16)])
+def test_pack_int4_tiles_is_the_dequantized_tile_copy(group, sdt):
+    """smoe_pack_int4_tiles = the bf16 weight tiles (smoe_pack_weight_tiles)
+    of the oracle's dequantized weights (q * s in fp32, rounded once to
+    bf16), bit for bit."""
+    from spider_moe_amd.quant import quantize_int4
+    n8 = nat()
+    say("pack int4 tiles", group, sdt)
+    w = torch.randn(3, 48, 256, generator=torch.Generator().manual_seed(9)) * 0.05
+    q = quantize_int4(w, group, sdt)
+    deq = torch.from_numpy(Q.int4_dequantize(q.packed.numpy(), q.scales.float().numpy(), group))
+    want = _tiles(n8, deq.to(torch.bfloat16).to(dev))
+    qp, qs = q.packed.contiguous().to(dev), q.scales.contiguous().to(dev)
+    got = torch.empty(3, 48, 256, dtype=torch.bfloat16, device=dev)
+    n8.check(n8.lib().smoe_pack_int4_tiles(qp.data_ptr(), qs.data_ptr(),
+                                           n8.F16 if sdt == torch.float16 else n8.F32, group, 3, 48,
+                                           256, got.data_ptr(), n8.stream_of(torch.device(dev))),
+             "pack_int4_tiles")
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+@pytest.mark.parametrize("act,n", [("gelu", 2304), ("swiglu", 2304), ("swiglu", 1100)])
+def test_large_int4_experts_ragged_groups(act, n):
+    """int4 experts (group 128, fp16 scales) at prefill sizes with skewed
+    routing, with the bf16 tiles of their dequantized weights: the ping-pong
+    GEMM (at n = 1100 its 128-row tiles) against the oracle over the
+    dequantized weights, and against the general int4 kernel (no tiles)."""
+    from spider_moe_amd.quant import interleave_gate_up, quantize_int4
+    n8 = nat()
+    say("large int4 experts", act, n)
+    h, u, e, k, group = 512, 768, 8, 2, 128
+    g = torch.Generator().manual_seed(29)
+    p = torch.tensor([0.45, 0.3, 0.12, 0.08, 0.05, 0.0, 0.0, 0.0])
+    idx = torch.multinomial(p.expand(n, e), k, replacement=False, generator=g)
+    idx[7, 1] = 5
+    w = torch.rand(n, k, generator=g)
+    msg = torch.randn(n, h, generator=g).to(torch.bfloat16)
+    nup = 2 * u if act == "swiglu" else u
+    qu = quantize_int4(torch.randn(e, nup, h, generator=g) * 0.04, group, torch.float16)
+    qd = quantize_int4(torch.randn(e, h, u, generator=g) * 0.04, group, torch.float16)
+    wu_f = torch.from_numpy(Q.int4_dequantize(qu.packed.numpy(), qu.scales.float().numpy(), group))
+    wd_f = torch.from_numpy(Q.int4_dequantize(qd.packed.numpy(), qd.scales.float().numpy(), group))
+    bu = torch.randn(e, u, generator=g) * 0.1
+    bd = torch.randn(e, h, generator=g) * 0.1
+    if act == "swiglu":
+        ref = _oracle_delta(msg.float(), idx, w, wu_f[:, u:], bu, wd_f, bd, w_gate=wu_f[:, :u])
+        pu = interleave_gate_up(qu.packed[:, :u], qu.packed[:, u:])
+        su = interleave_gate_up(qu.scales[:, :u], qu.scales[:, u:])
+        actc = n8.ACT_SWIGLU
+    else:
+        ref = _oracle_delta(msg.float(), idx, w, wu_f, bu, wd_f, bd)
+        pu, su = qu.packed, qu.scales
+        actc = n8.ACT_GELU
+    t = [x.contiguous().to(dev) for x in (pu, qd.packed, su, qd.scales, bu, bd)]
+    ex = _experts_struct(n8, n8.INT4, actc, e, h, u, t[0], t[1], s_up=t[2], s_down=t[3],
+                         b_up=t[4], b_down=t[5], group=group, scale_dtype=n8.F16)
+    plain = _run_delta(n8, ex, msg.to(dev), idx.to(torch.int32).to(dev), w.to(dev))
+    tiles = []
+    for q_, s_ in ((t[0], t[2]), (t[1], t[3])):
+        out = torch.empty(q_.shape[0], q_.shape[1], 2 * q_.shape[2], dtype=torch.bfloat16, device=dev)
+        n8.check(n8.lib().smoe_pack_int4_tiles(q_.data_ptr(), s_.data_ptr(), n8.F16, group,
+                                               q_.shape[0], q_.shape[1], 2 * q_.shape[2],
+                                               out.data_ptr(), n8.stream_of(torch.device(dev))),
+                 "pack_int4_tiles")
+        tiles.append(out)
+    ex.w_up_tiles, ex.w_down_tiles = tiles[0].data_ptr(), tiles[1].data_ptr()
+    got = _run_delta(n8, ex, msg.to(dev), idx.to(torch.int32).to(dev), w.to(dev))
+    scale = ref.abs().max()
+    assert torch.isfinite(got).all()
+    for out in (got, plain):
+        assert (out - ref).abs().max() <= 2e-2 * scale + 1e-6, float((out - ref).abs().max() / scale)
+
+
+@pytest.mark.parametrize("group,sdt", [(32, torch.float32), (128, torch.float16)])
 def test_int4_experts_match_oracle(group, sdt):
     from spider_moe_amd.quant import quantize_int4
     n8 = nat()
