@@ -1595,6 +1595,252 @@ __global__ __launch_bounds__(256, WGS) void k_gemm_stream(const GemmArgs p) {
   }
 }
 
+// int4 weights at the stream kernel's row counts, with the dequant beside
+// the MFMAs instead of before them: inside a chunk the 16 weights of tile
+// t+1 are widened (about 3 VALU operations per weight) in the same stretch
+// of code as tile t's MFMAs, so the VALU and the matrix pipe of a wave work
+// side by side; only tile 0's widening is exposed.  The activation
+// fragments of all live row tiles are read once per chunk.  The number of
+// live 16-row tiles of a pass is a template parameter (one instantiation per
+// count, chosen per pass), so tiles past the group's last row issue neither
+// MFMAs nor activation DMA, and the loop body has no branches to split it.
+// Waves whose 64 channels all lie past N_out skip the arithmetic.  Work
+// split, ring, swizzles, scale table and XCD-aware workgroup order are those
+// of k_gemm_stream.
+template <int EPI, int RT, int NS = 3>
+__global__ __launch_bounds__(256, 2) void k_gemm_stream4(const GemmArgs p) {
+  constexpr int TN = 4, WB = 32, CPR = 2;  // int4: 32 B per channel per 64-k chunk
+  constexpr int ROWS = RT * 16;
+  constexpr int W_BYTES = 256 * WB, A_BYTES = ROWS * 128, STAGE = W_BYTES + A_BYTES;
+  constexpr int W_LD = W_BYTES / 4096;
+  constexpr int SC_BYTES = kStreamScaleMax * 4;
+  static_assert(RT % 2 == 0 && RT >= 4 && RT <= 6, "whole DMA instructions per wave");
+  static_assert(NS * STAGE + SC_BYTES <= 80 * 1024, "two workgroups per CU");
+  static_assert(EPI != EPI_SWIGLU || TN == 4, "SwiGLU pairs channel c with c + 32");
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE + SC_BYTES];
+  float* sc = reinterpret_cast<float*>(ring + NS * STAGE);
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int q = lane >> 4, l16 = lane & 15;
+  int g, nb;
+  {
+    const int S = gridDim.x, T = S * gridDim.y;
+    const int bid = blockIdx.x + S * blockIdx.y;
+    const int x = bid & 7, local = bid >> 3, base = T >> 3, rem = T & 7;
+    const int logical = x * base + min(x, rem) + local;
+    g = logical / S;
+    nb = (logical - g * S) * 256;
+  }
+  int r_lo, r_hi;
+  if (p.G == 0) {
+    r_lo = 0;
+    r_hi = p.single_rows;
+  } else {
+    r_lo = p.grp_off[g];
+    r_hi = p.grp_off[g + 1];
+  }
+  if (r_hi <= r_lo) return;  // workgroup-uniform, before any barrier
+  const int KC = p.K / 64;
+  const int ng = p.K / p.group_size;
+  const int gshift = __builtin_ctz(p.group_size);  // power of two, >= 16 (launcher)
+  // the A rows of the first pass, requested beside the scales (its first
+  // DMA needs them)
+  int arow0[RT / 2];
+#pragma unroll
+  for (int j = 0; j < RT / 2; ++j) {
+    const int r = 8 * (4 * j + wave) + (lane >> 3);
+    const int pr = r_lo + r < r_hi ? r_lo + r : r_lo;
+    arow0[j] = p.a_rows ? p.a_rows[pr] : pr;
+  }
+  // the strip's group scales, channel-major [256][ng]: one contiguous run of
+  // the scale array (channels past N_out read the last channel's).  The
+  // loads are unconditional (indices clamped) and converted only after the
+  // last one is issued, so all are in flight at once; a guarded load with
+  // its conversion waits in its own block, one round trip per entry.
+  {
+    constexpr int SCJ = kStreamScaleMax / 256;
+    float scv[SCJ];
+    const int64_t sb = g * p.s_gstride + static_cast<int64_t>(nb) * ng;
+    const int last = (min(p.N_out, nb + 256) - nb) * ng - 1;
+    if (p.s_f16) {
+      const _Float16* s16 = reinterpret_cast<const _Float16*>(p.S) + sb;
+      _Float16 hv[SCJ];
+#pragma unroll
+      for (int j = 0; j < SCJ; ++j) hv[j] = s16[min(tid + 256 * j, last)];
+#pragma unroll
+      for (int j = 0; j < SCJ; ++j) scv[j] = static_cast<float>(hv[j]);
+    } else {
+      const float* s32 = reinterpret_cast<const float*>(p.S) + sb;
+#pragma unroll
+      for (int j = 0; j < SCJ; ++j) scv[j] = s32[min(tid + 256 * j, last)];
+    }
+#pragma unroll
+    for (int j = 0; j < SCJ; ++j)
+      if (tid + 256 * j < 256 * ng) sc[tid + 256 * j] = scv[j];
+  }
+  const bool live = nb + 64 * wave < p.N_out;  // wave-uniform: some channel of this wave is stored
+  const uint8_t* wsrc[W_LD];
+#pragma unroll
+  for (int j = 0; j < W_LD; ++j) {
+    const int b = (4 * j + wave) * 1024 + 16 * lane;
+    const int row = b / WB, pc = (b % WB) >> 4;
+    const int lc = sw_chunk<CPR>(row, pc);
+    const int n = min(nb + row, p.N_out - 1);  // channels past N_out: loaded, never stored
+    wsrc[j] = reinterpret_cast<const uint8_t*>(p.W) +
+              (g * p.w_gstride + static_cast<int64_t>(n) * p.ldw) / 2 + lc * 16;
+  }
+  const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A);
+  for (int m0 = r_lo; m0 < r_hi; m0 += ROWS) {  // passes (uniform)
+    auto pass = [&](auto live_tiles) {
+      constexpr int L = decltype(live_tiles)::value;  // live 16-row tiles of this pass
+      constexpr int A_LD = (L + 1) / 2, LD = W_LD + A_LD;  // a DMA instruction of the 4 waves: 32 rows
+      const uint16_t* asrc[A_LD];
+#pragma unroll
+      for (int j = 0; j < A_LD; ++j) {
+        const int r = 8 * (4 * j + wave) + (lane >> 3);
+        const int pr = m0 + r < r_hi ? m0 + r : r_lo;  // rows past the group: valid, never stored
+        const int ar = m0 == r_lo ? arow0[j] : (p.a_rows ? p.a_rows[pr] : pr);
+        asrc[j] = A + static_cast<int64_t>(ar) * p.lda + (sw_chunk<8>(r, lane & 7) << 3);
+      }
+      auto issue = [&](int kc) {  // DMA of chunk kc into ring slot kc % NS
+        uint8_t* base = ring + (kc % NS) * STAGE;
+#pragma unroll
+        for (int j = 0; j < W_LD; ++j)
+          __builtin_amdgcn_global_load_lds((gbl_vptr)(wsrc[j] + static_cast<int64_t>(kc) * WB),
+                                           (lds_vptr)(base + (4 * j + wave) * 1024), 16, 0, 0);
+#pragma unroll
+        for (int j = 0; j < A_LD; ++j)
+          __builtin_amdgcn_global_load_lds((gbl_vptr)(asrc[j] + kc * 64),
+                                           (lds_vptr)(base + W_BYTES + (4 * j + wave) * 1024), 16,
+                                           0, 0);
+      };
+      f32x4 acc[TN][L];
+#pragma unroll
+      for (int t = 0; t < TN; ++t)
+#pragma unroll
+        for (int rt = 0; rt < L; ++rt) acc[t][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      // prologue: chunks 0 .. NS-2 in flight, chunk 0 landed everywhere
+#pragma unroll
+      for (int st = 0; st < NS - 1; ++st)
+        if (st < KC) issue(st);
+      if (KC >= NS - 1) wait_vmcnt<(NS - 2) * LD>();
+      else wait_vmcnt<0>();
+      wait_lgkm0();  // the scale table is written
+      __builtin_amdgcn_s_barrier();
+      for (int kc = 0; kc < KC; ++kc) {
+        if (kc > 0) {
+          if (kc + NS - 2 < KC) wait_vmcnt<(NS - 2) * LD>();
+          else wait_vmcnt<0>();
+          wait_lgkm0();
+          __builtin_amdgcn_s_barrier();
+        }
+        if (kc + NS - 1 < KC) issue(kc + NS - 1);  // into the slot chunk kc-1 used
+        if (!live) continue;
+        const uint8_t* sw = ring + (kc % NS) * STAGE;
+        const uint8_t* sa = sw + W_BYTES;
+        const int kg = (kc * 64 + 16 * q) >> gshift;  // scale group of this lane's 16 k
+        WRaw<SMOE_INT4> wr[TN];
+#pragma unroll
+        for (int t = 0; t < TN; ++t) {
+          const int row = wave * 64 + t * 16 + l16;
+          wr[t].a = *reinterpret_cast<const u32x2*>(sw + row * WB + (sw_chunk<CPR>(row, q >> 1) << 4) +
+                                                    ((q & 1) << 3));
+          wr[t].s = sc[row * ng + kg];
+        }
+        bf16x8 alo[L], ahi[L];
+#pragma unroll
+        for (int rt = 0; rt < L; ++rt) {
+          const int r = rt * 16 + l16;
+          alo[rt] = *reinterpret_cast<const bf16x8*>(sa + r * 128 + (sw_chunk<8>(r, 2 * q) << 4));
+          ahi[rt] = *reinterpret_cast<const bf16x8*>(sa + r * 128 + (sw_chunk<8>(r, 2 * q + 1) << 4));
+        }
+        bf16x8 wlo, whi;
+        skinny_wconv<SMOE_INT4>(wr[0], wlo, whi);
+#pragma unroll
+        for (int t = 0; t < TN; ++t) {
+          bf16x8 nlo = wlo, nhi = whi;
+          if (t + 1 < TN) skinny_wconv<SMOE_INT4>(wr[t + 1], nlo, nhi);  // beside tile t's MFMAs
+#pragma unroll
+          for (int rt = 0; rt < L; ++rt) {
+            acc[t][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wlo, alo[rt], acc[t][rt], 0, 0, 0);
+            acc[t][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(whi, ahi[rt], acc[t][rt], 0, 0, 0);
+          }
+          wlo = nlo;
+          whi = nhi;
+        }
+      }
+      // lane: channels nb + 64 wave + 16 t + 4 q + (0..3) of row m0 + 16 rt + l16.
+      // Its bias values and row weights are loaded before any math (one
+      // memory round trip), at clamped indices for rows / channels never
+      // stored.
+      if (!live) return;
+      constexpr bool HAS_RS = EPI == EPI_DOWN || EPI == EPI_ROWSCALE;
+      f32x4 bq[TN];
+#pragma unroll
+      for (int t = 0; t < TN; ++t) {
+        const int c = min(nb + wave * 64 + 16 * t + 4 * q, p.N_out - 4);
+        const int b0 = EPI == EPI_SWIGLU ? (c >> 6) * 32 + (c & 31) : c;
+        bq[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (EPI != EPI_ROWSCALE && (EPI != EPI_SWIGLU || t < 2) && p.bias)
+          bq[t] = *reinterpret_cast<const f32x4*>(p.bias + g * p.bias_gstride + b0);
+      }
+      float rsv[L];
+#pragma unroll
+      for (int rt = 0; rt < L; ++rt)
+        rsv[rt] = HAS_RS ? p.row_scale[min(m0 + rt * 16 + l16, r_hi - 1)] : 1.f;
+      // Stores count in vmcnt too: with a load still outstanding at a join
+      // below, the compiler's wait there would also drain every store before
+      // it.  One explicit wait here, and the output type resolved outside
+      // the loops, leave the stores unserialised.
+      wait_vmcnt<0>();
+      auto emit = [&](auto f32_out) {
+#pragma unroll
+        for (int rt = 0; rt < L; ++rt) {
+          const int row = m0 + rt * 16 + l16;
+          if (row >= r_hi) continue;
+#pragma unroll
+          for (int t = 0; t < TN; ++t) {
+            const int c = nb + wave * 64 + 16 * t + 4 * q;
+            if (c >= p.N_out || (EPI == EPI_SWIGLU && t >= 2)) continue;
+            const f32x4 v = acc[t][rt];
+            float o[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              if constexpr (EPI == EPI_SWIGLU) o[i] = silu(v[i]) * (acc[t + 2][rt][i] + bq[t][i]);
+              else if constexpr (EPI == EPI_GELU) o[i] = gelu_erf(v[i] + bq[t][i]);
+              else if constexpr (EPI == EPI_DOWN) o[i] = (v[i] + bq[t][i]) * rsv[rt];
+              else if constexpr (EPI == EPI_ROWSCALE) o[i] = v[i] * rsv[rt];
+              else o[i] = v[i] + bq[t][i];  // EPI_F32_BIAS
+            }
+            const int col = EPI == EPI_SWIGLU ? (c >> 6) * 32 + (c & 31) : c;
+            const int64_t off = static_cast<int64_t>(row) * p.ldo + col;
+            if constexpr (decltype(f32_out)::value)
+              *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + off) = f32x4{o[0], o[1], o[2], o[3]};
+            else
+              *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + off) =
+                  u32x2{pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3])};
+          }
+        }
+      };
+      if (EPI == EPI_F32_BIAS || p.out_dtype == SMOE_F32) emit(std::true_type{});
+      else emit(std::false_type{});
+    };
+    const int live_rt = min(RT, (r_hi - m0 + 15) >> 4);  // uniform
+    switch (live_rt) {  // one instantiation per live tile count
+      case 1: pass(std::integral_constant<int, 1>{}); break;
+      case 2: pass(std::integral_constant<int, 2>{}); break;
+      case 3: pass(std::integral_constant<int, 3>{}); break;
+      case 4: pass(std::integral_constant<int, 4>{}); break;
+      case 5: pass(std::integral_constant<int, RT >= 5 ? 5 : RT>{}); break;
+      default: pass(std::integral_constant<int, RT>{}); break;
+    }
+    if (m0 + ROWS < r_hi) {  // another pass: every wave is done with the ring
+      wait_lgkm0();
+      __builtin_amdgcn_s_barrier();
+    }
+  }
+}
+
 // ------------------------------------------------- fp32 / any shape ----
 // SIMT tile GEMM with fp32 FMAs: the fp32 models' path (FMT = SMOE_F32, A
 // and W fp32) and the fallback for bf16 shapes the MFMA kernels do not take
@@ -1985,6 +2231,20 @@ int launch_stream_fmt(const GemmArgs& a, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 
+template <int RT, int NS = 3>
+int launch_stream4(const GemmArgs& a, hipStream_t s) {
+  const dim3 grid((a.N_out + 255) / 256, a.G == 0 ? 1 : a.G), block(256);
+  switch (a.epi) {
+    case EPI_F32_BIAS: SMOE_LAUNCH((k_gemm_stream4<EPI_F32_BIAS, RT, NS>), grid, block, 0, s, a); break;
+    case EPI_ROWSCALE: SMOE_LAUNCH((k_gemm_stream4<EPI_ROWSCALE, RT, NS>), grid, block, 0, s, a); break;
+    case EPI_GELU: SMOE_LAUNCH((k_gemm_stream4<EPI_GELU, RT, NS>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU: SMOE_LAUNCH((k_gemm_stream4<EPI_SWIGLU, RT, NS>), grid, block, 0, s, a); break;
+    case EPI_DOWN: SMOE_LAUNCH((k_gemm_stream4<EPI_DOWN, RT, NS>), grid, block, 0, s, a); break;
+    default: return SMOE_EINVAL;
+  }
+  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
 // Two workgroups per CU (one's dequant and waits overlap the other's MFMAs):
 // LDS per workgroup int4 3 x 20 KB + 16 KB scales, fp8 3 x 24 KB (64-row
 // passes), bf16 3 x 40 KB (one workgroup per CU).
@@ -1995,7 +2255,7 @@ int launch_stream(const GemmArgs& a, hipStream_t s) {
     case SMOE_INT4:
       if (256 * (a.K / a.group_size) > kStreamScaleMax || (a.group_size & (a.group_size - 1)))
         return SMOE_EUNSUPPORTED;
-      return launch_stream_fmt<SMOE_INT4, 6, 3, 2>(a, s);
+      return launch_stream4<6>(a, s);
     default: return SMOE_EUNSUPPORTED;
   }
 }
@@ -2007,6 +2267,7 @@ bool stream_aligned(const GemmArgs& a) {
   const int walign = a.fmt == SMOE_BF16 ? 8 : 16;  // elements per aligned load
   if (a.ldw % walign || a.w_gstride % walign) return false;
   if (a.fmt == SMOE_INT4 && a.group_size % 16) return false;
+  if (a.bias && a.bias_gstride % 4) return false;  // 16-byte bias loads (int4 epilogue)
   return a.fmt == SMOE_BF16 || a.fmt == SMOE_FP8_E4M3 || a.fmt == SMOE_INT4;
 }
 
@@ -2133,8 +2394,9 @@ int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
     // between more rows
     return rpg <= 8 || a.G == 0 ? launch_skinny<4, 1>(a, s) : launch_skinny<4, 2>(a, s);
   }
-  // a few dozen to 128 rows per group (mixed decode + prefill): weights
-  // streamed into registers, activations through LDS
+  // a few dozen to 128 rows per group (mixed decode + prefill): one
+  // workgroup per (group, 256-channel strip) over all the group's rows,
+  // weights and activations streamed through an LDS ring
   {
     const int rpg = a.G == 0 ? a.single_rows : a.max_rows / a.G;
     if (a.G > 0 && rpg <= 128 && a.N_out >= 128 && stream_aligned(a) &&

@@ -437,6 +437,54 @@ def test_large_int4_experts_ragged_groups(act, n):
         assert (out - ref).abs().max() <= 2e-2 * scale + 1e-6, float((out - ref).abs().max() / scale)
 
 
+@pytest.mark.parametrize("act,group,sdt", [("gelu", 32, torch.float32), ("gelu", 128, torch.float16),
+                                           ("swiglu", 64, torch.float16)])
+def test_stream_int4_experts_ragged_passes(act, group, sdt):
+    """int4 experts at the weight-streaming GEMM's row counts (60 rows per
+    expert on average) with groups of 0, 1, 18, 96, 97 and 150 rows: one
+    pass of 1, 2 and 6 live 16-row tiles, two passes with a 1-row and a
+    54-row second pass; U = 640 leaves half of the last 256-channel strip
+    (GELU up, 640 channels) past N_out, H = 384 half of the down GEMM's."""
+    from spider_moe_amd.quant import interleave_gate_up, quantize_int4
+    n8 = nat()
+    say("stream int4 experts", act, group, sdt)
+    h, u, e, k = 384, 640, 6, 2
+    counts = [0, 1, 18, 96, 97, 150]
+    flat = torch.tensor(sum(([x] * c for x, c in enumerate(counts)), []))
+    n = flat.numel() // k
+    idx = torch.stack([flat[:n], flat[n:]], 1)  # two different experts per token
+    assert (idx[:, 0] != idx[:, 1]).all()
+    g = torch.Generator().manual_seed(41)
+    w = torch.rand(n, k, generator=g)
+    msg = torch.randn(n, h, generator=g).to(torch.bfloat16)
+    nup = 2 * u if act == "swiglu" else u
+    qu = quantize_int4(torch.randn(e, nup, h, generator=g) * 0.05, group, sdt)
+    qd = quantize_int4(torch.randn(e, h, u, generator=g) * 0.04, group, sdt)
+    wu_f = torch.from_numpy(Q.int4_dequantize(qu.packed.numpy(), qu.scales.float().numpy(), group))
+    wd_f = torch.from_numpy(Q.int4_dequantize(qd.packed.numpy(), qd.scales.float().numpy(), group))
+    bu = torch.randn(e, u, generator=g) * 0.1
+    bd = torch.randn(e, h, generator=g) * 0.1
+    if act == "swiglu":
+        ref = _oracle_delta(msg.float(), idx, w, wu_f[:, u:], bu, wd_f, bd, w_gate=wu_f[:, :u])
+        pu = interleave_gate_up(qu.packed[:, :u], qu.packed[:, u:])
+        su = interleave_gate_up(qu.scales[:, :u], qu.scales[:, u:])
+        actc = n8.ACT_SWIGLU
+    else:
+        ref = _oracle_delta(msg.float(), idx, w, wu_f, bu, wd_f, bd)
+        pu, su = qu.packed, qu.scales
+        actc = n8.ACT_GELU
+    t = [x.contiguous().to(dev) for x in (pu, qd.packed, su, qd.scales, bu, bd)]
+    ex = _experts_struct(n8, n8.INT4, actc, e, h, u, t[0], t[1], s_up=t[2], s_down=t[3],
+                         b_up=t[4], b_down=t[5], group=group,
+                         scale_dtype=n8.F16 if sdt == torch.float16 else n8.F32)
+    got = _run_delta(n8, ex, msg.to(dev), idx.to(torch.int32).to(dev), w.to(dev))
+    scale = ref.abs().max()
+    assert torch.isfinite(got).all()
+    assert (got - ref).abs().max() <= 1e-2 * scale + 1e-6, float((got - ref).abs().max() / scale)
+    one = (idx == 1).any(1)  # the token of the one-row expert
+    assert one.sum() == 1 and (got[one] - ref[one]).abs().max() <= 1e-2 * scale + 1e-6
+
+
 @pytest.mark.parametrize("group,sdt", [(32, torch.float32), (128, torch.float16)])
 def test_int4_experts_match_oracle(group, sdt):
     from spider_moe_amd.quant import quantize_int4
