@@ -1328,52 +1328,59 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) acc[t][rt] += red[wave + j][t * RT + rt][lane];
   }
-  // lane: channels c0[t] + 4 q + (0..3) of row r_lo + 16 rt + l16
-  const bool f32o = EPI == EPI_F32_BIAS || p.out_dtype == SMOE_F32;
-  auto put4 = [&](int row, int col, const float (&o)[4]) {
-    const int64_t off = static_cast<int64_t>(row) * p.ldo + col;
-    if (f32o)
-      *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + off) = f32x4{o[0], o[1], o[2], o[3]};
-    else
-      *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + off) =
-          u32x2{pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3])};
-  };
+  // lane: channels c0[t] + 4 q + (0..3) of row r_lo + 16 rt + l16.
+  // Stores count in vmcnt too: one explicit wait for the epilogue operands
+  // here, and the output type resolved outside the loops, keep the compiler
+  // from draining each store before the next.
+  wait_vmcnt<0>();
+  auto emit = [&](auto f32_out) {
+    auto put4 = [&](int row, int col, const float (&o)[4]) {
+      const int64_t off = static_cast<int64_t>(row) * p.ldo + col;
+      if constexpr (decltype(f32_out)::value)
+        *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + off) = f32x4{o[0], o[1], o[2], o[3]};
+      else
+        *reinterpret_cast<u32x2*>(reinterpret_cast<uint16_t*>(p.out) + off) =
+            u32x2{pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3])};
+    };
 #pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const int row = r_lo + 16 * rt + l16;
-    if (row >= r_hi) continue;
-    if constexpr (EPI == EPI_SWIGLU) {
+    for (int rt = 0; rt < RT; ++rt) {
+      const int row = r_lo + 16 * rt + l16;
+      if (row >= r_hi) continue;
+      if constexpr (EPI == EPI_SWIGLU) {
 #pragma unroll
-      for (int t = 0; t < TNW / 2; ++t) {  // gate tile t, up tile t + TNW / 2
-        const int c = c0[t] + 4 * q;
-        if (c >= p.N_out) continue;
-        float o[4];
+        for (int t = 0; t < TNW / 2; ++t) {  // gate tile t, up tile t + TNW / 2
+          const int c = c0[t] + 4 * q;
+          if (c >= p.N_out) continue;
+          float o[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float gs = acc[t][rt][i] * esc[t][i];
-          const float us = acc[t + TNW / 2][rt][i] * esc[t + TNW / 2][i] + ebi[t][i];
-          o[i] = silu(gs) * us;
+          for (int i = 0; i < 4; ++i) {
+            const float gs = acc[t][rt][i] * esc[t][i];
+            const float us = acc[t + TNW / 2][rt][i] * esc[t + TNW / 2][i] + ebi[t][i];
+            o[i] = silu(gs) * us;
+          }
+          put4(row, (c >> 6) * 32 + (c & 31), o);
         }
-        put4(row, (c >> 6) * 32 + (c & 31), o);
-      }
-    } else {
+      } else {
 #pragma unroll
-      for (int t = 0; t < TNW; ++t) {
-        const int c = c0[t] + 4 * q;
-        if (c >= p.N_out) continue;
-        float o[4];
+        for (int t = 0; t < TNW; ++t) {
+          const int c = c0[t] + 4 * q;
+          if (c >= p.N_out) continue;
+          float o[4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float a = acc[t][rt][i];
-          if constexpr (EPI == EPI_ROWSCALE) o[i] = a * ers[rt];
-          else if constexpr (EPI == EPI_GELU) o[i] = gelu_erf(a * esc[t][i] + ebi[t][i]);
-          else if constexpr (EPI == EPI_DOWN) o[i] = (a * esc[t][i] + ebi[t][i]) * ers[rt];
-          else o[i] = a * esc[t][i] + ebi[t][i];  // EPI_F32_BIAS
+          for (int i = 0; i < 4; ++i) {
+            const float a = acc[t][rt][i];
+            if constexpr (EPI == EPI_ROWSCALE) o[i] = a * ers[rt];
+            else if constexpr (EPI == EPI_GELU) o[i] = gelu_erf(a * esc[t][i] + ebi[t][i]);
+            else if constexpr (EPI == EPI_DOWN) o[i] = (a * esc[t][i] + ebi[t][i]) * ers[rt];
+            else o[i] = a * esc[t][i] + ebi[t][i];  // EPI_F32_BIAS
+          }
+          put4(row, c, o);
         }
-        put4(row, c, o);
       }
     }
-  }
+  };
+  if (EPI == EPI_F32_BIAS || p.out_dtype == SMOE_F32) emit(std::true_type{});
+  else emit(std::false_type{});
 }
 
 // ------------------------------------------------------- weight stream ----
