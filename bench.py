@@ -47,7 +47,7 @@ GEMM_STAGES = ("edge_gemm", "up_gemm", "down_gemm")
 # group, N_out, format); rocprof summaries under profiles/ name them too
 GEMM_KERNEL = {
     ("c1", "up_gemm"): "k_gemm_pp<4,4,SwiGLU,320> (bf16 weight tiles, 8-wave ping-pong, LDS-DMA ring)",
-    ("c1", "down_gemm"): "k_gemm_pp<4,4,down,320> (bf16 weight tiles, 8-wave ping-pong, LDS-DMA ring)",
+    ("c1", "down_gemm"): "k_gemm_pp<4,4,down,320> (bf16 weight tiles, activations in the row-tile layout, 8-wave ping-pong, LDS-DMA ring)",
     ("c1", "edge_gemm"): "k_gemm_pp<4,4,rowscale,256> (bf16 weight tiles, 8-wave ping-pong, LDS-DMA ring)",
     ("c2", "up_gemm"): "k_gemm_decode<fp8,SwiGLU,4,1,2,3> (weight streaming, K split over 2 waves, 3-step register ring per wave)",
     ("c2", "down_gemm"): "k_gemm_decode<fp8,down,4,1,4,3> (weight streaming, K split over 4 waves)",
@@ -55,8 +55,8 @@ GEMM_KERNEL = {
     ("c3", "up_gemm"): "k_gemm_ring<128,3,4> (bf16 GELU, LDS-DMA ring, 2 workgroups/CU)",
     ("c3", "down_gemm"): "k_gemm_pp<4,4,down,320> (bf16 weight tiles, 8-wave ping-pong)",
     ("c3", "edge_gemm"): "k_gemm_pp<4,4,rowscale,256> (bf16 weight tiles, 8-wave ping-pong)",
-    ("c4", "up_gemm"): "k_gemm_stream<int4,GELU,6,3,2> (weight streaming, both operands by LDS-DMA ring, 2 workgroups/CU)",
-    ("c4", "down_gemm"): "k_gemm_stream<int4,down,6,3,2> (weight streaming, 2 workgroups/CU)",
+    ("c4", "up_gemm"): "k_gemm_stream4<GELU,6,3> (int4 weight streaming, dequant beside the MFMAs, LDS-DMA ring, 2 workgroups/CU)",
+    ("c4", "down_gemm"): "k_gemm_stream4<down,6,3> (int4 weight streaming, dequant beside the MFMAs, 2 workgroups/CU)",
     ("c4", "edge_gemm"): "k_gemm_pp<4,4,rowscale,320> (bf16 weight tiles, 320-row tiles: one per destination)",
 }
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.md")
