@@ -509,7 +509,7 @@ def test_int4_experts_match_oracle(group, sdt):
 
 
 @pytest.mark.parametrize("shape", [(24, 384, 640, 8), (60, 384, 640, 8), (40, 768, 1664, 4),
-                                   (20, 256, 640, 8)])
+                                   (20, 256, 640, 8), (180, 384, 640, 6)])
 @pytest.mark.parametrize("fmt,act", [("bf16", "gelu"), ("bf16", "swiglu"), ("fp8", "gelu"),
                                      ("fp8", "swiglu"), ("int4-g32-f32", "gelu"),
                                      ("int4-g128-f16", "gelu")])
@@ -519,7 +519,10 @@ def test_decode_experts_match_oracle(fmt, act, shape):
     64: no split), 384 (6) and 768 (12), down K = 640 (10) and 1664 (26:
     parts of 6 and 7 steps, so the ring's main loop runs); 16-row tiles (6
     rows per expert on average) and 32-row tiles (15 and 20); an expert with
-    more rows than one tile holds, an empty expert, a one-row expert."""
+    more rows than one tile holds, an empty expert, a one-row expert.  At
+    (180, 384, 640, 6) the experts hold 60 rows on average, the shape of the
+    medium-size stream GEMMs (a 256-channel strip over all of an expert's
+    rows), and expert 0's 180 rows take several passes."""
     from spider_moe_amd.quant import interleave_gate_up, interleave_gate_up_rows, quantize_int4
     n8 = nat()
     say("decode experts", fmt, act, shape)
