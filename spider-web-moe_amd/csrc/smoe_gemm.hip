@@ -1384,18 +1384,18 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
 }
 
 // ------------------------------------------------------- weight stream ----
-// Medium rows per group (a few dozen to ~128: mixed decode + prefill steps,
-// quantized experts).  The weights dominate the traffic and every weight is
+// Medium rows per group (a few dozen to ~128: mixed decode + prefill steps),
+// bf16 and fp8 weights (int4: k_gemm_stream4 below, the same work split).
+// The weights dominate the traffic and every weight is
 // used by all rows of its group, so a workgroup owns one group, a strip of
 // 256 output channels (wave w: channels 64 w .. 64 w + 63, four 16-channel
 // MFMA tiles) and the group's rows in passes of RT*16.  Both operands stream
 // global -> LDS by DMA (global_load_lds_dwordx4) through an NS-stage ring of
 // 64-wide K chunks, so the main loop's only vector-memory operations are the
 // DMAs and the explicit vmcnt waits stay exact:
-//   weights:     256 channel rows x 64 k in storage format (int4 32 B, fp8
-//                64 B, bf16 128 B per row); a lane reads the 16 k at
-//                16*(lane/16) of its channel and widens them to bf16 (int4:
-//                with the group scale from an LDS table of the strip)
+//   weights:     256 channel rows x 64 k in storage format (fp8 64 B, bf16
+//                128 B per row); a lane reads the 16 k at 16*(lane/16) of
+//                its channel and widens them to bf16
 //   activations: RT*16 rows x 64 k bf16 (128 B rows)
 //   MFMAs:       the step's two MFMAs take the low and the high 8 of the 16 k
 //                (the same permutation for both operands).
@@ -1429,12 +1429,8 @@ __global__ __launch_bounds__(256, WGS) void k_gemm_stream(const GemmArgs p) {
   static_assert(W_BYTES % 4096 == 0 && A_BYTES % 4096 == 0, "whole DMA instructions per wave");
   static_assert(NS >= 3, "ring depth");
   static_assert(EPI != EPI_SWIGLU || TN == 4, "SwiGLU pairs channel c with c + 32");
-  // one LDS object: the ring, then the int4 scale table (with a second LDS
-  // object the compiler waits for every outstanding DMA before reads of the
-  // table, draining the ring's prefetch)
-  constexpr int SC_BYTES = (FMT == SMOE_INT4 ? kStreamScaleMax : 1) * 4;
-  __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE + SC_BYTES];
-  float* sc = reinterpret_cast<float*>(ring + NS * STAGE);
+  static_assert(FMT == SMOE_BF16 || FMT == SMOE_FP8_E4M3, "int4: k_gemm_stream4");
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int q = lane >> 4, l16 = lane & 15;
@@ -1461,15 +1457,6 @@ __global__ __launch_bounds__(256, WGS) void k_gemm_stream(const GemmArgs p) {
   }
   if (r_hi <= r_lo) return;  // workgroup-uniform, before any barrier
   const int KC = p.K / 64;
-  const int ng = FMT == SMOE_INT4 ? p.K / p.group_size : 1;
-  const int gshift = FMT == SMOE_INT4 ? __builtin_ctz(p.group_size) : 0;  // power of two (launcher)
-  if constexpr (FMT == SMOE_INT4) {  // the strip's group scales, channel-major
-    for (int i = tid; i < 256 * ng; i += 256) {
-      const int ch = i / ng, kg = i - ch * ng;
-      const int n = min(nb + ch, p.N_out - 1);
-      sc[i] = load_scale(p.S, g * p.s_gstride + static_cast<int64_t>(n) * ng + kg, p.s_f16);
-    }
-  }
   // weight DMA: instruction j of wave w fills bytes [(4 j + w) KB, +1 KB) of
   // the stage's weight region; lane l writes byte b = that + 16 l, i.e. row
   // b / WB, physical chunk (b % WB) / 16 (which holds the logical chunk the
@@ -1534,7 +1521,6 @@ __global__ __launch_bounds__(256, WGS) void k_gemm_stream(const GemmArgs p) {
       if (kc + NS - 1 < KC) issue(kc + NS - 1);  // into the slot chunk kc-1 used
       const uint8_t* sw = ring + (kc % NS) * STAGE;
       const uint8_t* sa = sw + W_BYTES;
-      const int kg = (kc * 64 + 16 * q) >> gshift;  // int4 scale group of this lane's 16 k
       bf16x8 wlo[TN], whi[TN];
 #pragma unroll
       for (int t = 0; t < TN; ++t) {
@@ -1543,12 +1529,8 @@ __global__ __launch_bounds__(256, WGS) void k_gemm_stream(const GemmArgs p) {
         if constexpr (FMT == SMOE_BF16) {
           r.a = *reinterpret_cast<const u32x4*>(sw + row * WB + (sw_chunk<CPR>(row, 2 * q) << 4));
           r.b = *reinterpret_cast<const u32x4*>(sw + row * WB + (sw_chunk<CPR>(row, 2 * q + 1) << 4));
-        } else if constexpr (FMT == SMOE_FP8_E4M3) {
-          r.a = *reinterpret_cast<const u32x4*>(sw + row * WB + (sw_chunk<CPR>(row, q) << 4));
         } else {
-          r.a = *reinterpret_cast<const u32x2*>(sw + row * WB + (sw_chunk<CPR>(row, q >> 1) << 4) +
-                                                ((q & 1) << 3));
-          r.s = sc[row * ng + kg];
+          r.a = *reinterpret_cast<const u32x4*>(sw + row * WB + (sw_chunk<CPR>(row, q) << 4));
         }
         skinny_wconv<FMT>(r, wlo[t], whi[t]);
       }
@@ -1612,8 +1594,11 @@ __global__ __launch_bounds__(256, WGS) void k_gemm_stream(const GemmArgs p) {
 // count, chosen per pass), so tiles past the group's last row issue neither
 // MFMAs nor activation DMA, and the loop body has no branches to split it.
 // Waves whose 64 channels all lie past N_out skip the arithmetic.  Work
-// split, ring, swizzles, scale table and XCD-aware workgroup order are those
-// of k_gemm_stream.
+// split, ring, swizzles and XCD-aware workgroup order are those
+// of k_gemm_stream; the strip's group scales sit in an LDS table after the
+// ring, in the same LDS object (with a second LDS object the compiler waits
+// for every outstanding DMA before reads of the table, draining the ring's
+// prefetch).
 template <int EPI, int RT, int NS = 3>
 __global__ __launch_bounds__(256, 2) void k_gemm_stream4(const GemmArgs p) {
   constexpr int TN = 4, WB = 32, CPR = 2;  // int4: 32 B per channel per 64-k chunk
