@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define SMOE_ABI_VERSION 7
+#define SMOE_ABI_VERSION 8
 
 /* status codes (spider_kernels.h convention; see scalar.cpp:9,45,58) */
 #define SMOE_OK 0
