@@ -220,11 +220,12 @@ def run_workload(name, steps, warmup):
         # events (hipExtLaunchKernelGGL: the interval is the kernel's
         # execution); those launches cost the host ~15 us each, so the step
         # time comes from pass 1
-        dom_timer = nat.StageTimer(stages=[dom], capacity=steps * r + 16)
+        dom_timer = nat.StageTimer(stages=[dom], capacity=steps * r + 16, clock=True)
         dom_timer.start()
         for _ in range(steps):
             layer.forward_loops(h, x0, 0, r)
         dom_ms_list = dom_timer.stop().get(dom, [])
+        sclk = dom_timer.sclk_mhz()
         dom_timer.close()
         # pass 4 (weight-streaming GEMMs): the same launches with the 256 MB
         # Infinity Cache (MALL) evicted before every loop by a 1 GiB read, so
@@ -263,6 +264,10 @@ def run_workload(name, steps, warmup):
                  "kernel": GEMM_KERNEL.get((name, dom), dom),
                  "work_per_launch": f"{g_flops:.4g} flop, {g_bytes:.4g} B",
                  "avg_launch_ms": round(dom_ms, 4)})
+    if sclk is not None:
+        # the shader clock of the kernel's tiles (in-kernel s_memtime against
+        # the 100 MHz s_memrealtime); the peak assumes 2400 MHz
+        roof["sclk_mhz"] = round(sclk, 1)
     if cold_ms_list:
         cold_ms = sum(cold_ms_list) / len(cold_ms_list)
         cold = g_bytes / (cold_ms * 1e-3) / 1e9

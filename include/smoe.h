@@ -44,6 +44,9 @@ extern "C" {
 #define SMOE_ECAPACITY 3
 #define SMOE_EUNSUPPORTED (-2)
 #define SMOE_EHIP 4
+/* smoe_block_forward_scratch only: an earlier call on this GPU, enqueued on
+ * another stream, has not finished (its static workspace is in use) */
+#define SMOE_EBUSY 5
 
 /* element formats */
 #define SMOE_F32 0
@@ -223,8 +226,12 @@ SMOE_API int smoe_block_forward_exit(const smoe_block* blk, const void* h_in, co
  * decode-size steps: 64 tokens of the H 1024, E 16, U 2816 block need about
  * 2 MiB.  Every call on a GPU shares that GPU's array (the kernels write
  * every workspace byte they read, so nothing is cleared between calls):
- * calls that overlap in time on one GPU (two streams or two host threads)
- * race and give wrong results, so serialize them.  The call runs on the
+ * calls that overlap in time on one GPU would race, so they are detected:
+ * a call on a stream other than the previous call's, made while that call
+ * is still running on the GPU, returns SMOE_EBUSY and launches nothing
+ * (host threads are serialized around the check and the enqueue).  Calls
+ * on one stream never overlap.  Under HIP graph capture the check is
+ * skipped: the captured graph orders its own nodes.  The call runs on the
  * current device and `stream` must belong to it.  Arguments and results as
  * smoe_block_forward, bit for bit; no hipMalloc / hipFree or other
  * allocating routine is called. */
@@ -411,10 +418,19 @@ SMOE_API int smoe_pack_int4_tiles(const void* packed, const void* scales, int sc
 /* When `events` is not NULL, every later smoe_block_forward records
  * events[2*i] before and events[2*i+1] after the i-th launch of a stage in
  * `stage_mask` (bit s = stage s), for i < capacity, on the call's stream.
- * Process-wide and not thread-safe; pass NULL to stop.  smoe_profile_count
- * returns how many pairs were recorded and resets the counter; stage_of[i]
- * (may be NULL) receives the stage of pair i. */
+ * The setting belongs to the calling thread: it arms that thread's later
+ * calls only, and each thread counts its own pairs.  Pass NULL to stop.
+ * smoe_profile_count returns how many pairs this thread recorded and resets
+ * its counter; stage_of[i] (may be NULL) receives the stage of pair i. */
 SMOE_API int smoe_profile_stages(uint32_t stage_mask, void** events, int capacity);
+/* When `counters` (device memory, 2 x uint64, zeroed by the caller) is not
+ * NULL, every profiled launch of a single-GEMM stage that runs on the
+ * 256-column ping-pong GEMM adds its workgroups' shader-clock cycles to
+ * counters[0] and their 100 MHz wall-clock ticks to counters[1]:
+ * counters[0] / counters[1] * 100 is the MHz those tiles ran at.  Per
+ * calling thread; NULL stops it.  Diagnostics; no counterpart in the
+ * reference. */
+SMOE_API int smoe_profile_clock(void* counters);
 SMOE_API int smoe_profile_count(int32_t* stage_of, int capacity);
 /* hipEvent helpers for callers without a HIP binding. */
 SMOE_API int smoe_events_create(int n, void** events);

@@ -316,6 +316,32 @@ def block_forward(h, x0, w: BlockWeights, loop_idx: int, *, mode: str = "faithfu
     return out, aux
 
 
+def block_stats(aux: BlockAux, num_experts: int, out, exit_w, exit_b, *, logit_bf16: bool = False):
+    """The return_stats branch of model.py:327-345 over one loop's routing
+    (aux of block_forward, every source's top-m edges) and its output h'
+    [N, H]: expert / edge load (bincount over top-k / every edge,
+    normalised by max(sum, 1)), edge importance (scatter-add of the edge
+    softmax weights, normalised by max(sum, 1e-9)), aux_loss =
+    E * sum(load * mean_t probs), edge_loss = E * sum(edge_load *
+    importance), confidence = sigmoid(exit_head(h')) [N]."""
+    e = int(num_experts)
+    load = torch.bincount(aux.top_i.reshape(-1), minlength=e).float()
+    load = load / load.sum().clamp_min(1.0)
+    edge_load = torch.bincount(aux.edge_idx.reshape(-1), minlength=e).float()
+    edge_load = edge_load / edge_load.sum().clamp_min(1.0)
+    imp = torch.zeros(e, dtype=torch.float32).scatter_add(0, aux.edge_idx.reshape(-1),
+                                                            aux.edge_w.reshape(-1).float())
+    imp = imp / imp.sum().clamp_min(1e-9)
+    probs_mean = aux.probs.reshape(-1, e).mean(dim=0)
+    return {
+        "expert_load": load,
+        "edge_load": edge_load,
+        "aux_loss": e * torch.sum(load * probs_mean),
+        "edge_loss": e * torch.sum(edge_load * imp),
+        "confidence": torch.sigmoid(exit_logit(out, exit_w, exit_b, bf16=logit_bf16)),
+    }
+
+
 def block_loops(h, x0, w: BlockWeights, num_loops: int, **kw):
     """model.py:445-448: run the shared block num_loops times."""
     for r in range(num_loops):

@@ -16,6 +16,7 @@
 #include <mutex>
 #include <string>
 #include <type_traits>
+#include <vector>
 
 #include "smoe_common.hpp"
 #include "smoe_internal.hpp"
@@ -41,16 +42,20 @@ int hip_rc(int rc, const char* what) {
 }
 
 // ---- stage profiling (diagnostics) ----
-uint32_t g_prof_mask = 0;
-hipEvent_t* g_prof_ev = nullptr;
-int g_prof_cap = 0;
-int g_prof_n = 0;
-int32_t g_prof_stage[1 << 16];
+// Per calling thread: smoe_profile_stages arms the calls this thread makes
+// afterwards, and two threads profiling their own calls do not see each
+// other's events (the library keeps no other process-wide state).
+thread_local uint32_t g_prof_mask = 0;
+thread_local hipEvent_t* g_prof_ev = nullptr;
+thread_local int g_prof_cap = 0;
+thread_local int g_prof_n = 0;
+thread_local std::vector<int32_t> g_prof_stage;
 
 }  // namespace
 
 namespace smoe {
-hipEvent_t g_launch_ev[2] = {nullptr, nullptr};
+thread_local hipEvent_t g_launch_ev[2] = {nullptr, nullptr};
+thread_local unsigned long long* g_clock_ctr = nullptr;
 }  // namespace smoe
 
 namespace {
@@ -69,7 +74,7 @@ struct StageScope {
   bool ext = false;
   hipStream_t s;
   StageScope(int stage, hipStream_t st) : s(st) {
-    if (g_prof_ev && (g_prof_mask >> stage & 1u) && g_prof_n < g_prof_cap && g_prof_n < (1 << 16)) {
+    if (g_prof_ev && (g_prof_mask >> stage & 1u) && g_prof_n < g_prof_cap) {
       i = g_prof_n++;
       g_prof_stage[i] = stage;
       ext = one_gemm_stage(stage);
@@ -621,11 +626,16 @@ namespace {
 // every later use (the kernels' workspace argument) goes through it.
 __device__ __align__(256) unsigned char scratch[SMOE_SCRATCH_BYTES];
 constexpr int kMaxDevices = 64;
-std::mutex g_scratch_mu;
+std::mutex g_scratch_mu;  // held from the overlap check to the last launch
 void* g_scratch_ptr[kMaxDevices] = {};
+// Per device: an event recorded after the last scratch call's launches, on
+// its stream (made once, at the device's first call), and that stream.
+hipEvent_t g_scratch_done[kMaxDevices] = {};
+hipStream_t g_scratch_stream[kMaxDevices] = {};
 
-// Device address of the current device's scratch array.
-int scratch_address(hipStream_t s, void** out) {
+// Device address of the current device's scratch array (the caller holds
+// g_scratch_mu), and that device's id.
+int scratch_address(hipStream_t s, void** out, int* dev_out) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return fail(SMOE_EHIP, "hipGetDevice");
   if (dev < 0 || dev >= kMaxDevices) return fail(SMOE_EINVAL, "device id beyond 64");
@@ -634,16 +644,20 @@ int scratch_address(hipStream_t s, void** out) {
     if (hipStreamGetDevice(s, &sdev) != hipSuccess) return fail(SMOE_EHIP, "hipStreamGetDevice");
     if (sdev != dev) return fail(SMOE_EINVAL, "stream is not on the current device");
   }
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (!g_scratch_ptr[dev]) {
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || !p)
       return fail(SMOE_EHIP, (std::string("hipGetSymbolAddress(scratch): ") +
                               hipGetErrorString(e)).c_str());
+    hipEvent_t ev = nullptr;
+    if (hipEventCreateWithFlags(&ev, hipEventDisableTiming) != hipSuccess)
+      return fail(SMOE_EHIP, "hipEventCreateWithFlags(scratch)");
+    g_scratch_done[dev] = ev;
     g_scratch_ptr[dev] = p;
   }
   *out = g_scratch_ptr[dev];
+  *dev_out = dev;
   return SMOE_OK;
 }
 }  // namespace
@@ -663,10 +677,27 @@ SMOE_API int smoe_block_forward_scratch(const smoe_block* b, const void* h_in, c
                                     .c_str());
   hipStream_t s = static_cast<hipStream_t>(stream);
   void* ws = nullptr;
-  const int arc = scratch_address(s, &ws);
+  int dev = 0;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  const int arc = scratch_address(s, &ws, &dev);
   if (arc != SMOE_OK) return arc;
-  return block_forward(b, h_in, x0, h_out, N, loop_begin, num_loops, nullptr, ws,
-                       SMOE_SCRATCH_BYTES, stream);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cap) != hipSuccess) return fail(SMOE_EHIP, "hipStreamIsCapturing");
+  const bool captured = cap != hipStreamCaptureStatusNone;
+  if (!captured && g_scratch_stream[dev] != s) {
+    const hipError_t q = hipEventQuery(g_scratch_done[dev]);
+    if (q == hipErrorNotReady)
+      return fail(SMOE_EBUSY, "the previous smoe_block_forward_scratch call on this GPU is still "
+                              "running on another stream");
+    if (q != hipSuccess) return fail(SMOE_EHIP, "hipEventQuery(scratch)");
+  }
+  const int rc2 = block_forward(b, h_in, x0, h_out, N, loop_begin, num_loops, nullptr, ws,
+                                SMOE_SCRATCH_BYTES, stream);
+  if (rc2 != SMOE_OK || captured) return rc2;
+  if (hipEventRecord(g_scratch_done[dev], s) != hipSuccess)
+    return fail(SMOE_EHIP, "hipEventRecord(scratch)");
+  g_scratch_stream[dev] = s;
+  return SMOE_OK;
 }
 
 SMOE_API int smoe_pack_weight_tiles(const void* w, int format, int G, int N, int K, void* out,
@@ -689,6 +720,12 @@ SMOE_API int smoe_profile_stages(uint32_t stage_mask, void** events, int capacit
   g_prof_ev = reinterpret_cast<hipEvent_t*>(events);
   g_prof_cap = events ? capacity : 0;
   g_prof_n = 0;
+  g_prof_stage.assign(static_cast<size_t>(g_prof_cap), 0);
+  return SMOE_OK;
+}
+
+SMOE_API int smoe_profile_clock(void* counters) {
+  g_clock_ctr = static_cast<unsigned long long*>(counters);
   return SMOE_OK;
 }
 

@@ -763,6 +763,11 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
 
   int g, m0, rlo, rhi, n0;
   if (!big_tile<BM, BN, GM>(p, blockIdx.x, g, m0, rlo, rhi, n0)) return;  // workgroup-uniform
+  uint64_t clk0 = 0, wall0 = 0;
+  if (p.clk) {  // diagnostics (uniform): the tile's clock cycles and wall ticks
+    clk0 = __builtin_amdgcn_s_memtime();
+    wall0 = __builtin_amdgcn_s_memrealtime();
+  }
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int grp = wave >> 2;
   const int wm = grp, wn = wave & 3;
@@ -896,6 +901,12 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
   }
   // (no DMA is outstanding here; the epilogue synchronises before it reuses the ring)
   tile_epilogue<BM, BN, TM, TN, 512, EPI, WF>(p, acc, g, m0, rlo, rhi, n0, wm, wn, ring);
+  if (p.clk && tid == 0) {
+    const uint64_t dc = __builtin_amdgcn_s_memtime() - clk0;
+    const uint64_t dw = __builtin_amdgcn_s_memrealtime() - wall0;
+    atomicAdd(p.clk, static_cast<unsigned long long>(dc));
+    atomicAdd(p.clk + 1, static_cast<unsigned long long>(dw));
+  }
 }
 
 // --------------------------------------------------------------- skinny ----
@@ -2344,6 +2355,11 @@ bool gemm_takes_row_tiles(const GemmArgs& a) {
 }
 
 int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
+  if (g_launch_ev[0] && g_clock_ctr && !a.clk) {  // a profiled launch: its clock too
+    GemmArgs b = a;
+    b.clk = g_clock_ctr;
+    return launch_grouped_gemm(b, s);
+  }
   if (a.N_out <= 0 || a.K <= 0) return SMOE_EINVAL;
   if (a.W2) return SMOE_EINVAL;  // two weight segments: launch_front_gemm
   // pointers every launched workgroup dereferences

@@ -14,7 +14,10 @@ namespace smoe {
 // without the gaps two separate event packets would add; the launch clears
 // them.  Diagnostics state of one host thread at a time, like the stage
 // profiler that sets it.
-extern hipEvent_t g_launch_ev[2];
+extern thread_local hipEvent_t g_launch_ev[2];
+// Device counters [2] that a profiled GEMM launch (g_launch_ev set) passes to
+// its kernel as GemmArgs::clk (smoe_profile_clock); the calling thread's.
+extern thread_local unsigned long long* g_clock_ctr;
 
 #define SMOE_LAUNCH(kernel, grid, block, shm, stream, ...)                                   \
   do {                                                                                       \
@@ -76,6 +79,11 @@ struct GemmArgs {
   int ldw2 = 0;
   int n_split = 0;
   const float* bias2 = nullptr;
+  // diagnostics: when set, the ping-pong kernel adds each workgroup's
+  // shader-clock cycles (s_memtime) to clk[0] and its 100 MHz wall-clock
+  // ticks (s_memrealtime) to clk[1], so clk[0] / clk[1] * 100 MHz is the
+  // clock the launch ran at
+  unsigned long long* clk = nullptr;
 };
 
 int launch_grouped_gemm(const GemmArgs& a, hipStream_t s);

@@ -95,6 +95,7 @@ SIGNATURES = {
     "smoe_remap_ids": (_c_int, [_vp, ctypes.c_int64, _vp, _c_int, _vp, _vp]),
     "smoe_profile_stages": (_c_int, [ctypes.c_uint32, ctypes.POINTER(_vp), _c_int]),
     "smoe_profile_count": (_c_int, [ctypes.POINTER(ctypes.c_int32), _c_int]),
+    "smoe_profile_clock": (_c_int, [_vp]),
     "smoe_events_create": (_c_int, [_c_int, ctypes.POINTER(_vp)]),
     "smoe_events_destroy": (_c_int, [_c_int, ctypes.POINTER(_vp)]),
     "smoe_events_elapsed": (_c_int, [_c_int, ctypes.POINTER(_vp), ctypes.POINTER(ctypes.c_float)]),
@@ -206,8 +207,11 @@ class StageTimer:
     """HIP events around every launch of the selected stages of
     smoe_block_forward (smoe_profile_stages); durations in ms per stage."""
 
-    def __init__(self, stages=None, capacity: int = 8192):
+    def __init__(self, stages=None, capacity: int = 8192, clock: bool = False):
         self.cap = capacity
+        # clock: the profiled ping-pong GEMM launches also count their shader
+        # clock cycles and 100 MHz wall ticks (smoe_profile_clock)
+        self.clk = torch.zeros(2, dtype=torch.int64, device="cuda") if clock else None
         self.ev = (_vp * (2 * capacity))()
         check(lib().smoe_events_create(2 * capacity, self.ev), "smoe_events_create")
         ids = range(len(STAGES)) if stages is None else [STAGES.index(s) for s in stages]
@@ -215,18 +219,30 @@ class StageTimer:
 
     def start(self):
         check(lib().smoe_profile_stages(self.mask, self.ev, self.cap), "smoe_profile_stages")
+        if self.clk is not None:
+            self.clk.zero_()
+            check(lib().smoe_profile_clock(self.clk.data_ptr()), "smoe_profile_clock")
 
     def stop(self) -> dict:
         torch.cuda.synchronize()
         stage_of = (ctypes.c_int32 * self.cap)()
         n = lib().smoe_profile_count(stage_of, self.cap)
         check(lib().smoe_profile_stages(0, None, 0), "smoe_profile_stages")
+        check(lib().smoe_profile_clock(None), "smoe_profile_clock")
         ms = (ctypes.c_float * max(n, 1))()
         check(lib().smoe_events_elapsed(n, self.ev, ms), "smoe_events_elapsed")
         out: dict = {}
         for i in range(n):
             out.setdefault(STAGES[stage_of[i]], []).append(ms[i])
         return out
+
+    def sclk_mhz(self) -> float | None:
+        """The clock the profiled ping-pong GEMM tiles ran at (None when
+        not counted or no such launch ran)."""
+        if self.clk is None:
+            return None
+        c, w = (int(v) for v in self.clk.cpu())
+        return 100.0 * c / w if w > 0 else None
 
     def close(self):
         lib().smoe_events_destroy(2 * self.cap, self.ev)

@@ -39,6 +39,19 @@ class SwiGLUGate(nn.Module):
         return F.silu(g) * u
 
 
+# Count of parameter / submodule registrations in the process (torch's global
+# registration hooks): SpiderMoELayer re-lists its parameters when it moves.
+_REGISTRATIONS = [0]
+
+
+def _count_registration(module, name, value):
+    _REGISTRATIONS[0] += 1
+
+
+torch.nn.modules.module.register_module_parameter_registration_hook(_count_registration)
+torch.nn.modules.module.register_module_module_registration_hook(_count_registration)
+
+
 def _aligned(t: torch.Tensor) -> torch.Tensor:
     """The kernels read rows as 16-byte vectors: copy views whose storage
     offset breaks that alignment."""
@@ -110,6 +123,7 @@ class SpiderMoELayer(nn.Module):
         self._packed: _Packed | None = None
         self._packed_key = None
         self._plist = None
+        self._plist_gen = -1
         self._ws: torch.Tensor | None = None
         self._last_n = 0
         self._last_ws: torch.Tensor | None = None
@@ -198,21 +212,30 @@ class SpiderMoELayer(nn.Module):
         return "bf16" if self.router.weight.dtype == torch.bfloat16 else "f32"
 
     # ----------------------------------------------------------- packing ----
+    def _live_params(self):
+        """The layer's parameter objects.  Walking the module tree costs
+        more than the pack key (~0.7 ms at 64 experts), so the list is
+        cached and walked again only after a parameter or module was
+        registered anywhere in the process: assigning a new nn.Parameter,
+        load_state_dict(assign=True) and swapping a submodule all register
+        one (_REGISTRATIONS)."""
+        if self._plist is None or self._plist_gen != _REGISTRATIONS[0]:
+            self._plist_gen = _REGISTRATIONS[0]
+            self._plist = list(self.parameters())
+        return self._plist
+
     def _state_key(self):
-        # the parameter objects are listed once per pack (walking the module
-        # tree costs more than the key); a parameter that is modified in
-        # place, moved (.to) or re-typed changes its version, address or dtype
-        plist = self._plist if self._plist is not None else list(self.parameters())
+        # a parameter that is replaced, modified in place, moved (.to) or
+        # re-typed changes its identity, version, address or dtype
+        plist = self._live_params()
         return (self.expert_format, id(self._int4_w_up), id(self._fp8), self.weight_tiles,
-                len(plist), tuple([(p.data_ptr(), p._version, p.dtype) for p in plist]))
+                len(plist), tuple([(id(p), p.data_ptr(), p._version, p.dtype) for p in plist]))
 
     @torch.no_grad()
     def _pack(self) -> _Packed:
         key = self._state_key()
         if self._packed is not None and self._packed_key == key:
             return self._packed
-        self._plist = list(self.parameters())
-        key = self._state_key()
         expert_ids = {id(p) for p in self.experts.parameters()} if self.offload_experts else set()
         dev = nat.require_gpu(*[p for p in self.parameters() if id(p) not in expert_ids])
         act = self.router.weight.dtype

@@ -83,6 +83,14 @@ def test_block_matches_reference_golden_f32(name):
                                    rtol=1e-5, atol=1e-6)
         assert torch.equal(st["expert_load"].cpu(), torch.from_numpy(z[f"loop{r}/expert_load"]))
         assert torch.equal(st["edge_load"].cpu(), torch.from_numpy(z[f"loop{r}/edge_load"]))
+        for key in ("aux_loss", "edge_loss"):
+            ref = torch.tensor(float(z[f"loop{r}/{key}"]))
+            torch.testing.assert_close(st[key].float().cpu().reshape(()), ref, rtol=1e-5, atol=1e-6)
+        # confidence = sigmoid(exit_head(h')) of the reference's own output
+        conf = torch.sigmoid(B.exit_logit(torch.from_numpy(z[f"loop{r}/out"]).reshape(-1, out.shape[-1]),
+                                          torch.from_numpy(z["param/exit_head.weight"]),
+                                          float(z["param/exit_head.bias"].reshape(-1)[0])))
+        torch.testing.assert_close(st["confidence"].cpu().reshape(-1), conf, rtol=1e-5, atol=1e-6)
 
 
 @pytest.mark.parametrize("name", ["block_small", "block_mid"])
@@ -246,6 +254,61 @@ def test_multi_loop_call_equals_per_loop_calls():
             h = wl.layer(h, wl.x0, r)
     torch.cuda.synchronize()
     assert torch.equal(full, h)
+
+
+@pytest.mark.parametrize("n,e,k,m", [(64, 32, 4, 2), (48, 64, 2, 4)])
+@pytest.mark.parametrize("hid", [128, 512])
+def test_multi_loop_fused_front_equals_per_loop_calls(n, e, k, m, hid):
+    """In a multi-loop decode call each loop's LayerNorm is folded into the
+    next loop's fused front; one call over R loops equals R one-loop calls
+    bit for bit at token segments of 32 / 64 lanes and other expert and
+    edge counts than the c2 block."""
+    from spider_moe_amd.workloads import make_block
+    say("multi-loop fused front", n, e, k, m, hid)
+    wl = make_block("c1", tokens=n, hidden_size=hid, num_experts=e, top_k=k, edges_per_expert=m,
+                    expert_ffn_size=256, num_loops=3, expert_activation="swiglu", experts="bf16",
+                    std="fan_in")
+    with torch.no_grad():
+        full = wl.layer.forward_loops(wl.h, wl.x0, 0, 3)
+        h = wl.h
+        for r in range(3):
+            h = wl.layer(h, wl.x0, r)
+    torch.cuda.synchronize()
+    assert torch.equal(full, h)
+
+
+def test_replaced_parameters_are_repacked():
+    """The packed weights follow parameter objects that are replaced, not
+    only modified: a new nn.Parameter assigned to the router, an expert
+    module swapped in (built before the first call), and
+    load_state_dict(assign=True); after each, the block is teacher-forced
+    against the oracle on the layer's current weights."""
+    from torch import nn
+    from spider_moe_amd.workloads import make_block
+    say("replaced parameters")
+    wl = make_block("c1", tokens=200, hidden_size=128, num_experts=8, top_k=2, edges_per_expert=2,
+                    expert_ffn_size=256, num_loops=2, expert_activation="gelu", experts="bf16",
+                    std="fan_in")
+    layer = wl.layer
+    gen = torch.Generator().manual_seed(77)
+    spare = nn.Sequential(nn.Linear(128, 256), nn.GELU(), nn.Linear(256, 128)).to(dev, torch.bfloat16)
+    with torch.no_grad():
+        for p in spare.parameters():
+            p.copy_(torch.randn(p.shape, generator=gen) * p.shape[-1] ** -0.5)
+        before = layer(wl.h, wl.x0, 0)
+        layer.router.weight = nn.Parameter(torch.randn(layer.router.weight.shape, generator=gen)
+                                           .to(dev, torch.bfloat16) * 128 ** -0.5)
+        got, _ = _check_loop(layer, wl.h, wl.x0, 0, 1e-2)
+        assert not torch.equal(got, before)
+        layer.experts[5] = spare
+        got2, _ = _check_loop(layer, wl.h, wl.x0, 0, 1e-2)
+        assert not torch.equal(got2, got)
+        sd = {k: v.clone() for k, v in layer.state_dict().items()}
+        sd["edge_value.1.weight"] = torch.randn(sd["edge_value.1.weight"].shape, generator=gen).to(
+            dev, torch.bfloat16) * 128 ** -0.5
+        layer.load_state_dict(sd, assign=True)
+        got3, _ = _check_loop(layer, wl.h, wl.x0, 0, 1e-2)
+        assert not torch.equal(got3, got2)
 
 
 def test_lm_c0_matches_reference_logits():

@@ -57,6 +57,59 @@ def test_block_matches_reference_layer(name, mode):
 
 
 @pytest.mark.parametrize("name", ["block_small", "block_mid"])
+def test_block_stats_match_reference_layer(name):
+    """block_stats against the return_stats outputs the reference's layer
+    wrote (model.py:327-345): loads bit for bit, aux_loss / edge_loss to
+    float32 rounding; planted mistakes (load normalised per token instead
+    of per slot, probs summed instead of averaged, edge importance without
+    its softmax weights) miss the goldens."""
+    z, w, cfg = load_block(name)
+    hid, e = cfg["hidden_size"], cfg["num_experts"]
+    x0 = torch.from_numpy(z["x0"]).reshape(-1, hid)
+    ew = torch.from_numpy(z["param/exit_head.weight"]).reshape(-1)
+    eb = float(z["param/exit_head.bias"].reshape(-1)[0])
+    for r in range(cfg["num_loops"]):
+        h = torch.from_numpy(z[f"loop{r}/in"]).reshape(-1, hid)
+        out, aux = B.block_forward(h, x0, w, r)
+        st = B.block_stats(aux, e, out, ew, eb)
+        assert torch.equal(st["expert_load"], torch.from_numpy(z[f"loop{r}/expert_load"]))
+        assert torch.equal(st["edge_load"], torch.from_numpy(z[f"loop{r}/edge_load"]))
+        for key in ("aux_loss", "edge_loss"):
+            ref = torch.from_numpy(np.asarray(z[f"loop{r}/{key}"], dtype=np.float32)).reshape(())
+            torch.testing.assert_close(st[key].reshape(()), ref, rtol=1e-6, atol=1e-7)
+        n = h.shape[0]
+        ref_aux = float(z[f"loop{r}/aux_loss"])
+        per_token = st["expert_load"] * w.top_k  # bincount / N
+        assert abs(float(e * torch.sum(per_token * aux.probs.mean(0))) - ref_aux) > 1e-3
+        assert abs(float(e * torch.sum(st["expert_load"] * aux.probs.sum(0))) - ref_aux) > 1e-3
+        flat = torch.bincount(aux.edge_idx.reshape(-1), minlength=e).float()
+        ref_edge = float(z[f"loop{r}/edge_loss"])
+        assert abs(float(e * torch.sum(st["edge_load"] * flat / flat.sum())) - ref_edge) > 1e-5
+        assert st["confidence"].shape == (n,)
+
+
+def test_block_stats_confidence_known_answer():
+    """confidence = sigmoid(exit_head(h')) on the block's output: with the
+    exit head reading feature 0, h'[:, 0] = 0, ln 3, -ln 3 give 1/2, 3/4,
+    1/4; the bias shifts the logit (model.py:342, exit_head model.py:185)."""
+    out = torch.zeros(3, 4)
+    out[:, 0] = torch.tensor([0.0, float(np.log(3.0)), -float(np.log(3.0))])
+    ew = torch.tensor([1.0, 0.0, 0.0, 0.0])
+    aux = B.BlockAux(logits=torch.zeros(3, 2), probs=torch.full((3, 2), 0.5),
+                     top_w=torch.ones(3, 1), top_i=torch.zeros(3, 1, dtype=torch.long),
+                     edge_idx=torch.zeros(3, 2, 1, dtype=torch.long), edge_w=torch.ones(3, 2, 1),
+                     edge_gap=torch.zeros(3), router_gap=torch.zeros(3), msg=out, delta=out,
+                     coef=torch.zeros(3, 2))
+    conf = B.block_stats(aux, 2, out, ew, 0.0)["confidence"]
+    torch.testing.assert_close(conf, torch.tensor([0.5, 0.75, 0.25]), rtol=0, atol=1e-7)
+    shifted = B.block_stats(aux, 2, out, ew, float(np.log(3.0)))["confidence"]
+    torch.testing.assert_close(shifted[0], torch.tensor(0.75), rtol=0, atol=1e-7)
+    # aux_loss of uniform probs and all load on expert 0: E * 1 * 1/2 = 1
+    st = B.block_stats(aux, 2, out, ew, 0.0)
+    assert float(st["aux_loss"]) == 1.0 and float(st["edge_loss"]) == 2.0
+
+
+@pytest.mark.parametrize("name", ["block_small", "block_mid"])
 def test_block_int4_matches_reference_layer(name):
     from oracle import quant as Q
     z, w, cfg = load_block(name)

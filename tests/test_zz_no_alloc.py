@@ -61,3 +61,35 @@ def test_scratch_forward_refuses_oversized_workspace():
     torch.cuda.synchronize()
     assert rc == 3, rc  # SMOE_ECAPACITY
     assert b"static scratch" in nat.lib().smoe_last_error()
+
+
+def test_scratch_forward_detects_overlap_on_another_stream():
+    """The static workspace is shared: a call on a second stream while the
+    first stream's call is still queued behind a bounded spin (torch's
+    _sleep) is refused with SMOE_EBUSY and launches nothing; once the first
+    has finished, the second stream's call runs and both equal the
+    workspace forward."""
+    from spider_moe_amd import _native as nat
+    from spider_moe_amd.workloads import make_block
+    say("scratch forward: overlap on a second stream")
+    wl = make_block("c2", tokens=64)
+    layer = wl.layer
+    with torch.no_grad():
+        want = layer.forward_loops(wl.h, wl.x0)
+    torch.cuda.synchronize()
+    sa, sb = torch.cuda.Stream(), torch.cuda.Stream()
+    with torch.cuda.stream(sa):
+        torch.cuda._sleep(100_000_000)  # ~50 ms of spinning ahead of the call on stream a
+        rc_a, got_a = _scratch_forward(layer, wl.h, wl.x0, 0, layer.num_loops)
+    with torch.cuda.stream(sb):
+        rc_b, _ = _scratch_forward(layer, wl.h, wl.x0, 0, layer.num_loops)
+    err = nat.lib().smoe_last_error()
+    torch.cuda.synchronize()
+    assert rc_a == 0, rc_a
+    assert rc_b == 5, rc_b  # SMOE_EBUSY
+    assert b"still running" in err
+    with torch.cuda.stream(sb):
+        rc_c, got_c = _scratch_forward(layer, wl.h, wl.x0, 0, layer.num_loops)
+    torch.cuda.synchronize()
+    assert rc_c == 0, rc_c
+    assert torch.equal(got_a, want) and torch.equal(got_c, want)
