@@ -370,6 +370,60 @@ def run_decode_exit(steps, warmup):
     return res
 
 
+def run_forge_fp8(steps, warmup):
+    """The Forge fp8 x fp8 GEMM (fp8_linear(quantize_input=True): e4m3
+    activations and weights, v_mfma_f32_16x16x128_f8f6f4) alone on resident
+    codes, timed with HIP events around the launches; 2 N K N_out flop per
+    launch against the 5.0 PFLOP/s dense fp8 peak.  Also the activation
+    quantization (amax + cast) on its own."""
+    import torch
+    from spider_moe_amd import _native as nat
+    from spider_moe_amd.forge import quantize_fp8_input
+    from spider_moe_amd.quant import quantize_fp8_per_tensor
+
+    lib = nat.lib()
+    out_rows = []
+    for n, k, no in ((8192, 8192, 8192), (16384, 1024, 5632), (16384, 2816, 1024), (4096, 4096, 4096)):
+        g = torch.Generator().manual_seed(n + k)
+        x = torch.randn(n, k, generator=g).to("cuda", torch.bfloat16)
+        w = (torch.randn(no, k, generator=g) / k ** 0.5).to("cuda")
+        wc, ws = quantize_fp8_per_tensor(w)
+        wq = wc.view(torch.uint8).contiguous()
+        ws = ws.reshape(1).float().contiguous()
+        xq, xs = quantize_fp8_input(x, k)
+        out = torch.empty(n, no, dtype=torch.bfloat16, device="cuda")
+        st = nat.stream_of(x.device)
+
+        def gemm():
+            nat.check(lib.smoe_linear_fp8fp8(xq.data_ptr(), xs.data_ptr(), n, k, wq.data_ptr(),
+                                             ws.data_ptr(), None, no, 1, out.data_ptr(), nat.BF16,
+                                             st), "smoe_linear_fp8fp8")
+
+        for _ in range(warmup):
+            gemm()
+            quantize_fp8_input(x, k)
+        torch.cuda.synchronize()
+        e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        e0.record()
+        for _ in range(steps):
+            gemm()
+        e1.record()
+        for _ in range(steps):
+            quantize_fp8_input(x, k)
+        e2.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        qms = e1.elapsed_time(e2) / steps
+        tf = 2.0 * n * k * no / (ms * 1e-3) / 1e12
+        out_rows.append({"N": n, "K": k, "N_out": no, "gemm_ms": round(ms, 4),
+                         "tflops": round(tf, 1), "frac_of_fp8_peak": round(tf / 5000.0, 4),
+                         "quantize_ms": round(qms, 4),
+                         "quantize_gbs": round(n * k * 3 / (qms * 1e-3) / 1e9, 1)})
+        log("forge fp8", out_rows[-1])
+        del x, w, wq, xq, out
+    return out_rows
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -377,6 +431,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workloads", default="c1,c2,c3,c4")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--forge-fp8", action="store_true",
+                    help="only time the Forge fp8 x fp8 GEMM (quantize_input=True) on four shapes")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (to scale rocprof FETCH/WRITE_SIZE)")
     a = ap.parse_args()
@@ -395,6 +451,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes": a.copy_calibration, "copies": 3}), flush=True)
+        return
+    if a.forge_fp8:
+        print(json.dumps({"forge_fp8_gemm": run_forge_fp8(a.steps, a.warmup)}), flush=True)
         return
     names = [x for x in a.workloads.split(",") if x]
     results = {nm: run_workload(nm, a.steps, a.warmup) for nm in names}

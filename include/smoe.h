@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define SMOE_ABI_VERSION 8
+#define SMOE_ABI_VERSION 9
 
 /* status codes (spider_kernels.h convention; see scalar.cpp:9,45,58) */
 #define SMOE_OK 0
@@ -343,6 +343,40 @@ SMOE_API int smoe_select_topk(const float* logits, int N, int E, int K, int mode
 SMOE_API int smoe_linear(const void* x, int N, int K, const void* w, int w_format,
                          const float* w_scale, const float* bias, int N_out, int act, void* out,
                          int out_dtype, void* stream);
+
+/* e4m3 quantization on the device: per tensor, the activation side of
+ * fp8_linear(quantize_input=True) (forge/gemm/fp8.py:49-52; quantize_fp8 /
+ * compute_fp8_scale, spider_moe/quant.py:30-56) and its weights, or per row
+ * (per_row = 1: the per-output-channel scales of the block's fp8 experts,
+ * quant.py:146-169 with a row amax): scale = max(amax|x| / 448, 1e-12) in f32
+ * (a NaN in x gives a NaN scale), codes = e4m3fn(x / scale) rounded to
+ * nearest even, not saturating (|x / scale| > 464 -> NaN code).  Both
+ * divisions are IEEE, so the codes and scales are the bits torch gives on the
+ * CPU (torch's GPU kernels divide by a reciprocal, which moves the scale by
+ * an ulp and, rarely, a code by one step).  x [rows, cols] contiguous, f32 /
+ * bf16 / f16 -> codes [rows, ld_out] (ld_out >= cols, ld_out % 4 == 0;
+ * columns cols .. ld_out-1 get code 0) and scale f32 [1] or [rows] (device).
+ * Per tensor, the workspace (smoe_quantize_fp8_workspace_bytes) holds
+ * partial maxima; per row it is unused (may be NULL). */
+SMOE_API size_t smoe_quantize_fp8_workspace_bytes(void);
+SMOE_API int smoe_quantize_fp8_tensor(const void* x, int x_dtype, int rows, int cols, int ld_out,
+                                      int per_row, uint8_t* codes, float* scale, void* workspace,
+                                      size_t workspace_bytes, void* stream);
+
+/* out [N, N_out] = act(x_scale * w_scale * (xq [N,K] . wq^T) + bias) with
+ * both operands e4m3fn codes (per-tensor scales: device f32 [1] each):
+ * the fp8 x fp8 GEMM of fp8_linear(quantize_input=True)
+ * (forge/gemm/fp8.py:22-62), which the reference runs as a dequantize +
+ * F.linear.  v_mfma_f32_16x16x128_f8f6f4 multiplies the codes exactly and
+ * sums each block of 128 products below f32 precision (measured: within
+ * 2^-14 of the block's largest product), the blocks in f32; the scales and
+ * bias are applied in f32.
+ * K % 256 == 0 (pad both operands' rows with code 0: smoe_quantize_fp8_tensor
+ * with ld_out = K); bias f32 [N_out] or NULL; act SMOE_LINEAR_NONE / GELU
+ * (erf); out f32 or bf16, row-major [N, N_out]. */
+SMOE_API int smoe_linear_fp8fp8(const uint8_t* xq, const float* x_scale, int N, int K,
+                                const uint8_t* wq, const float* w_scale, const float* bias,
+                                int N_out, int act, void* out, int out_dtype, void* stream);
 
 /* out [N,H] = per token, the sum over its rows tok_row [N,K] (-1: none;
  * distinct rows, added in ascending row order) of y [R,H] times row_w [R]

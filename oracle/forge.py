@@ -8,8 +8,10 @@ Restatements, with torch on the CPU (the library the reference calls):
                    scale = max(amax(|w|) / 448, 1e-12); codes =
                    (w.float() / scale) -> e4m3; w_deq = (codes.float() *
                    scale) in the compute dtype (fp16 for half / bf16 inputs,
-                   else fp32); F.linear(x.to(compute), w_deq, bias); the
-                   result in x's dtype
+                   else fp32); with quantize_input, x likewise; F.linear(
+                   x_deq, w_deq, bias); the result in x's dtype
+  fp8_expert_ffn   fp8.py:65-76: fp8_linear (quantize_input), GELU,
+                   fp8_linear
   expert_ffn       fp8.py:65-75 / triton_kernels.py:113-123: linear, GELU
                    (erf), linear
   dispatch_ffn     forge/ep/dispatch.py:145-185: for each expert ascending
@@ -19,7 +21,10 @@ Restatements, with torch on the CPU (the library the reference calls):
 
 Pins (tests/test_oracle_native_forge.py): hand-computed known answers for the
 selection; the per-tensor scale and codes against the closed form and the
-e4m3 decode table of oracle/quant.py; the dispatch combine against a
+e4m3 decode table of oracle/quant.py; quantize_input against a known answer
+(values on the e4m3 grid pass unchanged), the scale-invariance of the codes
+(x and 2^j x give the same codes, the scale times 2^j) and a planted
+mistake (codes without the input scale); the dispatch combine against a
 per-token loop over the dense merged weights.
 """
 from __future__ import annotations
@@ -42,12 +47,26 @@ def fp8_quantize_per_tensor(w: torch.Tensor):
     return (w.float() / scale).to(torch.float8_e4m3fn), scale
 
 
-def fp8_linear(x: torch.Tensor, w: torch.Tensor, bias=None):
+def fp8_linear(x: torch.Tensor, w: torch.Tensor, bias=None, *, quantize_input: bool = False):
+    """fp8.py:22-62.  quantize_input: x is quantized per tensor as w is
+    (fp8.py:49-51) and dequantized in the compute dtype."""
     compute = torch.float16 if x.dtype in (torch.float16, torch.bfloat16) else torch.float32
     codes, scale = fp8_quantize_per_tensor(w)
     w_deq = (codes.float() * scale).to(compute)
+    if quantize_input:
+        xc, xs = fp8_quantize_per_tensor(x)
+        x_deq = (xc.float() * xs).to(compute)
+    else:
+        x_deq = x.to(compute)
     b = None if bias is None else bias.to(compute)
-    return F.linear(x.to(compute), w_deq, b).to(x.dtype)
+    return F.linear(x_deq, w_deq, b).to(x.dtype)
+
+
+def fp8_expert_ffn(x, w_up, b_up, w_down, b_down, *, quantize_input: bool = False):
+    """fp8.py:65-76: the up projection with the input quantized when asked,
+    GELU (erf), the down projection on fp8 weights only."""
+    h = F.gelu(fp8_linear(x, w_up, b_up, quantize_input=quantize_input))
+    return fp8_linear(h, w_down, b_down)
 
 
 def linear(x: torch.Tensor, w: torch.Tensor, bias=None):

@@ -1109,6 +1109,41 @@ SMOE_API int smoe_linear(const void* x, int N, int K, const void* w, int w_forma
   return SMOE_OK;
 }
 
+SMOE_API size_t smoe_quantize_fp8_workspace_bytes(void) { return quantize_fp8_workspace_bytes(); }
+
+SMOE_API int smoe_quantize_fp8_tensor(const void* x, int x_dtype, int rows, int cols, int ld_out,
+                                      int per_row, uint8_t* codes, float* scale, void* workspace,
+                                      size_t workspace_bytes, void* stream) {
+  if (rows < 0 || cols < 1 || ld_out < cols || ld_out % 4)
+    return fail(SMOE_EINVAL, "quantize shape (cols >= 1, ld_out >= cols, ld_out % 4 == 0)");
+  if (x_dtype != SMOE_F32 && x_dtype != SMOE_BF16 && x_dtype != SMOE_F16)
+    return fail(SMOE_EUNSUPPORTED, "quantize input dtype");
+  if (rows == 0) return SMOE_OK;
+  if (!x || !codes || !scale || (!per_row && !workspace)) return fail(SMOE_EINVAL, "null buffer");
+  if (!per_row && workspace_bytes < quantize_fp8_workspace_bytes())
+    return fail(SMOE_ECAPACITY, "workspace");
+  SMOE_TRY(launch_quantize_fp8(x, x_dtype, rows, cols, ld_out, per_row, codes, scale, workspace,
+                               static_cast<hipStream_t>(stream)),
+           "quantize fp8");
+  return SMOE_OK;
+}
+
+SMOE_API int smoe_linear_fp8fp8(const uint8_t* xq, const float* x_scale, int N, int K,
+                                const uint8_t* wq, const float* w_scale, const float* bias,
+                                int N_out, int act, void* out, int out_dtype, void* stream) {
+  if (N < 0 || K <= 0 || K % 256 || N_out <= 0)
+    return fail(SMOE_EINVAL, "fp8 x fp8 linear shape (K % 256 == 0: zero-padded codes)");
+  if (act != SMOE_LINEAR_NONE && act != SMOE_LINEAR_GELU) return fail(SMOE_EINVAL, "act");
+  if (out_dtype != SMOE_F32 && out_dtype != SMOE_BF16) return fail(SMOE_EUNSUPPORTED, "out dtype");
+  if (N == 0) return SMOE_OK;
+  if (!xq || !wq || !x_scale || !w_scale || !out) return fail(SMOE_EINVAL, "null buffer");
+  SMOE_TRY(launch_gemm_f8f8(xq, K, x_scale, wq, K, w_scale, bias, N, K, N_out,
+                            act == SMOE_LINEAR_GELU, out, out_dtype, N_out,
+                            static_cast<hipStream_t>(stream)),
+           "fp8 x fp8 GEMM");
+  return SMOE_OK;
+}
+
 SMOE_API int smoe_combine_rows(const void* y, int y_dtype, const float* row_w,
                                const int32_t* tok_row, int N, int K, int H, void* out,
                                int out_dtype, void* stream) {

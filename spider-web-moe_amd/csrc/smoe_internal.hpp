@@ -139,6 +139,16 @@ constexpr int kFrontMaxN = 64;
 // ---- Forge surfaces (smoe_forge.hip) ----
 // top-k of f32 logits [N, E] (E <= 64): mode 0 the router's softmax / top-k
 // / renorm, mode 1 top-k on the logits then softmax over the k values
+// fp8 x fp8 (smoe_fp8.hip): e4m3 quantization of x [rows, cols] into codes
+// [rows, ld_out] (zero codes past cols) + the f32 scale (per tensor, with a
+// workspace of quantize_fp8_workspace_bytes(), or per row); the GEMM over
+// those codes.
+size_t quantize_fp8_workspace_bytes();
+int launch_quantize_fp8(const void* x, int xdt, int rows, int cols, int ld_out, int per_row,
+                        uint8_t* codes, float* scale, void* workspace, hipStream_t s);
+int launch_gemm_f8f8(const uint8_t* xq, int ldx, const float* xs, const uint8_t* wq, int ldw,
+                     const float* ws, const float* bias, int N, int K, int N_out, int gelu,
+                     void* out, int odt, int ldo, hipStream_t s);
 int launch_select_topk(const float* logits, int N, int E, int K, int mode, float* top_w,
                        int32_t* top_idx, hipStream_t s);
 // out[t] = sum over the token's rows tok_row [N, K] of y[row] * row_w[row]

@@ -88,6 +88,11 @@ SIGNATURES = {
     "smoe_combine_epilogue": (_c_int, [_vp, _vp, _c_int, _vp, _c_int, _c_int, _c_int, _c_float,
                                        _c_float, _vp, _vp, _c_float, _vp, _vp]),
     "smoe_select_topk": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp, _vp]),
+    "smoe_quantize_fp8_workspace_bytes": (_sz, []),
+    "smoe_quantize_fp8_tensor": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp,
+                                          _vp, _sz, _vp]),
+    "smoe_linear_fp8fp8": (_c_int, [_vp, _vp, _c_int, _c_int, _vp, _vp, _vp, _c_int, _c_int, _vp,
+                                    _c_int, _vp]),
     "smoe_linear": (_c_int, [_vp, _c_int, _c_int, _vp, _c_int, _vp, _vp, _c_int, _c_int, _vp,
                              _c_int, _vp]),
     "smoe_combine_rows": (_c_int, [_vp, _c_int, _vp, _vp, _c_int, _c_int, _c_int, _vp, _c_int,
@@ -179,7 +184,7 @@ STAGES = ["router_gemm", "route_topk", "expert_plan", "edge_logits", "edge_topm"
           # bf16 steps of N <= 64: stages 0-5 as one GEMM and one routing workgroup
           "front_gemm", "front_route"]
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 _LIB = None
 
 

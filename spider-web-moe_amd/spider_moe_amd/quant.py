@@ -75,8 +75,42 @@ def dequantize_int4(packed, scales, shape, group_size, dtype=None):
     return w.view(shape)
 
 
+def _quantize_fp8_device(weight: torch.Tensor, per_row: bool):
+    """smoe_quantize_fp8_tensor: the reference's scale and cast with IEEE
+    divisions, the bits torch computes on the CPU (torch's GPU kernels
+    divide by a reciprocal: an ulp off in the scale and, rarely, one code
+    step off)."""
+    from . import _native as nat
+    w = weight.detach()
+    if w.dtype not in (torch.float32, torch.bfloat16, torch.float16):
+        w = w.float()
+    w = w.contiguous()
+    k = w.shape[-1]
+    rows = w.numel() // k if k else 0
+    kp = -(-k // 4) * 4
+    codes = torch.empty(rows, kp, dtype=torch.uint8, device=w.device)
+    scale = torch.empty(rows if per_row else 1, dtype=torch.float32, device=w.device)
+    lib = nat.lib()
+    wsp = None if per_row else torch.empty(lib.smoe_quantize_fp8_workspace_bytes(),
+                                           dtype=torch.uint8, device=w.device)
+    code = nat.F16 if w.dtype == torch.float16 else nat.dtype_code(w.dtype)
+    with torch.cuda.device(w.device):
+        nat.check(lib.smoe_quantize_fp8_tensor(w.data_ptr(), code, rows, k, kp, int(per_row),
+                                               codes.data_ptr(), scale.data_ptr(), nat.ptr(wsp),
+                                               0 if wsp is None else wsp.numel(),
+                                               nat.stream_of(w.device)),
+                  "smoe_quantize_fp8_tensor")
+    if kp != k:
+        codes = codes[:, :k].contiguous()
+    return codes.view(torch.float8_e4m3fn).view(w.shape), scale
+
+
 def quantize_fp8_per_channel(weight: torch.Tensor):
-    """[..., N, K] -> (float8_e4m3fn codes [..., N, K], float32 scale [..., N])."""
+    """[..., N, K] -> (float8_e4m3fn codes [..., N, K], float32 scale [..., N]).
+    On a GPU: the HIP quantizer (same bits as the CPU formula)."""
+    if weight.is_cuda and weight.numel():
+        codes, scale = _quantize_fp8_device(weight, per_row=True)
+        return codes, scale.view(weight.shape[:-1])
     w = weight.detach().float()
     scale = (w.abs().amax(dim=-1) / FP8_E4M3_MAX).clamp_min(1e-12)
     codes = (w / scale.unsqueeze(-1)).to(torch.float8_e4m3fn)
@@ -92,7 +126,11 @@ def quantize_fp8_per_tensor(weight: torch.Tensor):
     """One scale for the whole tensor, the format of the reference's
     quantize_fp8 / compute_fp8_scale (quant.py:30-56): scale = max(amax / 448,
     1e-12) (fp32, a 0-dim tensor), codes = (w.float() / scale) cast to
-    float8_e4m3fn (round to nearest even)."""
+    float8_e4m3fn (round to nearest even).  On a GPU: the HIP quantizer
+    (same bits as the CPU formula)."""
+    if weight.is_cuda and weight.numel():
+        codes, scale = _quantize_fp8_device(weight, per_row=False)
+        return codes, scale.reshape(())
     w = weight.detach().float()
     scale = (w.abs().amax() / FP8_E4M3_MAX).clamp_min(1e-12)
     return (w / scale).to(torch.float8_e4m3fn).contiguous(), scale

@@ -262,7 +262,7 @@ def test_forge_gemm_fp8_linear(dtype, n, kd, no):
     codes, scale = quantize_fp8_per_tensor(w.to(dev))
     oc, osc = OF.fp8_quantize_per_tensor(w)
     assert torch.equal(codes.view(torch.uint8).cpu(), oc.view(torch.uint8))
-    assert float(scale) == pytest.approx(float(osc), rel=2e-7)  # torch's division on the GPU
+    assert float(scale) == float(osc)  # IEEE divisions on the device, as on the CPU
     gemm = ForgeGEMM()
     got = gemm.linear_fp8(x.to(dev), w.to(dev), b.to(dev)).cpu().float()
     want = OF.fp8_linear(x, w, b).float()
@@ -271,8 +271,158 @@ def test_forge_gemm_fp8_linear(dtype, n, kd, no):
     assert err < 1.5e-2, err
     # the fp8 result stays near the unquantized product (a sanity bound)
     assert (got - ref).abs().max() / ref.abs().max() < 0.1
-    with pytest.raises(NotImplementedError):
-        gemm.linear_fp8(x.to(dev), w.to(dev), quantize_input=True)
+
+
+@pytest.mark.parametrize("per_row", [False, True])
+def test_quantize_fp8_weights_match_cpu_bits(per_row):
+    """Weights quantized on the device (per tensor for Forge, per output
+    channel for the block's fp8 experts) give the CPU formula's scales and
+    codes bit for bit, over shapes whose amax divides to scales off a
+    power of two; torch's own GPU division does not (it multiplies by a
+    reciprocal), which is why the HIP quantizer does it."""
+    from spider_moe_amd.quant import quantize_fp8_per_channel, quantize_fp8_per_tensor
+    from oracle import quant as OQ  # noqa: F401
+    say("quantize weights", "per_row" if per_row else "per_tensor")
+    for (r, c) in ((256, 512), (300, 1000), (1024, 2048), (7, 37)):
+        g = torch.Generator().manual_seed(r + c)
+        w = torch.randn(2, r, c, generator=g) / c ** 0.5
+        if per_row:
+            codes, scale = quantize_fp8_per_channel(w.to(dev))
+            ws = (w.abs().amax(dim=-1) / 448.0).clamp_min(1e-12)
+            wc = (w / ws.unsqueeze(-1)).to(torch.float8_e4m3fn)
+        else:
+            codes, scale = quantize_fp8_per_tensor(w.to(dev))
+            wc, ws = OF.fp8_quantize_per_tensor(w)
+        assert torch.equal(scale.cpu(), ws), (r, c)
+        assert torch.equal(codes.view(torch.uint8).cpu(), wc.view(torch.uint8)), (r, c)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_quantize_fp8_input_matches_torch_cast(dtype):
+    """smoe_quantize_fp8_tensor against quantize_fp8 (quant.py:30-56) on the
+    CPU: the same scale and the same e4m3 codes bit for bit, over random
+    values, exact midpoints between neighbouring codes (round to nearest
+    even) in the normal and subnormal ranges, and zeros; the K padding
+    holds code 0."""
+    from spider_moe_amd.forge import quantize_fp8_input
+    say("quantize_fp8_input", dtype)
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(37, 300, generator=g) * 3.0
+    x[0, 0] = 448.0                      # amax: scale 1 exactly
+    x[0, 1:] = 0.0
+    grid = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float()
+    grid = grid[torch.isfinite(grid)].unique()            # the 253 finite values, sorted
+    mids = (grid[1:] + grid[:-1]) / 2                     # exact ties, sign mixed
+    mids = mids * torch.where(torch.arange(mids.numel()) % 2 == 0, 1.0, -1.0)
+    x[1:1 + (mids.numel() + 299) // 300].view(-1)[:mids.numel()] = mids
+    x = x.to(dtype)
+    codes, scale = quantize_fp8_input(x.to(dev), 512)
+    oc, osc = OF.fp8_quantize_per_tensor(x)
+    assert float(scale) == float(osc)
+    c = codes.cpu()
+    assert torch.equal(c[:, :300], oc.view(torch.uint8)), int((c[:, :300] != oc.view(torch.uint8)).sum())
+    assert int(c[:, 300:].abs().sum()) == 0
+    # a scale off a power of two: the divisions themselves are compared
+    y = (torch.randn(64, 300, generator=g) * 1.7).to(dtype)
+    codes, scale = quantize_fp8_input(y.to(dev), 304)
+    oc, osc = OF.fp8_quantize_per_tensor(y)
+    assert float(scale) == float(osc)
+    assert torch.equal(codes.cpu()[:, :300], oc.view(torch.uint8))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("n,kd,no", [(5, 64, 128), (600, 512, 256), (1000, 1000, 300),
+                                     (257, 2048, 1024)])
+def test_forge_fp8_linear_quantize_input(dtype, n, kd, no):
+    """fp8_linear(quantize_input=True) (forge/gemm/fp8.py:49-52): e4m3 x
+    e4m3 on the f8f6f4 MFMA against the oracle, which dequantizes both
+    operands (fp16 compute for bf16 inputs, fp32 for fp32 inputs): fp32 to
+    1e-4 of the largest output, bf16 within the fp16 / bf16 roundings; K, N and
+    N_out off the kernel's 256 / 128 grid."""
+    from spider_moe_amd.forge import ForgeGEMM, fp8_linear, get_last_fp8_gemm_backend
+    say("forge_fp8_linear quantize_input", dtype, n, kd, no)
+    g = torch.Generator().manual_seed(n + kd + no)
+    x = torch.randn(n, kd, generator=g).to(dtype)
+    w = (torch.randn(no, kd, generator=g) / kd ** 0.5)
+    b = torch.randn(no, generator=g)
+    got = ForgeGEMM().linear_fp8(x.to(dev), w.to(dev), b.to(dev), quantize_input=True)
+    assert got.dtype == dtype and got.shape == (n, no)
+    got = got.cpu().float()
+    want = OF.fp8_linear(x, w, b, quantize_input=True).float()
+    err = (got - want).abs().max() / want.abs().max()
+    # f32: the oracle rounds x_deq, w_deq and each product; the kernel sums
+    # the exact code products and scales once
+    assert err < (1e-4 if dtype == torch.float32 else 1.5e-2), err
+    got2 = fp8_linear(x.to(dev), w.to(dev), b.to(dev), quantize_input=True).cpu().float()
+    assert torch.equal(got2, got)
+    assert get_last_fp8_gemm_backend()[0] == "hip_fp8xfp8_mfma_f8f6f4"
+
+
+def test_forge_fp8_linear_quantize_input_exact_on_the_grid():
+    """Inputs and weights already on the e4m3 grid of scale 1 (amax 448):
+    integer codes of magnitude <= 64 (plus one 448 each), so every product
+    and every partial sum is an integer below 2^24, exact in f32 in any
+    order.  The f8f6f4 MFMA multiplies the codes exactly but sums each
+    128-product block below f32 precision: measured within 2^-14 of the
+    block's largest product (the row and column holding 448 * 448 = 200704
+    are off by up to ~10); every other entry, whose products stay at or
+    below 64 * 64, is exact.  A wrong k pairing or a dropped block misses
+    by thousands."""
+    from spider_moe_amd.forge import fp8_linear
+    say("fp8 x fp8 exact")
+    grid = torch.arange(256, dtype=torch.uint8).view(torch.float8_e4m3fn).float()
+    grid = grid[torch.isfinite(grid) & (grid == grid.round()) & (grid.abs() <= 64)]
+    g = torch.Generator().manual_seed(5)
+    x = grid[torch.randint(0, grid.numel(), (70, 256), generator=g)]
+    w = grid[torch.randint(0, grid.numel(), (130, 256), generator=g)]
+    x[0, 0] = 448.0
+    w[0, 0] = 448.0
+    got = fp8_linear(x.to(dev), w.to(dev), quantize_input=True).cpu()
+    want = (x.double() @ w.double().t()).float()
+    assert torch.equal(got[1:, 1:], want[1:, 1:])
+    big = (x.double().abs() @ w.double().abs().t()).max(dim=-1).values  # bound per row
+    err = (got - want).abs().double()
+    assert bool((err[0] <= 448.0 * 448.0 * 2.0 ** -13).all()), float(err[0].max())
+    assert bool((err[:, 0] <= 448.0 * 448.0 * 2.0 ** -13).all()), float(err[:, 0].max())
+    assert float(big.min()) > 0
+
+
+def test_forge_fp8_expert_ffn_quantize_input():
+    """fp8_expert_ffn(quantize_input=True) (fp8.py:65-76): the up projection
+    e4m3 x e4m3 with GELU, the down projection on fp8 weights; fp32 inputs
+    (the reference's fp32 compute) and bf16 inputs."""
+    from spider_moe_amd.forge import fp8_expert_ffn
+    for dtype in (torch.float32, torch.bfloat16):
+        say("fp8_expert_ffn quantize_input", dtype)
+        g = torch.Generator().manual_seed(17)
+        h, u, n = 256, 512, 200
+        x = torch.randn(n, h, generator=g).to(dtype)
+        wu = (torch.randn(u, h, generator=g) / h ** 0.5).to(dtype)
+        bu = (torch.randn(u, generator=g) * 0.1).to(dtype)
+        wd = (torch.randn(h, u, generator=g) / u ** 0.5).to(dtype)
+        bd = (torch.randn(h, generator=g) * 0.1).to(dtype)
+        got = fp8_expert_ffn(x.to(dev), wu.to(dev), bu.to(dev), wd.to(dev), bd.to(dev),
+                             quantize_input=True)
+        assert got.dtype == dtype
+        got = got.cpu().float()
+        want = OF.fp8_expert_ffn(x, wu, bu, wd, bd, quantize_input=True).float()
+        err = (got - want).abs().max() / want.abs().max()
+        assert err < (1e-4 if dtype == torch.float32 else 3e-2), (dtype, err)
+
+
+def test_forge_fp8_linear_f32_inputs_keep_f32():
+    """f32 inputs on the fp8 weight path multiply in f32 (the reference's
+    compute dtype for f32, fp8.py:41-54): the dequantized codes times x in
+    f32, not x rounded to bf16."""
+    from spider_moe_amd.forge import ForgeGEMM
+    say("fp8 weights, f32 inputs")
+    g = torch.Generator().manual_seed(8)
+    x = torch.randn(300, 256, generator=g)
+    w = torch.randn(200, 256, generator=g) / 16
+    got = ForgeGEMM().linear_fp8(x.to(dev), w.to(dev)).cpu()
+    want = OF.fp8_linear(x, w)
+    assert got.dtype == torch.float32
+    assert torch.allclose(got, want, rtol=1e-5, atol=1e-5)
 
 
 @pytest.mark.parametrize("fp8", [False, True])

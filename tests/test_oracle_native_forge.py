@@ -158,6 +158,40 @@ def test_fp8_per_tensor_scale_and_codes():
     assert bool(((dec - q).abs() <= q.abs() * 2 ** -4 + 2 ** -10).all())
 
 
+def test_fp8_linear_quantize_input_known_answer_and_scale_invariance():
+    """quantize_input (forge/gemm/fp8.py:49-51): inputs already on the e4m3
+    grid of their own scale (amax 448 -> scale 1) pass unchanged, so the
+    product is exact; a power-of-two multiple of x gives the same codes with
+    the scale times that power, and the output scales with it; dropping the
+    input scale (multiplying the raw codes) misses by the scale."""
+    x = torch.tensor([[448.0, -224.0, 1.0, 0.0, 0.5, -3.0, 0.015625, 2.0 ** -9]])
+    w = torch.tensor([[1.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0],
+                      [0.0, 1.0, 1.0, 0.0, 0.0, 0.0, 0.0, 0.0],
+                      [0.0, 0.0, 0.0, 0.0, 1.0, 1.0, 1.0, 1.0]]) * 448.0
+    xc, xs = OF.fp8_quantize_per_tensor(x)
+    assert float(xs) == 1.0
+    assert torch.equal(xc.float(), x)
+    got = OF.fp8_linear(x, w, quantize_input=True)
+    want = torch.tensor([[448.0 * 448.0, -223.0 * 448.0,
+                          (0.5 - 3.0 + 0.015625 + 2.0 ** -9) * 448.0]])
+    assert torch.equal(got, want)
+    g = torch.Generator().manual_seed(12)
+    xr = torch.randn(6, 40, generator=g) * 0.3
+    wr = torch.randn(10, 40, generator=g) * 0.05
+    c1, s1 = OF.fp8_quantize_per_tensor(xr)
+    c2, s2 = OF.fp8_quantize_per_tensor(xr * 8.0)
+    assert torch.equal(c1.view(torch.uint8), c2.view(torch.uint8)) and float(s2) == 8.0 * float(s1)
+    y1 = OF.fp8_linear(xr, wr, quantize_input=True)
+    y2 = OF.fp8_linear(xr * 8.0, wr, quantize_input=True)
+    assert torch.allclose(y2, 8.0 * y1, rtol=1e-6, atol=1e-7)
+    # the quantized input stays within e4m3 rounding of the exact product
+    exact = xr @ (OF.fp8_quantize_per_tensor(wr)[0].float() * OF.fp8_quantize_per_tensor(wr)[1]).t()
+    assert (y1 - exact).abs().max() <= 0.07 * exact.abs().max()
+    wc, ws = OF.fp8_quantize_per_tensor(wr)
+    raw = c1.float() @ (wc.float() * ws).t()  # planted: no input scale
+    assert (raw - y1).abs().max() > 10 * (y1 - exact).abs().max()
+
+
 def test_dispatch_ffn_oracle_matches_per_token_loop():
     """The dispatch combine equals, per token, the sum over its experts in
     ascending order of expert_fn(e, x_t) times the merged weight (duplicate
