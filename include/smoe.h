@@ -75,8 +75,11 @@ extern "C" {
  * Shapes: 1 <= E <= 256.  f32 experts and bf16 GELU experts take any H
  * and U (shapes off the MFMA kernels' grid run a SIMT kernel); SwiGLU,
  * fp8 and int4 experts need H, U % 32 == 0 (SwiGLU U % 64, int4 the group
- * size dividing both).  Within a block (smoe_block) H % 8 == 0, H <= 4096,
- * E <= 64. */
+ * size dividing both).  Within a block (smoe_block) and the routing stages:
+ * H % 8 == 0, H <= 4096, E <= 256, 1 <= K, M <= min(E, 16) and
+ * min(E, K * M) <= 64 (the destinations a token can reach, one lane each);
+ * the reference takes any shape (model.py:165-185), these limits return
+ * SMOE_EINVAL. */
 typedef struct smoe_experts {
   int format;      /* SMOE_F32 / SMOE_BF16 / SMOE_FP8_E4M3 / SMOE_INT4 */
   int act;         /* SMOE_ACT_GELU / SMOE_ACT_SWIGLU */
@@ -243,7 +246,8 @@ SMOE_API int smoe_block_forward_scratch(const smoe_block* blk, const void* h_in,
 /* Router stage alone (model.py:255-258; spider_router_f32,
  * spider_kernels.h:26-28, with the logits GEMM of model.py:255 fused in):
  * x [N,H] act_dtype, router_w [E,H] act_dtype, loop_bias_row f32 [E] or NULL
- * -> logits f32 [N,E] (may be NULL), top_w f32 [N,K], top_idx i32 [N,K]. */
+ * -> logits f32 [N,E] (may be NULL), top_w f32 [N,K], top_idx i32 [N,K].
+ * 1 <= K <= min(E, 16), E <= 256. */
 SMOE_API size_t smoe_router_workspace_bytes(int N, int E);
 SMOE_API int smoe_router_topk(const void* x, int act_dtype, int N, int H, const void* router_w,
                               const float* loop_bias_row, int E, int K, float* logits,
@@ -318,7 +322,7 @@ SMOE_API int smoe_combine_epilogue(const void* h, const void* x0, int act_dtype,
 
 /* ---- Forge surfaces (spider_infer/forge) on the same kernels ---- */
 
-/* Top-k selection over f32 logits [N,E] (1 <= K <= E <= 64) -> top_w f32
+/* Top-k selection over f32 logits [N,E] (1 <= K <= min(E, 64), E <= 256) -> top_w f32
  * [N,K], top_idx i32 [N,K], descending.
  *   SMOE_SELECT_ROUTER: the block's router (model.py:256-258): softmax over
  *     the E logits, top-k, weights renormalised by max(sum, 1e-9);

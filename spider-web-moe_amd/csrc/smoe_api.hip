@@ -162,6 +162,20 @@ int check_experts(const smoe_experts& ex, int H) {
   return SMOE_OK;
 }
 
+// Experts, top-k and edges of a block or stage: E <= 256 (routing holds up to
+// 4 experts per lane), K, M <= 16 (per-token slot buckets) and at most 64
+// destinations per token, S = min(E, K * M) (one lane per entry in the
+// message combine).
+int check_ekm(int E, int K, int M) {
+  if (E < 1 || E > 256) return fail(SMOE_EINVAL, "E must be in [1, 256]");
+  if (K < 1 || K > E || K > 16) return fail(SMOE_EINVAL, "top_k must be in [1, min(E, 16)]");
+  if (M < 1 || M > E || M > 16)
+    return fail(SMOE_EINVAL, "edges_per_expert must be in [1, min(E, 16)]");
+  if ((E < K * M ? E : K * M) > 64)
+    return fail(SMOE_EINVAL, "min(E, top_k * edges_per_expert) must be <= 64");
+  return SMOE_OK;
+}
+
 int check_block(const smoe_block* b) {
   if (!b) return fail(SMOE_EINVAL, "null block");
   if (b->act_dtype != SMOE_F32 && b->act_dtype != SMOE_BF16)
@@ -169,9 +183,8 @@ int check_block(const smoe_block* b) {
   // H % 8: the row kernels' 8-wide vectors; GEMMs off the MFMA grid take
   // the SIMT kernel
   if (b->H <= 0 || b->H % 8 || b->H > 4096) return fail(SMOE_EINVAL, "H (H % 8 == 0, <= 4096)");
-  if (b->E < 1 || b->E > 64) return fail(SMOE_EINVAL, "E must be in [1, 64]");
-  if (b->K < 1 || b->K > b->E || b->K > 16) return fail(SMOE_EINVAL, "top_k");
-  if (b->M < 1 || b->M > b->E || b->M > 16) return fail(SMOE_EINVAL, "edges_per_expert");
+  const int rc = check_ekm(b->E, b->K, b->M);
+  if (rc != SMOE_OK) return rc;
   if (b->L < 0 || b->R < 1) return fail(SMOE_EINVAL, "loops");
   if (!b->router_w || !b->loop_bias || !b->edge_gen_w || !b->edge_loop_bias || !b->edge_value_w)
     return fail(SMOE_EINVAL, "block weights missing");
@@ -774,7 +787,7 @@ SMOE_API int smoe_router_topk(const void* x, int act_dtype, int N, int H, const 
                               float* top_w, int32_t* top_idx, void* ws, size_t ws_bytes,
                               void* stream) {
   if (act_dtype != SMOE_F32 && act_dtype != SMOE_BF16) return fail(SMOE_EUNSUPPORTED, "dtype");
-  if (N < 0 || H <= 0 || E < 1 || E > 64 || K < 1 || K > E || K > 16)
+  if (N < 0 || H <= 0 || E < 1 || E > 256 || K < 1 || K > E || K > 16)
     return fail(SMOE_EINVAL, "router shape");
   if (N == 0) return SMOE_OK;
   if (!x || !router_w || !top_w || !top_idx || !ws) return fail(SMOE_EINVAL, "null buffer");
@@ -881,12 +894,7 @@ int check_act(int adt, int H) {
   return SMOE_OK;
 }
 
-int check_ekm(int E, int K, int M) {
-  if (E < 1 || E > 64) return fail(SMOE_EINVAL, "E must be in [1, 64]");
-  if (K < 1 || K > E || K > 16) return fail(SMOE_EINVAL, "top_k");
-  if (M < 1 || M > E || M > 16) return fail(SMOE_EINVAL, "edges_per_expert");
-  return SMOE_OK;
-}
+
 
 // workspace of smoe_edge_topm
 struct TopmWs {
@@ -942,7 +950,7 @@ MsgWs msg_ws(int N, int H, int E, int K, int M, int adt) {
 }  // namespace
 
 SMOE_API size_t smoe_edge_topm_workspace_bytes(int N, int K, int E, int M) {
-  if (N < 0 || E < 1 || E > 64 || K < 1 || K > 16 || M < 1 || M > 16) return 0;
+  if (N < 0 || check_ekm(E, K, M) != SMOE_OK) return 0;
   return topm_ws(N, K, E, M).total;
 }
 
@@ -1004,7 +1012,7 @@ SMOE_API int smoe_edge_topm(const void* x, int act_dtype, int N, int H, const vo
 
 SMOE_API size_t smoe_edge_message_workspace_bytes(int N, int H, int E, int K, int M,
                                                   int act_dtype) {
-  if (N < 0 || H <= 0 || E < 1 || E > 64 || K < 1 || K > 16 || M < 1 || M > 16) return 0;
+  if (N < 0 || H <= 0 || check_ekm(E, K, M) != SMOE_OK) return 0;
   if (act_dtype != SMOE_F32 && act_dtype != SMOE_BF16) return 0;
   return msg_ws(N, H, E, K, M, act_dtype).total;
 }
@@ -1063,7 +1071,8 @@ SMOE_API int smoe_edge_message(const void* x, int act_dtype, int N, int H,
 
 SMOE_API int smoe_select_topk(const float* logits, int N, int E, int K, int mode, float* top_w,
                               int32_t* top_idx, void* stream) {
-  if (N < 0 || E < 1 || E > 64 || K < 1 || K > E) return fail(SMOE_EINVAL, "select shape");
+  if (N < 0 || E < 1 || E > 256 || K < 1 || K > E || K > 64)
+    return fail(SMOE_EINVAL, "select shape (1 <= K <= min(E, 64), E <= 256)");
   if (mode != SMOE_SELECT_ROUTER && mode != SMOE_SELECT_TOPK_SOFTMAX)
     return fail(SMOE_EINVAL, "select mode");
   if (N == 0) return SMOE_OK;

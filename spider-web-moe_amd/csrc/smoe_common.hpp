@@ -194,6 +194,43 @@ __device__ __forceinline__ void seg_argmax(float& v, int& i) {
   if constexpr (SEG >= 64) argmax_take(v, i, __shfl_xor(v, 32), __shfl_xor(i, 32));
 }
 
+// More than 64 entries per token (experts / destinations, up to 256): one
+// wave per token, lane l holding entries l, l + 64, .. (V slots).
+constexpr int kWideBig = 1 << 20;  // index of "no candidate"
+// The arg-max takes the lane's best candidate (the lowest index
+// on ties) into the wave's arg-max, so ties still go to the lowest index.
+template <int V>
+__device__ __forceinline__ void wide_argmax(const float (&x)[V], const bool (&cand)[V], float& cv,
+                                            int& ci) {
+  const int lane = threadIdx.x & 63;
+  cv = -INFINITY;
+  ci = kWideBig;
+#pragma unroll
+  for (int v = 0; v < V; ++v)
+    if (cand[v] && (ci == kWideBig || x[v] > cv)) {
+      cv = x[v];
+      ci = lane + 64 * v;
+    }
+  seg_argmax<64>(cv, ci);
+}
+
+// Distinct selected ids ascending across the V lane slots: slot v of lane l
+// holds id l + 64 v, so the rank counts the earlier slots' selections and
+// this slot's lower lanes.  Returns the number selected.
+template <int V>
+__device__ __forceinline__ int wide_ranks(const bool (&sel)[V], int (&rank)[V]) {
+  const int lane = threadIdx.x & 63;
+  const uint64_t lt = (1ull << lane) - 1ull;
+  int base = 0;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const uint64_t m = __ballot(sel[v]);
+    rank[v] = base + __popcll(m & lt);
+    base += __popcll(m);
+  }
+  return base;
+}
+
 // Inclusive prefix sum over the wave in lane order: Hillis-Steele within
 // each 16-lane row (DPP row_shr 1, 2, 4, 8, zero fill), then row_bcast15 /
 // row_bcast31 carry the row totals into the rows above.

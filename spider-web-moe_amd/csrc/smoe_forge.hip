@@ -59,6 +59,58 @@ __global__ __launch_bounds__(256) void k_select_topk(const float* __restrict__ l
   }
 }
 
+// k_select_topk for 64 < E <= 64 V: one wave per token, lane l holding
+// logits l, l + 64, .. (K <= 64 slots, lane j writes slot j).
+template <int V, int MODE>
+__global__ __launch_bounds__(256) void k_select_topk_w(const float* __restrict__ logits, int N,
+                                                       int E, int K, float* __restrict__ top_w,
+                                                       int32_t* __restrict__ top_idx) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= N) return;  // wave-uniform
+  float x[V];
+  bool in[V], sel[V];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    in[v] = lane + 64 * v < E;
+    x[v] = in[v] ? logits[static_cast<int64_t>(t) * E + lane + 64 * v] : -INFINITY;
+    mx = fmaxf(mx, x[v]);
+    sel[v] = false;
+  }
+  float sum = 1.f;
+  if (MODE == 0) {
+    mx = seg_max<64>(mx);
+    float part = 0.f;
+#pragma unroll
+    for (int v = 0; v < V; ++v) part += in[v] ? expf(x[v] - mx) : 0.f;
+    sum = seg_sum<64>(part);
+  }
+  float first = 0.f, acc = 0.f, slot_v = 0.f;
+  int slot_i = 0;
+#pragma unroll 1
+  for (int j = 0; j < K; ++j) {
+    bool cand[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) cand[v] = in[v] && !sel[v];
+    float cv;
+    int ci;
+    wide_argmax<V>(x, cand, cv, ci);
+#pragma unroll
+    for (int v = 0; v < V; ++v) sel[v] = sel[v] || (lane + 64 * v == ci);
+    first = j == 0 ? cv : first;
+    const float pj = MODE == 0 ? expf(cv - mx) / sum : expf(cv - first);
+    slot_v = lane == j ? pj : slot_v;
+    slot_i = lane == j ? ci : slot_i;
+    acc += pj;
+  }
+  const float denom = MODE == 0 ? fmaxf(acc, 1e-9f) : acc;
+  if (lane < K) {
+    top_w[static_cast<int64_t>(t) * K + lane] = slot_v / denom;
+    top_idx[static_cast<int64_t>(t) * K + lane] = slot_i;
+  }
+}
+
 // out[t] = sum over the token's rows (tok_row [N, K], -1 = none) in
 // ascending row order — rows are grouped by expert, so this is ascending
 // expert order, the order of the per-expert scatter-adds of
@@ -132,8 +184,23 @@ int rc() { return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP; }
 
 int launch_select_topk(const float* logits, int N, int E, int K, int mode, float* top_w,
                        int32_t* top_idx, hipStream_t s) {
-  if (E < 1 || E > 64 || K < 1 || K > E || (mode != 0 && mode != 1)) return SMOE_EINVAL;
+  if (E < 1 || E > 256 || K < 1 || K > E || K > 64 || (mode != 0 && mode != 1)) return SMOE_EINVAL;
   if (N <= 0) return SMOE_OK;
+  if (E > 64) {
+    const dim3 grid((N + 3) / 4), block(256);
+#define SMOE_SELW(V_)                                                                          \
+  do {                                                                                         \
+    if (mode == 0)                                                                             \
+      hipLaunchKernelGGL((k_select_topk_w<V_, 0>), grid, block, 0, s, logits, N, E, K, top_w, top_idx); \
+    else                                                                                       \
+      hipLaunchKernelGGL((k_select_topk_w<V_, 1>), grid, block, 0, s, logits, N, E, K, top_w, top_idx); \
+  } while (0)
+    if (E <= 128) SMOE_SELW(2);
+    else if (E <= 192) SMOE_SELW(3);
+    else SMOE_SELW(4);
+#undef SMOE_SELW
+    return rc();
+  }
   const int seg = E <= 16 ? 16 : (E <= 32 ? 32 : 64), per = 4 * (64 / seg);
   const dim3 grid((N + per - 1) / per), block(256);
 #define SMOE_SEL(SG)                                                                           \

@@ -24,6 +24,7 @@
 namespace smoe {
 
 constexpr int kBig = 1 << 20;
+constexpr int kPlanMaxGroups = 256;  // experts / destinations a block takes
 
 // ------------------------------------------------------------ router ----
 // Segment of token t (lane e of the segment: expert e, logit v, -inf past
@@ -112,13 +113,96 @@ __global__ __launch_bounds__(256) void k_route_topk(const float* __restrict__ lo
   topk_seg<SEG>(v, t, ok, live, E, K, top_idx, top_w, tok_e, tok_ew, nullptr, nullptr);
 }
 
-// segment width for E entries per token (E <= 64)
+// --------------------------------------------- more than 64 experts ----
+// The router of topk_seg for 64 < E <= 64 V: the same softmax, top-k on the
+// logits (ties to the lowest index), renorm by max(sum, 1e-9) in slot
+// order, tok_e / tok_ew ascending.
+template <int V>
+__global__ __launch_bounds__(256) void k_route_topk_w(const float* __restrict__ logits, int N,
+                                                      int E, int K, int32_t* __restrict__ top_idx,
+                                                      float* __restrict__ top_w,
+                                                      int32_t* __restrict__ tok_e,
+                                                      float* __restrict__ tok_ew,
+                                                      const int32_t* __restrict__ active) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= N) return;  // wave-uniform
+  const bool live = !active || active[t] != 0;
+  float x[V], ex[V];
+  bool in[V], sel[V];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    const int e = lane + 64 * v;
+    in[v] = e < E;
+    x[v] = in[v] ? logits[static_cast<int64_t>(t) * E + e] : -INFINITY;
+    mx = fmaxf(mx, x[v]);
+    sel[v] = false;
+  }
+  mx = seg_max<64>(mx);
+  float part = 0.f;
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    ex[v] = in[v] ? expf(x[v] - mx) : 0.f;
+    part += ex[v];
+  }
+  const float sum = seg_sum<64>(part);
+  float psum = 0.f, slot_p = 0.f;
+  int slot_i = 0;
+#pragma unroll 1
+  for (int j = 0; j < K; ++j) {
+    bool cand[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) cand[v] = in[v] && !sel[v];
+    float cv;
+    int ci;
+    wide_argmax<V>(x, cand, cv, ci);
+    const float pj = expf(cv - mx) / sum;
+#pragma unroll
+    for (int v = 0; v < V; ++v) sel[v] = sel[v] || (lane + 64 * v == ci);
+    slot_p = lane == j ? pj : slot_p;
+    slot_i = lane == j ? ci : slot_i;
+    psum += pj;
+  }
+  const float denom = fmaxf(psum, 1e-9f);
+  if (lane < K) {
+    top_idx[static_cast<int64_t>(t) * K + lane] = slot_i;
+    top_w[static_cast<int64_t>(t) * K + lane] = slot_p / denom;
+  }
+  if (!tok_e) return;
+  if (live) {
+    int rank[V];
+    wide_ranks<V>(sel, rank);
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+      if (sel[v]) {
+        tok_e[static_cast<int64_t>(t) * K + rank[v]] = lane + 64 * v;
+        tok_ew[static_cast<int64_t>(t) * K + rank[v]] = ex[v] / sum / denom;
+      }
+  } else if (lane < K) {
+    tok_e[static_cast<int64_t>(t) * K + lane] = -1;
+    tok_ew[static_cast<int64_t>(t) * K + lane] = 0.f;
+  }
+}
+
+// segment width for E entries per token (E <= 64); lane slots per wave for
+// wider E
 inline int seg_of(int E) { return E <= 16 ? 16 : (E <= 32 ? 32 : 64); }
+inline int wide_of(int E) { return (E + 63) / 64; }
 
 int launch_route_topk(const float* logits, int N, int E, int K, int32_t* top_idx, float* top_w,
                       int32_t* tok_e, float* tok_ew, const int32_t* active, hipStream_t s) {
-  if (E < 1 || E > 64 || K < 1 || K > E || K > 16) return SMOE_EINVAL;
+  if (E < 1 || E > kPlanMaxGroups || K < 1 || K > E || K > 16) return SMOE_EINVAL;
   if (N <= 0) return SMOE_OK;
+  if (E > 64) {
+    const dim3 grid((N + 3) / 4), block(256);
+    switch (wide_of(E)) {
+      case 2: hipLaunchKernelGGL(k_route_topk_w<2>, grid, block, 0, s, logits, N, E, K, top_idx, top_w, tok_e, tok_ew, active); break;
+      case 3: hipLaunchKernelGGL(k_route_topk_w<3>, grid, block, 0, s, logits, N, E, K, top_idx, top_w, tok_e, tok_ew, active); break;
+      default: hipLaunchKernelGGL(k_route_topk_w<4>, grid, block, 0, s, logits, N, E, K, top_idx, top_w, tok_e, tok_ew, active); break;
+    }
+    return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+  }
   const int seg = seg_of(E), per_block = 4 * (64 / seg);
   const dim3 grid((N + per_block - 1) / per_block), block(256);
   if (seg == 16)
@@ -287,12 +371,111 @@ __global__ __launch_bounds__(256) void k_edge_topm(const float* __restrict__ edg
   topm_seg<SEG, KB>(v, row, live, t, ok, E, M, S, edge_idx, edge_w, tok_d, tok_dc, nullptr, nullptr);
 }
 
+// topm_seg for 64 < E <= 64 V: one wave per token, lane l holding
+// destinations l, l + 64, ..; the same per-source top-m, fp32 softmax over
+// the m values in slot order, coefficients summed over the sources in
+// ascending order, nonzero destinations ascending into tok_d / tok_dc
+// (S <= 64 entries).
+template <int V, int KB>
+__global__ __launch_bounds__(256) void k_edge_topm_w(const float* __restrict__ edge_logit,
+                                                     const int32_t* __restrict__ tok_e,
+                                                     const int32_t* __restrict__ e_tokrow, int N,
+                                                     int E, int K, int M, int S,
+                                                     int32_t* __restrict__ edge_idx,
+                                                     float* __restrict__ edge_w,
+                                                     int32_t* __restrict__ tok_d,
+                                                     float* __restrict__ tok_dc) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= N) return;  // wave-uniform
+  const int64_t tb = static_cast<int64_t>(t) * K;
+  int src[KB], rw[KB];
+#pragma unroll
+  for (int j = 0; j < KB; ++j) {
+    const int jj = j < K ? j : K - 1;
+    src[j] = tok_e[tb + jj];
+    rw[j] = e_tokrow[tb + jj];
+  }
+  bool in[V];
+  float c[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) {
+    in[v] = lane + 64 * v < E;
+    c[v] = 0.f;
+  }
+#pragma unroll
+  for (int j = 0; j < KB; ++j) {
+    if (!(j < K && src[j] >= 0)) continue;  // uniform: sources are packed first
+    const int row = rw[j];
+    float x[V];
+    bool sel[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      x[v] = in[v] ? edge_logit[static_cast<int64_t>(row) * E + lane + 64 * v] : -INFINITY;
+      sel[v] = false;
+    }
+    float vmax = 0.f, den = 0.f, rec_v = 0.f;
+    int rec_i = 0;
+#pragma unroll 1
+    for (int i = 0; i < M; ++i) {
+      bool cand[V];
+#pragma unroll
+      for (int v = 0; v < V; ++v) cand[v] = in[v] && !sel[v];
+      float cv;
+      int ci;
+      wide_argmax<V>(x, cand, cv, ci);
+#pragma unroll
+      for (int v = 0; v < V; ++v) sel[v] = sel[v] || (lane + 64 * v == ci);
+      vmax = i == 0 ? cv : vmax;
+      rec_v = lane == i ? cv : rec_v;
+      rec_i = lane == i ? ci : rec_i;
+      den += expf(cv - vmax);
+    }
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+      if (sel[v]) c[v] += expf(x[v] - vmax) / den;
+    if (lane < M) {
+      edge_idx[static_cast<int64_t>(row) * M + lane] = rec_i;
+      edge_w[static_cast<int64_t>(row) * M + lane] = expf(rec_v - vmax) / den;
+    }
+  }
+  bool nz[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) nz[v] = in[v] && c[v] != 0.f;
+  int rank[V];
+  const int cnt = wide_ranks<V>(nz, rank);
+#pragma unroll
+  for (int v = 0; v < V; ++v)
+    if (nz[v] && rank[v] < S) {
+      tok_d[static_cast<int64_t>(t) * S + rank[v]] = lane + 64 * v;
+      tok_dc[static_cast<int64_t>(t) * S + rank[v]] = c[v];
+    }
+  if (lane >= cnt && lane < S) {
+    tok_d[static_cast<int64_t>(t) * S + lane] = -1;
+    tok_dc[static_cast<int64_t>(t) * S + lane] = 0.f;
+  }
+}
+
 int launch_edge_topm(const float* edge_logit, const int32_t* tok_e, const int32_t* e_tokrow,
                      int N, int E, int K, int M, int S, int32_t* edge_idx, float* edge_w,
                      int32_t* tok_d, float* tok_dc, hipStream_t s) {
-  if (E < 1 || E > 64 || M < 1 || M > E || M > 16 || S < 1 || S > 64 || K < 1 || K > 16)
+  if (E < 1 || E > kPlanMaxGroups || M < 1 || M > E || M > 16 || S < 1 || S > 64 || K < 1 ||
+      K > 16)
     return SMOE_EINVAL;
   if (N <= 0) return SMOE_OK;
+  if (E > 64) {
+    const dim3 grid((N + 3) / 4), block(256);
+#define SMOE_EDGE_TOPM_W(V_, KB)                                                                   hipLaunchKernelGGL((k_edge_topm_w<V_, KB>), grid, block, 0, s, edge_logit, tok_e, e_tokrow, N,                      E, K, M, S, edge_idx, edge_w, tok_d, tok_dc)
+#define SMOE_EDGE_TOPM_WK(V_)                   do {                                            if (K <= 2) SMOE_EDGE_TOPM_W(V_, 2);          else if (K <= 4) SMOE_EDGE_TOPM_W(V_, 4);     else if (K <= 8) SMOE_EDGE_TOPM_W(V_, 8);     else SMOE_EDGE_TOPM_W(V_, 16);              } while (0)
+    switch (wide_of(E)) {
+      case 2: SMOE_EDGE_TOPM_WK(2); break;
+      case 3: SMOE_EDGE_TOPM_WK(3); break;
+      default: SMOE_EDGE_TOPM_WK(4); break;
+    }
+#undef SMOE_EDGE_TOPM_WK
+#undef SMOE_EDGE_TOPM_W
+    return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+  }
   const int seg = seg_of(E), per_block = 4 * (64 / seg);
   const dim3 grid((N + per_block - 1) / per_block), block(256);
 #define SMOE_EDGE_TOPM(SG, KB)                                                                   \
@@ -357,6 +540,8 @@ int launch_gather_topm(const int32_t* src_idx, const int32_t* tok_e, const int32
 // once) and each adds the weights of its edges into d, as the fused top-m
 // does; the nonzero destinations, ascending, fill tok_d / tok_dc (S
 // entries per token, -1 / 0 past them).
+// V: destinations per lane (lane l holds l, l + 64, ..: E <= 64 V).
+template <int V>
 __global__ __launch_bounds__(256) void k_dest_coeffs(const int32_t* __restrict__ src_idx,
                                                      const int32_t* __restrict__ eidx,
                                                      const float* __restrict__ ew, int N, int K,
@@ -367,7 +552,9 @@ __global__ __launch_bounds__(256) void k_dest_coeffs(const int32_t* __restrict__
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= N) return;  // wave-uniform
   const int32_t* ts = src_idx + static_cast<int64_t>(t) * K;
-  float c = 0.f;
+  float c[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) c[v] = 0.f;
   int last = -1;
   for (int it = 0; it < K; ++it) {  // uniform: every lane scans the same slots
     int best = kBig, bj = 0;
@@ -381,19 +568,24 @@ __global__ __launch_bounds__(256) void k_dest_coeffs(const int32_t* __restrict__
     if (best == kBig) break;
     last = best;
     const int64_t b = (static_cast<int64_t>(t) * K + bj) * M;
-    for (int j = 0; j < M; ++j)
-      if (eidx[b + j] == lane) c += ew[b + j];
-  }
-  const bool nz = lane < E && c != 0.f;
-  const uint64_t m = __ballot(nz);
-  const int cnt = __popcll(m);
-  if (nz) {
-    const int rank = __popcll(m & ((1ull << lane) - 1));
-    if (rank < S) {
-      tok_d[static_cast<int64_t>(t) * S + rank] = lane;
-      tok_dc[static_cast<int64_t>(t) * S + rank] = c;
+    for (int j = 0; j < M; ++j) {
+      const int d = eidx[b + j];
+#pragma unroll
+      for (int v = 0; v < V; ++v)
+        if (d == lane + 64 * v) c[v] += ew[b + j];
     }
   }
+  bool nz[V];
+#pragma unroll
+  for (int v = 0; v < V; ++v) nz[v] = lane + 64 * v < E && c[v] != 0.f;
+  int rank[V];
+  const int cnt = wide_ranks<V>(nz, rank);
+#pragma unroll
+  for (int v = 0; v < V; ++v)
+    if (nz[v] && rank[v] < S) {
+      tok_d[static_cast<int64_t>(t) * S + rank[v]] = lane + 64 * v;
+      tok_dc[static_cast<int64_t>(t) * S + rank[v]] = c[v];
+    }
   if (lane >= cnt && lane < S) {
     tok_d[static_cast<int64_t>(t) * S + lane] = -1;
     tok_dc[static_cast<int64_t>(t) * S + lane] = 0.f;
@@ -402,10 +594,15 @@ __global__ __launch_bounds__(256) void k_dest_coeffs(const int32_t* __restrict__
 
 int launch_dest_coeffs(const int32_t* src_idx, const int32_t* eidx, const float* ew, int N, int K,
                        int M, int E, int S, int32_t* tok_d, float* tok_dc, hipStream_t s) {
-  if (E < 1 || E > 64 || S < 1 || S > 64 || K < 1 || M < 1) return SMOE_EINVAL;
+  if (E < 1 || E > kPlanMaxGroups || S < 1 || S > 64 || K < 1 || M < 1) return SMOE_EINVAL;
   if (N <= 0) return SMOE_OK;
-  hipLaunchKernelGGL(k_dest_coeffs, dim3((N + 3) / 4), dim3(256), 0, s, src_idx, eidx, ew, N, K, M,
-                     E, S, tok_d, tok_dc);
+  const dim3 grid((N + 3) / 4), block(256);
+  switch (wide_of(E)) {
+    case 1: hipLaunchKernelGGL(k_dest_coeffs<1>, grid, block, 0, s, src_idx, eidx, ew, N, K, M, E, S, tok_d, tok_dc); break;
+    case 2: hipLaunchKernelGGL(k_dest_coeffs<2>, grid, block, 0, s, src_idx, eidx, ew, N, K, M, E, S, tok_d, tok_dc); break;
+    case 3: hipLaunchKernelGGL(k_dest_coeffs<3>, grid, block, 0, s, src_idx, eidx, ew, N, K, M, E, S, tok_d, tok_dc); break;
+    default: hipLaunchKernelGGL(k_dest_coeffs<4>, grid, block, 0, s, src_idx, eidx, ew, N, K, M, E, S, tok_d, tok_dc); break;
+  }
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 

@@ -231,11 +231,30 @@ class SpiderMoELayer(nn.Module):
         return (self.expert_format, id(self._int4_w_up), id(self._fp8), self.weight_tiles,
                 len(plist), tuple([(id(p), p.data_ptr(), p._version, p.dtype) for p in plist]))
 
+    def _check_supported(self):
+        """The shapes the HIP block takes (the reference takes any,
+        model.py:165-185, config.py:41-52): a clear error before any launch."""
+        e, k, m, h = self.num_experts, self.top_k, self.edges_per_expert, self.hidden_size
+        bad = []
+        if not 1 <= e <= 256:
+            bad.append(f"num_experts {e} (1..256)")
+        if not 1 <= k <= min(e, 16):
+            bad.append(f"top_k {k} (1..min(num_experts, 16))")
+        if not 1 <= m <= min(e, 16):
+            bad.append(f"edges_per_expert {m} (1..min(num_experts, 16))")
+        if min(e, k * m) > 64:
+            bad.append(f"min(num_experts, top_k * edges_per_expert) = {min(e, k * m)} (<= 64)")
+        if h % 8 or h > 4096:
+            bad.append(f"hidden_size {h} (a multiple of 8, <= 4096)")
+        if bad:
+            raise ValueError("spider_moe_amd's HIP block does not take " + "; ".join(bad))
+
     @torch.no_grad()
     def _pack(self) -> _Packed:
         key = self._state_key()
         if self._packed is not None and self._packed_key == key:
             return self._packed
+        self._check_supported()
         expert_ids = {id(p) for p in self.experts.parameters()} if self.offload_experts else set()
         dev = nat.require_gpu(*[p for p in self.parameters() if id(p) not in expert_ids])
         act = self.router.weight.dtype

@@ -341,10 +341,45 @@ STAGE_SPECS = [
     dict(dtype="bf16", act="gelu", experts="fp8"),
     dict(dtype="bf16", act="gelu", experts="int4"),
     dict(dtype="f32", act="gelu", experts="bf16"),
+    dict(dtype="bf16", act="gelu", experts="bf16", e=128, k=4, m=4),
 ]
 
 
-@pytest.mark.parametrize("spec", STAGE_SPECS, ids=lambda s: f"{s['dtype']}-{s['act']}-{s['experts']}")
+@pytest.mark.parametrize("e,k,m,dtype,act", [(128, 4, 4, "bf16", "gelu"), (256, 2, 2, "bf16", "swiglu"),
+                                             (96, 3, 5, "f32", "gelu"), (65, 16, 4, "bf16", "gelu")])
+def test_block_wide_experts(e, k, m, dtype, act):
+    """More than 64 experts (the routing kernels hold up to four experts or
+    destinations per lane, one wave per token): every loop teacher-forced
+    against the oracle with the full checks (routing bit-exact off
+    near-ties, both plans, per-source edges, message, delta, output)."""
+    from spider_moe_amd.workloads import make_block
+    say("wide experts", e, k, m, dtype, act)
+    wl = make_block("c1", tokens=300, hidden_size=128, num_experts=e, top_k=k, edges_per_expert=m,
+                    expert_ffn_size=256, num_loops=2, expert_activation=act, experts=dtype,
+                    dtype=dtype, std="fan_in")
+    h = wl.h
+    for r in range(2):
+        h, rep = _check_loop(wl.layer, h, wl.x0, r, 1e-2 if dtype == "bf16" else 1e-4)
+        assert int((rep.get("experts_touched", 1))) >= 1
+
+
+def test_block_rejects_unsupported_shapes_clearly():
+    """Shapes past the kernels' limits raise a ValueError that names them,
+    before any launch."""
+    from spider_moe_amd import ModelConfig, SpiderMoELayer
+    say("unsupported shapes")
+    for over, word in ((dict(num_experts=300, top_k=2, edges_per_expert=2), "num_experts"),
+                       (dict(num_experts=128, top_k=20, edges_per_expert=2), "top_k"),
+                       (dict(num_experts=128, top_k=16, edges_per_expert=8), r"top_k \* edges")):
+        cfg = ModelConfig(vocab_size=64, num_heads=4, hidden_size=64, num_loops=1,
+                          expert_ffn_size=64, **over)
+        layer = SpiderMoELayer(cfg).to(dev)
+        with pytest.raises(ValueError, match=word):
+            with torch.no_grad():
+                layer(torch.zeros(1, 2, 64, device=dev), torch.zeros(1, 2, 64, device=dev), 0)
+
+
+@pytest.mark.parametrize("spec", STAGE_SPECS, ids=lambda s: f"{s['dtype']}-{s['act']}-{s['experts']}-{s.get('e', 8)}")
 def test_stage_entries_compose_block_forward(spec):
     """The stage entry points chained the way model.py:240-317 chains the
     stages (smoe_router_topk -> smoe_edge_topm -> smoe_edge_message ->
@@ -356,7 +391,8 @@ def test_stage_entries_compose_block_forward(spec):
     from spider_moe_amd import _native as nat
     from spider_moe_amd.workloads import make_block
     say("stage entries", spec)
-    wl = make_block("c1", tokens=300, hidden_size=128, num_experts=8, top_k=2, edges_per_expert=3,
+    wl = make_block("c1", tokens=300, hidden_size=128, num_experts=spec.get("e", 8),
+                    top_k=spec.get("k", 2), edges_per_expert=spec.get("m", 3),
                     expert_ffn_size=256, num_loops=2, expert_activation=spec["act"],
                     experts=spec["experts"], dtype=spec["dtype"], group_size=64, std="fan_in")
     layer, r = wl.layer, 1

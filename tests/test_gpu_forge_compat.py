@@ -197,7 +197,8 @@ def test_native_loop_runs_a_spiderw_bundle(tmp_path):
 
 
 # ---------------------------------------------------------- forge ----
-@pytest.mark.parametrize("n,e,k", [(1, 4, 2), (500, 16, 2), (1000, 64, 6), (37, 40, 40)])
+@pytest.mark.parametrize("n,e,k", [(1, 4, 2), (500, 16, 2), (1000, 64, 6), (37, 40, 40),
+                                   (300, 200, 5), (50, 256, 64), (70, 65, 1)])
 def test_forge_select_route(n, e, k):
     from spider_moe_amd.forge import ForgeConfig, ForgeSelect
     say("forge_select", n, e, k)

@@ -29,9 +29,11 @@ def nat():
 
 # ------------------------------------------------------------- router ----
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("e,k", [(4, 2), (16, 2), (32, 4), (64, 2), (64, 8)])
+@pytest.mark.parametrize("e,k", [(4, 2), (16, 2), (32, 4), (64, 2), (64, 8), (100, 3), (200, 16),
+                                 (256, 4)])
 @pytest.mark.parametrize("n", [1000, 40])  # 40 tokens: the decode (weight-streaming) GEMM
 def test_router_topk_matches_oracle(dtype, e, k, n):
+    """E > 64: one wave per token, up to four experts per lane."""
     n8 = nat()
     h = 256
     say("router", dtype, e, k, n)

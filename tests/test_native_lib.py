@@ -171,7 +171,8 @@ def test_workspace_layout_is_consistent(nat):
     assert small.total - small.h_tmp2 >= 64 * 1024 * 2
 
 
-@pytest.mark.parametrize("bad", [dict(K=0), dict(K=17), dict(E=65), dict(M=0), dict(H=1000),
+@pytest.mark.parametrize("bad", [dict(K=0), dict(K=17), dict(E=257), dict(E=128, K=16, M=8),
+                                 dict(M=0), dict(H=1000),
                                  dict(act_dtype=7), dict(format=9), dict(U=100),
                                  dict(format=3, group_size=48)])
 def test_invalid_block_is_rejected_without_launch(nat, bad):
@@ -256,7 +257,7 @@ def test_stage_entries_reject_bad_arguments(nat):
         return lib.smoe_edge_message(a["x"], a["adt"], a["n"], a["h"], a["w"], a["t"], a["e"],
                                      a["k"], a["m"], a["src"], a["ei"], a["ew"], a["out"], a["odt"],
                                      a["ws"], a["wsb"], None)
-    assert msg(e=65) == 1
+    assert msg(e=257) == 1
     assert msg(odt=nat.INT4) == -2
     assert msg(ei=None) == 1
     assert msg(wsb=16) == 3
