@@ -52,6 +52,16 @@ torch.nn.modules.module.register_module_parameter_registration_hook(_count_regis
 torch.nn.modules.module.register_module_module_registration_hook(_count_registration)
 
 
+def _share(stack: torch.Tensor, params) -> None:
+    """Re-point each parameter's storage at its slice of the stacked copy the
+    kernels read (same values, same shape and dtype), so the weights are
+    held once, not twice.  In-place updates of a parameter then write the
+    stack too and bump the parameter's version, which repacks."""
+    for i, p in enumerate(params):
+        if p.shape == stack[i].shape and p.dtype == stack.dtype and p.device == stack.device:
+            p.data = stack[i]
+
+
 def _aligned(t: torch.Tensor) -> torch.Tensor:
     """The kernels read rows as 16-byte vectors: copy views whose storage
     offset breaks that alignment."""
@@ -120,6 +130,12 @@ class SpiderMoELayer(nn.Module):
         # stream and the prefill GEMM read with contiguous 1 KB loads; False
         # saves that memory (same results either way)
         self.weight_tiles = True
+        # int4 experts at prefill sizes (>= 256 rows per expert): the
+        # ping-pong GEMM reads a bf16 copy of the dequantized weights, 4x the
+        # int4 bytes, made on the first such call when it fits this many
+        # bytes (0: never; prefill-size int4 calls then run the general int4
+        # kernel, about twice as slow, and the weights stay int4 only)
+        self.int4_dequant_tiles_max_bytes = 1 << 30
         self._packed: _Packed | None = None
         self._packed_key = None
         self._plist = None
@@ -279,6 +295,7 @@ class SpiderMoELayer(nn.Module):
         emb = f32(self.loop_embedding.weight)
         edge_lb = keep(torch.empty(r, e * e, device=dev, dtype=torch.float32))
         edge_value = keep(torch.stack([m.weight.detach() for m in self.edge_value]))
+        _share(edge_value, [m.weight for m in self.edge_value])
         lib = nat.lib()
         nat.check(lib.smoe_edge_loop_bias(edge_w.data_ptr(), adt, edge_b.data_ptr(),
                                           emb.data_ptr() if lemb > 0 else None, e, h, lemb, r,
@@ -325,6 +342,9 @@ class SpiderMoELayer(nn.Module):
             ex.format = adt
             w_up = keep(gate_up(torch.stack([m[0].weight.detach() for m in self.experts])))
             w_down = keep(torch.stack([m[2].weight.detach() for m in self.experts]))
+            if not swiglu:  # the interleaved [gate; up] stack is not a slice per expert
+                _share(w_up, [m[0].weight for m in self.experts])
+            _share(w_down, [m[2].weight for m in self.experts])
             s_up = s_down = None
             b_up = b_down = None
             if not swiglu:
@@ -368,15 +388,26 @@ class SpiderMoELayer(nn.Module):
         d.alpha, d.beta, d.eps = self.residual_scale, self.reinject_weight, self.norm.eps
         # exit gate: exit_head weight [H] then bias, fp32
         k.exit_wb = f32(torch.cat([self.exit_head.weight.reshape(-1), self.exit_head.bias.reshape(-1)]))
-        self._packed, self._packed_key = k, key
+        # the parameters that now live in the stacks moved: the key after the move
+        self._packed, self._packed_key = k, self._state_key()
         return k
+
+    def int4_dequant_tiles_bytes(self) -> int:
+        """Bytes of the bf16 dequant copy prefill-size int4 calls would make
+        (both expert weight stacks, 2 bytes a weight)."""
+        if self._int4_w_up is None:
+            return 0
+        return 2 * 2 * (self._int4_w_up.packed.numel() + self._int4_w_down.packed.numel())
 
     def _int4_prefill_tiles(self, k: _Packed, n: int, dev) -> None:
         """int4 experts with weight_tiles: on the first call whose expert
         groups reach the large-tile GEMM's size (n * top_k >= 256 per expert),
         the bf16 tiles of the dequantized weights (smoe_pack_int4_tiles), 4x
-        the int4 bytes; decode-size calls keep the packed int4 alone."""
+        the int4 bytes, if they fit int4_dequant_tiles_max_bytes;
+        decode-size calls keep the packed int4 alone."""
         if k.int4_tiles_src is None or n * self.top_k < 256 * self.num_experts:
+            return
+        if self.int4_dequant_tiles_bytes() > int(self.int4_dequant_tiles_max_bytes):
             return
         w_up, s_up, w_down, s_down = k.int4_tiles_src
         ex = k.desc.experts

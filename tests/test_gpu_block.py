@@ -143,6 +143,61 @@ def test_block_small_bf16_per_loop(spec):
         h, rep = _check_loop(wl.layer, h, wl.x0, r, 1e-2)
 
 
+def test_packed_weights_share_the_parameters_storage():
+    """Packing stacks the edge-value and expert weights for the kernels and
+    makes their weight tile copy; the nn.Linear parameters then become
+    views of the stacks, so packing adds one copy of those weights (the
+    tiles), not two, and the state_dict still reads and loads the same
+    values.  An in-place update repacks and the block follows it."""
+    from spider_moe_amd.workloads import make_block
+    say("packed weights share storage")
+    wl = make_block("c1", tokens=64, hidden_size=256, num_experts=8, top_k=2, edges_per_expert=2,
+                    expert_ffn_size=512, num_loops=1, expert_activation="gelu", experts="bf16",
+                    std="fan_in")
+    layer = wl.layer
+    sd0 = {k: v.clone() for k, v in layer.state_dict().items()}
+    torch.cuda.synchronize()
+    heavy = sum(p.numel() * p.element_size() for n, p in layer.named_parameters()
+                if n.startswith("edge_value") or (n.startswith("experts") and n.endswith("weight")))
+    before = torch.cuda.memory_allocated()
+    with torch.no_grad():
+        out = layer(wl.h, wl.x0, 0)
+    torch.cuda.synchronize()
+    grown = torch.cuda.memory_allocated() - before - layer._ws.numel()
+    assert grown <= 1.1 * heavy, (grown, heavy)
+    ev = layer._pack().desc.edge_value_w
+    assert layer.edge_value[0].weight.data_ptr() == ev  # a view of the stack
+    sd1 = layer.state_dict()
+    assert all(torch.equal(sd0[k], sd1[k]) for k in sd0)
+    with torch.no_grad():
+        layer.experts[2][2].weight.mul_(-1.0)
+        out2, _ = _check_loop(layer, wl.h, wl.x0, 0, 1e-2)
+    assert not torch.equal(out, out2)
+
+
+def test_int4_dequant_copy_respects_its_byte_budget():
+    """The bf16 dequant copy of prefill-size int4 calls is made only within
+    int4_dequant_tiles_max_bytes: with a budget of 0 the weights stay int4
+    (no copy, the general int4 kernel) and the block still matches the
+    oracle; with the default budget the copy appears and the output is
+    the same to the dequant rounding."""
+    from spider_moe_amd.workloads import make_block
+    say("int4 dequant copy budget")
+    wl = make_block("c1", tokens=2048, hidden_size=256, num_experts=8, top_k=2, edges_per_expert=2,
+                    expert_ffn_size=512, num_loops=1, expert_activation="gelu", experts="int4",
+                    group_size=64, std="fan_in")
+    layer = wl.layer
+    assert layer.int4_dequant_tiles_bytes() == 2 * 2 * 8 * 256 * 512  # two stacks, bf16
+    layer.int4_dequant_tiles_max_bytes = 0
+    got, _ = _check_loop(layer, wl.h, wl.x0, 0, 1e-2)
+    ex = layer._pack().desc.experts
+    assert not ex.w_up_tiles and not ex.w_down_tiles
+    layer.int4_dequant_tiles_max_bytes = 1 << 30
+    got2, _ = _check_loop(layer, wl.h, wl.x0, 0, 1e-2)
+    ex = layer._pack().desc.experts
+    assert ex.w_up_tiles and ex.w_down_tiles
+
+
 @pytest.mark.parametrize("experts,act", [("fp8", "swiglu"), ("int4", "gelu"), ("int4", "swiglu")])
 def test_block_prefill_quantized_experts(experts, act):
     """Quantized experts at prefill size (2048 tokens over 8 experts: ~512
