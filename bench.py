@@ -424,6 +424,52 @@ def run_forge_fp8(steps, warmup):
     return out_rows
 
 
+def run_quant_prefill(steps, warmup):
+    """The c1 prefill block (H1024 E16 k2 m2 U2816 SwiGLU, 16384 tokens, 6
+    loops) with its experts in bf16, fp8-e4m3 (per-channel scales) and int4
+    (group 128, fp16 scales): ms per step and the expert GEMMs' time per
+    step, each format on its own weights (the same seeded draws before
+    quantization)."""
+    import torch
+    from spider_moe_amd import _native as nat
+    from spider_moe_amd.workloads import make_block
+
+    out = {}
+    for fmt in ("bf16", "fp8", "int4"):
+        wl = make_block("c1", experts=fmt, group_size=128)
+        layer, h, x0 = wl.layer, wl.h, wl.x0
+        with torch.no_grad():
+            for _ in range(warmup):
+                layer.forward_loops(h, x0)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                layer.forward_loops(h, x0)
+            e1.record()
+            torch.cuda.synchronize()
+            timer = nat.StageTimer(stages=["up_gemm", "down_gemm"], capacity=steps * 12 + 16)
+            timer.start()
+            for _ in range(steps):
+                layer.forward_loops(h, x0)
+            st = timer.stop()
+            timer.close()
+        ex = layer._pack().desc.experts
+        out[fmt] = {"ms_per_step": round(e0.elapsed_time(e1) / steps, 4),
+                    "up_gemm_ms_per_step": round(sum(st.get("up_gemm", [0])) / steps, 4),
+                    "down_gemm_ms_per_step": round(sum(st.get("down_gemm", [0])) / steps, 4),
+                    "expert_weight_tiles": bool(ex.w_up_tiles),
+                    "expert_weight_bytes": int(sum(t.numel() * t.element_size()
+                                                   for t in layer._pack().keep
+                                                   if t.dtype in (torch.uint8, torch.bfloat16)
+                                                   and t.dim() == 3 and t.shape[0] == 16
+                                                   and t.shape[1] in (1024, 5632)))}
+        log("quant prefill", fmt, out[fmt])
+        del wl, layer
+        torch.cuda.empty_cache()
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -431,6 +477,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workloads", default="c1,c2,c3,c4")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--quant-prefill", action="store_true",
+                    help="only time the c1 prefill block with bf16, fp8 and int4 experts")
     ap.add_argument("--forge-fp8", action="store_true",
                     help="only time the Forge fp8 x fp8 GEMM (quantize_input=True) on four shapes")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
@@ -451,6 +499,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_bytes": a.copy_calibration, "copies": 3}), flush=True)
+        return
+    if a.quant_prefill:
+        print(json.dumps({"quant_prefill": run_quant_prefill(a.steps, a.warmup)}), flush=True)
         return
     if a.forge_fp8:
         print(json.dumps({"forge_fp8_gemm": run_forge_fp8(a.steps, a.warmup)}), flush=True)

@@ -96,10 +96,10 @@ typedef struct smoe_experts {
   /* optional: w_up / w_down in the weight tile layout, NULL to read the
    * row-major weights.  bf16 and fp8 (smoe_pack_weight_tiles): read instead
    * of them by the decode weight stream and the ping-pong GEMM (bit-identical
-   * results for bf16).  int4 (smoe_pack_int4_tiles): the bf16 tiles of the
-   * dequantized weights, read by the ping-pong GEMM at prefill sizes (>= 256
-   * rows per expert) in place of the general int4 kernel; the decode and
-   * stream kernels keep reading the packed int4. */
+   * results for bf16).  int4 (smoe_pack_int4_qtiles): the int4 tile layout,
+   * read by the ping-pong GEMM at prefill sizes (>= 256 rows per expert) in
+   * place of the general int4 kernel; the decode and stream kernels keep
+   * reading the packed int4. */
   const void* w_up_tiles;
   const void* w_down_tiles;
 } smoe_experts;
@@ -442,16 +442,20 @@ SMOE_API int smoe_remap_ids(const int32_t* ids, int64_t n, const int32_t* map, i
 SMOE_API int smoe_pack_weight_tiles(const void* w, int format, int G, int N, int K, void* out,
                                     void* stream);
 
-/* int4 weights (packed [G,N,K/2] as quant.py:119-143 packs them, scales
- * [G,N,K/group_size] of scale_dtype SMOE_F32 / SMOE_F16) -> the bf16 weight
- * tile layout of their dequantized values, out [G,N,K] bf16: q * s rounded
- * once to bf16, the values the int4 GEMM kernels multiply.  For the
- * smoe_experts w_up_tiles / w_down_tiles of int4 experts: prefill-size
- * expert GEMMs then run on the bf16 ping-pong kernel, at 4x the int4 bytes
- * of memory.  N % 16, K % 64,
- * group_size % 8, K % group_size.  No counterpart in the reference. */
-SMOE_API int smoe_pack_int4_tiles(const void* packed, const void* scales, int scale_dtype,
-                                  int group_size, int G, int N, int K, void* out, void* stream);
+/* int4 weights (packed [G,N,K/2] as quant.py:119-143 packs them: element
+ * 2i in the low nibble of byte i) -> the same bytes in the int4 tile layout
+ * the ping-pong GEMM reads, out [G*N*K/2] bytes: per group, 64-row quad Q
+ * and 32-k stage st, a 1 KB block at ((g*N/64 + Q)*K/32 + st)*1024 of four
+ * 16-row tiles (256 B each), lane l of tile t holding the 4 bytes of row
+ * 64Q + 16t + l%16 with k = 32st + 8(l/16) .. +7.  For the smoe_experts
+ * w_up_tiles / w_down_tiles of int4 experts: prefill-size expert GEMMs
+ * (>= 256 rows per expert, N_out % 256 == 0, 32 | group_size, K/group_size
+ * <= 32) then run on the ping-pong kernel, which widens the nibbles to bf16
+ * (q * s) in registers, with no memory beyond the int4 bytes.  N % 64,
+ * K % 32.  No counterpart in the reference (it dequantizes per call,
+ * model.py:299-303). */
+SMOE_API int smoe_pack_int4_qtiles(const void* packed, int G, int N, int K, void* out,
+                                   void* stream);
 
 /* When `events` is not NULL, every later smoe_block_forward records
  * events[2*i] before and events[2*i+1] after the i-th launch of a stage in

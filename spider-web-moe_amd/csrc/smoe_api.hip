@@ -277,7 +277,7 @@ void expert_gemms(const smoe_experts& ex, const void* msg, const int32_t* off, c
   up.lda = H;
   up.a_rows = rows;
   up.W = ex.w_up;
-  up.Wt = ex.w_up_tiles;  // int4: the bf16 tiles of the dequantized weights
+  up.Wt = ex.w_up_tiles;  // int4: its int4 tile copy (smoe_pack_int4_qtiles)
   up.w_gstride = static_cast<int64_t>(nup) * H;
   up.ldw = H;
   up.S = ex.s_up;
@@ -719,12 +719,10 @@ SMOE_API int smoe_pack_weight_tiles(const void* w, int format, int G, int N, int
                 "smoe_pack_weight_tiles");
 }
 
-SMOE_API int smoe_pack_int4_tiles(const void* packed, const void* scales, int scale_dtype,
-                                  int group_size, int G, int N, int K, void* out, void* stream) {
-  if (scale_dtype != SMOE_F32 && scale_dtype != SMOE_F16) return fail(SMOE_EINVAL, "scale dtype");
-  return hip_rc(launch_pack_int4_tiles(packed, scales, scale_dtype == SMOE_F16, group_size, G, N, K,
-                                       out, static_cast<hipStream_t>(stream)),
-                "smoe_pack_int4_tiles");
+SMOE_API int smoe_pack_int4_qtiles(const void* packed, int G, int N, int K, void* out,
+                                   void* stream) {
+  return hip_rc(launch_pack_int4_qtiles(packed, G, N, K, out, static_cast<hipStream_t>(stream)),
+                "smoe_pack_int4_qtiles");
 }
 
 SMOE_API int smoe_profile_stages(uint32_t stage_mask, void** events, int capacity) {

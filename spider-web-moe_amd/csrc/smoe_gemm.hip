@@ -730,6 +730,8 @@ __global__ __launch_bounds__(256, NS <= 3 ? 2 : 1) void k_gemm_ring(const GemmAr
 // BM = 256 (wave tile 128 x 64) for many rows per group; BM = 128 (wave tile
 // 64 x 64, two workgroups per CU) when groups hold a few hundred rows and a
 // 256-row tile would be mostly padding.
+constexpr int kPpScaleMax = 8192;  // int4 scale-table entries per 256-channel tile (K / gs <= 32)
+
 template <int NS, int GM, int EPI, int BM, bool PK = false, int WF = SMOE_BF16>
 __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmArgs p) {
   // WF: the weight format.  fp8-e4m3 weights come from their weight tile
@@ -738,24 +740,41 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
   // fragment reads widen the codes to bf16 (exact) in registers; the
   // per-channel scale is applied in the epilogue.  Half the W bytes of bf16
   // through the DMA and LDS.
-  static_assert(WF == SMOE_BF16 || (WF == SMOE_FP8_E4M3 && PK), "fp8 weights need the tile copy");
+  // int4 weights come from their int4 tile copy (smoe_pack_int4_qtiles: a
+  // stage of a 64-row quad is one 1 KB block of lane-ordered 4-byte
+  // fragments): waves 0-3 each DMA one quad, a quarter of the W bytes of
+  // bf16, and a fragment read is one 4-byte LDS load whose 8 nibbles are
+  // widened to bf16 in registers as q * s (the row's group scale, from a
+  // table of the tile's 256 channels x K / group_size scales loaded into LDS
+  // before the main loop, kept in the part of the ring that only the
+  // output staging uses), rounded once to bf16 — the values every int4
+  // kernel here multiplies.
+  static_assert(WF == SMOE_BF16 || ((WF == SMOE_FP8_E4M3 || WF == SMOE_INT4) && PK),
+                "fp8 / int4 weights need their tile copy");
   constexpr bool F8 = WF == SMOE_FP8_E4M3;
+  constexpr bool I4 = WF == SMOE_INT4;
   constexpr int BN = 256, TM = BM / 2, TN = 64;
   constexpr int FM = TM / 16, FN = TN / 16;
-  constexpr int A_BYTES = BM * 64, B_BYTES = BN * (F8 ? 32 : 64), STAGE = A_BYTES + B_BYTES;
+  constexpr int A_BYTES = BM * 64, B_BYTES = BN * (I4 ? 16 : F8 ? 32 : 64), STAGE = A_BYTES + B_BYTES;
   // DMA instructions (16 rows each; fp8 W: 32 rows) per stage: A_INS of A,
   // B_LD per wave of W.  With BM = 320 the 20 A instructions do not split
   // evenly over the 8 waves: waves 0-3 issue 3, waves 4-7 issue 2, and each
-  // wave's vmcnt waits count its own.
-  constexpr int A_INS = BM / 16, B_LD = BN / (F8 ? 32 : 16) / 8;
+  // wave's vmcnt waits count its own.  int4 W: one quad per wave 0-3.
+  constexpr int A_INS = BM / 16, B_LD = I4 ? 1 : BN / (F8 ? 32 : 16) / 8;
   constexpr int A_LD = (A_INS + 7) / 8;                  // most per wave
   constexpr int A_HI = A_INS % 8 == 0 ? 8 : A_INS % 8;   // waves issuing A_LD of them
-  constexpr int LD = A_LD + B_LD, LD_LO = (A_INS / 8) + B_LD;
+  // int4: waves 0-3 issue the W DMA, and (A_HI = 4) the extra A one, so
+  // waves 0-3 and 4-7 are the two counts
+  static_assert(!I4 || A_HI == 4 || A_HI == 8, "int4: waves 0-3 issue the most DMAs");
+  constexpr int LD = A_LD + B_LD;
+  constexpr int LD_LO = I4 ? (A_HI == 8 ? A_LD : A_INS / 8) : (A_INS / 8) + B_LD;
   constexpr int OUT_BYTES = BM * ((EPI == EPI_SWIGLU) ? BN / 2 : BN) * 2;
   // the ring also stages the output tile, in one pass: it grows to the tile
   // when that is larger (320 x 256 bf16 is exactly 160 KB; two passes
-  // through the 144 KB ring cost a barrier and a half-idle store phase)
-  constexpr int RING = NS * STAGE > OUT_BYTES ? NS * STAGE : OUT_BYTES;
+  // through the 144 KB ring cost a barrier and a half-idle store phase).
+  // int4: the scale table follows the stages, inside that allocation.
+  constexpr int SC_BYTES = I4 ? kPpScaleMax * 4 : 0;
+  constexpr int RING = NS * STAGE + SC_BYTES > OUT_BYTES ? NS * STAGE + SC_BYTES : OUT_BYTES;
   static_assert(RING <= 163840, "LDS of one workgroup");
   static_assert(NS >= 2, "ring depth");
   static_assert(BM == 128 || BM == 256 || BM == 320, "block rows");
@@ -772,16 +791,42 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
   const int grp = wave >> 2;
   const int wm = grp, wn = wave & 3;
   const bool a_hi = wave < A_HI;  // issues A_LD A instructions (else A_LD - 1)
+  const bool w_hi = !I4 || wave < 4;  // issues the stage's W DMA (int4: waves 0-3)
   // s_waitcnt vmcnt(n stages of this wave's DMA in flight)
   auto wait_stages = [&](auto n_stages) {
     constexpr int n = decltype(n_stages)::value;
     if constexpr (LD == LD_LO) {
       wait_vmcnt<n * LD>();
     } else {
-      if (a_hi) wait_vmcnt<n * LD>();
+      if (I4 ? w_hi : a_hi) wait_vmcnt<n * LD>();
       else wait_vmcnt<n * LD_LO>();
     }
   };
+  // int4: the tile's group scales, channel-major [256][ng], into LDS.  The
+  // loads are unconditional (indices clamped; channels past N_out read the
+  // last one's) and go out before the DMA prologue, so the wait for the
+  // first stage covers them too.
+  float* stab = reinterpret_cast<float*>(ring + NS * STAGE);
+  int ng = 1, gshift = 0;
+  float scv[I4 ? kPpScaleMax / 512 : 1];
+  if constexpr (I4) {
+    ng = p.K / p.group_size;
+    gshift = __builtin_ctz(p.group_size);
+    const int64_t sb = g * p.s_gstride + static_cast<int64_t>(n0) * ng;
+    const int last = (min(p.N_out, n0 + BN) - n0) * ng - 1;
+    if (p.s_f16) {
+      const _Float16* s16 = reinterpret_cast<const _Float16*>(p.S) + sb;
+      _Float16 hv[kPpScaleMax / 512];
+#pragma unroll
+      for (int j = 0; j < kPpScaleMax / 512; ++j) hv[j] = s16[min(tid + 512 * j, last)];
+#pragma unroll
+      for (int j = 0; j < kPpScaleMax / 512; ++j) scv[j] = static_cast<float>(hv[j]);
+    } else {
+      const float* s32 = reinterpret_cast<const float*>(p.S) + sb;
+#pragma unroll
+      for (int j = 0; j < kPpScaleMax / 512; ++j) scv[j] = s32[min(tid + 512 * j, last)];
+    }
+  }
 
   // DMA sources: instruction j of wave w covers rows 16 (8 j + w) ..; with
   // At, the 1 KB row-tile block of that band (bands past the buffer's last
@@ -809,7 +854,12 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
 #pragma unroll
     for (int j = 0; j < B_LD; ++j) {
       const int r = (8 * j + wave) * 16 + pr;
-      if constexpr (F8) {  // lanes 0-31: tile 2 (8 j + w), 32-63: the next; 512 B of each per stage
+      if constexpr (I4) {  // quad n0 / 64 + wave (waves 4-7: never issued)
+        const int quads = p.N_out >> 6;
+        const int qd = min((n0 >> 6) + (wave & 3), quads - 1);
+        bsrc[j] = reinterpret_cast<const uint8_t*>(p.Wt) +
+                  (static_cast<int64_t>(g) * quads + qd) * (p.K >> 5) * 1024 + 16 * lane;
+      } else if constexpr (F8) {  // lanes 0-31: tile 2 (8 j + w), 32-63: the next; 512 B of each per stage
         const int t = n0 + (2 * (8 * j + wave) + (lane >> 5)) * 16;
         const int tile = (t < p.N_out ? t : n0) >> 4;
         bsrc[j] = reinterpret_cast<const uint8_t*>(p.Wt) +
@@ -837,20 +887,36 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
                                          (lds_vptr)(base + (8 * j + wave) * 1024), 16, 0, 0);
 #pragma unroll
     for (int j = 0; j < B_LD; ++j)  // tile layout: each stage's (half) block is the next 1 KB (512 B)
-      __builtin_amdgcn_global_load_lds((gbl_vptr)(bsrc[j] + stage * (F8 ? 512 : PK ? 1024 : 64)),
-                                       (lds_vptr)(base + A_BYTES + (8 * j + wave) * 1024), 16, 0, 0);
+      if (w_hi)  // wave-uniform
+        __builtin_amdgcn_global_load_lds(
+            (gbl_vptr)(bsrc[j] + stage * (I4 ? 1024 : F8 ? 512 : PK ? 1024 : 64)),
+            (lds_vptr)(base + A_BYTES + (8 * j + wave) * 1024), 16, 0, 0);
   };
   const int fr = lane & 15, fc = lane >> 4;
   // the lane's A fragment of strip i at a_lds + 1024 i: the swizzled 64-byte
   // rows, or the row-tile block's lane-ordered fragments
   const int a_lds = p.At ? wm * TM * 64 + 16 * lane : swz32(wm * TM + fr, fc);
   bf16x8 wf[FN], af[FM];
+  float sj[I4 ? FN : 1];  // int4: the lane's rows' scales of the current group
+  int kg_cur = -1;
   auto read_frags = [&](int stage) {
+    if constexpr (I4) {
+      const int kg = (stage * 32) >> gshift;
+      if (kg != kg_cur) {  // uniform: a new scale group every group_size / 32 stages
+        kg_cur = kg;
+#pragma unroll
+        for (int j = 0; j < FN; ++j) sj[j] = stab[(wn * TN + j * 16 + fr) * ng + kg];
+      }
+    }
     const uint8_t* sa = ring + (stage % NS) * STAGE;
     const uint8_t* sb = sa + A_BYTES;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      if constexpr (F8) {  // tile tt's half block: row fr, k 8 fc.. at 16 fr + 256 (fc >> 1) + 8 (fc & 1)
+      if constexpr (I4) {  // quad wn, tile j: the lane's 8 nibbles at 4 lane
+        const uint32_t w4 =
+            *reinterpret_cast<const uint32_t*>(sb + wn * 1024 + j * 256 + 4 * lane);
+        wf[j] = __builtin_bit_cast(bf16x8, int4x8_to_bf16x8(w4, sj[j]));
+      } else if constexpr (F8) {  // tile tt's half block: row fr, k 8 fc.. at 16 fr + 256 (fc >> 1) + 8 (fc & 1)
         const int tt = wn * TN / 16 + j;
         const u32x2 c = *reinterpret_cast<const u32x2*>(
             sb + (tt >> 1) * 1024 + (tt & 1) * 512 + 16 * fr + 256 * (fc >> 1) + 8 * (fc & 1));
@@ -877,8 +943,14 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
 #pragma unroll
   for (int st = 0; st < NS - 1; ++st)
     if (st < KT) issue(st);
+  if constexpr (I4) {
+#pragma unroll
+    for (int j = 0; j < kPpScaleMax / 512; ++j)
+      if (tid + 512 * j < BN * ng) stab[tid + 512 * j] = scv[j];
+  }
   if (KT >= NS - 1) wait_stages(std::integral_constant<int, NS - 2>{});
   else wait_vmcnt<0>();
+  if constexpr (I4) wait_lgkm0();  // the scale table is written
   __builtin_amdgcn_s_barrier();
   if (grp == 1) __builtin_amdgcn_s_barrier();  // group 1 starts half a step behind
   for (int k = 0; k < KT; ++k) {
@@ -1948,39 +2020,39 @@ int launch_pack_weight_tiles(const void* w, int fmt, int G, int N, int K, void* 
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 
-// int4 weights -> the bf16 weight tile layout of their dequantized values:
-// one thread per 16-byte fragment (8 consecutive k of one row), from the 4
-// packed bytes holding those k and the row's group scale: q * s rounded once
-// to bf16 (int4x8_to_bf16x8), the values every int4 GEMM here multiplies.
-__global__ __launch_bounds__(256) void k_pack_int4_tiles(const uint8_t* __restrict__ q,
-                                                         const void* __restrict__ sc, int s_f16,
-                                                         int gs, int64_t frags, int N, int K,
-                                                         uint16_t* __restrict__ out) {
+// int4 weights (packed [G, N, K/2], element 2i in the low nibble of byte i)
+// -> the int4 tile layout the ping-pong GEMM reads, the same bytes
+// rearranged: per group, per 64-row quad Q and 32-k stage st, a 1 KB block
+// ((g * N/64 + Q) * K/32 + st) * 1024 holding the quad's four 16-row tiles
+// (256 B each) of lane-ordered MFMA fragments: lane l of tile t takes the 4
+// packed bytes of row 64 Q + 16 t + l % 16 that hold k = 32 st + 8 (l / 16)
+// .. +7.  A stage of a 256-channel tile is then four contiguous 1 KB DMAs,
+// and a lane's fragment one 4-byte LDS read.  One thread per 4-byte word.
+__global__ __launch_bounds__(256) void k_pack_int4_qtiles(const uint8_t* __restrict__ q,
+                                                          int64_t words, int N, int K,
+                                                          uint8_t* __restrict__ out) {
   const int64_t f = blockIdx.x * static_cast<int64_t>(256) + threadIdx.x;
-  if (f >= frags) return;
+  if (f >= words) return;
   const int l = static_cast<int>(f & 63);
-  const int64_t blk = f >> 6;  // (g*T + t)*C + c
-  const int C = K / 32, T = N / 16;
-  const int c = static_cast<int>(blk % C);
-  const int64_t gt = blk / C;  // g*T + t
-  const int64_t g = gt / T, t = gt % T;
-  const int64_t row = g * N + 16 * t + (l & 15);
-  const int k = 32 * c + 8 * (l >> 4);
-  const uint32_t w = *reinterpret_cast<const uint32_t*>(q + row * (K / 2) + k / 2);
-  const float s = load_scale(sc, row * (K / gs) + k / gs, s_f16);
-  *reinterpret_cast<u32x4*>(out + f * 8) = int4x8_to_bf16x8(w, s);
+  const int t = static_cast<int>((f >> 6) & 3);
+  const int64_t blk = f >> 8;  // (g * N/64 + Q) * K/32 + st
+  const int S = K / 32, QN = N / 64;
+  const int st = static_cast<int>(blk % S);
+  const int64_t gq = blk / S;
+  const int64_t g = gq / QN, qd = gq % QN;
+  const int64_t row = g * N + 64 * qd + 16 * t + (l & 15);
+  const int k = 32 * st + 8 * (l >> 4);
+  *reinterpret_cast<uint32_t*>(out + f * 4) =
+      *reinterpret_cast<const uint32_t*>(q + row * (K / 2) + k / 2);
 }
 
-int launch_pack_int4_tiles(const void* q, const void* scales, int s_f16, int gs, int G, int N, int K,
-                           void* out, hipStream_t s) {
-  if (!q || !scales || !out || G < 1 || N < 16 || K < 64 || N % 16 || K % 64 || gs <= 0 || gs % 8 ||
-      K % gs)
-    return SMOE_EINVAL;
+int launch_pack_int4_qtiles(const void* q, int G, int N, int K, void* out, hipStream_t s) {
+  if (!q || !out || G < 1 || N < 64 || K < 32 || N % 64 || K % 32) return SMOE_EINVAL;
   if (reinterpret_cast<uintptr_t>(q) % 4 || reinterpret_cast<uintptr_t>(out) % 16) return SMOE_EINVAL;
-  const int64_t frags = static_cast<int64_t>(G) * N * K / 8;
-  hipLaunchKernelGGL(k_pack_int4_tiles, dim3(static_cast<unsigned>((frags + 255) / 256)), dim3(256),
-                     0, s, reinterpret_cast<const uint8_t*>(q), scales, s_f16, gs, frags, N, K,
-                     reinterpret_cast<uint16_t*>(out));
+  const int64_t words = static_cast<int64_t>(G) * N * K / 8;
+  hipLaunchKernelGGL(k_pack_int4_qtiles, dim3(static_cast<unsigned>((words + 255) / 256)), dim3(256),
+                     0, s, reinterpret_cast<const uint8_t*>(q), words, N, K,
+                     reinterpret_cast<uint8_t*>(out));
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 
@@ -2082,10 +2154,26 @@ int launch_pp_fp8(const GemmArgs& a, hipStream_t s) {
 // bf16 weights with a weight tile copy: the W operand's DMA reads each
 // 16-row x 32-k block as one contiguous 1 KB of lane-ordered fragments;
 // fp8 weights always come from their tile copy
+// int4 weights (their int4 tile copy; the expert FFN's epilogues)
+template <int NS, int GM, int BM>
+int launch_pp_int4(const GemmArgs& a, hipStream_t s) {
+  const int tiles = max_tiles(a, BM) * ((a.N_out + 255) / 256);
+  if (tiles == 0) return SMOE_OK;
+  const dim3 grid(tiles), block(512);
+  constexpr int I4 = SMOE_INT4;
+  switch (a.epi) {
+    case EPI_GELU: SMOE_LAUNCH((k_gemm_pp<NS, GM, EPI_GELU, BM, true, I4>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU: SMOE_LAUNCH((k_gemm_pp<NS, GM, EPI_SWIGLU, BM, true, I4>), grid, block, 0, s, a); break;
+    case EPI_DOWN: SMOE_LAUNCH((k_gemm_pp<NS, GM, EPI_DOWN, BM, true, I4>), grid, block, 0, s, a); break;
+    default: return SMOE_EINVAL;
+  }
+  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
 template <int NS, int GM, int BM>
 int launch_pp(const GemmArgs& a, hipStream_t s) {
   if (a.fmt == SMOE_FP8_E4M3) return launch_pp_fp8<NS, GM, BM>(a, s);
-  if (a.fmt == SMOE_INT4) return launch_pp_fmt<NS, GM, BM, true>(a, s);  // bf16 dequant tiles
+  if (a.fmt == SMOE_INT4) return launch_pp_int4<NS, GM, BM>(a, s);
   return a.Wt && a.fmt == SMOE_BF16 && a.N_out % 16 == 0 ? launch_pp_fmt<NS, GM, BM, true>(a, s)
                                    : launch_pp_fmt<NS, GM, BM, false>(a, s);
 }
@@ -2340,11 +2428,16 @@ bool pp_rows_320(const GemmArgs& a, int rpg) {
 }
 
 // Weights the ping-pong kernels read: bf16; fp8-e4m3 from its tile copy;
-// int4 from the bf16 tile copy of its dequantized values (neither for the
-// edge projection's row-scale epilogue).
+// int4 from its int4 tile copy, with 32 | group_size and at most
+// kPpScaleMax / 256 scale groups along K (neither for the edge
+// projection's row-scale epilogue).
 bool pp_weights(const GemmArgs& a) {
-  return a.fmt == SMOE_BF16 || ((a.fmt == SMOE_FP8_E4M3 || a.fmt == SMOE_INT4) && a.Wt &&
-                                a.N_out % 16 == 0 && a.epi != EPI_ROWSCALE);
+  if (a.fmt == SMOE_INT4)
+    return a.Wt && a.N_out % 64 == 0 && a.epi != EPI_ROWSCALE && a.group_size > 0 &&
+           a.group_size % 32 == 0 && (a.group_size & (a.group_size - 1)) == 0 &&
+           a.K % a.group_size == 0 && 256 * (a.K / a.group_size) <= kPpScaleMax;
+  return a.fmt == SMOE_BF16 || (a.fmt == SMOE_FP8_E4M3 && a.Wt && a.N_out % 16 == 0 &&
+                                a.epi != EPI_ROWSCALE);
 }
 
 bool gemm_takes_row_tiles(const GemmArgs& a) {

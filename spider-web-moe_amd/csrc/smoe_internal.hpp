@@ -95,8 +95,7 @@ inline int64_t row_tile_elems(int64_t rows, int64_t cols) { return (rows + 15) /
 // bf16 / fp8 w [G,N,K] -> the weight tile layout (smoe_pack_weight_tiles)
 int launch_pack_weight_tiles(const void* w, int fmt, int G, int N, int K, void* out, hipStream_t s);
 // int4 [G,N,K/2] + group scales -> bf16 tiles of the dequantized weights
-int launch_pack_int4_tiles(const void* q, const void* scales, int s_f16, int gs, int G, int N, int K,
-                           void* out, hipStream_t s);
+int launch_pack_int4_qtiles(const void* q, int G, int N, int K, void* out, hipStream_t s);
 // One bf16 GEMM over a few rows (G == 0, single_rows <= 64) with f32 logits
 // out (EPI_F32_BIAS) from two weight segments: the router and all edge
 // generator rows of a small decode step in one pass.

@@ -78,7 +78,7 @@ SIGNATURES = {
     "smoe_expert_delta": (_c_int, [ctypes.POINTER(SmoeExperts), _vp, _vp, _vp, _c_int, _c_int,
                                    _vp, _c_int, _vp, _sz, _vp]),
     "smoe_pack_weight_tiles": (_c_int, [_vp, _c_int, _c_int, _c_int, _c_int, _vp, _vp]),
-    "smoe_pack_int4_tiles": (_c_int, [_vp, _vp, _c_int, _c_int, _c_int, _c_int, _c_int, _vp, _vp]),
+    "smoe_pack_int4_qtiles": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _vp]),
     "smoe_edge_topm_workspace_bytes": (_sz, [_c_int, _c_int, _c_int, _c_int]),
     "smoe_edge_topm": (_c_int, [_vp, _c_int, _c_int, _c_int, _vp, _c_int, _vp, _c_int, _c_int,
                                 _c_int, _vp, _vp, _vp, _vp, _sz, _vp]),

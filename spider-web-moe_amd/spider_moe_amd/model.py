@@ -75,9 +75,6 @@ class _Packed:
         self.keep = []
         self.desc = nat.SmoeBlock()
         self.ws_need = {}  # tokens -> workspace bytes
-        # int4 experts: the sources of their bf16 dequant tiles, made on the
-        # first call with prefill-size expert groups (None once made / unused)
-        self.int4_tiles_src = None
 
 
 class SpiderMoELayer(nn.Module):
@@ -125,17 +122,14 @@ class SpiderMoELayer(nn.Module):
         self._int4_b_up = None
         self._int4_b_down = None
         self._fp8 = None  # (codes_up, scale_up, codes_down, scale_down)
-        # bf16 weights also get a copy in the weight tile layout (lane-ordered
-        # MFMA fragments, 1 KB per 16 rows x 32 k), which the decode weight
-        # stream and the prefill GEMM read with contiguous 1 KB loads; False
-        # saves that memory (same results either way)
+        # bf16 / fp8 weights also get a copy in the weight tile layout
+        # (lane-ordered MFMA fragments, 1 KB per 16 rows x 32 k), which the
+        # decode weight stream and the prefill GEMM read with contiguous 1 KB
+        # loads; int4 experts a copy of their bytes in the int4 tile layout,
+        # which the prefill GEMM widens in registers.  False saves that
+        # memory (same results for bf16 / fp8; int4 prefill then runs the
+        # general int4 kernel)
         self.weight_tiles = True
-        # int4 experts at prefill sizes (>= 256 rows per expert): the
-        # ping-pong GEMM reads a bf16 copy of the dequantized weights, 4x the
-        # int4 bytes, made on the first such call when it fits this many
-        # bytes (0: never; prefill-size int4 calls then run the general int4
-        # kernel, about twice as slow, and the weights stay int4 only)
-        self.int4_dequant_tiles_max_bytes = 1 << 30
         self._packed: _Packed | None = None
         self._packed_key = None
         self._plist = None
@@ -365,13 +359,21 @@ class SpiderMoELayer(nn.Module):
                       "smoe_pack_weight_tiles")
             return out
 
+        def int4_tiles(q):  # the same bytes in the int4 tile layout (smoe_pack_int4_qtiles)
+            if q is None or not self.weight_tiles or q.shape[1] % 64 or (2 * q.shape[2]) % 32:
+                return None
+            out = keep(torch.empty_like(q))
+            nat.check(lib.smoe_pack_int4_qtiles(q.data_ptr(), q.shape[0], q.shape[1], 2 * q.shape[2],
+                                                out.data_ptr(), nat.stream_of(dev)),
+                      "smoe_pack_int4_qtiles")
+            return out
+
         if ex.format == nat.FP8_E4M3:
             ex.w_up_tiles = nat.ptr(tiles(w_up, nat.FP8_E4M3))
             ex.w_down_tiles = nat.ptr(tiles(w_down, nat.FP8_E4M3))
         elif ex.format == nat.INT4:
-            if self.weight_tiles and all(q.shape[1] % 16 == 0 and (2 * q.shape[2]) % 64 == 0
-                                         for q in (w_up, w_down)):
-                k.int4_tiles_src = (w_up, s_up, w_down, s_down)
+            ex.w_up_tiles = nat.ptr(int4_tiles(w_up))
+            ex.w_down_tiles = nat.ptr(int4_tiles(w_down))
         elif ex.format == nat.BF16:
             ex.w_up_tiles = nat.ptr(tiles(w_up))
             ex.w_down_tiles = nat.ptr(tiles(w_down))
@@ -391,38 +393,6 @@ class SpiderMoELayer(nn.Module):
         # the parameters that now live in the stacks moved: the key after the move
         self._packed, self._packed_key = k, self._state_key()
         return k
-
-    def int4_dequant_tiles_bytes(self) -> int:
-        """Bytes of the bf16 dequant copy prefill-size int4 calls would make
-        (both expert weight stacks, 2 bytes a weight)."""
-        if self._int4_w_up is None:
-            return 0
-        return 2 * 2 * (self._int4_w_up.packed.numel() + self._int4_w_down.packed.numel())
-
-    def _int4_prefill_tiles(self, k: _Packed, n: int, dev) -> None:
-        """int4 experts with weight_tiles: on the first call whose expert
-        groups reach the large-tile GEMM's size (n * top_k >= 256 per expert),
-        the bf16 tiles of the dequantized weights (smoe_pack_int4_tiles), 4x
-        the int4 bytes, if they fit int4_dequant_tiles_max_bytes;
-        decode-size calls keep the packed int4 alone."""
-        if k.int4_tiles_src is None or n * self.top_k < 256 * self.num_experts:
-            return
-        if self.int4_dequant_tiles_bytes() > int(self.int4_dequant_tiles_max_bytes):
-            return
-        w_up, s_up, w_down, s_down = k.int4_tiles_src
-        ex = k.desc.experts
-        lib = nat.lib()
-        ptrs = []
-        for q, sc in ((w_up, s_up), (w_down, s_down)):
-            g, rows, half = q.shape
-            out = torch.empty(g, rows, 2 * half, dtype=torch.bfloat16, device=dev)
-            nat.check(lib.smoe_pack_int4_tiles(q.data_ptr(), sc.data_ptr(), ex.scale_dtype,
-                                               ex.group_size, g, rows, 2 * half, out.data_ptr(),
-                                               nat.stream_of(dev)), "smoe_pack_int4_tiles")
-            k.keep.append(out)
-            ptrs.append(out.data_ptr())
-        ex.w_up_tiles, ex.w_down_tiles = ptrs
-        k.int4_tiles_src = None
 
     def workspace_bytes(self, n: int, packed: _Packed | None = None) -> int:
         """Bytes of the native workspace a call over n tokens needs."""
@@ -463,7 +433,6 @@ class SpiderMoELayer(nn.Module):
             return self._run_offload(h2, x2, loop_begin, num_loops, gate).view(b, t, width)
         out = torch.empty_like(h2)
         k = self._pack()
-        self._int4_prefill_tiles(k, n, dev)
         if workspace is None:
             ws = self._workspace(n, dev, k)
         else:

@@ -175,36 +175,40 @@ def test_packed_weights_share_the_parameters_storage():
     assert not torch.equal(out, out2)
 
 
-def test_int4_dequant_copy_respects_its_byte_budget():
-    """The bf16 dequant copy of prefill-size int4 calls is made only within
-    int4_dequant_tiles_max_bytes: with a budget of 0 the weights stay int4
-    (no copy, the general int4 kernel) and the block still matches the
-    oracle; with the default budget the copy appears and the output is
-    the same to the dequant rounding."""
+def test_int4_prefill_keeps_weights_int4():
+    """int4 experts at prefill size run the ping-pong GEMM on their int4
+    tile copy (the same bytes as the int4 weights, widened in registers):
+    packing adds no more than the int4 bytes, and the block matches the
+    oracle with the copy and without it (weight_tiles = False: the general
+    int4 kernel)."""
     from spider_moe_amd.workloads import make_block
-    say("int4 dequant copy budget")
+    say("int4 prefill on int4 tiles")
     wl = make_block("c1", tokens=2048, hidden_size=256, num_experts=8, top_k=2, edges_per_expert=2,
                     expert_ffn_size=512, num_loops=1, expert_activation="gelu", experts="int4",
                     group_size=64, std="fan_in")
     layer = wl.layer
-    assert layer.int4_dequant_tiles_bytes() == 2 * 2 * 8 * 256 * 512  # two stacks, bf16
-    layer.int4_dequant_tiles_max_bytes = 0
+    qbytes = layer._int4_w_up.packed.numel() + layer._int4_w_down.packed.numel()
+    torch.cuda.synchronize()
+    before = torch.cuda.memory_allocated()
     got, _ = _check_loop(layer, wl.h, wl.x0, 0, 1e-2)
     ex = layer._pack().desc.experts
-    assert not ex.w_up_tiles and not ex.w_down_tiles
-    layer.int4_dequant_tiles_max_bytes = 1 << 30
-    got2, _ = _check_loop(layer, wl.h, wl.x0, 0, 1e-2)
-    ex = layer._pack().desc.experts
     assert ex.w_up_tiles and ex.w_down_tiles
+    grown = torch.cuda.memory_allocated() - before - layer._ws.numel()
+    heavy_tiles = 2 * 8 * 256 * 256 * 2  # the bf16 edge-value tile copy
+    assert grown <= qbytes + heavy_tiles + (4 << 20), (grown, qbytes)
+    layer.weight_tiles = False
+    plain, _ = _check_loop(layer, wl.h, wl.x0, 0, 1e-2)
+    assert not layer._pack().desc.experts.w_up_tiles
+    assert (got.float() - plain.float()).abs().max() <= 2e-2
 
 
 @pytest.mark.parametrize("experts,act", [("fp8", "swiglu"), ("int4", "gelu"), ("int4", "swiglu")])
 def test_block_prefill_quantized_experts(experts, act):
     """Quantized experts at prefill size (2048 tokens over 8 experts: ~512
     rows each), so the expert GEMMs run on the large-tile kernel: fp8 from
-    its weight tiles, int4 from the bf16 tiles of its dequantized weights,
-    which the layer makes on this first prefill-size call.  Per loop against
-    the oracle (routing, plans, edges, message, delta, output)."""
+    its weight tiles, int4 from its int4 tile copy (nibbles widened in
+    registers).  Per loop against the oracle (routing, plans, edges,
+    message, delta, output)."""
     from spider_moe_amd.workloads import make_block
     say("prefill quantized block", experts, act)
     wl = make_block("c1", tokens=2048, hidden_size=256, num_experts=8, top_k=2, edges_per_expert=2,
@@ -215,7 +219,7 @@ def test_block_prefill_quantized_experts(experts, act):
         h, _ = _check_loop(wl.layer, h, wl.x0, r, 1e-2)
     if experts == "int4":
         ex = wl.layer._pack().desc.experts
-        assert ex.w_up_tiles and ex.w_down_tiles  # the dequant tiles were made and read
+        assert ex.w_up_tiles and ex.w_down_tiles  # the tile copies were made and read
 
 
 @pytest.mark.parametrize("n,e,k,m", [(1, 16, 2, 2), (37, 16, 2, 2), (64, 32, 4, 2), (48, 64, 2, 4),

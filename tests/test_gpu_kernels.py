@@ -365,34 +365,43 @@ def test_large_fp8_experts_ragged_groups(act, n):
         assert (out - ref).abs().max() <= 2e-2 * scale + 1e-6, float((out - ref).abs().max() / scale)
 
 
-@pytest.mark.parametrize("group,sdt", [(32, torch.float32), (128, torch.float16)])
-def test_pack_int4_tiles_is_the_dequantized_tile_copy(group, sdt):
-    """smoe_pack_int4_tiles = the bf16 weight tiles (smoe_pack_weight_tiles)
-    of the oracle's dequantized weights (q * s in fp32, rounded once to
-    bf16), bit for bit."""
+def _int4_qtiles_ref(packed: torch.Tensor) -> torch.Tensor:
+    """The int4 tile layout on the CPU: row 64 Q + 16 t + r, bytes
+    16 st + 4 fc .. +3 of the packed row -> block (g, Q, st), tile t, lane
+    16 fc + r, 4 bytes each."""
+    g, n, kb = packed.shape
+    k = 2 * kb
+    p = packed.reshape(g, n // 64, 4, 16, k // 32, 4, 4)  # g, Q, t, r, st, fc, byte
+    return p.permute(0, 1, 4, 2, 5, 3, 6).contiguous().reshape(-1)
+
+
+@pytest.mark.parametrize("n,kd", [(64, 32), (192, 256), (128, 2816)])
+def test_pack_int4_qtiles_layout(n, kd):
+    """smoe_pack_int4_qtiles rearranges the packed bytes into the int4 tile
+    layout, byte for byte (checked against the layout written out on the
+    CPU), and holds every byte exactly once."""
     from spider_moe_amd.quant import quantize_int4
     n8 = nat()
-    say("pack int4 tiles", group, sdt)
-    w = torch.randn(3, 48, 256, generator=torch.Generator().manual_seed(9)) * 0.05
-    q = quantize_int4(w, group, sdt)
-    deq = torch.from_numpy(Q.int4_dequantize(q.packed.numpy(), q.scales.float().numpy(), group))
-    want = _tiles(n8, deq.to(torch.bfloat16).to(dev))
-    qp, qs = q.packed.contiguous().to(dev), q.scales.contiguous().to(dev)
-    got = torch.empty(3, 48, 256, dtype=torch.bfloat16, device=dev)
-    n8.check(n8.lib().smoe_pack_int4_tiles(qp.data_ptr(), qs.data_ptr(),
-                                           n8.F16 if sdt == torch.float16 else n8.F32, group, 3, 48,
-                                           256, got.data_ptr(), n8.stream_of(torch.device(dev))),
-             "pack_int4_tiles")
+    say("pack int4 qtiles", n, kd)
+    w = torch.randn(3, n, kd, generator=torch.Generator().manual_seed(9)) * 0.05
+    q = quantize_int4(w, 32, torch.float32)
+    qp = q.packed.contiguous()
+    got = torch.empty_like(qp, device=dev)
+    n8.check(n8.lib().smoe_pack_int4_qtiles(qp.to(dev).data_ptr(), 3, n, kd, got.data_ptr(),
+                                            n8.stream_of(torch.device(dev))), "pack_int4_qtiles")
     torch.cuda.synchronize()
-    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    want = _int4_qtiles_ref(qp)
+    assert torch.equal(got.cpu().reshape(-1), want)
+    assert torch.equal(torch.sort(want).values, torch.sort(qp.reshape(-1)).values)
 
 
 @pytest.mark.parametrize("act,n", [("gelu", 2304), ("swiglu", 2304), ("swiglu", 1100)])
 def test_large_int4_experts_ragged_groups(act, n):
     """int4 experts (group 128, fp16 scales) at prefill sizes with skewed
-    routing, with the bf16 tiles of their dequantized weights: the ping-pong
-    GEMM (at n = 1100 its 128-row tiles) against the oracle over the
-    dequantized weights, and against the general int4 kernel (no tiles)."""
+    routing, with their int4 tile copy: the ping-pong GEMM (256-row tiles,
+    nibbles widened in registers) against the oracle over the dequantized
+    weights, and against the general int4 kernel (no tiles), which
+    multiplies the same bf16(q * s) values: equal to f32 summation order."""
     from spider_moe_amd.quant import interleave_gate_up, quantize_int4
     n8 = nat()
     say("large int4 experts", act, n)
@@ -424,12 +433,11 @@ def test_large_int4_experts_ragged_groups(act, n):
                          b_up=t[4], b_down=t[5], group=group, scale_dtype=n8.F16)
     plain = _run_delta(n8, ex, msg.to(dev), idx.to(torch.int32).to(dev), w.to(dev))
     tiles = []
-    for q_, s_ in ((t[0], t[2]), (t[1], t[3])):
-        out = torch.empty(q_.shape[0], q_.shape[1], 2 * q_.shape[2], dtype=torch.bfloat16, device=dev)
-        n8.check(n8.lib().smoe_pack_int4_tiles(q_.data_ptr(), s_.data_ptr(), n8.F16, group,
-                                               q_.shape[0], q_.shape[1], 2 * q_.shape[2],
-                                               out.data_ptr(), n8.stream_of(torch.device(dev))),
-                 "pack_int4_tiles")
+    for q_ in (t[0], t[1]):
+        out = torch.empty_like(q_)
+        n8.check(n8.lib().smoe_pack_int4_qtiles(q_.data_ptr(), q_.shape[0], q_.shape[1],
+                                                2 * q_.shape[2], out.data_ptr(),
+                                                n8.stream_of(torch.device(dev))), "pack_int4_qtiles")
         tiles.append(out)
     ex.w_up_tiles, ex.w_down_tiles = tiles[0].data_ptr(), tiles[1].data_ptr()
     got = _run_delta(n8, ex, msg.to(dev), idx.to(torch.int32).to(dev), w.to(dev))
@@ -437,6 +445,8 @@ def test_large_int4_experts_ragged_groups(act, n):
     assert torch.isfinite(got).all()
     for out in (got, plain):
         assert (out - ref).abs().max() <= 2e-2 * scale + 1e-6, float((out - ref).abs().max() / scale)
+    # the same bf16 weights on both kernels: only the f32 summation order differs
+    assert (got - plain).abs().max() <= 2e-3 * scale, float((got - plain).abs().max() / scale)
 
 
 @pytest.mark.parametrize("act,group,sdt", [("gelu", 32, torch.float32), ("gelu", 128, torch.float16),
