@@ -242,7 +242,8 @@ void make_layout(const smoe_block* b, int N, smoe_ws_layout* l) {
   l->d_rows = z.take(n * S * 4);
   l->d_roww = z.take(n * S * 4);
   l->d_tokrow = z.take(n * S * 4);
-  l->proj = z.take(n * S * H * esize(b->act_dtype));
+  // decode loops: the edge projection's rows at d * N + t (launch_decode_edge)
+  l->proj = z.take(n * (decode_ok(b, N) ? E : S) * H * esize(b->act_dtype));
   l->msg = z.take(n * H * esize(fdt));
   // act: plan rows, row-major or in the row-tile layout (run_experts)
   l->act = z.take(row_tile_elems(n * K, U) * esize(fdt));
@@ -451,20 +452,82 @@ int block_forward(const smoe_block* b, const void* h_in, const void* x0, void* h
       fa.sel_idx = at<int32_t>(ws, l.sel_idx);
       fa.sel_w = at<float>(ws, l.sel_w);
       STAGE(SMOE_STAGE_FRONT_GEMM, launch_decode_front(fa, s), "decode front");
-      STAGE(SMOE_STAGE_FRONT_ROUTE,
-            launch_decode_plan(at<int32_t>(ws, l.top_idx), at<float>(ws, l.top_w),
-                               at<int32_t>(ws, l.sel_idx), at<float>(ws, l.sel_w), N, E, K, M, S,
-                               at<int32_t>(ws, l.tok_e), at<float>(ws, l.tok_ew),
-                               at<int32_t>(ws, l.e_cnt), at<int32_t>(ws, l.e_acnt),
-                               at<int32_t>(ws, l.e_off), at<int32_t>(ws, l.e_rows),
-                               at<float>(ws, l.e_roww), at<int32_t>(ws, l.e_tokrow),
-                               at<int32_t>(ws, l.edge_idx), at<float>(ws, l.edge_w),
-                               at<int32_t>(ws, l.tok_d), at<float>(ws, l.tok_dc),
-                               at<int32_t>(ws, l.d_cnt), at<int32_t>(ws, l.d_acnt),
-                               at<int32_t>(ws, l.d_off), at<int32_t>(ws, l.d_rows),
-                               at<float>(ws, l.d_roww), at<int32_t>(ws, l.d_tokrow), s),
-            "decode plans");
       cur = in_r;
+      DecPlan dp;
+      dp.top_idx = at<int32_t>(ws, l.top_idx);
+      dp.top_w = at<float>(ws, l.top_w);
+      dp.sel_idx = at<int32_t>(ws, l.sel_idx);
+      dp.sel_w = at<float>(ws, l.sel_w);
+      dp.N = N;
+      dp.E = E;
+      dp.K = K;
+      dp.M = M;
+      dp.S = S;
+      dp.tok_e = at<int32_t>(ws, l.tok_e);
+      dp.tok_ew = at<float>(ws, l.tok_ew);
+      dp.e_cnt = at<int32_t>(ws, l.e_cnt);
+      dp.e_acnt = at<int32_t>(ws, l.e_acnt);
+      dp.e_off = at<int32_t>(ws, l.e_off);
+      dp.e_rows = at<int32_t>(ws, l.e_rows);
+      dp.e_roww = at<float>(ws, l.e_roww);
+      dp.e_tokrow = at<int32_t>(ws, l.e_tokrow);
+      dp.edge_idx = at<int32_t>(ws, l.edge_idx);
+      dp.edge_w = at<float>(ws, l.edge_w);
+      dp.tok_d = at<int32_t>(ws, l.tok_d);
+      dp.tok_dc = at<float>(ws, l.tok_dc);
+      dp.d_cnt = at<int32_t>(ws, l.d_cnt);
+      dp.d_acnt = at<int32_t>(ws, l.d_acnt);
+      dp.d_off = at<int32_t>(ws, l.d_off);
+      dp.d_rows = at<int32_t>(ws, l.d_rows);
+      dp.d_roww = at<float>(ws, l.d_roww);
+      dp.d_tokrow = at<int32_t>(ws, l.d_tokrow);
+      // the edge projection with the plans beside it (one launch), where
+      // its kernel takes the shape
+      GemmArgs pg;
+      pg.fmt = SMOE_BF16;
+      pg.epi = EPI_ROWSCALE;
+      pg.A = cur;
+      pg.lda = H;
+      pg.W = b->edge_value_w;
+      pg.Wt = b->edge_value_w_tiles;
+      pg.w_gstride = static_cast<int64_t>(H) * H;
+      pg.ldw = H;
+      pg.K = H;
+      pg.N_out = H;
+      pg.G = E;
+      pg.max_rows = N * S;
+      pg.out = at<void>(ws, l.proj);
+      pg.ldo = H;
+      pg.out_dtype = adt;
+      pg.sel_idx = dp.sel_idx;
+      pg.sel_w = dp.sel_w;
+      pg.sel_km = K * M;
+      pg.sel_n = N;
+      int erc = SMOE_EUNSUPPORTED;
+      if (b->edge_value_w_tiles) {
+        STAGE(SMOE_STAGE_EDGE_GEMM, (erc = launch_decode_edge(pg, dp, s)) == SMOE_EUNSUPPORTED ? SMOE_OK : erc,
+              "decode edge projection");
+      }
+      if (erc == SMOE_OK) {
+        STAGE(SMOE_STAGE_MSG_COMBINE,
+              launch_msg_combine(at<void>(ws, l.proj), adt, at<int32_t>(ws, l.tok_d),
+                                 at<int32_t>(ws, l.d_tokrow), N, S, H, at<void>(ws, l.msg), fdt, s,
+                                 N),
+              "msg combine");
+        rc = run_experts(b->experts, at<void>(ws, l.msg), at<int32_t>(ws, l.e_off),
+                         at<int32_t>(ws, l.e_rows), at<float>(ws, l.e_roww), N * K,
+                         at<void>(ws, l.act), at<void>(ws, l.y), s);
+        if (rc != SMOE_OK) return rc;
+        if (i + 1 < num_loops) continue;  // the epilogue: in the next loop's front
+        STAGE(SMOE_STAGE_EPILOGUE,
+              launch_epilogue(cur, x0, adt, at<void>(ws, l.y), fdt, at<int32_t>(ws, l.tok_e),
+                              at<float>(ws, l.tok_ew), at<int32_t>(ws, l.e_tokrow), N, K, H,
+                              b->alpha, b->beta, b->ln_w, b->ln_b, b->eps, h_out, gate, s),
+              "epilogue");
+        cur = h_out;
+        continue;
+      }
+      STAGE(SMOE_STAGE_FRONT_ROUTE, launch_decode_plan(dp, s), "decode plans");
     } else if (front) {
       // 1-6 fused: [router | all edge generator rows] logits, then routing
       const int ldf = E + E * E;

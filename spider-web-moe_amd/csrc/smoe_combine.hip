@@ -17,12 +17,15 @@
 namespace smoe {
 
 // CPL = 8-element chunks per lane (H <= 512 * CPL)
-// Lane j (< S) holds the token's j-th (destination, row) entry.
-template <int CPL, int PDT, int MDT>
+// Lane j (< S) holds the token's j-th (destination, row) entry.  DENSE: the
+// row of destination d is d * dense_n + t (the decode edge projection's
+// layout), else d_tokrow's.
+template <int CPL, int PDT, int MDT, bool DENSE>
 __global__ __launch_bounds__(256) void k_msg_combine(const void* __restrict__ proj,
                                                      const int32_t* __restrict__ tok_d,
                                                      const int32_t* __restrict__ d_tokrow, int N,
-                                                     int S, int H, void* __restrict__ msg) {
+                                                     int S, int H, void* __restrict__ msg,
+                                                     int dense_n) {
   const int lane = threadIdx.x & 63;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= N) return;
@@ -30,7 +33,7 @@ __global__ __launch_bounds__(256) void k_msg_combine(const void* __restrict__ pr
   // branch for the compiler to wait at
   const int64_t e = static_cast<int64_t>(t) * S + (lane < S ? lane : S - 1);
   const int d = tok_d[e];
-  const int r = d_tokrow[e];
+  const int r = DENSE ? d * dense_n + t : d_tokrow[e];
   const int my_row = (lane < S && d >= 0) ? r : -1;  // ascending destination (tok_d is sorted)
   float acc[CPL][8];
 #pragma unroll
@@ -181,14 +184,19 @@ int last_rc() { return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP; }
 }  // namespace
 
 int launch_msg_combine(const void* proj, int pdt, const int32_t* tok_d, const int32_t* d_tokrow,
-                       int N, int S, int H, void* msg, int mdt, hipStream_t s) {
-  if (S < 1 || S > 64) return SMOE_EINVAL;  // one lane per entry
+                       int N, int S, int H, void* msg, int mdt, hipStream_t s, int dense_n) {
+  if (S < 1 || S > 64 || dense_n < 0 || (dense_n > 0 && dense_n < N)) return SMOE_EINVAL;
   if (N <= 0) return SMOE_OK;
   return by_cpl(H, [&](auto cpl) {
     return by_dt(pdt, [&](auto pd) {
       return by_dt(mdt, [&](auto md) {
-        hipLaunchKernelGGL((k_msg_combine<decltype(cpl)::value, decltype(pd)::value, decltype(md)::value>),
-                           dim3((N + 3) / 4), dim3(256), 0, s, proj, tok_d, d_tokrow, N, S, H, msg);
+        constexpr int C = decltype(cpl)::value, P = decltype(pd)::value, Q = decltype(md)::value;
+        if (dense_n > 0)
+          hipLaunchKernelGGL((k_msg_combine<C, P, Q, true>), dim3((N + 3) / 4), dim3(256), 0, s,
+                             proj, tok_d, d_tokrow, N, S, H, msg, dense_n);
+        else
+          hipLaunchKernelGGL((k_msg_combine<C, P, Q, false>), dim3((N + 3) / 4), dim3(256), 0, s,
+                             proj, tok_d, d_tokrow, N, S, H, msg, 0);
         return last_rc();
       });
     });

@@ -3,8 +3,8 @@
 // (topk_seg, plan64_wave, seg_argmax).
 //
 // Decode steps spend most of a loop's time outside the weight streams when
-// every routing stage is its own launch.  Here a loop takes two launches
-// before its edge GEMM:
+// every routing stage is its own launch.  Here a loop takes one launch
+// before its edge projection:
 //
 //  k_decode_front (strip, 16-token tile; 16 waves): the tile's input rows go
 //   to LDS as bf16 — for loops after the first, as the previous loop's
@@ -21,12 +21,15 @@
 //   operations of topm_seg) and, for each token that selected s, writes its
 //   destinations and softmax weights at s's rank among the token's sources.
 //
-//  k_decode_plan (one workgroup, two waves that share no data): wave 0 sorts
+//  the plans (decode_plan_body: two waves that share no data): wave 0 sorts
 //   each token's top-k by expert (tok_e / tok_ew), builds the expert plan
 //   (plan64_wave) and puts each source's edges at its plan row; wave 1 sums
 //   each token's destination coefficients over its sources in ascending
 //   order (the order topm_seg adds them), lists them ascending (tok_d /
-//   tok_dc) and builds the destination plan.
+//   tok_dc) and builds the destination plan.  They run in one workgroup of
+//   the edge projection (k_decode_edge), beside its weight streams, which
+//   read the front's selections directly; k_decode_plan runs them alone
+//   for the shapes k_decode_edge does not take.
 //
 // The previous loop's epilogue is folded into the next front, so a call
 // ends with one k_epilogue after its last loop.
@@ -270,138 +273,31 @@ int launch_decode_front(const DecFront& a, hipStream_t s) {
   return decode_front_h<false>(a, s);
 }
 
-// Plans of a decode loop (N <= 64 tokens, S <= 16 destinations per token);
-// KB >= K and KMB >= K * M (compile-time buckets).  Lane t = token t.
-constexpr int kDecMaxS = 16;
+// Plans of a decode loop in one workgroup of their own (decode_plan_body).
 template <int KB, int KMB>
-__global__ __launch_bounds__(128) void k_decode_plan(
-    const int32_t* __restrict__ top_idx, const float* __restrict__ top_w,
-    const int32_t* __restrict__ sel_idx, const float* __restrict__ sel_w, int N, int E, int K,
-    int M, int S, int32_t* __restrict__ tok_e, float* __restrict__ tok_ew,
-    int32_t* __restrict__ e_cnt, int32_t* __restrict__ e_acnt, int32_t* __restrict__ e_off,
-    int32_t* __restrict__ e_rows, float* __restrict__ e_roww, int32_t* __restrict__ e_tokrow,
-    int32_t* __restrict__ edge_idx, float* __restrict__ edge_w, int32_t* __restrict__ tok_d,
-    float* __restrict__ tok_dc, int32_t* __restrict__ d_cnt, int32_t* __restrict__ d_acnt,
-    int32_t* __restrict__ d_off, int32_t* __restrict__ d_rows, float* __restrict__ d_roww,
-    int32_t* __restrict__ d_tokrow) {
-  __shared__ int32_t s_te[kFrontMaxN * KB], s_etr[kFrontMaxN * KB];
-  __shared__ float s_tw[kFrontMaxN * KB];
-  __shared__ float s_c[kFrontMaxN * 65];
-  __shared__ int32_t s_td[kFrontMaxN * kDecMaxS], s_dtr[kFrontMaxN * kDecMaxS];
-  __shared__ float s_tc[kFrontMaxN * kDecMaxS];
-  __shared__ uint64_t s_km[2][64], s_am[2][64];
-  __shared__ int s_off[2][64];
-  const int t = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const bool tv = t < N;
-  const int tc = tv ? t : 0;
-  const int km = K * M;
-  if (wave == 0) {
-    // the token's top-k sorted by expert (ids are distinct: rank = # smaller),
-    // its sources' edges (in that order already) loaded alongside
-    int ti[KB], ei[KMB];
-    float tw[KB], ew[KMB];
-#pragma unroll
-    for (int j = 0; j < KB; ++j) {
-      const int jj = j < K ? j : K - 1;
-      ti[j] = top_idx[tc * K + jj];
-      tw[j] = top_w[tc * K + jj];
-    }
-#pragma unroll
-    for (int u = 0; u < KMB; ++u) {
-      const int uu = u < km ? u : km - 1;
-      ei[u] = sel_idx[tc * km + uu];
-      ew[u] = sel_w[tc * km + uu];
-    }
-    if (tv)
-#pragma unroll
-      for (int j = 0; j < KB; ++j) {
-        if (j >= K) break;
-        int rank = 0;
-#pragma unroll
-        for (int i = 0; i < KB; ++i) rank += (i < K && ti[i] < ti[j]) ? 1 : 0;
-        s_te[t * K + rank] = ti[j];
-        s_tw[t * K + rank] = tw[j];
-        tok_e[t * K + rank] = ti[j];
-        tok_ew[t * K + rank] = tw[j];
-      }
-    plan64_wave(s_te, s_tw, N, K, E, 0, e_cnt, e_acnt, e_off, e_rows, e_roww, s_etr, s_km[0],
-                s_am[0], s_off[0]);
-    if (tv)
-#pragma unroll
-      for (int u = 0; u < KMB; ++u) {
-        if (u >= km) break;
-        const int j = u / M, i = u - j * M;
-        const int row = s_etr[t * K + j];
-        if (i == 0) e_tokrow[t * K + j] = row;
-        if (row >= 0) {
-          edge_idx[static_cast<int64_t>(row) * M + i] = ei[u];
-          edge_w[static_cast<int64_t>(row) * M + i] = ew[u];
-        }
-      }
-  } else {
-    // destination coefficients: sum over the sources in ascending order
-    int ei[KMB];
-    float ew[KMB];
-#pragma unroll
-    for (int u = 0; u < KMB; ++u) {
-      const int uu = u < km ? u : km - 1;
-      ei[u] = sel_idx[tc * km + uu];
-      ew[u] = sel_w[tc * km + uu];
-    }
-    float* crow = s_c + tc * 65;
-    if (tv) {
-      for (int d = 0; d < E; ++d) crow[d] = 0.f;
-#pragma unroll
-      for (int u = 0; u < KMB; ++u)
-        if (u < km) crow[ei[u]] += ew[u];
-      int cnt = 0;
-      for (int d = 0; d < E; ++d) {
-        const float c = crow[d];
-        if (c != 0.f) {
-          s_td[t * S + cnt] = d;
-          s_tc[t * S + cnt] = c;
-          ++cnt;
-        }
-      }
-      for (int j = cnt; j < S; ++j) {
-        s_td[t * S + j] = -1;
-        s_tc[t * S + j] = 0.f;
-      }
-      for (int j = 0; j < S; ++j) {
-        tok_d[t * S + j] = s_td[t * S + j];
-        tok_dc[t * S + j] = s_tc[t * S + j];
-      }
-    }
-    plan64_wave(s_td, s_tc, N, S, E, 1, d_cnt, d_acnt, d_off, d_rows, d_roww, s_dtr, s_km[1],
-                s_am[1], s_off[1]);
-    if (tv)
-      for (int j = 0; j < S; ++j) d_tokrow[t * S + j] = s_dtr[t * S + j];
-  }
+__global__ __launch_bounds__(128) void k_decode_plan(const DecPlan q) {
+  __shared__ __attribute__((aligned(16))) uint8_t lds[decode_plan_lds_bytes<KB>()];
+  decode_plan_body<KB, KMB>(q, lds);
 }
 
-int launch_decode_plan(const int32_t* top_idx, const float* top_w, const int32_t* sel_idx,
-                       const float* sel_w, int N, int E, int K, int M, int S, int32_t* tok_e,
-                       float* tok_ew, int32_t* e_cnt, int32_t* e_acnt, int32_t* e_off,
-                       int32_t* e_rows, float* e_roww, int32_t* e_tokrow, int32_t* edge_idx,
-                       float* edge_w, int32_t* tok_d, float* tok_dc, int32_t* d_cnt,
-                       int32_t* d_acnt, int32_t* d_off, int32_t* d_rows, float* d_roww,
-                       int32_t* d_tokrow, hipStream_t s) {
-  if (N < 1 || N > kFrontMaxN || E < 1 || E > 64 || K < 1 || K > 16 || K > E || M < 1 ||
-      M > E || M > 16 || S < 1 || S > kDecMaxS || S != (E < K * M ? E : K * M))
-    return SMOE_EINVAL;
-  const int km = K * M;
-#define SMOE_DPLAN(KB_, KMB_)                                                                  \
-  hipLaunchKernelGGL((k_decode_plan<KB_, KMB_>), dim3(1), dim3(128), 0, s, top_idx, top_w,      \
-                     sel_idx, sel_w, N, E, K, M, S, tok_e, tok_ew, e_cnt, e_acnt, e_off, e_rows, \
-                     e_roww, e_tokrow, edge_idx, edge_w, tok_d, tok_dc, d_cnt, d_acnt, d_off,    \
-                     d_rows, d_roww, d_tokrow)
+bool decode_plan_fits(const DecPlan& q) {
+  const int N = q.N, E = q.E, K = q.K, M = q.M, S = q.S;
+  return N >= 1 && N <= kFrontMaxN && E >= 1 && E <= 64 && K >= 1 && K <= 16 && K <= E &&
+         M >= 1 && M <= E && M <= 16 && S >= 1 && S <= kDecMaxS &&
+         S == (E < K * M ? E : K * M) && K * M <= 64;
+}
+
+int launch_decode_plan(const DecPlan& q, hipStream_t s) {
+  if (!decode_plan_fits(q)) return SMOE_EINVAL;
+  const int K = q.K, km = q.K * q.M;
+#define SMOE_DPLAN(KB_, KMB_) \
+  hipLaunchKernelGGL((k_decode_plan<KB_, KMB_>), dim3(1), dim3(128), 0, s, q)
   if (K <= 2 && km <= 4) SMOE_DPLAN(2, 4);
   else if (K <= 2 && km <= 8) SMOE_DPLAN(2, 8);
   else if (K <= 4 && km <= 8) SMOE_DPLAN(4, 8);
   else if (K <= 4 && km <= 16) SMOE_DPLAN(4, 16);
   else if (K <= 8 && km <= 32) SMOE_DPLAN(8, 32);
-  else if (km <= 64) SMOE_DPLAN(16, 64);
-  else return SMOE_EINVAL;
+  else SMOE_DPLAN(16, 64);
 #undef SMOE_DPLAN
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }

@@ -22,6 +22,7 @@
 
 #include "smoe_common.hpp"
 #include "smoe_internal.hpp"
+#include "smoe_plan64.hpp"
 
 namespace smoe {
 
@@ -1228,22 +1229,82 @@ template <> struct DRaw<SMOE_BF16> { u32x4 a, b; };
 template <> struct DRaw<SMOE_FP8_E4M3> { u32x4 a; };
 template <> struct DRaw<SMOE_INT4> { u32x2 a; float s; };
 
-template <int FMT, int EPI, int TNW, int RT, int KSPLIT, int D, bool PK = false>
-__global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
+// The position of the j-th set bit (0-based) of m; j < popcount(m).
+__device__ __forceinline__ int nth_set_bit(uint64_t m, int j) {
+  int pos = 0;
+#pragma unroll
+  for (int w = 32; w >= 1; w >>= 1) {
+    const uint64_t lo = m & ((1ull << w) - 1ull);
+    const int c = __popcll(lo);
+    const bool up = j >= c;
+    j = up ? j - c : j;
+    m = up ? (m >> w) : lo;
+    pos += up ? w : 0;
+  }
+  return pos;
+}
+
+// SEL: the decode edge projection's row selection (GemmArgs::sel_*): row
+// tile gy is tile gy % sel_tpg of destination gy / sel_tpg, whose rows are
+// found from the front's selections by a ballot over the tokens (lane t);
+// its weights are known before any load.  red: LDS of
+// (KSPLIT > 1 ? 4 : 1) * TNW * RT * 64 f32x4.
+template <int FMT, int EPI, int TNW, int RT, int KSPLIT, int D, bool PK, bool SEL>
+__device__ __forceinline__ void decode_gemm(const GemmArgs& p, int gy, f32x4* red) {
   constexpr int ESZ2 = FMT == SMOE_BF16 ? 4 : (FMT == SMOE_FP8_E4M3 ? 2 : 1);  // 2 x bytes/elt
   constexpr int CS = 4 / KSPLIT;  // channel slices per workgroup
   static_assert(4 % KSPLIT == 0, "KSPLIT divides the 4 waves");
   static_assert(EPI != EPI_SWIGLU || TNW == 2 || TNW == 4, "SwiGLU slices pair gate and up tiles");
   static_assert(!PK || FMT != SMOE_INT4, "the weight tile layout holds bf16 or fp8 weights");
+  static_assert(!SEL || EPI == EPI_ROWSCALE, "row selection: the edge projection");
   constexpr int BLK = 512 * ESZ2;  // bytes of one 64-k step of a 16-row tile
-  __shared__ f32x4 red[KSPLIT > 1 ? 4 : 1][TNW * RT][64];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int q = lane >> 4, l16 = lane & 15;
   const int kp = wave % KSPLIT, slice = blockIdx.x * CS + wave / KSPLIT;
   int g, r_lo, r_hi;
-  {
+  int stok[RT];     // SEL: the token of the lane's row in each 16-row tile, -1 past the tile's rows
+  int atok[RT];     // SEL: the token whose A row the lane loads (past the rows: the tile's first)
+  float scoef[RT];  // SEL: its coefficient (the row scale)
+  if constexpr (SEL) {
+    g = gy / p.sel_tpg;
+    const int tile = gy - g * p.sel_tpg;
+    // lane t: c[t, g], token t's selected edges to g summed in order (the
+    // destination plan's coefficient, the same operations); sel_km is a
+    // multiple of 4 and at most 16
+    const int km = p.sel_km, kv = km >> 2;
+    const int tt = lane < p.sel_n ? lane : 0;
+    const int32_t* si = p.sel_idx + static_cast<int64_t>(tt) * km;
+    const float* sw = p.sel_w + static_cast<int64_t>(tt) * km;
+    i32x4 iv[4];
+    f32x4 wv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {  // unconditional loads at clamped indices
+      const int jj = j < kv ? j : kv - 1;
+      iv[j] = reinterpret_cast<const i32x4*>(si)[jj];
+      wv[j] = reinterpret_cast<const f32x4*>(sw)[jj];
+    }
+    float c = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (j < kv && iv[j][i] == g) c += wv[j][i];
+    const uint64_t mask = __ballot(lane < p.sel_n && c != 0.f);
+    const int cnt = __popcll(mask);
+    r_lo = 16 * RT * tile;
+    if (r_lo >= cnt) return;  // uniform, before any barrier
+    r_hi = min(cnt, r_lo + 16 * RT);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int j = r_lo + 16 * rt + l16;
+      const int tok = nth_set_bit(mask, j < r_hi ? j : r_lo);  // past the rows: a valid token, never stored
+      atok[rt] = tok;
+      stok[rt] = j < r_hi ? tok : -1;
+      scoef[rt] = __shfl(c, tok);
+    }
+  } else {
     int m0, mrows;
-    if (!find_tile(p, 16 * RT, blockIdx.y, g, m0, mrows)) return;  // uniform, before any barrier
+    if (!find_tile(p, 16 * RT, gy, g, m0, mrows)) return;  // uniform, before any barrier
     r_lo = m0;
     r_hi = m0 + mrows;
   }
@@ -1278,9 +1339,14 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
   const uint16_t* arow[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    int r = r_lo + 16 * rt + l16;
-    r = r < r_hi ? r : r_lo;  // rows past the tile: a valid row, never stored
-    const int ar = p.a_rows ? p.a_rows[r] : r;
+    int ar;
+    if constexpr (SEL) {
+      ar = atok[rt];
+    } else {
+      int r = r_lo + 16 * rt + l16;
+      r = r < r_hi ? r : r_lo;  // rows past the tile: a valid row, never stored
+      ar = p.a_rows ? p.a_rows[r] : r;
+    }
     arow[rt] = A + static_cast<int64_t>(ar) * p.lda;
   }
   const int steps = p.K / 64;
@@ -1385,7 +1451,8 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     const int r = min(r_lo + 16 * rt + l16, r_hi - 1);
-    ers[rt] = (EPI == EPI_ROWSCALE || EPI == EPI_DOWN) ? p.row_scale[r] : 1.0f;
+    if constexpr (SEL) ers[rt] = scoef[rt];
+    else ers[rt] = (EPI == EPI_ROWSCALE || EPI == EPI_DOWN) ? p.row_scale[r] : 1.0f;
   }
   // the last 2D - 1 steps at most: refills only where a step is left
 #pragma unroll
@@ -1401,7 +1468,7 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
 #pragma unroll
       for (int t = 0; t < TNW; ++t)
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) red[wave][t * RT + rt][lane] = acc[t][rt];
+        for (int rt = 0; rt < RT; ++rt) red[(wave * TNW * RT + t * RT + rt) * 64 + lane] = acc[t][rt];
     __syncthreads();
     if (kp > 0) return;
 #pragma unroll
@@ -1409,7 +1476,8 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
 #pragma unroll
       for (int t = 0; t < TNW; ++t)
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) acc[t][rt] += red[wave + j][t * RT + rt][lane];
+        for (int rt = 0; rt < RT; ++rt)
+          acc[t][rt] += red[((wave + j) * TNW * RT + t * RT + rt) * 64 + lane];
   }
   // lane: channels c0[t] + 4 q + (0..3) of row r_lo + 16 rt + l16.
   // Stores count in vmcnt too: one explicit wait for the epilogue operands
@@ -1427,8 +1495,13 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
     };
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      const int row = r_lo + 16 * rt + l16;
-      if (row >= r_hi) continue;
+      int row = r_lo + 16 * rt + l16;
+      if constexpr (SEL) {
+        if (stok[rt] < 0) continue;
+        row = g * p.sel_n + stok[rt];
+      } else if (row >= r_hi) {
+        continue;
+      }
       if constexpr (EPI == EPI_SWIGLU) {
 #pragma unroll
         for (int t = 0; t < TNW / 2; ++t) {  // gate tile t, up tile t + TNW / 2
@@ -1464,6 +1537,31 @@ __global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
   };
   if (EPI == EPI_F32_BIAS || p.out_dtype == SMOE_F32) emit(std::true_type{});
   else emit(std::false_type{});
+}
+
+template <int FMT, int EPI, int TNW, int RT, int KSPLIT, int D, bool PK = false>
+__global__ __launch_bounds__(256) void k_gemm_decode(const GemmArgs p) {
+  __shared__ f32x4 red[(KSPLIT > 1 ? 4 : 1) * TNW * RT * 64];
+  decode_gemm<FMT, EPI, TNW, RT, KSPLIT, D, PK, false>(p, blockIdx.y, red);
+}
+
+// The decode edge projection (bf16 weight tiles, row selection from the
+// front's top-m) and, in the first workgroup, the loop's plans
+// (decode_plan_body; the rest of grid row 0 exits at once).  Row 0 is
+// dispatched first, so the plans start with the weight streams even when
+// the grid exceeds one round of workgroup slots.  One LDS allocation serves
+// either role.
+template <int RT, int KSPLIT>
+__global__ __launch_bounds__(256) void k_decode_edge(const GemmArgs p, const DecPlan q) {
+  constexpr int RED = (KSPLIT > 1 ? 4 : 1) * 4 * RT * 64 * 16;
+  constexpr int PLAN = decode_plan_lds_bytes<4>();
+  __shared__ __attribute__((aligned(16))) uint8_t lds[RED > PLAN ? RED : PLAN];
+  if (blockIdx.y == 0) {  // uniform
+    if (blockIdx.x == 0) decode_plan_body<4, 16>(q, lds);
+    return;
+  }
+  decode_gemm<SMOE_BF16, EPI_ROWSCALE, 4, RT, KSPLIT, 3, true, true>(
+      p, blockIdx.y - 1, reinterpret_cast<f32x4*>(lds));
 }
 
 // ------------------------------------------------------- weight stream ----
@@ -2539,6 +2637,44 @@ int launch_grouped_gemm(const GemmArgs& a, hipStream_t s) {
   if (a.N_out <= 64)
     return b64 ? launch_mfma<64, 64, 64, 4, 1>(a, s) : launch_mfma<64, 64, 32, 4, 1>(a, s);
   return b64 ? launch_mfma<128, 128, 64, 2, 2>(a, s) : launch_mfma<128, 128, 32, 2, 2>(a, s);
+}
+
+int launch_decode_edge(const GemmArgs& a, const DecPlan& q, hipStream_t s) {
+  const int E = a.G, N = a.sel_n, km = a.sel_km;
+  if (!a.sel_idx || !a.sel_w || !a.A || !a.Wt || !a.out) return SMOE_EINVAL;
+  if (a.fmt != SMOE_BF16 || a.epi != EPI_ROWSCALE || a.N_out < 128 || a.N_out % 16 ||
+      a.K % 64 || !skinny_aligned(a) || km < 4 || km > 16 || km % 4 ||
+      reinterpret_cast<uintptr_t>(a.sel_idx) % 16 || reinterpret_cast<uintptr_t>(a.sel_w) % 16 ||
+      N < 1 || N > kFrontMaxN || E < 1 || E > 64 || q.K > 4 || q.N != N || q.E != E ||
+      q.K * q.M != km || !decode_plan_fits(q))
+    return SMOE_EUNSUPPORTED;
+  // row tiles and K split as launch_decode picks them for the same groups
+  // through the destination plan, so both give the same bits
+  const int rows = N * q.S;
+  const int rpg = rows / E;
+  if (rpg > 32) return SMOE_EUNSUPPORTED;  // launch_grouped_gemm's decode range
+  const int rt = rpg <= 8 ? 1 : 2;
+  const int steps = a.K / 64;
+  const int tiles = max(min(E, rows), (rows + 16 * rt - 1) / (16 * rt));
+  const long long strips = (long long)((a.N_out + 63) / 64) * tiles;
+  const int cus = device_cus();
+  const long long want = 8LL * (cus > 0 ? cus : 256);
+  int ksplit = 1;
+  while (ksplit < 4 && strips * ksplit < want && steps / (2 * ksplit) >= 3) ksplit *= 2;
+  GemmArgs b = a;
+  b.sel_tpg = (N + 16 * rt - 1) / (16 * rt);
+  const int slices = (a.N_out + 63) / 64, cs = 4 / ksplit;
+  const dim3 grid((slices + cs - 1) / cs, 1 + E * b.sel_tpg, 1);  // the plans' row, then the tiles
+  auto go = [&](auto rtc, auto ksc) {
+    SMOE_LAUNCH((k_decode_edge<decltype(rtc)::value, decltype(ksc)::value>), grid, dim3(256), 0, s,
+                b, q);
+    return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+  };
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I4 = std::integral_constant<int, 4>;
+  if (rt == 1) return ksplit == 1 ? go(I1{}, I1{}) : ksplit == 2 ? go(I1{}, I2{}) : go(I1{}, I4{});
+  return ksplit == 1 ? go(I2{}, I1{}) : ksplit == 2 ? go(I2{}, I2{}) : go(I2{}, I4{});
 }
 
 }  // namespace smoe

@@ -84,6 +84,15 @@ struct GemmArgs {
   // ticks (s_memrealtime) to clk[1], so clk[0] / clk[1] * 100 MHz is the
   // clock the launch ran at
   unsigned long long* clk = nullptr;
+  // decode edge projection (launch_decode_edge): group g's rows are the
+  // tokens t < sel_n whose destination coefficient c[t, g] (their selected
+  // edges to g, sel_idx / sel_w [sel_n, sel_km], summed in order) is
+  // nonzero, in token order; A row t, out row g * sel_n + t, row scale
+  // c[t, g]; grp_off / a_rows / row_scale unused.  sel_tpg: row tiles per
+  // group.
+  const int32_t* sel_idx = nullptr;
+  const float* sel_w = nullptr;
+  int sel_km = 0, sel_n = 0, sel_tpg = 0;
 };
 
 int launch_grouped_gemm(const GemmArgs& a, hipStream_t s);
@@ -200,16 +209,31 @@ struct DecFront {
 // shapes the decode loop takes (else the general stages run)
 bool decode_front_fits(int N, int H, int E, int K, int M, int S, int ldw);
 int launch_decode_front(const DecFront& a, hipStream_t s);
-// k_decode_plan: one workgroup: the tokens' sources ascending (tok_e /
+// The plans of a decode loop: the tokens' sources ascending (tok_e /
 // tok_ew), the expert plan and each source row's edges at its plan row; the
 // destination coefficients (tok_d / tok_dc) and the destination plan.
-int launch_decode_plan(const int32_t* top_idx, const float* top_w, const int32_t* sel_idx,
-                       const float* sel_w, int N, int E, int K, int M, int S, int32_t* tok_e,
-                       float* tok_ew, int32_t* e_cnt, int32_t* e_acnt, int32_t* e_off,
-                       int32_t* e_rows, float* e_roww, int32_t* e_tokrow, int32_t* edge_idx,
-                       float* edge_w, int32_t* tok_d, float* tok_dc, int32_t* d_cnt,
-                       int32_t* d_acnt, int32_t* d_off, int32_t* d_rows, float* d_roww,
-                       int32_t* d_tokrow, hipStream_t s);
+struct DecPlan {
+  const int32_t* top_idx = nullptr;  // [N, K] and [N, K]: the router top-k
+  const float* top_w = nullptr;
+  const int32_t* sel_idx = nullptr;  // [N, K, M] and [N, K, M]: the sources' top-m
+  const float* sel_w = nullptr;
+  int N = 0, E = 0, K = 0, M = 0, S = 0;
+  int32_t *tok_e = nullptr, *e_cnt = nullptr, *e_acnt = nullptr, *e_off = nullptr,
+          *e_rows = nullptr, *e_tokrow = nullptr, *edge_idx = nullptr, *tok_d = nullptr,
+          *d_cnt = nullptr, *d_acnt = nullptr, *d_off = nullptr, *d_rows = nullptr,
+          *d_tokrow = nullptr;
+  float *tok_ew = nullptr, *e_roww = nullptr, *edge_w = nullptr, *tok_dc = nullptr,
+        *d_roww = nullptr;
+};
+bool decode_plan_fits(const DecPlan& q);
+// k_decode_plan: the plans in one workgroup of their own
+int launch_decode_plan(const DecPlan& q, hipStream_t s);
+// The decode edge projection (bf16 weight tiles, EPI_ROWSCALE, the sel_*
+// fields of `a` set) with the loop's plans in one more workgroup, which runs
+// beside the weight streams: the projection reads only the front's
+// selections.  SMOE_EUNSUPPORTED for shapes it does not take (the caller
+// runs launch_decode_plan and the grouped GEMM instead).
+int launch_decode_edge(const GemmArgs& a, const DecPlan& q, hipStream_t s);
 int launch_edge_loop_bias(const void* wg, int act_dtype, const float* bg, const float* emb, int E,
                           int H, int L, int R, float* out, hipStream_t s);
 
@@ -223,9 +247,11 @@ struct ExitGate {
   int32_t* active;
   int32_t* loops;
 };
+// dense_n > 0: the projection rows of launch_decode_edge (token t's row of
+// destination d at d * dense_n + t; d_tokrow unused)
 int launch_msg_combine(const void* proj, int proj_dtype, const int32_t* tok_d,
                        const int32_t* d_tokrow, int N, int S, int H, void* msg, int msg_dtype,
-                       hipStream_t s);
+                       hipStream_t s, int dense_n = 0);
 int launch_epilogue(const void* h, const void* x0, int act_dtype, const void* y, int y_dtype,
                     const int32_t* tok_e, const float* tok_ew, const int32_t* e_tokrow, int N,
                     int K, int H, float alpha, float beta, const float* ln_w, const float* ln_b,

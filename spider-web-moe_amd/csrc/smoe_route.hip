@@ -19,6 +19,7 @@
 // from wave ballots (deterministic, no atomics on the output order).
 #include "smoe_common.hpp"
 #include "smoe_internal.hpp"
+#include "smoe_plan64.hpp"
 #include "smoe_rows.hpp"
 
 namespace smoe {
@@ -883,65 +884,6 @@ inline int plan_small_win(int C, int G) {
   int win = 64;
   while (win > 8 && C * ((G + win - 1) / win) < 16) win >>= 1;
   return win;
-}
-
-// Plan of <= 64 tokens over <= 64 groups by one wave, lane t = token t
-// (tok_g, tok_w and tokrow in LDS or global memory): each valid entry sets bit t of its
-// group's token masks (kept, positive weight) by an LDS atomic OR; lane g
-// counts group g by popcount and a wave scan gives the offsets; a kept
-// entry's row is off[g] + the number of earlier tokens in its group's mask.
-// The plan the multi-wave forms write (stable token order, tokrow -1 for
-// every entry not kept), in one wave and without a workgroup barrier: the
-// wave's LDS operations complete in order.  km / am: 64 words of LDS each;
-// soff: 64.
-__device__ __forceinline__ void plan64_wave(const int32_t* tok_g, const float* tok_w, int N, int S,
-                                            int G, int drop, int32_t* __restrict__ cnt,
-                                            int32_t* __restrict__ acnt, int32_t* __restrict__ off,
-                                            int32_t* __restrict__ rows, float* __restrict__ roww,
-                                            int32_t* tokrow, uint64_t* km, uint64_t* am,
-                                            int* soff) {
-  const int t = threadIdx.x & 63;
-  const bool tv = t < N;
-  km[t] = 0ull;
-  am[t] = 0ull;
-  const uint64_t bit = 1ull << t, below = bit - 1ull;
-  int prev = -1;
-  bool open = tv;
-  for (int j = 0; j < S; ++j) {
-    const int g = tv ? tok_g[t * S + j] : -1;
-    const float w = tv ? tok_w[t * S + j] : 0.f;
-    open = open && g > prev && g < G;  // g > prev >= -1, so g >= 0
-    prev = open ? g : prev;
-    if (open && (!drop || w > 0.f)) atomicOr(&km[g], bit);
-    if (open && !drop && w > 0.f) atomicOr(&am[g], bit);
-  }
-  const int gl = t < G ? t : 0;
-  const int c = t < G ? __popcll(km[gl]) : 0;
-  const int a = t < G ? (drop ? c : __popcll(am[gl])) : 0;
-  const int incl = wave_incl_scan(c);
-  if (t < G) {
-    cnt[t] = c;
-    acnt[t] = a;
-    off[t] = incl - c;
-    soff[t] = incl - c;
-  }
-  if (t == 0) off[G] = __builtin_amdgcn_readlane(incl, 63);
-  prev = -1;
-  open = tv;
-  for (int j = 0; j < S; ++j) {
-    const int g = tv ? tok_g[t * S + j] : -1;
-    const float w = tv ? tok_w[t * S + j] : 0.f;
-    open = open && g > prev && g < G;
-    prev = open ? g : prev;
-    const bool kept = open && (!drop || w > 0.f);
-    const int gc = kept ? g : 0;
-    const int row = soff[gc] + __popcll(km[gc] & below);
-    if (tv) tokrow[t * S + j] = kept ? row : -1;
-    if (kept) {
-      rows[row] = t;
-      roww[row] = w;
-    }
-  }
 }
 
 // Plans of <= 64 tokens over <= 64 groups outside the fused front (fp32
