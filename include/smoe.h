@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define SMOE_ABI_VERSION 9
+#define SMOE_ABI_VERSION 10
 
 /* status codes (spider_kernels.h convention; see scalar.cpp:9,45,58) */
 #define SMOE_OK 0
@@ -414,7 +414,9 @@ SMOE_API int smoe_remap_ids(const int32_t* ids, int64_t n, const int32_t* map, i
 #define SMOE_STAGE_UP_GEMM 8
 #define SMOE_STAGE_DOWN_GEMM 9
 #define SMOE_STAGE_EPILOGUE 10
-/* bf16 steps of N <= 64 run stages 0-5 as these two launches */
+/* bf16 steps of N <= 64 run stages 0-5 as these two launches; decode loops
+ * (H <= 1024) as FRONT_GEMM alone (k_decode_front), their plans running
+ * inside the EDGE_GEMM launch */
 #define SMOE_STAGE_FRONT_GEMM 11  /* router + all edge-generator logits, one GEMM */
 #define SMOE_STAGE_FRONT_ROUTE 12 /* top-k, expert plan, top-m, destination plan */
 #define SMOE_NUM_STAGES 13

@@ -184,7 +184,7 @@ STAGES = ["router_gemm", "route_topk", "expert_plan", "edge_logits", "edge_topm"
           # bf16 steps of N <= 64: stages 0-5 as one GEMM and one routing workgroup
           "front_gemm", "front_route"]
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 _LIB = None
 
 

@@ -121,7 +121,7 @@ def test_exports_the_reference_host_abi(nat):
 
 def test_identity(nat):
     lib = nat.lib()
-    assert lib.smoe_abi_version() == 9
+    assert lib.smoe_abi_version() == 10
     assert lib.smoe_backend_name() == b"hip-gfx950"
     assert lib.smoe_backend_caps() == 0b1111
 
