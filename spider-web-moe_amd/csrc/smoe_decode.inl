@@ -89,7 +89,39 @@ __global__ __launch_bounds__(1024) void k_decode_front(const DecFront a) {
   const int strip = blockIdx.x, t0 = blockIdx.y * TT;
   const bool src = strip > 0;
   const int E = a.E, N = a.N;
-  // 1 weight fragments (lane: row l16 of tile ct, k 8q.. of step wave +
+  // 1 what the LayerNorm of token `wave` waits on goes out first: the
+  // token's expert rows' indices, its h and x0 rows, and this thread's share
+  // of the LayerNorm parameters (one element per thread, shared through LDS:
+  // every wave normalises with the same ones).  The weight fragments follow,
+  // so a wait for the token's operands does not wait for them (vmcnt counts
+  // in issue order).
+  __shared__ float lnp[PRO ? 2 * H : 1];
+  const int j = wave;
+  const int t = t0 + j;
+  const bool tv = t < N;  // wave-uniform
+  float hv[CPL][8], xv[CPL][8];
+  int te = -1, tr = 0;
+  float tw = 0.f, pw = 1.f, pb = 0.f;
+  if constexpr (PRO) {
+    const int pi = threadIdx.x < H ? threadIdx.x : 0;
+    if (a.ln_w) pw = a.ln_w[pi];
+    if (a.ln_b) pb = a.ln_b[pi];
+    const int tc = tv ? t : 0;  // rows past N: token 0's (never stored)
+    const int64_t e = static_cast<int64_t>(tc) * a.K + (lane < a.K ? lane : a.K - 1);
+    te = a.tok_e[e];
+    tw = a.tok_ew[e];
+    tr = a.e_tokrow[e];
+#pragma unroll
+    for (int c = 0; c < CPL; ++c) {  // columns past H load column 0 (not stored)
+      const int col = (lane + 64 * c) * 8;
+      const int64_t o = static_cast<int64_t>(tc) * H + (col < H ? col : 0);
+      load8<SMOE_BF16>(a.h, o, hv[c]);
+      load8<SMOE_BF16>(a.x0, o, xv[c]);
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // 2 weight fragments (lane: row l16 of tile ct, k 8q.. of step wave +
   // 16 st): the router's, and (strips > 0) the source's E edge rows; rows
   // past E read row E - 1 (never stored), steps past the last read step 0
   // (not multiplied)
@@ -111,38 +143,45 @@ __global__ __launch_bounds__(1024) void k_decode_front(const DecFront a) {
         ws[st][ct] = u32x4{0u, 0u, 0u, 0u};
     }
   }
-  // 2 token `wave` of the tile -> LDS (bf16); rows past N are zeros
+  // 3 token `wave` of the tile -> LDS (bf16); rows past N are zeros
   {
-    const int j = wave;
-    const int t = t0 + j;
     float o[CPL][8];
-    if (t < N) {  // wave-uniform
-      if constexpr (PRO) {
-        float hv[CPL][8], xv[CPL][8], gw[CPL][8], gb[CPL][8];
-        ln_load<CPL, SMOE_BF16>(a.h, a.x0, a.ln_w, a.ln_b, t, H, hv, xv, gw, gb);
 #pragma unroll
-        for (int c = 0; c < CPL; ++c)
+    for (int c = 0; c < CPL; ++c)
 #pragma unroll
-          for (int i = 0; i < 8; ++i) o[c][i] = 0.f;
-        const int64_t e = static_cast<int64_t>(t) * a.K + (lane < a.K ? lane : a.K - 1);
-        const int te = a.tok_e[e];
-        const float tw = a.tok_ew[e];
-        const int tr = a.e_tokrow[e];
+      for (int i = 0; i < 8; ++i) o[c][i] = 0.f;
+    if constexpr (PRO) {
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      if (threadIdx.x < H) {
+        lnp[threadIdx.x] = pw;
+        lnp[H + threadIdx.x] = pb;
+      }
+      if (tv) {  // the previous loop's expert rows, then its epilogue's LayerNorm
         const int my_row = (lane < a.K && te >= 0 && tw > 0.f) ? tr : -1;
         gather_add<CPL, SMOE_BF16>(a.y, H, my_row, __ballot(my_row >= 0), o);
-        ln_row<CPL>(hv, xv, gw, gb, o, H, a.alpha, a.beta, a.eps, o);  // in place
-      } else {
+      }
+      __syncthreads();  // the LayerNorm parameters are in LDS
+      if (tv) {
+        float gw[CPL][8], gb[CPL][8];
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
           const int col = (lane + 64 * c) * 8;
-          load8<SMOE_BF16>(a.h, static_cast<int64_t>(t) * H + (col < H ? col : 0), o[c]);
+          const int cc = col < H ? col : 0;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) {
+            gw[c][i] = lnp[cc + i];
+            gb[c][i] = lnp[H + cc + i];
+          }
         }
+        ln_row<CPL>(hv, xv, gw, gb, o, H, a.alpha, a.beta, a.eps, o);  // in place
       }
-    } else {
+    } else if (tv) {
 #pragma unroll
-      for (int c = 0; c < CPL; ++c)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) o[c][i] = 0.f;
+      for (int c = 0; c < CPL; ++c) {
+        const int col = (lane + 64 * c) * 8;
+        load8<SMOE_BF16>(a.h, static_cast<int64_t>(t) * H + (col < H ? col : 0), o[c]);
+      }
     }
 #pragma unroll
     for (int c = 0; c < CPL; ++c) {
@@ -152,7 +191,7 @@ __global__ __launch_bounds__(1024) void k_decode_front(const DecFront a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) pk[i] = pack_bf2(o[c][2 * i], o[c][2 * i + 1]);
         *reinterpret_cast<u32x4*>(xa + j * LDX + col) = pk;
-        if (PRO && strip == 0 && t < N)
+        if (PRO && strip == 0 && tv)
           *reinterpret_cast<u32x4*>(reinterpret_cast<uint16_t*>(a.h_out) +
                                     static_cast<int64_t>(t) * H + col) = pk;
       }
