@@ -6,15 +6,18 @@
 // every routing stage is its own launch.  Here a loop takes one launch
 // before its edge projection:
 //
-//  k_decode_front (strip, 16-token tile; 16 waves): the tile's input rows go
+//  k_decode_front (strip, 8-token tile; 16 waves): the tile's input rows go
 //   to LDS as bf16 — for loops after the first, as the previous loop's
 //   LayerNorm (ln_row over h_{r-1}, x0 and the previous loop's expert rows,
 //   the operations of k_epilogue in its order, so the rows are the bits that
 //   kernel writes; the router strip stores them as the loop's input).  Wave
-//   w normalises token w, so the 16 latency chains overlap.  The router
-//   rows and the strip's own weights are requested first, so their latency
-//   hides behind that.  One 16 x 16 x 32 MFMA per 32-k step and 16-channel
-//   tile, K split over the waves and added in wave order, + bias.  Every
+//   w < 8 normalises token w, so the latency chains overlap; the
+//   LayerNorm's operands are requested first and the router rows and the
+//   strip's own weights after them.  8-token tiles put twice the
+//   workgroups of 16-token ones on the chip, each moving half the rows
+//   (C2: 0.297 -> 0.290 ms per step; 4-token tiles 0.308).  One 16 x 16 x
+//   32 MFMA per 32-k step and 16-channel tile (rows past the tile's tokens
+//   are zeros), K split over the waves and added in wave order, + bias.  Every
 //   strip then runs the router top-k of its tokens (topk_seg; the same bits
 //   in every strip, since the logits are computed the same way); strip 0
 //   writes it, strip s + 1 runs top-m over source s's logits (topm_row, the
@@ -66,22 +69,24 @@ __device__ __forceinline__ void topm_row(float v, int t, bool ok, bool sel_src, 
   }
 }
 
+constexpr int kFrontTile = 8;  // tokens per workgroup of k_decode_front
 // CPL: row chunks per lane (H); SEG: lanes per token (E); ET: 16-channel
 // tiles of E; NS: H / 128; PRO: the input rows are the previous loop's
 // LayerNorm.
 template <int CPL, int SEG, int ET, int NS, bool PRO>
 __global__ __launch_bounds__(1024) void k_decode_front(const DecFront a) {
-  constexpr int TT = 16;                    // tokens per tile (one per wave)
+  constexpr int TT = kFrontTile;            // tokens per tile (one per wave of the first TT)
+  constexpr int TR = 16;                    // MFMA rows (tokens past TT: zero rows)
   constexpr int NW = 16;                    // waves
   constexpr int H = NS * 128;
   constexpr int KST = H / 32;               // 32-k steps
   constexpr int NSW = (KST + NW - 1) / NW;  // steps per wave (the last may be short)
   constexpr int LDX = H + 8;                // LDS row pitch (bf16): 16-byte reads conflict-free
   constexpr int LTW = ET * 16 + 1;
-  constexpr int XA_BYTES = TT * LDX * 2, RED_BYTES = NW * 2 * ET * 64 * 16;
+  constexpr int XA_BYTES = TR * LDX * 2, RED_BYTES = NW * 2 * ET * 64 * 16;
   // the input rows, then (once every wave's MFMAs are done) the waves' partials
   __shared__ __attribute__((aligned(16))) uint8_t smem[XA_BYTES > RED_BYTES ? XA_BYTES : RED_BYTES];
-  __shared__ float lt[2][TT][LTW];          // [router | the strip's source] logits
+  __shared__ float lt[2][TR][LTW];          // [router | the strip's source] logits
   uint16_t* xa = reinterpret_cast<uint16_t*>(smem);
   f32x4* red = reinterpret_cast<f32x4*>(smem);  // [NW][2 ET][64]
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -98,7 +103,7 @@ __global__ __launch_bounds__(1024) void k_decode_front(const DecFront a) {
   __shared__ float lnp[PRO ? 2 * H : 1];
   const int j = wave;
   const int t = t0 + j;
-  const bool tv = t < N;  // wave-uniform
+  const bool tv = j < TT && t < N;  // wave-uniform
   float hv[CPL][8], xv[CPL][8];
   int te = -1, tr = 0;
   float tw = 0.f, pw = 1.f, pb = 0.f;
@@ -267,7 +272,7 @@ bool decode_front_fits(int N, int H, int E, int K, int M, int S, int ldw) {
 namespace {
 template <int CPL, int NS, bool PRO>
 int decode_front_e(const DecFront& a, hipStream_t s) {
-  const dim3 grid(a.E + 1, (a.N + 15) / 16), block(1024);
+  const dim3 grid(a.E + 1, (a.N + kFrontTile - 1) / kFrontTile), block(1024);
   const int et = (a.E + 15) / 16;
 #define SMOE_DFRONT(SG, ET_)                                                              \
   do {                                                                                    \
