@@ -54,9 +54,11 @@ __device__ __forceinline__ int count_tiles(const GemmArgs& p, int BM) {
   return total;
 }
 
-// The tile-th BM-row tile in group order: group, first row, rows.
+// The tile-th BM-row tile in group order: group, first row, rows.  skip:
+// the first `skip` tiles of every group are left out of the count (their
+// workgroups find them directly).
 __device__ __forceinline__ bool find_tile(const GemmArgs& p, int BM, int tile, int& g, int& m0,
-                                          int& mrows) {
+                                          int& mrows, int skip = 0) {
   if (p.G == 0) {
     const int t = (p.single_rows + BM - 1) / BM;
     if (tile >= t) return false;
@@ -69,6 +71,7 @@ __device__ __forceinline__ bool find_tile(const GemmArgs& p, int BM, int tile, i
   for (int b = 0; b < p.G; b += 64) {
     int lo, hi, t;
     group_chunk(p, BM, b, lo, hi, t);
+    t = max(t - skip, 0);
     const int incl = wave_incl_scan(t) + acc;
     const uint64_t m = __ballot(tile < incl);  // empty groups never come first
     if (m) {
@@ -76,7 +79,7 @@ __device__ __forceinline__ bool find_tile(const GemmArgs& p, int BM, int tile, i
       g = b + f;
       const int excl = __builtin_amdgcn_readlane(incl - t, f);
       const int glo = __builtin_amdgcn_readlane(lo, f), ghi = __builtin_amdgcn_readlane(hi, f);
-      m0 = glo + (tile - excl) * BM;
+      m0 = glo + (tile - excl + skip) * BM;
       mrows = min(BM, ghi - m0);
       return true;
     }
@@ -1302,12 +1305,20 @@ __device__ __forceinline__ void decode_gemm(const GemmArgs& p, int gy, f32x4* re
       stok[rt] = j < r_hi ? tok : -1;
       scoef[rt] = __shfl(c, tok);
     }
+  } else if (p.G > 0 && gy < p.G) {
+    // the first tile of group gy: the weights are requested before its rows
+    // are looked up (below)
+    g = gy;
+    r_lo = r_hi = 0;
   } else {
+    // a group's later tiles (rows past its first 16 * RT), in group order
     int m0, mrows;
-    if (!find_tile(p, 16 * RT, gy, g, m0, mrows)) return;  // uniform, before any barrier
+    if (!find_tile(p, 16 * RT, p.G > 0 ? gy - p.G : gy, g, m0, mrows, p.G > 0 ? 1 : 0))
+      return;  // uniform, before any barrier
     r_lo = m0;
     r_hi = m0 + mrows;
   }
+  const bool early = !SEL && p.G > 0 && gy < p.G;  // uniform
   int c0[TNW];  // first channel of each tile (slices past N_out: clamped rows, never stored)
 #pragma unroll
   for (int t = 0; t < TNW; ++t)
@@ -1335,26 +1346,13 @@ __device__ __forceinline__ void decode_gemm(const GemmArgs& p, int gy, f32x4* re
                  (static_cast<int64_t>(g) * (p.N_out >> 4) + tile) * (p.K >> 6) * BLK + 16 * lane;
     }
   }
-  const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A);
-  const uint16_t* arow[RT];
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    int ar;
-    if constexpr (SEL) {
-      ar = atok[rt];
-    } else {
-      int r = r_lo + 16 * rt + l16;
-      r = r < r_hi ? r : r_lo;  // rows past the tile: a valid row, never stored
-      ar = p.a_rows ? p.a_rows[r] : r;
-    }
-    arow[rt] = A + static_cast<int64_t>(ar) * p.lda;
-  }
   const int steps = p.K / 64;
   const int s_begin = kp * steps / KSPLIT, nst = (kp + 1) * steps / KSPLIT - s_begin;
   const int last = min(s_begin + max(nst - 1, 0), steps - 1);
   DRaw<FMT> wr[D][TNW];
   u32x4 av[D][RT][2];
-  auto fetch = [&](int d, int i) {  // ring slot d <- step s_begin + i (clamped to the slice)
+  const uint16_t* arow[RT];
+  auto fetch_w = [&](int d, int i) {  // ring slot d <- step s_begin + i (clamped): weights
     const int k0 = 64 * min(s_begin + i, last);
 #pragma unroll
     for (int t = 0; t < TNW; ++t) {
@@ -1376,6 +1374,9 @@ __device__ __forceinline__ void decode_gemm(const GemmArgs& p, int gy, f32x4* re
                                 p.s_f16);
       }
     }
+  };
+  auto fetch_a = [&](int d, int i) {  // ... and activations
+    const int k0 = 64 * min(s_begin + i, last);
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       if constexpr (FMT == SMOE_BF16) {
@@ -1388,6 +1389,30 @@ __device__ __forceinline__ void decode_gemm(const GemmArgs& p, int gy, f32x4* re
       }
     }
   };
+  auto fetch = [&](int d, int i) {
+    fetch_w(d, i);
+    fetch_a(d, i);
+  };
+  if (early) {  // the first steps' weights go out before the group's rows are read
+#pragma unroll
+    for (int d = 0; d < D; ++d) fetch_w(d, d);
+    r_lo = p.grp_off[g];
+    r_hi = min(p.grp_off[g + 1], r_lo + 16 * RT);
+    if (r_hi <= r_lo) return;  // uniform (an empty group), before any barrier
+  }
+  const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A);
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    int ar;
+    if constexpr (SEL) {
+      ar = atok[rt];
+    } else {
+      int r = r_lo + 16 * rt + l16;
+      r = r < r_hi ? r : r_lo;  // rows past the tile: a valid row, never stored
+      ar = p.a_rows ? p.a_rows[r] : r;
+    }
+    arow[rt] = A + static_cast<int64_t>(ar) * p.lda;
+  }
   f32x4 acc[TNW][RT];
 #pragma unroll
   for (int t = 0; t < TNW; ++t)
@@ -1420,8 +1445,13 @@ __device__ __forceinline__ void decode_gemm(const GemmArgs& p, int gy, f32x4* re
       }
     }
   };
+  if (early) {
 #pragma unroll
-  for (int d = 0; d < D; ++d) fetch(d, d);  // a slice of < D steps: its last step again (unused)
+    for (int d = 0; d < D; ++d) fetch_a(d, d);
+  } else {
+#pragma unroll
+    for (int d = 0; d < D; ++d) fetch(d, d);  // a slice of < D steps: its last step again (unused)
+  }
   int s = 0;
   for (; s + 2 * D <= nst; s += D) {  // slot d holds step s + d; every refill is a real step
 #pragma unroll
