@@ -51,7 +51,7 @@ GEMM_KERNEL = {
     ("c1", "edge_gemm"): "k_gemm_pp<4,4,rowscale,256> (bf16 weight tiles, 8-wave ping-pong, LDS-DMA ring)",
     ("c2", "up_gemm"): "k_gemm_decode<fp8,SwiGLU,4,1,2,3> (weight streaming, K split over 2 waves, 3-step register ring per wave)",
     ("c2", "down_gemm"): "k_gemm_decode<fp8,down,4,1,4,3> (weight streaming, K split over 4 waves)",
-    ("c2", "edge_gemm"): "k_gemm_decode<bf16,rowscale,4,2,4,3> (weight streaming, K split over 4 waves)",
+    ("c2", "edge_gemm"): "k_decode_edge<2,4> (bf16 weight tiles, rows found from the front's selections, K split over 4 waves; the loop's plans in workgroup 0)",
     ("c3", "up_gemm"): "k_gemm_ring<128,3,4> (bf16 GELU, LDS-DMA ring, 2 workgroups/CU)",
     ("c3", "down_gemm"): "k_gemm_pp<4,4,down,320> (bf16 weight tiles, 8-wave ping-pong)",
     ("c3", "edge_gemm"): "k_gemm_pp<4,4,rowscale,256> (bf16 weight tiles, 8-wave ping-pong)",
