@@ -223,13 +223,17 @@ def test_block_prefill_quantized_experts(experts, act):
 
 
 @pytest.mark.parametrize("n,e,k,m", [(1, 16, 2, 2), (37, 16, 2, 2), (64, 32, 4, 2), (48, 64, 2, 4),
-                                     (64, 16, 3, 3), (65, 16, 2, 2), (200, 64, 2, 4)])
+                                     (64, 16, 3, 3), (65, 16, 2, 2), (200, 64, 2, 4),
+                                     (64, 32, 4, 4), (64, 8, 2, 2), (64, 4, 2, 2)])
 def test_block_small_steps_fused_front(n, e, k, m):
-    """bf16 steps of N <= 64 tokens run stages 1-6 as one logits GEMM over
-    the router and every edge-generator row plus one routing workgroup
-    (top-k, expert plan, top-m, destination plan); N = 65 and 200 take the
-    separate stages.  Routing, plans, edges, message, delta and outputs
-    against the oracle for two loops, at E 16 / 32 / 64."""
+    """Decode-size steps (N <= 64 tokens) run the decode loop: the front
+    (logits, top-k, top-m) and the edge projection with the loop's plans in
+    one of its workgroups, or, where that kernel does not take the shape
+    (k * m not a multiple of 4 or above 16, more than 32 rows per
+    destination: E 4 here), the plan launch and the grouped GEMM; N = 65
+    and 200 take the separate stages.  Routing, plans, edges, message, delta
+    and outputs against the oracle for two loops, at E 4 to 64 and k * m
+    from 4 to 16."""
     from spider_moe_amd.workloads import make_block
     say("fused front", n, e, k, m)
     wl = make_block("c1", tokens=n, hidden_size=128, num_experts=e, top_k=k, edges_per_expert=m,
@@ -315,7 +319,7 @@ def test_multi_loop_call_equals_per_loop_calls():
     assert torch.equal(full, h)
 
 
-@pytest.mark.parametrize("n,e,k,m", [(64, 32, 4, 2), (48, 64, 2, 4)])
+@pytest.mark.parametrize("n,e,k,m", [(64, 32, 4, 2), (48, 64, 2, 4), (64, 32, 4, 4), (64, 4, 2, 2)])
 @pytest.mark.parametrize("hid", [128, 512])
 def test_multi_loop_fused_front_equals_per_loop_calls(n, e, k, m, hid):
     """In a multi-loop decode call each loop's LayerNorm is folded into the
