@@ -37,9 +37,17 @@ FLAGS = [
 ]
 
 
+# Per-file additions.  smoe_front.hip: MFMA accumulators in VGPRs; left to
+# choose, the compiler puts the logits kernel's 80 accumulators in AGPRs and
+# rotates them with ~100 v_accvgpr moves per two K stages.
+FILE_FLAGS = {
+    "smoe_front.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{r.stderr}")

@@ -204,6 +204,35 @@ bool front_ok(const smoe_block* b, int N) {
          b->M <= 16 && S <= 64 && b->H % 64 == 0 && (E + E * E) % 4 == 0 && E % 4 == 0 && (b->H + b->L) % 8 == 0;
 }
 
+// Prefill steps whose router and edge logits come out of one pass
+// (launch_front_logits over [router | every edge generator row], at most 320
+// channels: E <= 16), routed per token on them (launch_route_dense) and
+// planned in one set of launches (launch_plan2, its three-kernel form: C * E
+// > 512).  The per-source edges wait in the edge_logit region in slot order
+// (2 M <= E: they fit) until the expert plan's scatter moves them.
+bool prefill_front_ok(const smoe_block* b, int N) {
+  const int E = b->E, S = (E < b->K * b->M) ? E : b->K * b->M;
+  const int64_t C = (static_cast<int64_t>(N) + 63) / 64;
+  return b->act_dtype == SMOE_BF16 && N > kFrontMaxN && C * E > 512 && E % 4 == 0 && E <= 16 &&
+         b->K <= 16 && b->M <= 16 && 2 * b->M <= E && S <= 64 && b->H % 64 == 0 &&
+         (b->H + b->L) % 8 == 0;
+}
+
+// Router logits (G == 0, f32 out): bf16 batches of >= 64 row tiles on the
+// one-pass logits kernel (a workgroup per 64 rows and every channel, h read
+// once: C3's 16384 x 1024 -> 32 logits 24 -> ~8 us), the rest on the
+// grouped GEMM.
+int launch_router_logits(const GemmArgs& rg, hipStream_t s) {
+  auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (rg.fmt == SMOE_BF16 && rg.G == 0 && rg.single_rows >= 64 * 64 && rg.K % 64 == 0 &&
+      rg.N_out % 4 == 0 && rg.ldo % 4 == 0 && rg.lda % 8 == 0 && rg.ldw % 8 == 0 && !rg.W2 &&
+      a16(rg.A) && a16(rg.W) && a16(rg.out)) {
+    const int rc = launch_front_logits(rg, s);
+    if (rc != SMOE_EUNSUPPORTED) return rc;
+  }
+  return launch_grouped_gemm(rg, s);
+}
+
 // bf16 decode steps the two-launch decode loop takes (k_decode_front +
 // k_decode_plan in place of the front GEMM, the routing workgroup and the
 // previous loop's epilogue); the early-exit gate keeps the general loop.
@@ -249,8 +278,9 @@ void make_layout(const smoe_block* b, int N, smoe_ws_layout* l) {
   l->act = z.take(row_tile_elems(n * K, U) * esize(fdt));
   l->y = z.take(n * K * H * esize(fdt));
   l->h_tmp = z.take(n * H * esize(b->act_dtype));
-  l->scratch = z.take(plan_scratch_bytes(N, E));
-  l->front = z.take(front_ok(b, N) ? n * (E + E * E) * 4 : 0);
+  const bool pf = prefill_front_ok(b, N);
+  l->scratch = z.take(plan_scratch_bytes(N, E) * (pf ? 2 : 1));  // launch_plan2: both plans'
+  l->front = z.take(front_ok(b, N) || pf ? n * (E + E * E) * 4 : 0);
   const bool dec = decode_ok(b, N);
   l->sel_idx = z.take(dec ? n * K * M * 4 : 0);
   l->sel_w = z.take(dec ? n * K * M * 4 : 0);
@@ -411,6 +441,7 @@ int block_forward(const smoe_block* b, const void* h_in, const void* x0, void* h
 
   const bool dec = !gate && decode_ok(b, N);
   const bool front = front_ok(b, N);
+  const bool pfront = !dec && !front && prefill_front_ok(b, N);
   const int32_t* active = gate ? gate->active : nullptr;
   const void* cur = h_in;
   for (int i = 0; i < num_loops; ++i) {
@@ -564,6 +595,68 @@ int block_forward(const smoe_block* b, const void* h_in, const void* x0, void* h
                                at<int32_t>(ws, l.d_rows), at<float>(ws, l.d_roww),
                                at<int32_t>(ws, l.d_tokrow), active, s),
             "front routing");
+    } else if (pfront) {
+      // 1-6: [router | every edge generator row] logits in one pass, routing
+      // per token on them, both plans in one set of launches
+      const int ldf = E + E * E;
+      GemmArgs fg;
+      fg.fmt = SMOE_BF16;
+      fg.epi = EPI_F32_BIAS;
+      fg.A = cur;
+      fg.lda = H;
+      fg.W = b->router_w;
+      fg.ldw = H;
+      fg.K = H;
+      fg.N_out = ldf;
+      fg.G = 0;
+      fg.single_rows = N;
+      fg.out = at<float>(ws, l.front);
+      fg.ldo = ldf;
+      fg.bias = b->loop_bias + static_cast<int64_t>(r) * E;
+      fg.W2 = b->edge_gen_w;
+      fg.ldw2 = H + L;
+      fg.n_split = E;
+      fg.bias2 = b->edge_loop_bias + static_cast<int64_t>(r) * E * E;
+      STAGE(SMOE_STAGE_FRONT_GEMM, launch_front_logits(fg, s), "front logits");
+      // the per-source edges in slot order wait in the edge_logit region
+      int32_t* slot_idx = at<int32_t>(ws, l.edge_logit);
+      float* slot_w = reinterpret_cast<float*>(slot_idx + static_cast<int64_t>(N) * K * M);
+      STAGE(SMOE_STAGE_FRONT_ROUTE,
+            launch_route_dense(at<float>(ws, l.front), ldf, N, E, K, M, S, at<float>(ws, l.logits),
+                               at<int32_t>(ws, l.top_idx), at<float>(ws, l.top_w),
+                               at<int32_t>(ws, l.tok_e), at<float>(ws, l.tok_ew), slot_idx, slot_w,
+                               at<int32_t>(ws, l.tok_d), at<float>(ws, l.tok_dc), active, s),
+            "dense routing");
+      PlanSpec pe, pd;
+      pe.tok_g = at<int32_t>(ws, l.tok_e);
+      pe.tok_w = at<float>(ws, l.tok_ew);
+      pe.S = K;
+      pe.G = E;
+      pe.drop = 0;
+      pe.cnt = at<int32_t>(ws, l.e_cnt);
+      pe.acnt = at<int32_t>(ws, l.e_acnt);
+      pe.off = at<int32_t>(ws, l.e_off);
+      pe.rows = at<int32_t>(ws, l.e_rows);
+      pe.roww = at<float>(ws, l.e_roww);
+      pe.tokrow = at<int32_t>(ws, l.e_tokrow);
+      pe.pay_idx = slot_idx;
+      pe.pay_w = slot_w;
+      pe.out_idx = at<int32_t>(ws, l.edge_idx);
+      pe.out_w = at<float>(ws, l.edge_w);
+      pe.pay_m = M;
+      pd.tok_g = at<int32_t>(ws, l.tok_d);
+      pd.tok_w = at<float>(ws, l.tok_dc);
+      pd.S = S;
+      pd.G = E;
+      pd.drop = 1;
+      pd.cnt = at<int32_t>(ws, l.d_cnt);
+      pd.acnt = at<int32_t>(ws, l.d_acnt);
+      pd.off = at<int32_t>(ws, l.d_off);
+      pd.rows = at<int32_t>(ws, l.d_rows);
+      pd.roww = at<float>(ws, l.d_roww);
+      pd.tokrow = at<int32_t>(ws, l.d_tokrow);
+      STAGE(SMOE_STAGE_EXPERT_PLAN, launch_plan2(pe, pd, N, at<void>(ws, l.scratch), s),
+            "expert + destination plans");
     } else {
 
     // 1 router logits (+ loop bias)
@@ -582,7 +675,7 @@ int block_forward(const smoe_block* b, const void* h_in, const void* x0, void* h
     rg.ldo = E;
     rg.bias = b->loop_bias + static_cast<int64_t>(r) * E;
     rg.bias_gstride = 0;
-    STAGE(SMOE_STAGE_ROUTER_GEMM, launch_grouped_gemm(rg, s), "router GEMM");
+    STAGE(SMOE_STAGE_ROUTER_GEMM, launch_router_logits(rg, s), "router logits");
     // 2 top-k
     STAGE(SMOE_STAGE_ROUTE_TOPK, launch_route_topk(at<float>(ws, l.logits), N, E, K, at<int32_t>(ws, l.top_idx),
                                at<float>(ws, l.top_w), at<int32_t>(ws, l.tok_e),
@@ -872,7 +965,7 @@ SMOE_API int smoe_router_topk(const void* x, int act_dtype, int N, int H, const 
   rg.out = lg;
   rg.ldo = E;
   rg.bias = loop_bias_row;
-  SMOE_TRY(launch_grouped_gemm(rg, s), "router GEMM");
+  SMOE_TRY(launch_router_logits(rg, s), "router logits");
   SMOE_TRY(launch_route_topk(lg, N, E, K, top_idx, top_w, te, tw, nullptr, s), "route_topk");
   return SMOE_OK;
 }

@@ -258,6 +258,27 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
+// s_waitcnt vmcnt(n) (gfx9 encoding; expcnt / lgkmcnt left at "no wait")
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (0xF << 8));
+}
+// s_waitcnt lgkmcnt(0) (vmcnt / expcnt left at "no wait")
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+
+// address spaces of global_load_lds's operands
+typedef __attribute__((address_space(3))) void* lds_vptr;
+typedef __attribute__((address_space(1))) void* gbl_vptr;
+
+// LDS rows of 16*CPR bytes: logical 16-byte chunk c of row r sits at chunk
+// c ^ ((r / (16 / CPR)) % CPR), so the 16 rows one ds_read phase touches
+// cover all 64 banks once (the map is an involution)
+template <int CPR>
+__device__ __forceinline__ int sw_chunk(int r, int c) {
+  return c ^ ((r / (16 / CPR)) & (CPR - 1));
+}
+
 __device__ __forceinline__ void wave_argmax(float& v, int& i) {
   argmax_dpp<kDppXor1>(v, i);
   argmax_dpp<kDppXor2>(v, i);

@@ -1,0 +1,185 @@
+// Prefill logits of the Spider-MoE block in one pass over the hidden states.
+//
+// The router logits (spider_moe/model.py:255-256: h W_r^T + the loop's
+// router bias) and, when the expert count is small, the edge generator
+// logits of every source expert (model.py:261-268: [h, loop embedding]
+// W_g^T + b_g, the embedding's part folded into the per-loop edge bias) come
+// out of one GEMM over [W_r; W_g], so the edge logits need neither the
+// expert plan (to group the selected (token, source) rows) nor a second read
+// of h.  At E = 16 that is 16 + 256 output channels per token: a GEMM far
+// too narrow for the ping-pong tiles and too wide for the skinny kernel,
+// with its own shape here.
+#include "smoe_common.hpp"
+#include "smoe_internal.hpp"
+
+namespace smoe {
+namespace {
+
+constexpr int kFlRows = 64;   // rows (tokens) per workgroup
+constexpr int kFlStages = 6;  // activation ring: 64 rows x 64 k (8 KB) per stage
+constexpr int kFlMaxTpw = 5;  // 16-channel tiles per wave: N_out <= 320
+
+// A workgroup owns 64 consecutive rows and every output channel; wave w
+// takes the 16-channel tiles w, w + 4, .. (TPW of them; a wave past the last
+// tile repeats its previous one, whose loads then hit in cache, and stores
+// nothing for it).  Output channel c < n_split reads W row c (ldw apart) and
+// adds bias[c]; c >= n_split reads W2 row c - n_split (ldw2) and adds
+// bias2[c - n_split].
+//   activations: 64 rows x 64 k per stage, global -> LDS by DMA into a
+//                kFlStages ring (128-byte rows, sw_chunk<8> swizzle),
+//                kFlStages - 1 stages ahead
+//   weights:     global -> registers, each lane the two 16-byte pieces of
+//                its channel row at k 8q.. and 32 + 8q.. of a 64-k stage
+//                (the MFMA operand layout), two stages ahead; the weights
+//                (at most 320 rows) stay in the L2 that every workgroup
+//                reads them from
+//   MFMAs:       per stage and tile, two v_mfma_f32_16x16x32_bf16 per
+//                16-row tile (k 0-31 and 32-63)
+// Per stage the wave issues A(s + 5) and then W(s + 2); the wait for stage
+// s counts the loads issued after W(s) (those of one stage: 2 DMAs and
+// 2 TPW weight loads), and W(s) was issued after A(s), so one vmcnt wait
+// covers both.  One barrier per stage.
+template <int TPW>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_front_logits(const GemmArgs p) {
+  constexpr int NS = kFlStages, STAGE = kFlRows * 128, PA = NS - 1;
+  constexpr int WAITN = 2 + 2 * TPW;
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int q = lane >> 4, l16 = lane & 15;
+  const int N = p.single_rows, m0 = blockIdx.x * kFlRows;
+  const int NT = (p.N_out + 15) >> 4;
+  const int KS = p.K >> 6;
+  const int nsplit = p.W2 ? p.n_split : p.N_out;
+  const uint16_t* W = reinterpret_cast<const uint16_t*>(p.W);
+  const uint16_t* W2 = reinterpret_cast<const uint16_t*>(p.W2);
+  const uint16_t* wrow[TPW];
+  {
+    int prev = NT - 1;
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const int tl = wave + 4 * t < NT ? wave + 4 * t : prev;
+      prev = tl;
+      const int c = min(16 * tl + l16, p.N_out - 1);
+      wrow[t] = c < nsplit ? W + static_cast<int64_t>(c) * p.ldw
+                           : W2 + static_cast<int64_t>(c - nsplit) * p.ldw2;
+    }
+  }
+  const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A);
+  const uint16_t* asrc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int r = 8 * (4 * j + wave) + (lane >> 3);
+    const int row = min(m0 + r, N - 1);  // rows past N: a valid row, never stored
+    asrc[j] = A + static_cast<int64_t>(row) * p.lda + (sw_chunk<8>(r, lane & 7) << 3);
+  }
+  auto issue_a = [&](int s) {  // stage s (past the end: the last again) into slot s % NS
+    const int sc = min(s, KS - 1);
+    uint8_t* base = ring + (s % NS) * STAGE;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      __builtin_amdgcn_global_load_lds((gbl_vptr)(asrc[j] + sc * 64),
+                                       (lds_vptr)(base + (4 * j + wave) * 1024), 16, 0, 0);
+  };
+  u32x4 wa[2][TPW], wb[2][TPW];
+  auto fetch_w = [&](int d, int s) {  // register slot d <- stage s (clamped)
+    const int k0 = 64 * min(s, KS - 1);
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      wa[d][t] = *reinterpret_cast<const u32x4*>(wrow[t] + k0 + 8 * q);
+      wb[d][t] = *reinterpret_cast<const u32x4*>(wrow[t] + k0 + 32 + 8 * q);
+    }
+  };
+  f32x4 acc[TPW][4];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t)
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) acc[t][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // prologue, in the order the waits assume: A(0), W(0), A(1..PA-1), W(1)
+  issue_a(0);
+  fetch_w(0, 0);
+#pragma unroll
+  for (int s = 1; s < PA; ++s) issue_a(s);
+  fetch_w(1, 1);
+  auto step = [&](int d, int s) {
+    wait_vmcnt<WAITN>();  // A(s) and W(s) have landed (this wave's part)
+    wait_lgkm0();         // and this wave's reads of stage s - 1 are done
+    __builtin_amdgcn_s_barrier();
+    issue_a(s + PA);  // into the slot of stage s - 1
+    const uint8_t* sa = ring + (s % NS) * STAGE;
+    bf16x8 alo[4], ahi[4];
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      const int r = 16 * rt + l16;
+      alo[rt] = *reinterpret_cast<const bf16x8*>(sa + r * 128 + (sw_chunk<8>(r, q) << 4));
+      ahi[rt] = *reinterpret_cast<const bf16x8*>(sa + r * 128 + (sw_chunk<8>(r, 4 + q) << 4));
+    }
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+      for (int rt = 0; rt < 4; ++rt) {
+        acc[t][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8, wa[d][t]), alo[rt], acc[t][rt], 0, 0, 0);
+        acc[t][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            __builtin_bit_cast(bf16x8, wb[d][t]), ahi[rt], acc[t][rt], 0, 0, 0);
+      }
+    fetch_w(d, s + 2);
+  };
+  int s0 = 0;
+  for (; s0 + 2 <= KS; s0 += 2) {  // stage s in register slot s % 2
+    step(0, s0);
+    step(1, s0 + 1);
+  }
+  if (s0 < KS) step(0, s0);  // odd KS: the last stage (even, slot 0)
+  wait_vmcnt<0>();  // the clamped refills past the end have landed before the workgroup ends
+  // lane: channels 16 tile + 4 q + (0..3) of rows m0 + 16 rt + l16
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int c = 16 * (wave + 4 * t) + 4 * q;
+    if (wave + 4 * t >= NT || c >= p.N_out) continue;  // N_out % 4 == 0: c .. c + 3 all stored
+    float bv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int n = c + i;
+      const float* bp = n < nsplit ? p.bias : p.bias2;
+      bv[i] = bp ? bp[n < nsplit ? n : n - nsplit] : 0.f;
+    }
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      const int row = m0 + 16 * rt + l16;
+      if (row >= N) continue;
+      const f32x4 v = acc[t][rt];
+      *reinterpret_cast<f32x4*>(reinterpret_cast<float*>(p.out) + static_cast<int64_t>(row) * p.ldo + c) =
+          f32x4{v[0] + bv[0], v[1] + bv[1], v[2] + bv[2], v[3] + bv[3]};
+    }
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
+
+int launch_front_logits(const GemmArgs& a, hipStream_t s) {
+  if (a.fmt != SMOE_BF16 || a.epi != EPI_F32_BIAS || a.G != 0 || a.single_rows < 1 || !a.A ||
+      !a.W || !a.out || a.N_out <= 0 || a.K < 64)
+    return SMOE_EINVAL;
+  if (a.K % 64 || a.N_out % 4 || a.ldo % 4 || a.ldo < a.N_out || a.lda % 8 || a.lda < a.K ||
+      a.ldw % 8 || a.ldw < a.K)
+    return SMOE_EINVAL;
+  if (a.W2 && (a.n_split < 0 || a.n_split > a.N_out || a.n_split % 4 || a.ldw2 % 8 || a.ldw2 < a.K ||
+               !aligned16(a.W2)))
+    return SMOE_EINVAL;
+  if (!aligned16(a.A) || !aligned16(a.W) || !aligned16(a.out)) return SMOE_EINVAL;
+  const int nt = (a.N_out + 15) / 16, tpw = (nt + 3) / 4;
+  if (tpw > kFlMaxTpw) return SMOE_EUNSUPPORTED;
+  const dim3 grid(static_cast<unsigned>((a.single_rows + kFlRows - 1) / kFlRows)), block(256);
+  switch (tpw) {
+    case 1: hipLaunchKernelGGL(k_front_logits<1>, grid, block, 0, s, a); break;
+    case 2: hipLaunchKernelGGL(k_front_logits<2>, grid, block, 0, s, a); break;
+    case 3: hipLaunchKernelGGL(k_front_logits<3>, grid, block, 0, s, a); break;
+    case 4: hipLaunchKernelGGL(k_front_logits<4>, grid, block, 0, s, a); break;
+    default: hipLaunchKernelGGL(k_front_logits<5>, grid, block, 0, s, a); break;
+  }
+  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
+}  // namespace smoe

@@ -577,18 +577,6 @@ __device__ __forceinline__ int swz32(int row, int chunk) {
   return row * 64 + ((chunk ^ ((row >> 1) & 3)) << 4);
 }
 
-// s_waitcnt vmcnt(n) (gfx9 encoding; expcnt / lgkmcnt left at "no wait")
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (0xF << 8));
-}
-// s_waitcnt lgkmcnt(0) (vmcnt / expcnt left at "no wait")
-__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
-
-typedef __attribute__((address_space(3))) void* lds_vptr;
-typedef __attribute__((address_space(1))) void* gbl_vptr;
-
 template <int BN, int NS, int GM, int EPI, bool PK = false>
 // A ring of 3 stages (72 KB of LDS at BN = 128) lets two workgroups share a
 // CU (registers are held to 256 per lane by the launch bound), so one's
@@ -1620,12 +1608,6 @@ constexpr int stream_wb() {  // bytes of one channel's 64-k slice
   return FMT == SMOE_BF16 ? 128 : (FMT == SMOE_FP8_E4M3 ? 64 : 32);
 }
 constexpr int kStreamScaleMax = 4096;  // int4 scale-table entries per strip
-
-// physical 16-byte chunk of logical chunk c in row r (rows of 16*CPR bytes)
-template <int CPR>
-__device__ __forceinline__ int sw_chunk(int r, int c) {
-  return c ^ ((r / (16 / CPR)) & (CPR - 1));
-}
 
 template <int FMT, int EPI, int RT, int NS, int WGS>
 __global__ __launch_bounds__(256, WGS) void k_gemm_stream(const GemmArgs p) {

@@ -110,6 +110,13 @@ int launch_pack_int4_qtiles(const void* q, int G, int N, int K, void* out, hipSt
 // generator rows of a small decode step in one pass.
 int launch_front_gemm(const GemmArgs& a, hipStream_t s);
 
+// Prefill logits in one pass (k_front_logits): bf16 A [single_rows, K] (G ==
+// 0) times W rows (channels < n_split, ldw) and W2 rows (the rest, ldw2; W2
+// null: every channel from W) -> f32 out [rows, ldo] plus bias / bias2;
+// N_out <= 320, n_split and N_out multiples of 4, K % 64 == 0.
+// SMOE_EUNSUPPORTED past 320 output channels.
+int launch_front_logits(const GemmArgs& a, hipStream_t s);
+
 // ---- routing ----
 int launch_route_topk(const float* logits, int N, int E, int K, int32_t* top_idx, float* top_w,
                       int32_t* tok_e, float* tok_ew, const int32_t* active, hipStream_t s);
@@ -126,6 +133,34 @@ int launch_gather_topm(const int32_t* src_idx, const int32_t* tok_e, const int32
 int launch_dest_coeffs(const int32_t* src_idx, const int32_t* eidx, const float* ew, int N, int K,
                        int M, int E, int S, int32_t* tok_d, float* tok_dc, hipStream_t s);
 size_t plan_scratch_bytes(int N, int G);
+// Prefill routing over the dense logits of launch_front_logits (E <= 16):
+// top-k, per-source top-m in slot order (rows t*K + j of slot_idx / slot_w
+// [N*K, M]) and the tokens' destination coefficients.
+int launch_route_dense(const float* front, int ldf, int N, int E, int K, int M, int S,
+                       float* logits, int32_t* top_idx, float* top_w, int32_t* tok_e,
+                       float* tok_ew, int32_t* slot_idx, float* slot_w, int32_t* tok_d,
+                       float* tok_dc, const int32_t* active, hipStream_t s);
+// One plan's operands for launch_plan2 (those of launch_plan), with an
+// optional payload of pay_m values per entry moved from slot order to the
+// plan rows by the scatter (first plan only).
+struct PlanSpec {
+  const int32_t* tok_g = nullptr;
+  const float* tok_w = nullptr;
+  int S = 0, G = 0, drop = 0;
+  int32_t *cnt = nullptr, *acnt = nullptr, *off = nullptr, *rows = nullptr;
+  float* roww = nullptr;
+  int32_t* tokrow = nullptr;
+  const int32_t* pay_idx = nullptr;
+  const float* pay_w = nullptr;
+  int32_t* out_idx = nullptr;
+  float* out_w = nullptr;
+  int pay_m = 0;
+};
+// Two plans over the same N tokens in one rank, one scan and one scatter
+// launch (scratch: plan_scratch_bytes(N, a.G) + plan_scratch_bytes(N, b.G)).
+// Where launch_plan would take a one-workgroup form, the two run as two
+// launch_plan calls (no payload then).
+int launch_plan2(const PlanSpec& a, const PlanSpec& b, int N, void* scratch, hipStream_t s);
 int launch_plan(const int32_t* tok_g, const float* tok_w, int N, int S, int G, int drop_nonpos,
                 int32_t* cnt, int32_t* acnt, int32_t* off, int32_t* rows, float* roww,
                 int32_t* tokrow, void* scratch, hipStream_t s);

@@ -774,11 +774,10 @@ __global__ __launch_bounds__(256) void k_plan_rank(const int32_t* __restrict__ t
 
 // One wave per group: chunk counts -> exclusive chunk prefixes (in place),
 // group totals -> cnt, positive-weight totals -> acnt.
-__global__ __launch_bounds__(64) void k_plan_scan(int C, int32_t* __restrict__ ccnt,
-                                                  const int32_t* __restrict__ cacnt,
-                                                  int32_t* __restrict__ cnt,
-                                                  int32_t* __restrict__ acnt) {
-  const int g = blockIdx.x, lane = threadIdx.x;
+__device__ __forceinline__ void scan_group(int g, int C, int32_t* __restrict__ ccnt,
+                                           const int32_t* __restrict__ cacnt,
+                                           int32_t* __restrict__ cnt, int32_t* __restrict__ acnt) {
+  const int lane = threadIdx.x;
   int32_t* row = ccnt + static_cast<int64_t>(g) * C;
   const int32_t* arow = cacnt + static_cast<int64_t>(g) * C;
   int run = 0;  // sum of all earlier passes
@@ -807,6 +806,13 @@ __global__ __launch_bounds__(64) void k_plan_scan(int C, int32_t* __restrict__ c
     cnt[g] = run;
     acnt[g] = a;
   }
+}
+
+__global__ __launch_bounds__(64) void k_plan_scan(int C, int32_t* __restrict__ ccnt,
+                                                  const int32_t* __restrict__ cacnt,
+                                                  int32_t* __restrict__ cnt,
+                                                  int32_t* __restrict__ acnt) {
+  scan_group(blockIdx.x, C, ccnt, cacnt, cnt, acnt);
 }
 
 __global__ __launch_bounds__(256) void k_plan_scatter(const int32_t* __restrict__ tok_g,
@@ -1049,6 +1055,192 @@ int launch_plan(const int32_t* tok_g, const float* tok_w, int N, int S, int G, i
   hipLaunchKernelGGL(k_plan_scan, dim3(G), dim3(64), 0, s, C, ccnt, cacnt, cnt, acnt);
   hipLaunchKernelGGL(k_plan_scatter, dim3((N + 255) / 256), dim3(256), 0, s, tok_g, tok_w, N, S,
                      G, C, ccnt, cnt, off, rows, roww, tokrow);
+  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
+// ------------------------------------------- prefill front routing ----
+// Routing over the dense logits of k_front_logits (front: f32 [N, ldf],
+// router logits in columns [0, E), the edge logits of source s in columns
+// E + s E .. E + s E + E - 1), one segment of 16 lanes per token (E <= 16):
+// the router top-k of topk_seg, then top-m (topm_seg) over the edge logits
+// of each selected source, read from the token's own row, so no expert plan
+// is needed first.  The sources go in ascending order, as the expert plan
+// orders them; their edges go to slot rows t * K + j of slot_idx / slot_w
+// [N*K, M], which the expert plan's scatter (launch_plan2) moves to the plan
+// rows.  Also writes logits [N, E] (the statistics read them).
+template <int KB>
+__global__ __launch_bounds__(256) void k_route_dense(
+    const float* __restrict__ front, int ldf, int N, int E, int K, int M, int S,
+    float* __restrict__ logits, int32_t* __restrict__ top_idx, float* __restrict__ top_w,
+    int32_t* __restrict__ tok_e, float* __restrict__ tok_ew, int32_t* __restrict__ slot_idx,
+    float* __restrict__ slot_w, int32_t* __restrict__ tok_d, float* __restrict__ tok_dc,
+    const int32_t* __restrict__ active) {
+  constexpr int SEG = 16, TPW = 64 / SEG;
+  const int lane = threadIdx.x & 63;
+  const int t0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * TPW;
+  if (t0 >= N) return;  // wave-uniform
+  const int e = lane & (SEG - 1);
+  const int le = e < E ? e : E - 1;
+  const int t = t0 + lane / SEG;
+  const bool ok = t < N;
+  const float* row = front + static_cast<int64_t>(ok ? t : N - 1) * ldf;
+  const float v = row[le];
+  const bool live = !active || active[ok ? t : N - 1] != 0;
+  if (ok && e < E) logits[static_cast<int64_t>(t) * E + e] = v;
+  uint64_t m = topk_seg<SEG>(v, t, ok, live, E, K, top_idx, top_w, tok_e, tok_ew, nullptr, nullptr);
+  if (!live) m = 0;  // a token that has left: no sources (tok_e holds -1)
+  float ev[KB];
+  int rw[KB];
+  bool lv[KB];
+#pragma unroll
+  for (int j = 0; j < KB; ++j) {  // the selected sources, ascending
+    const int sj = m ? __builtin_ctzll(m) : 0;
+    lv[j] = ok && j < K && m != 0;
+    m &= m - 1;
+    rw[j] = t * K + j;
+    ev[j] = row[E + sj * E + le];
+  }
+  topm_seg<SEG, KB>(ev, rw, lv, t, ok, E, M, S, slot_idx, slot_w, tok_d, tok_dc, nullptr, nullptr);
+}
+
+int launch_route_dense(const float* front, int ldf, int N, int E, int K, int M, int S,
+                       float* logits, int32_t* top_idx, float* top_w, int32_t* tok_e,
+                       float* tok_ew, int32_t* slot_idx, float* slot_w, int32_t* tok_d,
+                       float* tok_dc, const int32_t* active, hipStream_t s) {
+  if (E < 1 || E > 16 || K < 1 || K > E || K > 16 || M < 1 || M > E || S < 1 || S > 64 ||
+      ldf < E + E * E || !front)
+    return SMOE_EINVAL;
+  if (N <= 0) return SMOE_OK;
+  const dim3 grid((N + 15) / 16), block(256);
+#define SMOE_ROUTE_DENSE(KB)                                                                     \
+  hipLaunchKernelGGL((k_route_dense<KB>), grid, block, 0, s, front, ldf, N, E, K, M, S, logits,  \
+                     top_idx, top_w, tok_e, tok_ew, slot_idx, slot_w, tok_d, tok_dc, active)
+  if (K <= 1) SMOE_ROUTE_DENSE(1);
+  else if (K <= 2) SMOE_ROUTE_DENSE(2);
+  else if (K <= 4) SMOE_ROUTE_DENSE(4);
+  else if (K <= 8) SMOE_ROUTE_DENSE(8);
+  else SMOE_ROUTE_DENSE(16);
+#undef SMOE_ROUTE_DENSE
+  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
+// Two plans (the expert plan and the destination plan of one loop) in one
+// set of rank / scan / scatter launches: each launch's workgroups are split
+// between the plans, which use the same device code as launch_plan (so the
+// same results).  The first plan may carry a payload: pay_m values per entry
+// (slot order, entry (t, j) at (t * S + j) * pay_m) that its scatter copies
+// to the entry's plan row (row * pay_m) — the per-source edges.
+struct Plan2 {
+  const int32_t* tok_g;
+  const float* tok_w;
+  int S, G, drop, W;
+  int32_t *cnt, *acnt, *off, *rows;
+  float* roww;
+  int32_t* tokrow;
+  int32_t *ccnt, *cacnt;
+  const int32_t* pay_idx;
+  const float* pay_w;
+  int32_t* out_idx;
+  float* out_w;
+  int pay_m;
+};
+
+__global__ __launch_bounds__(256) void k_plan2_rank(const Plan2 a, const Plan2 b, int N, int C) {
+  int item = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const bool second = item >= C * a.W;  // wave-uniform
+  const Plan2& p = second ? b : a;
+  if (second) item -= C * a.W;
+  if (item >= C * p.W) return;
+  const int win = (p.G + p.W - 1) / p.W;
+  const int chunk = item / p.W, g0 = (item % p.W) * win;
+  rank_chunk(p.tok_g, p.tok_w, N, p.S, p.G, p.drop, chunk * 64, g0, win, p.ccnt + chunk,
+             p.cacnt + chunk, C, p.tokrow);
+}
+
+__global__ __launch_bounds__(64) void k_plan2_scan(const Plan2 a, const Plan2 b, int C) {
+  const bool second = static_cast<int>(blockIdx.x) >= a.G;
+  const Plan2& p = second ? b : a;
+  scan_group(second ? blockIdx.x - a.G : blockIdx.x, C, p.ccnt, p.cacnt, p.cnt, p.acnt);
+}
+
+__global__ __launch_bounds__(256) void k_plan2_scatter(const Plan2 a, const Plan2 b, int N, int C) {
+  __shared__ int goff[kPlanMaxG + 1], wsum[4];
+  const int nb = (N + 255) / 256;
+  const bool second = static_cast<int>(blockIdx.x) >= nb;
+  const Plan2& p = second ? b : a;
+  const int blk = second ? blockIdx.x - nb : blockIdx.x;
+  block_group_offsets(p.cnt, p.G, goff, wsum);
+  if (blk == 0)
+    for (int g = threadIdx.x; g <= p.G; g += 256) p.off[g] = goff[g];
+  const int t = blk * 256 + threadIdx.x;
+  if (t >= N) return;
+  scatter_token(p.tok_g, p.tok_w, t, p.S, p.G, p.ccnt + (t >> 6), C, goff, p.rows, p.roww, p.tokrow);
+  if (p.pay_m <= 0) return;
+  const int64_t e0 = static_cast<int64_t>(t) * p.S;
+  for (int j = 0; j < p.S; ++j) {
+    const int row = p.tokrow[e0 + j];  // this thread's own store above: -1 for dropped entries
+    if (row < 0) continue;
+    for (int i = 0; i < p.pay_m; ++i) {
+      p.out_idx[static_cast<int64_t>(row) * p.pay_m + i] = p.pay_idx[(e0 + j) * p.pay_m + i];
+      p.out_w[static_cast<int64_t>(row) * p.pay_m + i] = p.pay_w[(e0 + j) * p.pay_m + i];
+    }
+  }
+}
+
+namespace {
+int plan_windows(int C, int G) {  // as launch_plan: about 256 rank waves
+  int W = (G + 63) / 64;
+  while (C * W < 256 && (G + W - 1) / W > 8) W *= 2;
+  return W;
+}
+}  // namespace
+
+int launch_plan2(const PlanSpec& pa, const PlanSpec& pb, int N, void* scratch, hipStream_t s) {
+  for (const PlanSpec* p : {&pa, &pb})
+    if (p->G < 1 || p->G > kPlanMaxG || p->S < 1 || p->S > kPlanMaxS) return SMOE_EINVAL;
+  if (N < 0) return SMOE_EINVAL;
+  const int C = (N + 63) / 64;
+  if (N <= 64 || C * pa.G <= 512 || C * pb.G <= 512) {  // launch_plan's one-workgroup forms
+    if (pa.pay_m > 0) return SMOE_EINVAL;
+    int rc = launch_plan(pa.tok_g, pa.tok_w, N, pa.S, pa.G, pa.drop, pa.cnt, pa.acnt, pa.off,
+                         pa.rows, pa.roww, pa.tokrow, scratch, s);
+    if (rc != SMOE_OK) return rc;
+    return launch_plan(pb.tok_g, pb.tok_w, N, pb.S, pb.G, pb.drop, pb.cnt, pb.acnt, pb.off,
+                       pb.rows, pb.roww, pb.tokrow, scratch, s);
+  }
+  Plan2 a, b;
+  int32_t* z = reinterpret_cast<int32_t*>(scratch);
+  Plan2* dst[2] = {&a, &b};
+  const PlanSpec* src[2] = {&pa, &pb};
+  for (int i = 0; i < 2; ++i) {
+    const PlanSpec& p = *src[i];
+    Plan2& q = *dst[i];
+    q.tok_g = p.tok_g;
+    q.tok_w = p.tok_w;
+    q.S = p.S;
+    q.G = p.G;
+    q.drop = p.drop;
+    q.W = plan_windows(C, p.G);
+    q.cnt = p.cnt;
+    q.acnt = p.acnt;
+    q.off = p.off;
+    q.rows = p.rows;
+    q.roww = p.roww;
+    q.tokrow = p.tokrow;
+    q.ccnt = z;
+    q.cacnt = z + static_cast<int64_t>(C) * p.G;
+    z += 2 * static_cast<int64_t>(C) * p.G;
+    q.pay_idx = p.pay_idx;
+    q.pay_w = p.pay_w;
+    q.out_idx = p.out_idx;
+    q.out_w = p.out_w;
+    q.pay_m = p.pay_m;
+  }
+  if (b.pay_m > 0) return SMOE_EINVAL;  // the payload rides with the first plan
+  const int items = C * (a.W + b.W);
+  hipLaunchKernelGGL(k_plan2_rank, dim3((items + 3) / 4), dim3(256), 0, s, a, b, N, C);
+  hipLaunchKernelGGL(k_plan2_scan, dim3(a.G + b.G), dim3(64), 0, s, a, b, C);
+  hipLaunchKernelGGL(k_plan2_scatter, dim3(2 * ((N + 255) / 256)), dim3(256), 0, s, a, b, N, C);
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 

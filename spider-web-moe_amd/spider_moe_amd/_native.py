@@ -181,7 +181,9 @@ SPIDER_HOST_SIGNATURES = {
 
 STAGES = ["router_gemm", "route_topk", "expert_plan", "edge_logits", "edge_topm", "dest_plan",
           "edge_gemm", "msg_combine", "up_gemm", "down_gemm", "epilogue",
-          # bf16 steps of N <= 64: stages 0-5 as one GEMM and one routing workgroup
+          # stages 0-5 as one logits GEMM and its routing: bf16 steps of N <= 64
+          # (one routing workgroup) and bf16 prefill at E <= 16 (the plans
+          # count under expert_plan)
           "front_gemm", "front_route"]
 
 ABI_VERSION = 10

@@ -247,6 +247,42 @@ def test_block_small_steps_fused_front(n, e, k, m):
     assert int(rt["d_cnt"].sum()) == int((rt["tok_d"] >= 0).sum())
 
 
+@pytest.mark.parametrize("n,e,k,m", [(2112, 16, 2, 2), (4160, 8, 2, 4), (8256, 4, 1, 2),
+                                     (2800, 12, 3, 3), (4160, 32, 2, 2), (4096, 64, 2, 4)])
+def test_block_prefill_one_pass_logits(n, e, k, m):
+    """Prefill steps at E <= 16 (N past the one-workgroup plans) run the
+    one-pass front: [router | every edge generator row] logits in one GEMM,
+    top-k and per-source top-m from each token's own row, and both plans in
+    one set of launches that also moves the edges to their plan rows.  At E
+    32 and 64 the router logits alone take the one-pass kernel.  Routing,
+    plans, edges, message, delta and outputs against the oracle for two
+    loops (ragged N, k 1-3, m 2-4); the stage events show which stages ran.
+    Weights N(0, 0.02) as in the workloads: with fan-in weights at hidden
+    128 the expert delta reaches 4.6 and one output element of 270 k
+    (|ref| 0.074) misses 1e-2 by 5%, on this path and on the separate
+    stages alike (bf16 storage of the expert outputs); message and delta
+    are compared at their own scale either way."""
+    from spider_moe_amd import _native as nat
+    from spider_moe_amd.workloads import make_block
+    say("prefill one-pass logits", n, e, k, m)
+    wl = make_block("c1", tokens=n, hidden_size=128, num_experts=e, top_k=k, edges_per_expert=m,
+                    expert_ffn_size=256, num_loops=2, expert_activation="swiglu", experts="bf16")
+    timer = nat.StageTimer(stages=["router_gemm", "edge_logits", "front_gemm", "front_route"],
+                           capacity=64)
+    timer.start()
+    with torch.no_grad():
+        wl.layer(wl.h, wl.x0, 0)
+    ran = set(timer.stop())
+    want = {"front_gemm", "front_route"} if e <= 16 else {"router_gemm", "edge_logits"}
+    assert ran == want, ran
+    h = wl.h
+    for r in range(2):
+        h, rep = _check_loop(wl.layer, h, wl.x0, r, 1e-2)
+    rt = wl.layer.last_routing()
+    assert int(rt["e_cnt"].sum()) == n * k
+    assert int(rt["d_cnt"].sum()) == int((rt["tok_d"] >= 0).sum())
+
+
 def test_block_skewed_empty_experts():
     from spider_moe_amd.workloads import make_block
     say("skewed small")
