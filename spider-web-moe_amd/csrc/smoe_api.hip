@@ -205,11 +205,11 @@ bool front_ok(const smoe_block* b, int N) {
 }
 
 // Prefill steps whose router and edge logits come out of one pass
-// (launch_front_logits over [router | every edge generator row], at most 320
-// channels: E <= 16), routed per token on them (launch_route_dense) and
-// planned in one set of launches (launch_plan2, its three-kernel form: C * E
-// > 512).  The per-source edges wait in the edge_logit region in slot order
-// (2 M <= E: they fit) until the expert plan's scatter moves them.
+// (launch_front_prefill: [router | every edge generator row], at most 272
+// channels, E <= 16), routed and ranked in the same workgroups, where the
+// separate stages would run the plans' three-kernel form (C * E > 512).  The
+// per-source edges wait in the edge_logit region in slot order (2 M <= E:
+// they fit) until the expert plan's scatter moves them.
 bool prefill_front_ok(const smoe_block* b, int N) {
   const int E = b->E, S = (E < b->K * b->M) ? E : b->K * b->M;
   const int64_t C = (static_cast<int64_t>(N) + 63) / 64;
@@ -279,8 +279,8 @@ void make_layout(const smoe_block* b, int N, smoe_ws_layout* l) {
   l->y = z.take(n * K * H * esize(fdt));
   l->h_tmp = z.take(n * H * esize(b->act_dtype));
   const bool pf = prefill_front_ok(b, N);
-  l->scratch = z.take(plan_scratch_bytes(N, E) * (pf ? 2 : 1));  // launch_plan2: both plans'
-  l->front = z.take(front_ok(b, N) || pf ? n * (E + E * E) * 4 : 0);
+  l->scratch = z.take(plan_scratch_bytes(N, E) * (pf ? 2 : 1));  // the prefill front: both plans'
+  l->front = z.take(front_ok(b, N) ? n * (E + E * E) * 4 : 0);
   const bool dec = decode_ok(b, N);
   l->sel_idx = z.take(dec ? n * K * M * 4 : 0);
   l->sel_w = z.take(dec ? n * K * M * 4 : 0);
@@ -596,9 +596,11 @@ int block_forward(const smoe_block* b, const void* h_in, const void* x0, void* h
                                at<int32_t>(ws, l.d_tokrow), active, s),
             "front routing");
     } else if (pfront) {
-      // 1-6: [router | every edge generator row] logits in one pass, routing
-      // per token on them, both plans in one set of launches
-      const int ldf = E + E * E;
+      // 1-6 in one launch per 64-token chunk (logits of the router and every
+      // edge generator row, top-k, per-source top-m, destination
+      // coefficients, both plans' chunk ranks), then the plans' scan and
+      // scatter, which also moves the per-source edges (slot order, in the
+      // edge_logit region meanwhile) to their expert-plan rows
       GemmArgs fg;
       fg.fmt = SMOE_BF16;
       fg.epi = EPI_F32_BIAS;
@@ -607,29 +609,43 @@ int block_forward(const smoe_block* b, const void* h_in, const void* x0, void* h
       fg.W = b->router_w;
       fg.ldw = H;
       fg.K = H;
-      fg.N_out = ldf;
+      fg.N_out = E + E * E;
       fg.G = 0;
       fg.single_rows = N;
-      fg.out = at<float>(ws, l.front);
-      fg.ldo = ldf;
       fg.bias = b->loop_bias + static_cast<int64_t>(r) * E;
       fg.W2 = b->edge_gen_w;
       fg.ldw2 = H + L;
       fg.n_split = E;
       fg.bias2 = b->edge_loop_bias + static_cast<int64_t>(r) * E * E;
-      STAGE(SMOE_STAGE_FRONT_GEMM, launch_front_logits(fg, s), "front logits");
-      // the per-source edges in slot order wait in the edge_logit region
-      int32_t* slot_idx = at<int32_t>(ws, l.edge_logit);
-      float* slot_w = reinterpret_cast<float*>(slot_idx + static_cast<int64_t>(N) * K * M);
-      STAGE(SMOE_STAGE_FRONT_ROUTE,
-            launch_route_dense(at<float>(ws, l.front), ldf, N, E, K, M, S, at<float>(ws, l.logits),
-                               at<int32_t>(ws, l.top_idx), at<float>(ws, l.top_w),
-                               at<int32_t>(ws, l.tok_e), at<float>(ws, l.tok_ew), slot_idx, slot_w,
-                               at<int32_t>(ws, l.tok_d), at<float>(ws, l.tok_dc), active, s),
-            "dense routing");
+      const int C = (N + 63) / 64;
+      int32_t* ccnt = at<int32_t>(ws, l.scratch);  // expert plan [E, C] x 2, then destination
+      FrontPrefill fp;
+      fp.N = N;
+      fp.E = E;
+      fp.K = K;
+      fp.M = M;
+      fp.S = S;
+      fp.C = C;
+      fp.logits = at<float>(ws, l.logits);
+      fp.top_idx = at<int32_t>(ws, l.top_idx);
+      fp.top_w = at<float>(ws, l.top_w);
+      fp.tok_e = at<int32_t>(ws, l.tok_e);
+      fp.tok_ew = at<float>(ws, l.tok_ew);
+      fp.slot_idx = at<int32_t>(ws, l.edge_logit);
+      fp.slot_w = reinterpret_cast<float*>(fp.slot_idx + static_cast<int64_t>(N) * K * M);
+      fp.tok_d = at<int32_t>(ws, l.tok_d);
+      fp.tok_dc = at<float>(ws, l.tok_dc);
+      fp.e_tokrow = at<int32_t>(ws, l.e_tokrow);
+      fp.d_tokrow = at<int32_t>(ws, l.d_tokrow);
+      fp.e_ccnt = ccnt;
+      fp.e_cacnt = ccnt + static_cast<int64_t>(C) * E;
+      fp.d_ccnt = ccnt + 2 * static_cast<int64_t>(C) * E;
+      fp.d_cacnt = ccnt + 3 * static_cast<int64_t>(C) * E;
+      fp.active = active;
+      STAGE(SMOE_STAGE_FRONT_GEMM, launch_front_prefill(fg, fp, s), "prefill front");
       PlanSpec pe, pd;
-      pe.tok_g = at<int32_t>(ws, l.tok_e);
-      pe.tok_w = at<float>(ws, l.tok_ew);
+      pe.tok_g = fp.tok_e;
+      pe.tok_w = fp.tok_ew;
       pe.S = K;
       pe.G = E;
       pe.drop = 0;
@@ -638,14 +654,14 @@ int block_forward(const smoe_block* b, const void* h_in, const void* x0, void* h
       pe.off = at<int32_t>(ws, l.e_off);
       pe.rows = at<int32_t>(ws, l.e_rows);
       pe.roww = at<float>(ws, l.e_roww);
-      pe.tokrow = at<int32_t>(ws, l.e_tokrow);
-      pe.pay_idx = slot_idx;
-      pe.pay_w = slot_w;
+      pe.tokrow = fp.e_tokrow;
+      pe.pay_idx = fp.slot_idx;
+      pe.pay_w = fp.slot_w;
       pe.out_idx = at<int32_t>(ws, l.edge_idx);
       pe.out_w = at<float>(ws, l.edge_w);
       pe.pay_m = M;
-      pd.tok_g = at<int32_t>(ws, l.tok_d);
-      pd.tok_w = at<float>(ws, l.tok_dc);
+      pd.tok_g = fp.tok_d;
+      pd.tok_w = fp.tok_dc;
       pd.S = S;
       pd.G = E;
       pd.drop = 1;
@@ -654,8 +670,8 @@ int block_forward(const smoe_block* b, const void* h_in, const void* x0, void* h
       pd.off = at<int32_t>(ws, l.d_off);
       pd.rows = at<int32_t>(ws, l.d_rows);
       pd.roww = at<float>(ws, l.d_roww);
-      pd.tokrow = at<int32_t>(ws, l.d_tokrow);
-      STAGE(SMOE_STAGE_EXPERT_PLAN, launch_plan2(pe, pd, N, at<void>(ws, l.scratch), s),
+      pd.tokrow = fp.d_tokrow;
+      STAGE(SMOE_STAGE_EXPERT_PLAN, launch_plan2_finish(pe, pd, N, ccnt, s),
             "expert + destination plans");
     } else {
 

@@ -11,6 +11,7 @@
 // with its own shape here.
 #include "smoe_common.hpp"
 #include "smoe_internal.hpp"
+#include "smoe_routing.hpp"
 
 namespace smoe {
 namespace {
@@ -40,10 +41,10 @@ constexpr int kFlMaxTpw = 5;  // 16-channel tiles per wave: N_out <= 320
 // 2 TPW weight loads), and W(s) was issued after A(s), so one vmcnt wait
 // covers both.  One barrier per stage.
 template <int TPW>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_front_logits(const GemmArgs p) {
+__device__ __forceinline__ void logits_mainloop(const GemmArgs& p, uint8_t* ring,
+                                                f32x4 (&acc)[TPW][4]) {
   constexpr int NS = kFlStages, STAGE = kFlRows * 128, PA = NS - 1;
   constexpr int WAITN = 2 + 2 * TPW;
-  __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int q = lane >> 4, l16 = lane & 15;
   const int N = p.single_rows, m0 = blockIdx.x * kFlRows;
@@ -89,7 +90,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
       wb[d][t] = *reinterpret_cast<const u32x4*>(wrow[t] + k0 + 32 + 8 * q);
     }
   };
-  f32x4 acc[TPW][4];
 #pragma unroll
   for (int t = 0; t < TPW; ++t)
 #pragma unroll
@@ -131,6 +131,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   }
   if (s0 < KS) step(0, s0);  // odd KS: the last stage (even, slot 0)
   wait_vmcnt<0>();  // the clamped refills past the end have landed before the workgroup ends
+}
+
+template <int TPW>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_front_logits(const GemmArgs p) {
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[kFlStages * kFlRows * 128];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q = lane >> 4, l16 = lane & 15;
+  const int N = p.single_rows, m0 = blockIdx.x * kFlRows;
+  const int NT = (p.N_out + 15) >> 4;
+  const int nsplit = p.W2 ? p.n_split : p.N_out;
+  f32x4 acc[TPW][4];
+  logits_mainloop<TPW>(p, ring, acc);
   // lane: channels 16 tile + 4 q + (0..3) of rows m0 + 16 rt + l16
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
@@ -152,6 +164,109 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
           f32x4{v[0] + bv[0], v[1] + bv[1], v[2] + bv[2], v[3] + bv[3]};
     }
   }
+}
+
+// The one-pass prefill front (E <= 16): a workgroup's 64 tokens are one
+// chunk of the dispatch plans, so after its logits GEMM the workgroup also
+// routes them and ranks them for both plans, with the logits in LDS:
+//   1 the GEMM above over [router | every edge generator row]; the tile of
+//     [64, E + E*E] logits (+ biases) goes to LDS (over the ring) and the
+//     router logits also to `logits` (the statistics read them)
+//   2 wave w routes tokens 16 w .. 16 w + 15, a segment of 16 lanes per token
+//     (topk_seg, then topm_seg over the token's selected sources, ascending),
+//     writing what k_route_topk / k_edge_topm write (edges in slot order,
+//     rows t * K + j of slot_idx / slot_w) and copies of the tokens' sources
+//     and destinations in LDS
+//   3 wave 0 ranks the chunk for the expert plan, wave 1 for the destination
+//     plan (rank_chunk over the LDS copies, all groups in one window),
+//     writing the chunk's column of each plan's [G, C] count matrices and the
+//     entries' ranks; launch_plan2_finish scans and scatters.
+// The logits tile ends the GEMM's ring (its DMAs have landed, every wave is
+// past its last read) and reuses its bytes.
+template <int KB>
+constexpr int fp_smem_bytes() {
+  return (kFlRows * 272 * 4 > kFlStages * kFlRows * 128 ? kFlRows * 272 * 4
+                                                        : kFlStages * kFlRows * 128) +
+         kFlRows * 16 * 8 + kFlRows * KB * 8;
+}
+
+template <int TPW, int KB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_front_prefill(
+    const GemmArgs p, const FrontPrefill f) {
+  constexpr int FT = kFlRows * 272 * 4 > kFlStages * kFlRows * 128 ? kFlRows * 272 * 4
+                                                                  : kFlStages * kFlRows * 128;
+  __shared__ __attribute__((aligned(1024))) uint8_t smem[fp_smem_bytes<KB>()];
+  float* ft = reinterpret_cast<float*>(smem);                  // [64, ldf] logits
+  int32_t* s_d = reinterpret_cast<int32_t*>(smem + FT);        // [64, S <= 16] destinations
+  float* s_dc = reinterpret_cast<float*>(s_d + kFlRows * 16);  // and coefficients
+  int32_t* s_e = reinterpret_cast<int32_t*>(s_dc + kFlRows * 16);  // [64, K] sources
+  float* s_ew = reinterpret_cast<float*>(s_e + kFlRows * KB);      // and weights
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q = lane >> 4, l16 = lane & 15;
+  const int N = f.N, E = f.E, K = f.K, ldf = p.N_out;
+  const int chunk = blockIdx.x, t0 = chunk * kFlRows;
+  const int NT = (p.N_out + 15) >> 4;
+  f32x4 acc[TPW][4];
+  logits_mainloop<TPW>(p, smem, acc);
+  wait_lgkm0();
+  __syncthreads();  // every wave is past its last ring read
+  // 1 the logits tile (+ biases) into LDS, the router's columns to memory
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const int c = 16 * (wave + 4 * t) + 4 * q;
+    if (wave + 4 * t >= NT || c >= ldf) continue;  // ldf % 4 == 0
+    float bv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int n = c + i;
+      bv[i] = n < E ? p.bias[n] : p.bias2[n - E];
+    }
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      const int r = 16 * rt + l16;
+      const f32x4 v = acc[t][rt];
+      const f32x4 o = f32x4{v[0] + bv[0], v[1] + bv[1], v[2] + bv[2], v[3] + bv[3]};
+      *reinterpret_cast<f32x4*>(ft + r * ldf + c) = o;
+      if (c < E && t0 + r < N)  // E % 4 == 0: the four columns are all router logits
+        *reinterpret_cast<f32x4*>(f.logits + static_cast<int64_t>(t0 + r) * E + c) = o;
+    }
+  }
+  __syncthreads();
+  // 2 routing: 4 passes of 4 tokens per wave
+  const int e = lane & 15, le = e < E ? e : E - 1;
+#pragma unroll 1
+  for (int ps = 0; ps < 4; ++ps) {
+    const int tl = 16 * wave + 4 * ps + (lane >> 4);
+    const int t = t0 + tl;
+    const bool ok = t < N;
+    const float* row = ft + tl * ldf;
+    const float v = row[le];
+    const bool live = !f.active || f.active[ok ? t : N - 1] != 0;
+    uint64_t m = topk_seg<16>(v, t, ok, live, E, K, f.top_idx, f.top_w, f.tok_e, f.tok_ew, s_e,
+                              s_ew, tl);
+    if (!live) m = 0;  // a token that has left: no sources (tok_e holds -1)
+    float ev[KB];
+    int rw[KB];
+    bool lv[KB];
+#pragma unroll
+    for (int j = 0; j < KB; ++j) {  // the selected sources, ascending
+      const int sj = m ? __builtin_ctzll(m) : 0;
+      lv[j] = ok && j < K && m != 0;
+      m &= m - 1;
+      rw[j] = t * K + j;
+      ev[j] = row[E + sj * E + le];
+    }
+    topm_seg<16, KB>(ev, rw, lv, t, ok, E, f.M, f.S, f.slot_idx, f.slot_w, f.tok_d, f.tok_dc, s_d,
+                     s_dc, tl);
+  }
+  __syncthreads();
+  // 3 the chunk's ranks: wave 0 the expert plan, wave 1 the destination plan
+  if (wave == 0)
+    rank_chunk(s_e, s_ew, N, K, E, 0, t0, 0, 64, f.e_ccnt + chunk, f.e_cacnt + chunk, f.C,
+               f.e_tokrow, t0);
+  else if (wave == 1)
+    rank_chunk(s_d, s_dc, N, f.S, E, 1, t0, 0, 64, f.d_ccnt + chunk, f.d_cacnt + chunk, f.C,
+               f.d_tokrow, t0);
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -179,6 +294,41 @@ int launch_front_logits(const GemmArgs& a, hipStream_t s) {
     case 4: hipLaunchKernelGGL(k_front_logits<4>, grid, block, 0, s, a); break;
     default: hipLaunchKernelGGL(k_front_logits<5>, grid, block, 0, s, a); break;
   }
+  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
+int launch_front_prefill(const GemmArgs& a, const FrontPrefill& f, hipStream_t s) {
+  if (a.fmt != SMOE_BF16 || a.epi != EPI_F32_BIAS || a.G != 0 || !a.A || !a.W || !a.W2 ||
+      !a.bias || !a.bias2 || a.K < 64 || a.K % 64 || a.lda % 8 || a.lda < a.K || a.ldw % 8 ||
+      a.ldw < a.K || a.ldw2 % 8 || a.ldw2 < a.K)
+    return SMOE_EINVAL;
+  if (f.E < 4 || f.E > 16 || f.E % 4 || a.N_out != f.E + f.E * f.E || a.n_split != f.E ||
+      a.single_rows != f.N || f.N < 1 || f.K < 1 || f.K > f.E || f.M < 1 || f.M > f.E ||
+      f.S < 1 || f.S > f.E || f.C != (f.N + kFlRows - 1) / kFlRows)
+    return SMOE_EINVAL;
+  if (!f.logits || !f.top_idx || !f.top_w || !f.tok_e || !f.tok_ew || !f.slot_idx || !f.slot_w ||
+      !f.tok_d || !f.tok_dc || !f.e_tokrow || !f.d_tokrow || !f.e_ccnt || !f.e_cacnt ||
+      !f.d_ccnt || !f.d_cacnt)
+    return SMOE_EINVAL;
+  if (!aligned16(a.A) || !aligned16(a.W) || !aligned16(a.W2) || !aligned16(f.logits))
+    return SMOE_EINVAL;
+  const int tpw = ((a.N_out + 15) / 16 + 3) / 4;
+  const dim3 grid(static_cast<unsigned>(f.C)), block(256);
+#define SMOE_FP(T, KB) hipLaunchKernelGGL((k_front_prefill<T, KB>), grid, block, 0, s, a, f)
+#define SMOE_FP_K(T)                 \
+  do {                               \
+    if (f.K <= 2) SMOE_FP(T, 2);     \
+    else if (f.K <= 4) SMOE_FP(T, 4); \
+    else SMOE_FP(T, 16);             \
+  } while (0)
+  switch (tpw) {  // E 4, 8, 12, 16: 20, 72, 156, 272 channels
+    case 1: SMOE_FP_K(1); break;
+    case 2: SMOE_FP_K(2); break;
+    case 3: SMOE_FP_K(3); break;
+    default: SMOE_FP_K(5); break;
+  }
+#undef SMOE_FP_K
+#undef SMOE_FP
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 

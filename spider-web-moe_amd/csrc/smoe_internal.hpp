@@ -133,13 +133,6 @@ int launch_gather_topm(const int32_t* src_idx, const int32_t* tok_e, const int32
 int launch_dest_coeffs(const int32_t* src_idx, const int32_t* eidx, const float* ew, int N, int K,
                        int M, int E, int S, int32_t* tok_d, float* tok_dc, hipStream_t s);
 size_t plan_scratch_bytes(int N, int G);
-// Prefill routing over the dense logits of launch_front_logits (E <= 16):
-// top-k, per-source top-m in slot order (rows t*K + j of slot_idx / slot_w
-// [N*K, M]) and the tokens' destination coefficients.
-int launch_route_dense(const float* front, int ldf, int N, int E, int K, int M, int S,
-                       float* logits, int32_t* top_idx, float* top_w, int32_t* tok_e,
-                       float* tok_ew, int32_t* slot_idx, float* slot_w, int32_t* tok_d,
-                       float* tok_dc, const int32_t* active, hipStream_t s);
 // One plan's operands for launch_plan2 (those of launch_plan), with an
 // optional payload of pay_m values per entry moved from slot order to the
 // plan rows by the scatter (first plan only).
@@ -156,11 +149,33 @@ struct PlanSpec {
   float* out_w = nullptr;
   int pay_m = 0;
 };
-// Two plans over the same N tokens in one rank, one scan and one scatter
-// launch (scratch: plan_scratch_bytes(N, a.G) + plan_scratch_bytes(N, b.G)).
-// Where launch_plan would take a one-workgroup form, the two run as two
-// launch_plan calls (no payload then).
-int launch_plan2(const PlanSpec& a, const PlanSpec& b, int N, void* scratch, hipStream_t s);
+// The scan and scatter of two plans over the same N tokens whose chunk
+// counts and ranks are in place (launch_front_prefill): one launch each.
+// scratch: plan a's [G, C] count and positive-count matrices, then plan
+// b's (plan_scratch_bytes(N, a.G) + plan_scratch_bytes(N, b.G)).
+int launch_plan2_finish(const PlanSpec& a, const PlanSpec& b, int N, void* scratch, hipStream_t s);
+// The prefill front's routing outputs (launch_front_prefill).
+struct FrontPrefill {
+  int N = 0, E = 0, K = 0, M = 0, S = 0, C = 0;  // C = ceil(N / 64) plan chunks
+  float* logits = nullptr;
+  int32_t* top_idx = nullptr;
+  float* top_w = nullptr;
+  int32_t* tok_e = nullptr;
+  float* tok_ew = nullptr;
+  int32_t* slot_idx = nullptr;  // per-source edges in slot order [N*K, M]
+  float* slot_w = nullptr;
+  int32_t* tok_d = nullptr;
+  float* tok_dc = nullptr;
+  int32_t* e_tokrow = nullptr;  // the entries' ranks within their chunk (plan scratch)
+  int32_t* d_tokrow = nullptr;
+  int32_t *e_ccnt = nullptr, *e_cacnt = nullptr, *d_ccnt = nullptr, *d_cacnt = nullptr;
+  const int32_t* active = nullptr;
+};
+// Prefill steps at E <= 16 (E % 4 == 0): the logits GEMM over [router | every
+// edge generator row] (a: A, W = router, W2 = edge generator rows, n_split
+// = E, bias / bias2, N_out = E + E*E), then in the same workgroups top-k,
+// per-source top-m, destination coefficients and both plans' chunk ranks.
+int launch_front_prefill(const GemmArgs& a, const FrontPrefill& f, hipStream_t s);
 int launch_plan(const int32_t* tok_g, const float* tok_w, int N, int S, int G, int drop_nonpos,
                 int32_t* cnt, int32_t* acnt, int32_t* off, int32_t* rows, float* roww,
                 int32_t* tokrow, void* scratch, hipStream_t s);

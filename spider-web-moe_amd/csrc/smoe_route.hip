@@ -21,80 +21,14 @@
 #include "smoe_internal.hpp"
 #include "smoe_plan64.hpp"
 #include "smoe_rows.hpp"
+#include "smoe_routing.hpp"
 
 namespace smoe {
 
-constexpr int kBig = 1 << 20;
 constexpr int kPlanMaxGroups = 256;  // experts / destinations a block takes
 
 // ------------------------------------------------------------ router ----
-// Segment of token t (lane e of the segment: expert e, logit v, -inf past
-// E); tokens with !ok compute but store nothing.  tok_e2 / tok_ew2 (may be
-// null) receive a second copy of tok_e / tok_ew (indexed t * K + slot).
-// The K loop stays rolled: unrolled copies overflow the instruction cache of
-// the single-workgroup front, which runs each instruction a few times only.
-// p of the selected expert is recomputed from its logit (the same ops on the
-// same value as p itself).
-// live == false (a token that has left the orbit under an exit gate): the
-// token's tok_e / tok_ew slots are all -1 / 0, so every plan, the edge
-// stages and the expert GEMMs skip it; top_idx / top_w are still written.
-// Returns the segment's mask of selected experts (bit e = expert e).
-template <int SEG>
-__device__ __forceinline__ uint64_t topk_seg(float v, int t, bool ok, bool live, int E, int K,
-                                         int32_t* __restrict__ top_idx, float* __restrict__ top_w,
-                                         int32_t* __restrict__ tok_e, float* __restrict__ tok_ew,
-                                         int32_t* tok_e2, float* tok_ew2) {
-  const int lane = threadIdx.x & 63;
-  const int e = lane & (SEG - 1), sbase = lane - e;
-  const bool in = e < E;
-  v = in ? v : -INFINITY;
-  const float mx = seg_max<SEG>(v);
-  const float ex = in ? expf(v - mx) : 0.f;
-  const float sum = seg_sum<SEG>(ex);
-  const float p = ex / sum;
-  bool sel = false;
-  float psum = 0.f, slot_p = 0.f;
-  int slot_i = 0;
-#pragma unroll 1
-  for (int j = 0; j < K; ++j) {
-    float cv = (in && !sel) ? v : -INFINITY;
-    int ci = (in && !sel) ? e : kBig;
-    seg_argmax<SEG>(cv, ci);
-    const float pj = expf(cv - mx) / sum;
-    sel = sel || e == ci;
-    slot_p = e == j ? pj : slot_p;
-    slot_i = e == j ? ci : slot_i;
-    psum += pj;  // slot order, as torch sums the k values
-  }
-  const float denom = fmaxf(psum, 1e-9f);
-  if (ok && e < K) {
-    top_idx[static_cast<int64_t>(t) * K + e] = slot_i;
-    top_w[static_cast<int64_t>(t) * K + e] = slot_p / denom;
-  }
-  // distinct experts of the token in ascending order (lane order)
-  const uint64_t segm = SEG == 64 ? ~0ull : ((1ull << SEG) - 1);
-  const uint64_t m = (__ballot(sel) >> sbase) & segm;
-  if (!tok_e) return m;  // top-k only (the decode front: its plan kernel sorts the sources)
-  if (ok && live && sel) {
-    const int rank = __popcll(m & ((1ull << e) - 1));
-    tok_e[static_cast<int64_t>(t) * K + rank] = e;
-    tok_ew[static_cast<int64_t>(t) * K + rank] = p / denom;
-    if (tok_e2) {
-      tok_e2[t * K + rank] = e;
-      tok_ew2[t * K + rank] = p / denom;
-    }
-  }
-  if (ok && !live && e < K) {
-    tok_e[static_cast<int64_t>(t) * K + e] = -1;
-    tok_ew[static_cast<int64_t>(t) * K + e] = 0.f;
-    if (tok_e2) {
-      tok_e2[t * K + e] = -1;
-      tok_ew2[t * K + e] = 0.f;
-    }
-  }
-  return m;
-}
-
+// (topk_seg: smoe_routing.hpp)
 template <int SEG>
 __global__ __launch_bounds__(256) void k_route_topk(const float* __restrict__ logits, int N, int E,
                                                     int K, int32_t* __restrict__ top_idx,
@@ -265,73 +199,7 @@ int launch_merge_slots(const int32_t* idx, const float* w, int N, int K, int E, 
 }
 
 // ------------------------------------------------------------- edges ----
-// Segment of token t, lane d of the segment = destination d.  Source slot j
-// of the token has logit v[j] (lane d: the logit of edge s_j -> d), plan
-// row row[j] and is live when j < K and the slot holds a source (dead slots
-// compute on garbage and store nothing; tokens with !ok store nothing).
-// Writes top-m and softmax weights per source row (edge_idx / edge_w at the
-// plan row) and the token's destination coefficients (tok_d / tok_dc, and a
-// second copy in tok_d2 / tok_dc2 when not null, indexed t * S + slot).
-template <int SEG, int KB>
-__device__ __forceinline__ void topm_seg(const float (&v)[KB], const int (&row)[KB],
-                                         const bool (&live)[KB], int t, bool ok, int E, int M,
-                                         int S, int32_t* __restrict__ edge_idx,
-                                         float* __restrict__ edge_w, int32_t* __restrict__ tok_d,
-                                         float* __restrict__ tok_dc, int32_t* tok_d2,
-                                         float* tok_dc2) {
-  const int lane = threadIdx.x & 63;
-  const int d = lane & (SEG - 1), sbase = lane - d;
-  const bool in = d < E;
-  float c = 0.f;
-#pragma unroll
-  for (int j = 0; j < KB; ++j) {
-    if (!__ballot(live[j])) continue;  // uniform (sources are packed first)
-    const float vj = (in && live[j]) ? v[j] : -INFINITY;
-    bool sel = false;
-    float vmax = 0.f, den = 0.f, rec_v = 0.f;
-    int rec_i = 0;
-#pragma unroll 1
-    for (int i = 0; i < M; ++i) {  // rolled, as the top-k loop
-      float cv = (in && !sel) ? vj : -INFINITY;
-      int ci = (in && !sel) ? d : kBig;
-      seg_argmax<SEG>(cv, ci);
-      sel = sel || d == ci;
-      vmax = i == 0 ? cv : vmax;
-      rec_v = d == i ? cv : rec_v;
-      rec_i = d == i ? ci : rec_i;
-      den += expf(cv - vmax);  // softmax over the m values, slot order
-    }
-    if (live[j]) {
-      if (sel) c += expf(vj - vmax) / den;
-      if (ok && d < M) {
-        edge_idx[static_cast<int64_t>(row[j]) * M + d] = rec_i;
-        edge_w[static_cast<int64_t>(row[j]) * M + d] = expf(rec_v - vmax) / den;
-      }
-    }
-  }
-  const bool nz = in && c != 0.f;
-  const uint64_t segm = SEG == 64 ? ~0ull : ((1ull << SEG) - 1);
-  const uint64_t m = (__ballot(nz) >> sbase) & segm;
-  const int cnt = __popcll(m);
-  if (ok && nz) {
-    const int rank = __popcll(m & ((1ull << d) - 1));
-    tok_d[static_cast<int64_t>(t) * S + rank] = d;
-    tok_dc[static_cast<int64_t>(t) * S + rank] = c;
-    if (tok_d2) {
-      tok_d2[t * S + rank] = d;
-      tok_dc2[t * S + rank] = c;
-    }
-  }
-  if (ok && d >= cnt && d < S) {
-    tok_d[static_cast<int64_t>(t) * S + d] = -1;
-    tok_dc[static_cast<int64_t>(t) * S + d] = 0.f;
-    if (tok_d2) {
-      tok_d2[t * S + d] = -1;
-      tok_dc2[t * S + d] = 0.f;
-    }
-  }
-}
-
+// (topm_seg: smoe_routing.hpp)
 // The segment's KB source slots (KB >= K, a compile-time bucket): their
 // sources and plan rows (every lane reads the same entries, one load each),
 // then all their logit rows at once (rows in expert-plan order; slots past K
@@ -608,96 +476,7 @@ int launch_dest_coeffs(const int32_t* src_idx, const int32_t* eidx, const float*
 }
 
 // -------------------------------------------------------------- plan ----
-// Entries: tok_g [N,S] and tok_w [N,S], S <= 256.  A token's valid entries
-// are the prefix of strictly ascending groups in [0, G); from the first
-// entry that is not greater than the previous one or not in [0, G) on, the
-// row is padding (the producers write the token's groups ascending followed
-// by -1 pads).  A valid entry is kept when !drop_nonpos || w > 0.
-//
-// Tokens are cut into chunks of 64 (one wave, one token per lane) and groups
-// into windows of at most 64.
-//   rank:    one wave per (chunk, window): each lane turns its token's
-//            entries into bit masks over the window (present / kept /
-//            positive weight); one ballot per group gives the chunk's count
-//            (kept in the lane of that group) and each kept entry's rank
-//            among the chunk's earlier tokens
-//   scan:    one wave per group: exclusive scan of the chunk counts
-//   scatter: group offsets by a workgroup scan of the group totals, then
-//            row = off[g] + chunk prefix + rank -> rows / row_w / tok_row
-// Token order inside a group is preserved (stable) and no atomics are used,
-// so the plan is bit-exact run to run.
-constexpr int kPlanMaxG = 256;
-constexpr int kPlanMaxS = 256;
-
-// One wave ranks tokens [t0, t0 + 64) for groups [g0, g0 + win) (win <= 64):
-// cnt[g * cs] / acnt[g * cs] get the chunk's kept / positive-weight counts,
-// tokrow the rank of each kept entry among the chunk's earlier tokens and -1
-// for every other entry (the g0 == 0 wave writes the padding entries).
-// acnt is only counted when drop == 0 (otherwise it equals cnt).
-template <typename P>
-__device__ __forceinline__ void rank_chunk(const int32_t* __restrict__ tok_g,
-                                           const float* __restrict__ tok_w, int N, int S, int G,
-                                           int drop, int t0, int g0, int win, P cnt, P acnt,
-                                           int cs, int32_t* __restrict__ tokrow) {
-  const int lane = threadIdx.x & 63;
-  const int t = t0 + lane;
-  const bool valid = t < N;
-  const int nb = G - g0 < win ? G - g0 : win;
-  const int64_t e0 = static_cast<int64_t>(t) * S;
-  uint64_t gm = 0, km = 0, am = 0;
-  int below = 0;  // valid entries with a group < g0
-  if (valid) {
-    int prev = -1;
-    bool open = true;
-    for (int j0 = 0; j0 < S; j0 += 8) {
-      int gv[8];
-      float wv[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {  // unconditional (clamped) loads: issued together
-        const int jj = j0 + u < S ? j0 + u : S - 1;
-        gv[u] = tok_g[e0 + jj];
-        wv[u] = tok_w[e0 + jj];
-      }
-#pragma unroll
-      for (int u = 0; u < 8; ++u) gv[u] = j0 + u < S ? gv[u] : -1;
-#pragma unroll
-      for (int u = 0; u < 8; ++u) {  // branch-free, so no load is sunk behind a branch
-        const int g = gv[u];
-        open = open && g > prev && g < G;  // g > prev >= -1, so g >= 0
-        prev = open ? g : prev;
-        below += (open && g < g0) ? 1 : 0;
-        const int b = g - g0;
-        const uint64_t bit = (open && b >= 0 && b < nb) ? (1ull << (b & 63)) : 0ull;
-        const bool pos = wv[u] > 0.f;
-        gm |= bit;
-        km |= (!drop || pos) ? bit : 0ull;
-        am |= pos ? bit : 0ull;
-        if (!open && g0 == 0 && j0 + u < S) tokrow[e0 + j0 + u] = -1;
-      }
-    }
-  }
-  int mycnt = 0, myacnt = 0;
-  for (int b = 0; b < nb; ++b) {
-    const uint64_t bit = 1ull << b;
-    const uint64_t m = __ballot((km & bit) != 0);
-    mycnt = lane == b ? static_cast<int>(__popcll(m)) : mycnt;
-    if (!drop) {
-      const uint64_t ma = __ballot((am & bit) != 0);
-      myacnt = lane == b ? static_cast<int>(__popcll(ma)) : myacnt;
-    }
-    if (gm & bit) {
-      const int j = below + static_cast<int>(__popcll(gm & (bit - 1)));
-      const int r = __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(m >> 32),
-                                              __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(m), 0));
-      tokrow[e0 + j] = (km & bit) ? r : -1;
-    }
-  }
-  if (lane < nb) {
-    cnt[(g0 + lane) * cs] = mycnt;
-    acnt[(g0 + lane) * cs] = drop ? mycnt : myacnt;
-  }
-}
-
+// (the plan's outline and rank_chunk: smoe_routing.hpp)
 // Scatter of one token: row = goff[g] + base[g * bs] + rank (group offset,
 // the chunk's prefix inside the group, the rank inside the chunk).
 template <typename P>
@@ -1058,82 +837,17 @@ int launch_plan(const int32_t* tok_g, const float* tok_w, int N, int S, int G, i
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 
-// ------------------------------------------- prefill front routing ----
-// Routing over the dense logits of k_front_logits (front: f32 [N, ldf],
-// router logits in columns [0, E), the edge logits of source s in columns
-// E + s E .. E + s E + E - 1), one segment of 16 lanes per token (E <= 16):
-// the router top-k of topk_seg, then top-m (topm_seg) over the edge logits
-// of each selected source, read from the token's own row, so no expert plan
-// is needed first.  The sources go in ascending order, as the expert plan
-// orders them; their edges go to slot rows t * K + j of slot_idx / slot_w
-// [N*K, M], which the expert plan's scatter (launch_plan2) moves to the plan
-// rows.  Also writes logits [N, E] (the statistics read them).
-template <int KB>
-__global__ __launch_bounds__(256) void k_route_dense(
-    const float* __restrict__ front, int ldf, int N, int E, int K, int M, int S,
-    float* __restrict__ logits, int32_t* __restrict__ top_idx, float* __restrict__ top_w,
-    int32_t* __restrict__ tok_e, float* __restrict__ tok_ew, int32_t* __restrict__ slot_idx,
-    float* __restrict__ slot_w, int32_t* __restrict__ tok_d, float* __restrict__ tok_dc,
-    const int32_t* __restrict__ active) {
-  constexpr int SEG = 16, TPW = 64 / SEG;
-  const int lane = threadIdx.x & 63;
-  const int t0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * TPW;
-  if (t0 >= N) return;  // wave-uniform
-  const int e = lane & (SEG - 1);
-  const int le = e < E ? e : E - 1;
-  const int t = t0 + lane / SEG;
-  const bool ok = t < N;
-  const float* row = front + static_cast<int64_t>(ok ? t : N - 1) * ldf;
-  const float v = row[le];
-  const bool live = !active || active[ok ? t : N - 1] != 0;
-  if (ok && e < E) logits[static_cast<int64_t>(t) * E + e] = v;
-  uint64_t m = topk_seg<SEG>(v, t, ok, live, E, K, top_idx, top_w, tok_e, tok_ew, nullptr, nullptr);
-  if (!live) m = 0;  // a token that has left: no sources (tok_e holds -1)
-  float ev[KB];
-  int rw[KB];
-  bool lv[KB];
-#pragma unroll
-  for (int j = 0; j < KB; ++j) {  // the selected sources, ascending
-    const int sj = m ? __builtin_ctzll(m) : 0;
-    lv[j] = ok && j < K && m != 0;
-    m &= m - 1;
-    rw[j] = t * K + j;
-    ev[j] = row[E + sj * E + le];
-  }
-  topm_seg<SEG, KB>(ev, rw, lv, t, ok, E, M, S, slot_idx, slot_w, tok_d, tok_dc, nullptr, nullptr);
-}
-
-int launch_route_dense(const float* front, int ldf, int N, int E, int K, int M, int S,
-                       float* logits, int32_t* top_idx, float* top_w, int32_t* tok_e,
-                       float* tok_ew, int32_t* slot_idx, float* slot_w, int32_t* tok_d,
-                       float* tok_dc, const int32_t* active, hipStream_t s) {
-  if (E < 1 || E > 16 || K < 1 || K > E || K > 16 || M < 1 || M > E || S < 1 || S > 64 ||
-      ldf < E + E * E || !front)
-    return SMOE_EINVAL;
-  if (N <= 0) return SMOE_OK;
-  const dim3 grid((N + 15) / 16), block(256);
-#define SMOE_ROUTE_DENSE(KB)                                                                     \
-  hipLaunchKernelGGL((k_route_dense<KB>), grid, block, 0, s, front, ldf, N, E, K, M, S, logits,  \
-                     top_idx, top_w, tok_e, tok_ew, slot_idx, slot_w, tok_d, tok_dc, active)
-  if (K <= 1) SMOE_ROUTE_DENSE(1);
-  else if (K <= 2) SMOE_ROUTE_DENSE(2);
-  else if (K <= 4) SMOE_ROUTE_DENSE(4);
-  else if (K <= 8) SMOE_ROUTE_DENSE(8);
-  else SMOE_ROUTE_DENSE(16);
-#undef SMOE_ROUTE_DENSE
-  return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
-}
-
-// Two plans (the expert plan and the destination plan of one loop) in one
-// set of rank / scan / scatter launches: each launch's workgroups are split
-// between the plans, which use the same device code as launch_plan (so the
-// same results).  The first plan may carry a payload: pay_m values per entry
-// (slot order, entry (t, j) at (t * S + j) * pay_m) that its scatter copies
-// to the entry's plan row (row * pay_m) — the per-source edges.
+// The scan and scatter of two plans (the expert plan and the destination
+// plan of one loop) whose chunk ranks are in place, one launch each: each
+// launch's workgroups are split between the plans, which use the same device
+// code as launch_plan (so the same results).  The first plan may carry a
+// payload: pay_m values per entry (slot order, entry (t, j) at
+// (t * S + j) * pay_m) that its scatter copies to the entry's plan row
+// (row * pay_m) — the per-source edges.
 struct Plan2 {
   const int32_t* tok_g;
   const float* tok_w;
-  int S, G, drop, W;
+  int S, G, drop;
   int32_t *cnt, *acnt, *off, *rows;
   float* roww;
   int32_t* tokrow;
@@ -1144,18 +858,6 @@ struct Plan2 {
   float* out_w;
   int pay_m;
 };
-
-__global__ __launch_bounds__(256) void k_plan2_rank(const Plan2 a, const Plan2 b, int N, int C) {
-  int item = blockIdx.x * 4 + (threadIdx.x >> 6);
-  const bool second = item >= C * a.W;  // wave-uniform
-  const Plan2& p = second ? b : a;
-  if (second) item -= C * a.W;
-  if (item >= C * p.W) return;
-  const int win = (p.G + p.W - 1) / p.W;
-  const int chunk = item / p.W, g0 = (item % p.W) * win;
-  rank_chunk(p.tok_g, p.tok_w, N, p.S, p.G, p.drop, chunk * 64, g0, win, p.ccnt + chunk,
-             p.cacnt + chunk, C, p.tokrow);
-}
 
 __global__ __launch_bounds__(64) void k_plan2_scan(const Plan2 a, const Plan2 b, int C) {
   const bool second = static_cast<int>(blockIdx.x) >= a.G;
@@ -1187,27 +889,12 @@ __global__ __launch_bounds__(256) void k_plan2_scatter(const Plan2 a, const Plan
   }
 }
 
-namespace {
-int plan_windows(int C, int G) {  // as launch_plan: about 256 rank waves
-  int W = (G + 63) / 64;
-  while (C * W < 256 && (G + W - 1) / W > 8) W *= 2;
-  return W;
-}
-}  // namespace
-
-int launch_plan2(const PlanSpec& pa, const PlanSpec& pb, int N, void* scratch, hipStream_t s) {
+int launch_plan2_finish(const PlanSpec& pa, const PlanSpec& pb, int N, void* scratch,
+                        hipStream_t s) {
   for (const PlanSpec* p : {&pa, &pb})
     if (p->G < 1 || p->G > kPlanMaxG || p->S < 1 || p->S > kPlanMaxS) return SMOE_EINVAL;
-  if (N < 0) return SMOE_EINVAL;
+  if (N < 1 || !scratch || pb.pay_m > 0) return SMOE_EINVAL;  // the payload rides with the first plan
   const int C = (N + 63) / 64;
-  if (N <= 64 || C * pa.G <= 512 || C * pb.G <= 512) {  // launch_plan's one-workgroup forms
-    if (pa.pay_m > 0) return SMOE_EINVAL;
-    int rc = launch_plan(pa.tok_g, pa.tok_w, N, pa.S, pa.G, pa.drop, pa.cnt, pa.acnt, pa.off,
-                         pa.rows, pa.roww, pa.tokrow, scratch, s);
-    if (rc != SMOE_OK) return rc;
-    return launch_plan(pb.tok_g, pb.tok_w, N, pb.S, pb.G, pb.drop, pb.cnt, pb.acnt, pb.off,
-                       pb.rows, pb.roww, pb.tokrow, scratch, s);
-  }
   Plan2 a, b;
   int32_t* z = reinterpret_cast<int32_t*>(scratch);
   Plan2* dst[2] = {&a, &b};
@@ -1220,7 +907,6 @@ int launch_plan2(const PlanSpec& pa, const PlanSpec& pb, int N, void* scratch, h
     q.S = p.S;
     q.G = p.G;
     q.drop = p.drop;
-    q.W = plan_windows(C, p.G);
     q.cnt = p.cnt;
     q.acnt = p.acnt;
     q.off = p.off;
@@ -1236,9 +922,6 @@ int launch_plan2(const PlanSpec& pa, const PlanSpec& pb, int N, void* scratch, h
     q.out_w = p.out_w;
     q.pay_m = p.pay_m;
   }
-  if (b.pay_m > 0) return SMOE_EINVAL;  // the payload rides with the first plan
-  const int items = C * (a.W + b.W);
-  hipLaunchKernelGGL(k_plan2_rank, dim3((items + 3) / 4), dim3(256), 0, s, a, b, N, C);
   hipLaunchKernelGGL(k_plan2_scan, dim3(a.G + b.G), dim3(64), 0, s, a, b, C);
   hipLaunchKernelGGL(k_plan2_scatter, dim3(2 * ((N + 255) / 256)), dim3(256), 0, s, a, b, N, C);
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;

@@ -251,10 +251,11 @@ def test_block_small_steps_fused_front(n, e, k, m):
                                      (2800, 12, 3, 3), (4160, 32, 2, 2), (4096, 64, 2, 4)])
 def test_block_prefill_one_pass_logits(n, e, k, m):
     """Prefill steps at E <= 16 (N past the one-workgroup plans) run the
-    one-pass front: [router | every edge generator row] logits in one GEMM,
-    top-k and per-source top-m from each token's own row, and both plans in
-    one set of launches that also moves the edges to their plan rows.  At E
-    32 and 64 the router logits alone take the one-pass kernel.  Routing,
+    one-pass front: per 64-token chunk one workgroup computes the logits of
+    the router and every edge generator row, top-k, per-source top-m from
+    each token's own row and both plans' chunk ranks; one scan and one
+    scatter launch finish both plans and move the edges to their plan rows.
+    At E 32 and 64 the router logits alone take the one-pass kernel.  Routing,
     plans, edges, message, delta and outputs against the oracle for two
     loops (ragged N, k 1-3, m 2-4); the stage events show which stages ran.
     Weights N(0, 0.02) as in the workloads: with fan-in weights at hidden
@@ -273,7 +274,7 @@ def test_block_prefill_one_pass_logits(n, e, k, m):
     with torch.no_grad():
         wl.layer(wl.h, wl.x0, 0)
     ran = set(timer.stop())
-    want = {"front_gemm", "front_route"} if e <= 16 else {"router_gemm", "edge_logits"}
+    want = {"front_gemm"} if e <= 16 else {"router_gemm", "edge_logits"}
     assert ran == want, ran
     h = wl.h
     for r in range(2):
