@@ -449,18 +449,21 @@ def test_large_int4_experts_ragged_groups(act, n):
     assert (got - plain).abs().max() <= 2e-3 * scale, float((got - plain).abs().max() / scale)
 
 
-@pytest.mark.parametrize("act,group,sdt", [("gelu", 32, torch.float32), ("gelu", 128, torch.float16),
-                                           ("swiglu", 64, torch.float16)])
-def test_stream_int4_experts_ragged_passes(act, group, sdt):
+@pytest.mark.parametrize("act,group,sdt,h", [("gelu", 32, torch.float32, 384),
+                                             ("gelu", 128, torch.float16, 384),
+                                             ("swiglu", 64, torch.float16, 384),
+                                             ("gelu", 32, torch.float16, 448)])
+def test_stream_int4_experts_ragged_passes(act, group, sdt, h):
     """int4 experts at the weight-streaming GEMM's row counts (60 rows per
     expert on average) with groups of 0, 1, 18, 96, 97 and 150 rows: one
     pass of 1, 2 and 6 live 16-row tiles, two passes with a 1-row and a
     54-row second pass; U = 640 leaves half of the last 256-channel strip
-    (GELU up, 640 channels) past N_out, H = 384 half of the down GEMM's."""
+    (GELU up, 640 channels) past N_out, H = 384 half of the down GEMM's; H
+    = 448 gives the up GEMM an odd number of 64-k chunks (7)."""
     from spider_moe_amd.quant import interleave_gate_up, quantize_int4
     n8 = nat()
-    say("stream int4 experts", act, group, sdt)
-    h, u, e, k = 384, 640, 6, 2
+    say("stream int4 experts", act, group, sdt, h)
+    u, e, k = 640, 6, 2
     counts = [0, 1, 18, 96, 97, 150]
     flat = torch.tensor(sum(([x] * c for x, c in enumerate(counts)), []))
     n = flat.numel() // k
