@@ -19,6 +19,16 @@ namespace {
 constexpr int kFlRows = 64;   // rows (tokens) per workgroup
 constexpr int kFlStages = 6;  // activation ring: 64 rows x 64 k (8 KB) per stage
 constexpr int kFlMaxTpw = 5;  // 16-channel tiles per wave: N_out <= 320
+// Weight stages in flight per wave (register ring) and the activation DMA's
+// cache policy.  C1's prefill front (rocprof, same box): 38.9 us per launch
+// with 2 stages and the default policy, 40.0 with 3 stages and non-temporal
+// activations, 39.9 / 39.7 with either alone.
+constexpr int kFlAhead = 2;
+constexpr int kFlAPolicy = 0;
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
 
 // A workgroup owns 64 consecutive rows and every output channel; wave w
 // takes the 16-channel tiles w, w + 4, .. (TPW of them; a wave past the last
@@ -31,20 +41,21 @@ constexpr int kFlMaxTpw = 5;  // 16-channel tiles per wave: N_out <= 320
 //                kFlStages - 1 stages ahead
 //   weights:     global -> registers, each lane the two 16-byte pieces of
 //                its channel row at k 8q.. and 32 + 8q.. of a 64-k stage
-//                (the MFMA operand layout), two stages ahead; the weights
+//                (the MFMA operand layout), kFlAhead stages ahead; the weights
 //                (at most 320 rows) stay in the L2 that every workgroup
 //                reads them from
 //   MFMAs:       per stage and tile, two v_mfma_f32_16x16x32_bf16 per
 //                16-row tile (k 0-31 and 32-63)
-// Per stage the wave issues A(s + 5) and then W(s + 2); the wait for stage
-// s counts the loads issued after W(s) (those of one stage: 2 DMAs and
-// 2 TPW weight loads), and W(s) was issued after A(s), so one vmcnt wait
-// covers both.  One barrier per stage.
-template <int TPW>
+// Per stage the wave issues A(s + 5) and then W(s + D); the wait for stage
+// s counts the loads issued after W(s) (those of D - 1 stages: 2 DMAs and
+// 2 TPW weight loads each), and W(s) was issued after A(s), so one vmcnt
+// wait covers both.  One barrier per stage.
+template <int TPW, int D = kFlAhead>
 __device__ __forceinline__ void logits_mainloop(const GemmArgs& p, uint8_t* ring,
                                                 f32x4 (&acc)[TPW][4]) {
   constexpr int NS = kFlStages, STAGE = kFlRows * 128, PA = NS - 1;
-  constexpr int WAITN = 2 + 2 * TPW;
+  constexpr int WAITN = (D - 1) * (2 + 2 * TPW);
+  static_assert(PA >= D && WAITN < 64, "A(s) goes out before W(s); vmcnt range");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int q = lane >> 4, l16 = lane & 15;
   const int N = p.single_rows, m0 = blockIdx.x * kFlRows;
@@ -79,9 +90,10 @@ __device__ __forceinline__ void logits_mainloop(const GemmArgs& p, uint8_t* ring
 #pragma unroll
     for (int j = 0; j < 2; ++j)
       __builtin_amdgcn_global_load_lds((gbl_vptr)(asrc[j] + sc * 64),
-                                       (lds_vptr)(base + (4 * j + wave) * 1024), 16, 0, 0);
+                                       (lds_vptr)(base + (4 * j + wave) * 1024), 16, 0,
+                                       kFlAPolicy);
   };
-  u32x4 wa[2][TPW], wb[2][TPW];
+  u32x4 wa[D][TPW], wb[D][TPW];
   auto fetch_w = [&](int d, int s) {  // register slot d <- stage s (clamped)
     const int k0 = 64 * min(s, KS - 1);
 #pragma unroll
@@ -94,12 +106,14 @@ __device__ __forceinline__ void logits_mainloop(const GemmArgs& p, uint8_t* ring
   for (int t = 0; t < TPW; ++t)
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) acc[t][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  // prologue, in the order the waits assume: A(0), W(0), A(1..PA-1), W(1)
-  issue_a(0);
-  fetch_w(0, 0);
+  // prologue, in the order the waits assume: A(0), W(0), .., A(D-1), W(D-1), A(D..PA-1)
 #pragma unroll
-  for (int s = 1; s < PA; ++s) issue_a(s);
-  fetch_w(1, 1);
+  for (int s = 0; s < D; ++s) {
+    issue_a(s);
+    fetch_w(s, s);
+  }
+#pragma unroll
+  for (int s = D; s < PA; ++s) issue_a(s);
   auto step = [&](int d, int s) {
     wait_vmcnt<WAITN>();  // A(s) and W(s) have landed (this wave's part)
     wait_lgkm0();         // and this wave's reads of stage s - 1 are done
@@ -122,14 +136,15 @@ __device__ __forceinline__ void logits_mainloop(const GemmArgs& p, uint8_t* ring
         acc[t][rt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
             __builtin_bit_cast(bf16x8, wb[d][t]), ahi[rt], acc[t][rt], 0, 0, 0);
       }
-    fetch_w(d, s + 2);
+    fetch_w(d, s + D);
   };
   int s0 = 0;
-  for (; s0 + 2 <= KS; s0 += 2) {  // stage s in register slot s % 2
-    step(0, s0);
-    step(1, s0 + 1);
-  }
-  if (s0 < KS) step(0, s0);  // odd KS: the last stage (even, slot 0)
+  for (; s0 + D <= KS; s0 += D)  // stage s in register slot s % D
+#pragma unroll
+    for (int d = 0; d < D; ++d) step(d, s0 + d);
+#pragma unroll
+  for (int d = 0; d + 1 < D; ++d)  // the last KS % D stages
+    if (s0 + d < KS) step(d, s0 + d);
   wait_vmcnt<0>();  // the clamped refills past the end have landed before the workgroup ends
 }
 
@@ -269,10 +284,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
                f.d_tokrow, t0);
 }
 
-bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
-
-}  // namespace
-
 int launch_front_logits(const GemmArgs& a, hipStream_t s) {
   if (a.fmt != SMOE_BF16 || a.epi != EPI_F32_BIAS || a.G != 0 || a.single_rows < 1 || !a.A ||
       !a.W || !a.out || a.N_out <= 0 || a.K < 64)
@@ -288,11 +299,11 @@ int launch_front_logits(const GemmArgs& a, hipStream_t s) {
   if (tpw > kFlMaxTpw) return SMOE_EUNSUPPORTED;
   const dim3 grid(static_cast<unsigned>((a.single_rows + kFlRows - 1) / kFlRows)), block(256);
   switch (tpw) {
-    case 1: hipLaunchKernelGGL(k_front_logits<1>, grid, block, 0, s, a); break;
-    case 2: hipLaunchKernelGGL(k_front_logits<2>, grid, block, 0, s, a); break;
-    case 3: hipLaunchKernelGGL(k_front_logits<3>, grid, block, 0, s, a); break;
-    case 4: hipLaunchKernelGGL(k_front_logits<4>, grid, block, 0, s, a); break;
-    default: hipLaunchKernelGGL(k_front_logits<5>, grid, block, 0, s, a); break;
+    case 1: SMOE_LAUNCH(k_front_logits<1>, grid, block, 0, s, a); break;
+    case 2: SMOE_LAUNCH(k_front_logits<2>, grid, block, 0, s, a); break;
+    case 3: SMOE_LAUNCH(k_front_logits<3>, grid, block, 0, s, a); break;
+    case 4: SMOE_LAUNCH(k_front_logits<4>, grid, block, 0, s, a); break;
+    default: SMOE_LAUNCH(k_front_logits<5>, grid, block, 0, s, a); break;
   }
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
@@ -314,7 +325,7 @@ int launch_front_prefill(const GemmArgs& a, const FrontPrefill& f, hipStream_t s
     return SMOE_EINVAL;
   const int tpw = ((a.N_out + 15) / 16 + 3) / 4;
   const dim3 grid(static_cast<unsigned>(f.C)), block(256);
-#define SMOE_FP(T, KB) hipLaunchKernelGGL((k_front_prefill<T, KB>), grid, block, 0, s, a, f)
+#define SMOE_FP(T, KB) SMOE_LAUNCH((k_front_prefill<T, KB>), grid, block, 0, s, a, f)
 #define SMOE_FP_K(T)                 \
   do {                               \
     if (f.K <= 2) SMOE_FP(T, 2);     \
