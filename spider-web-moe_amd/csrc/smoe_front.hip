@@ -25,6 +25,7 @@ constexpr int kFlMaxTpw = 5;  // 16-channel tiles per wave: N_out <= 320
 // activations, 39.9 / 39.7 with either alone.
 constexpr int kFlAhead = 2;
 constexpr int kFlAPolicy = 0;
+constexpr int kFpWaves = 8;  // waves of the prefill front's workgroup (two per SIMD)
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
@@ -50,11 +51,13 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 // s counts the loads issued after W(s) (those of D - 1 stages: 2 DMAs and
 // 2 TPW weight loads each), and W(s) was issued after A(s), so one vmcnt
 // wait covers both.  One barrier per stage.
-template <int TPW, int D = kFlAhead>
+template <int TPW, int NW = 4, int D = kFlAhead>
 __device__ __forceinline__ void logits_mainloop(const GemmArgs& p, uint8_t* ring,
                                                 f32x4 (&acc)[TPW][4]) {
   constexpr int NS = kFlStages, STAGE = kFlRows * 128, PA = NS - 1;
-  constexpr int WAITN = (D - 1) * (2 + 2 * TPW);
+  constexpr int ALD = 8 / NW;  // activation DMAs per wave per stage (8 x 1 KB)
+  constexpr int WAITN = (D - 1) * (ALD + 2 * TPW);
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves");
   static_assert(PA >= D && WAITN < 64, "A(s) goes out before W(s); vmcnt range");
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int q = lane >> 4, l16 = lane & 15;
@@ -69,7 +72,7 @@ __device__ __forceinline__ void logits_mainloop(const GemmArgs& p, uint8_t* ring
     int prev = NT - 1;
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
-      const int tl = wave + 4 * t < NT ? wave + 4 * t : prev;
+      const int tl = wave + NW * t < NT ? wave + NW * t : prev;
       prev = tl;
       const int c = min(16 * tl + l16, p.N_out - 1);
       wrow[t] = c < nsplit ? W + static_cast<int64_t>(c) * p.ldw
@@ -77,10 +80,10 @@ __device__ __forceinline__ void logits_mainloop(const GemmArgs& p, uint8_t* ring
     }
   }
   const uint16_t* A = reinterpret_cast<const uint16_t*>(p.A);
-  const uint16_t* asrc[2];
+  const uint16_t* asrc[ALD];
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int r = 8 * (4 * j + wave) + (lane >> 3);
+  for (int j = 0; j < ALD; ++j) {
+    const int r = 8 * (NW * j + wave) + (lane >> 3);
     const int row = min(m0 + r, N - 1);  // rows past N: a valid row, never stored
     asrc[j] = A + static_cast<int64_t>(row) * p.lda + (sw_chunk<8>(r, lane & 7) << 3);
   }
@@ -88,9 +91,9 @@ __device__ __forceinline__ void logits_mainloop(const GemmArgs& p, uint8_t* ring
     const int sc = min(s, KS - 1);
     uint8_t* base = ring + (s % NS) * STAGE;
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < ALD; ++j)
       __builtin_amdgcn_global_load_lds((gbl_vptr)(asrc[j] + sc * 64),
-                                       (lds_vptr)(base + (4 * j + wave) * 1024), 16, 0,
+                                       (lds_vptr)(base + (NW * j + wave) * 1024), 16, 0,
                                        kFlAPolicy);
   };
   u32x4 wa[D][TPW], wb[D][TPW];
@@ -183,11 +186,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
 
 // The one-pass prefill front (E <= 16): a workgroup's 64 tokens are one
 // chunk of the dispatch plans, so after its logits GEMM the workgroup also
-// routes them and ranks them for both plans, with the logits in LDS:
+// routes them and ranks them for both plans, with the logits in LDS.  Eight
+// waves (two per SIMD, so one wave's barrier and LDS round trips overlap the
+// other's MFMAs: C1 38.7 -> 35.3 us per launch against four waves):
 //   1 the GEMM above over [router | every edge generator row]; the tile of
 //     [64, E + E*E] logits (+ biases) goes to LDS (over the ring) and the
 //     router logits also to `logits` (the statistics read them)
-//   2 wave w routes tokens 16 w .. 16 w + 15, a segment of 16 lanes per token
+//   2 wave w routes tokens 8 w .. 8 w + 7, a segment of 16 lanes per token
 //     (topk_seg, then topm_seg over the token's selected sources, ascending),
 //     writing what k_route_topk / k_edge_topm write (edges in slot order,
 //     rows t * K + j of slot_idx / slot_w) and copies of the tokens' sources
@@ -206,7 +211,7 @@ constexpr int fp_smem_bytes() {
 }
 
 template <int TPW, int KB>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) void k_front_prefill(
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2))) void k_front_prefill(
     const GemmArgs p, const FrontPrefill f) {
   constexpr int FT = kFlRows * 272 * 4 > kFlStages * kFlRows * 128 ? kFlRows * 272 * 4
                                                                   : kFlStages * kFlRows * 128;
@@ -222,14 +227,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
   const int chunk = blockIdx.x, t0 = chunk * kFlRows;
   const int NT = (p.N_out + 15) >> 4;
   f32x4 acc[TPW][4];
-  logits_mainloop<TPW>(p, smem, acc);
+  logits_mainloop<TPW, kFpWaves>(p, smem, acc);
   wait_lgkm0();
   __syncthreads();  // every wave is past its last ring read
   // 1 the logits tile (+ biases) into LDS, the router's columns to memory
 #pragma unroll
   for (int t = 0; t < TPW; ++t) {
-    const int c = 16 * (wave + 4 * t) + 4 * q;
-    if (wave + 4 * t >= NT || c >= ldf) continue;  // ldf % 4 == 0
+    const int c = 16 * (wave + kFpWaves * t) + 4 * q;
+    if (wave + kFpWaves * t >= NT || c >= ldf) continue;  // ldf % 4 == 0
     float bv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -247,11 +252,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1))) voi
     }
   }
   __syncthreads();
-  // 2 routing: 4 passes of 4 tokens per wave
+  // 2 routing: 2 passes of 4 tokens per wave
   const int e = lane & 15, le = e < E ? e : E - 1;
 #pragma unroll 1
-  for (int ps = 0; ps < 4; ++ps) {
-    const int tl = 16 * wave + 4 * ps + (lane >> 4);
+  for (int ps = 0; ps < kFlRows / (4 * kFpWaves); ++ps) {
+    const int tl = (kFlRows / kFpWaves) * wave + 4 * ps + (lane >> 4);
     const int t = t0 + tl;
     const bool ok = t < N;
     const float* row = ft + tl * ldf;
@@ -323,8 +328,8 @@ int launch_front_prefill(const GemmArgs& a, const FrontPrefill& f, hipStream_t s
     return SMOE_EINVAL;
   if (!aligned16(a.A) || !aligned16(a.W) || !aligned16(a.W2) || !aligned16(f.logits))
     return SMOE_EINVAL;
-  const int tpw = ((a.N_out + 15) / 16 + 3) / 4;
-  const dim3 grid(static_cast<unsigned>(f.C)), block(256);
+  const int tpw = ((a.N_out + 15) / 16 + kFpWaves - 1) / kFpWaves;
+  const dim3 grid(static_cast<unsigned>(f.C)), block(64 * kFpWaves);
 #define SMOE_FP(T, KB) SMOE_LAUNCH((k_front_prefill<T, KB>), grid, block, 0, s, a, f)
 #define SMOE_FP_K(T)                 \
   do {                               \
@@ -332,11 +337,10 @@ int launch_front_prefill(const GemmArgs& a, const FrontPrefill& f, hipStream_t s
     else if (f.K <= 4) SMOE_FP(T, 4); \
     else SMOE_FP(T, 16);             \
   } while (0)
-  switch (tpw) {  // E 4, 8, 12, 16: 20, 72, 156, 272 channels
+  switch (tpw) {  // E 4, 8, 12, 16: 20, 72, 156, 272 channels over 8 waves
     case 1: SMOE_FP_K(1); break;
     case 2: SMOE_FP_K(2); break;
-    case 3: SMOE_FP_K(3); break;
-    default: SMOE_FP_K(5); break;
+    default: SMOE_FP_K(3); break;
   }
 #undef SMOE_FP_K
 #undef SMOE_FP
