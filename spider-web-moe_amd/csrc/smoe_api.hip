@@ -233,9 +233,10 @@ int launch_router_logits(const GemmArgs& rg, hipStream_t s) {
   return launch_grouped_gemm(rg, s);
 }
 
-// bf16 decode steps the two-launch decode loop takes (k_decode_front +
-// k_decode_plan in place of the front GEMM, the routing workgroup and the
-// previous loop's epilogue); the early-exit gate keeps the general loop.
+// bf16 decode steps the fused decode loop takes (k_decode_front and the
+// plans beside the edge projection, in place of the front GEMM, the routing
+// workgroup and the previous loop's epilogue, whose early-exit gate the
+// next front takes).
 bool decode_ok(const smoe_block* b, int N) {
   const int E = b->E, S = (E < b->K * b->M) ? E : b->K * b->M;
   return b->act_dtype == SMOE_BF16 && b->experts.format != SMOE_F32 &&
@@ -439,7 +440,7 @@ int block_forward(const smoe_block* b, const void* h_in, const void* x0, void* h
   const int adt = b->act_dtype, fdt = l.ffn_dtype;
   const int gfmt = adt == SMOE_F32 ? SMOE_F32 : SMOE_BF16;  // router / edge weights
 
-  const bool dec = !gate && decode_ok(b, N);
+  const bool dec = decode_ok(b, N);
   const bool front = front_ok(b, N);
   const bool pfront = !dec && !front && prefill_front_ok(b, N);
   const int32_t* active = gate ? gate->active : nullptr;
@@ -482,6 +483,12 @@ int block_forward(const smoe_block* b, const void* h_in, const void* x0, void* h
       fa.top_w = at<float>(ws, l.top_w);
       fa.sel_idx = at<int32_t>(ws, l.sel_idx);
       fa.sel_w = at<float>(ws, l.sel_w);
+      if (gate) {  // the previous loop's exit decision, in this loop's front
+        fa.active = gate->active;
+        fa.loops = gate->loops;
+        fa.exit_wb = gate->exit_wb;
+        fa.threshold = gate->threshold;
+      }
       STAGE(SMOE_STAGE_FRONT_GEMM, launch_decode_front(fa, s), "decode front");
       cur = in_r;
       DecPlan dp;
@@ -512,6 +519,7 @@ int block_forward(const smoe_block* b, const void* h_in, const void* x0, void* h
       dp.d_rows = at<int32_t>(ws, l.d_rows);
       dp.d_roww = at<float>(ws, l.d_roww);
       dp.d_tokrow = at<int32_t>(ws, l.d_tokrow);
+      dp.active = active;
       // the edge projection with the plans beside it (one launch), where
       // its kernel takes the shape
       GemmArgs pg;

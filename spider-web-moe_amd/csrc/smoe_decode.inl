@@ -101,9 +101,20 @@ __global__ __launch_bounds__(1024) void k_decode_front(const DecFront a) {
   // so a wait for the token's operands does not wait for them (vmcnt counts
   // in issue order).
   __shared__ float lnp[PRO ? 2 * H : 1];
+  __shared__ int s_live[TT];  // the tile's tokens in orbit for this loop (the gate's)
   const int j = wave;
   const int t = t0 + j;
   const bool tv = j < TT && t < N;  // wave-uniform
+  // the gate: whether the token is in orbit on entry, its loop count, and
+  // (PRO with exit_wb) the exit head weights, all requested first
+  const bool gate = a.active != nullptr;
+  const bool gate_here = PRO && gate && a.exit_wb != nullptr;
+  int live_in = 1, loops_in = 0;
+  if (gate && tv) {
+    live_in = a.active[t];
+    if (gate_here && a.loops) loops_in = a.loops[t];
+  }
+  float ewv[PRO ? CPL : 1][8];
   float hv[CPL][8], xv[CPL][8];
   int te = -1, tr = 0;
   float tw = 0.f, pw = 1.f, pb = 0.f;
@@ -123,6 +134,12 @@ __global__ __launch_bounds__(1024) void k_decode_front(const DecFront a) {
       load8<SMOE_BF16>(a.h, o, hv[c]);
       load8<SMOE_BF16>(a.x0, o, xv[c]);
     }
+    if (gate_here)
+#pragma unroll
+      for (int c = 0; c < CPL; ++c) {
+        const int col = (lane + 64 * c) * 8;
+        load8<SMOE_F32>(a.exit_wb, col < H ? col : 0, ewv[c]);
+      }
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
   }
@@ -149,6 +166,7 @@ __global__ __launch_bounds__(1024) void k_decode_front(const DecFront a) {
     }
   }
   // 3 token `wave` of the tile -> LDS (bf16); rows past N are zeros
+  int live = live_in;  // in orbit for this loop's routing (after the gate)
   {
     float o[CPL][8];
 #pragma unroll
@@ -162,12 +180,17 @@ __global__ __launch_bounds__(1024) void k_decode_front(const DecFront a) {
         lnp[threadIdx.x] = pw;
         lnp[H + threadIdx.x] = pb;
       }
-      if (tv) {  // the previous loop's expert rows, then its epilogue's LayerNorm
+      if (tv && live_in) {  // the previous loop's expert rows, then its epilogue's LayerNorm
         const int my_row = (lane < a.K && te >= 0 && tw > 0.f) ? tr : -1;
         gather_add<CPL, SMOE_BF16>(a.y, H, my_row, __ballot(my_row >= 0), o);
       }
       __syncthreads();  // the LayerNorm parameters are in LDS
-      if (tv) {
+      if (tv && !live_in) {  // out of orbit: h passes through (k_epilogue's gate)
+#pragma unroll
+        for (int c = 0; c < CPL; ++c)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[c][i] = hv[c][i];
+      } else if (tv) {
         float gw[CPL][8], gb[CPL][8];
 #pragma unroll
         for (int c = 0; c < CPL; ++c) {
@@ -180,6 +203,25 @@ __global__ __launch_bounds__(1024) void k_decode_front(const DecFront a) {
           }
         }
         ln_row<CPL>(hv, xv, gw, gb, o, H, a.alpha, a.beta, a.eps, o);  // in place
+        if (gate_here) {  // k_epilogue's exit decision on the stored (bf16) row
+          float g = 0.f;
+#pragma unroll
+          for (int c = 0; c < CPL; ++c) {
+            const int col = (lane + 64 * c) * 8;
+            if (col < H)
+#pragma unroll
+              for (int i = 0; i < 8; ++i) g += bf2f(f2bf(o[c][i])) * ewv[c][i];
+          }
+          // a bf16 model's exit_head is a bf16 Linear: its output (the logit)
+          // is rounded to bf16 before the fp32 sigmoid (model.py:467)
+          const float z = bf2f(f2bf(wave_sum(g) + a.exit_wb[H]));
+          const bool out = 1.0f / (1.0f + expf(-z)) > a.threshold;
+          live = out ? 0 : 1;
+          if (strip == 0 && lane == 0) {
+            if (out) a.active[t] = 0;
+            if (a.loops) a.loops[t] = loops_in + 1;
+          }
+        }
       }
     } else if (tv) {
 #pragma unroll
@@ -202,6 +244,7 @@ __global__ __launch_bounds__(1024) void k_decode_front(const DecFront a) {
       }
     }
   }
+  if (j < TT && lane == 0) s_live[j] = live;
   lds_barrier();
   // 3 logits: this wave's k steps, then the waves' partials in wave order
   f32x4 acc[2 * ET];
@@ -250,10 +293,17 @@ __global__ __launch_bounds__(1024) void k_decode_front(const DecFront a) {
     const bool ok = t < N;
     const int ec = e < E ? e : 0;
     const float v = lt[0][j][ec];
-    const uint64_t m = topk_seg<SEG>(v, t, ok && !src, true, E, a.K, a.top_idx, a.top_w, nullptr,
-                                     nullptr, nullptr, nullptr);
+    const bool live_t = s_live[j] != 0;
+    uint64_t m = topk_seg<SEG>(v, t, ok && !src, live_t, E, a.K, a.top_idx, a.top_w, nullptr,
+                               nullptr, nullptr, nullptr);
+    if (!live_t) m = 0;  // out of orbit: no sources, so no strip writes its edges
     if (!src) {
       if (ok && e < E) a.logits[static_cast<int64_t>(t) * E + e] = v;
+      if (ok && !live_t)  // its selections select nothing (c[t, g] = 0 for every g)
+        for (int u = e; u < a.K * a.M; u += SEG) {
+          a.sel_idx[static_cast<int64_t>(t) * a.K * a.M + u] = 0;
+          a.sel_w[static_cast<int64_t>(t) * a.K * a.M + u] = 0.f;
+        }
     } else {
       const int s = strip - 1;
       const bool sel_src = (m >> s) & 1ull;

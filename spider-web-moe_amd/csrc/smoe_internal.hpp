@@ -255,6 +255,14 @@ struct DecFront {
   float* top_w = nullptr;
   int32_t* sel_idx = nullptr;  // [N, K, M] top-m destinations of each selected source
   float* sel_w = nullptr;      // their softmax weights
+  // the early-exit gate (ExitGate), or active null: tokens with active[t] ==
+  // 0 take no part in the loop (with y set, their h passes through); with y
+  // and exit_wb set, the previous loop's epilogue gate is taken here on the
+  // LayerNorm rows (k_epilogue's operations), updating active and loops
+  const float* exit_wb = nullptr;
+  float threshold = 0.f;
+  int32_t* active = nullptr;
+  int32_t* loops = nullptr;
 };
 // shapes the decode loop takes (else the general stages run)
 bool decode_front_fits(int N, int H, int E, int K, int M, int S, int ldw);
@@ -274,6 +282,7 @@ struct DecPlan {
           *d_tokrow = nullptr;
   float *tok_ew = nullptr, *e_roww = nullptr, *edge_w = nullptr, *tok_dc = nullptr,
         *d_roww = nullptr;
+  const int32_t* active = nullptr;  // the early-exit gate's: tokens with 0 take no part
 };
 bool decode_plan_fits(const DecPlan& q);
 // k_decode_plan: the plans in one workgroup of their own

@@ -99,6 +99,7 @@ __device__ __forceinline__ void decode_plan_body(const DecPlan& q, uint8_t* lds)
   const bool tv = t < N;
   const int tc = tv ? t : 0;
   const int km = K * M;
+  const bool live = !q.active || q.active[tc] != 0;  // a token out of orbit: no sources
   if (wave == 0) {
     // the token's top-k sorted by expert (ids are distinct: rank = # smaller),
     // its sources' edges (in that order already) loaded alongside
@@ -116,7 +117,7 @@ __device__ __forceinline__ void decode_plan_body(const DecPlan& q, uint8_t* lds)
       ei[u] = q.sel_idx[tc * km + uu];
       ew[u] = q.sel_w[tc * km + uu];
     }
-    if (tv)
+    if (tv && live)
 #pragma unroll
       for (int j = 0; j < KB; ++j) {
         if (j >= K) break;
@@ -127,6 +128,13 @@ __device__ __forceinline__ void decode_plan_body(const DecPlan& q, uint8_t* lds)
         s_tw[t * K + rank] = tw[j];
         q.tok_e[t * K + rank] = ti[j];
         q.tok_ew[t * K + rank] = tw[j];
+      }
+    else if (tv)
+      for (int j = 0; j < K; ++j) {
+        s_te[t * K + j] = -1;
+        s_tw[t * K + j] = 0.f;
+        q.tok_e[t * K + j] = -1;
+        q.tok_ew[t * K + j] = 0.f;
       }
     plan64_wave(s_te, s_tw, N, K, E, 0, q.e_cnt, q.e_acnt, q.e_off, q.e_rows, q.e_roww, s_etr,
                 s_km, s_am, s_off);
@@ -157,7 +165,7 @@ __device__ __forceinline__ void decode_plan_body(const DecPlan& q, uint8_t* lds)
       for (int d = 0; d < E; ++d) crow[d] = 0.f;
 #pragma unroll
       for (int u = 0; u < KMB; ++u)
-        if (u < km) crow[ei[u]] += ew[u];
+        if (u < km && live) crow[ei[u]] += ew[u];
       int cnt = 0;
       for (int d = 0; d < E; ++d) {
         const float c = crow[d];
