@@ -481,6 +481,8 @@ def main():
                     help="only time the c1 prefill block with bf16, fp8 and int4 experts")
     ap.add_argument("--forge-fp8", action="store_true",
                     help="only time the Forge fp8 x fp8 GEMM (quantize_input=True) on four shapes")
+    ap.add_argument("--decode-exit", action="store_true",
+                    help="only time the c2 decode step with the early-exit gate (eager and graph)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain device copy of BYTES (to scale rocprof FETCH/WRITE_SIZE)")
     a = ap.parse_args()
@@ -505,6 +507,9 @@ def main():
         return
     if a.forge_fp8:
         print(json.dumps({"forge_fp8_gemm": run_forge_fp8(a.steps, a.warmup)}), flush=True)
+        return
+    if a.decode_exit:
+        print(json.dumps({"decode_exit": run_decode_exit(a.steps, a.warmup)}), flush=True)
         return
     names = [x for x in a.workloads.split(",") if x]
     results = {nm: run_workload(nm, a.steps, a.warmup) for nm in names}
