@@ -564,18 +564,25 @@ def test_stage_entries_compose_block_forward(spec):
 
 
 # ------------------------------------------------ early-exit decode ----
-EXIT_CASES = [dict(kind="bf16", tokens=64), dict(kind="bf16", tokens=300), dict(kind="f32", tokens=0)]
+EXIT_CASES = [dict(kind="bf16", tokens=64), dict(kind="bf16", tokens=300),
+              dict(kind="bf16", tokens=48, hid=512, e=32, k=4, m=2),
+              dict(kind="bf16", tokens=64, hid=256, e=64, k=2, m=4),
+              dict(kind="f32", tokens=0)]
+EXIT_IDS = lambda c: "-".join(str(c[x]) for x in ("kind", "tokens", "hid", "e", "k", "m") if x in c)
 
 
 def _exit_layer(case):
-    """bf16 SwiGLU blocks at N = 64 (fused routing front) and N = 300
-    (separate routing stages), and the reference fp32 golden block."""
+    """bf16 SwiGLU blocks at N <= 64 (the fused decode loop, whose next
+    loop's front takes the exit decision; E 16 / 32 / 64, so 16-, 32- and
+    64-lane routing segments) and N = 300 (separate routing stages), and the
+    reference fp32 golden block."""
     if case["kind"] == "f32":
         z, layer = _layer_from_golden("block_small")
         return layer, torch.from_numpy(z["loop0/in"]).to(dev), torch.from_numpy(z["x0"]).to(dev)
     from spider_moe_amd.workloads import make_block
-    wl = make_block("c1", tokens=case["tokens"], hidden_size=128, num_experts=16, top_k=2,
-                    edges_per_expert=2, expert_ffn_size=256, num_loops=3,
+    wl = make_block("c1", tokens=case["tokens"], hidden_size=case.get("hid", 128),
+                    num_experts=case.get("e", 16), top_k=case.get("k", 2),
+                    edges_per_expert=case.get("m", 2), expert_ffn_size=256, num_loops=3,
                     expert_activation="swiglu", experts="bf16")
     return wl.layer, wl.h, wl.x0
 
@@ -586,7 +593,7 @@ def _set_exit(layer, w, b):
         layer.exit_head.bias.fill_(b)
 
 
-@pytest.mark.parametrize("case", EXIT_CASES, ids=lambda c: f"{c['kind']}-{c['tokens']}")
+@pytest.mark.parametrize("case", EXIT_CASES, ids=EXIT_IDS)
 def test_exit_gate_forced_and_never(case):
     """exit bias +20: every token leaves after the first loop and keeps it
     (tests/test_early_exit_compaction.py:51-70); bias -20: the full loop run
@@ -610,7 +617,7 @@ def test_exit_gate_forced_and_never(case):
         assert bool((active == 1).all()) and bool((loops == r).all())
 
 
-@pytest.mark.parametrize("case", EXIT_CASES[:2], ids=lambda c: f"{c['kind']}-{c['tokens']}")
+@pytest.mark.parametrize("case", [c for c in EXIT_CASES if c["kind"] == "bf16"], ids=EXIT_IDS)
 def test_exit_gate_partial_teacher_forced(case):
     """A random exit_head: tokens leave at different loops.  Teacher-forced
     against the ungated block run loop by loop on every token: a token's
