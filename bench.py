@@ -55,8 +55,8 @@ GEMM_KERNEL = {
     ("c3", "up_gemm"): "k_gemm_ring<128,3,4> (bf16 GELU, LDS-DMA ring, 2 workgroups/CU)",
     ("c3", "down_gemm"): "k_gemm_pp<4,4,down,320> (bf16 weight tiles, 8-wave ping-pong)",
     ("c3", "edge_gemm"): "k_gemm_pp<4,4,rowscale,256> (bf16 weight tiles, 8-wave ping-pong)",
-    ("c4", "up_gemm"): "k_gemm_stream4<GELU,6,3> (int4 weight streaming, dequant beside the MFMAs, LDS-DMA ring, 2 workgroups/CU)",
-    ("c4", "down_gemm"): "k_gemm_stream4<down,6,3> (int4 weight streaming, dequant beside the MFMAs, 2 workgroups/CU)",
+    ("c4", "up_gemm"): "k_gemm_stream4<GELU,6,3,3> (int4 weight streaming, 192-channel strips, dequant beside the MFMAs, LDS-DMA ring, 2 workgroups/CU)",
+    ("c4", "down_gemm"): "k_gemm_stream4<down,6,3,4> (int4 weight streaming, 256-channel strips, dequant beside the MFMAs, 2 workgroups/CU)",
     ("c4", "edge_gemm"): "k_gemm_pp<4,4,rowscale,320> (bf16 weight tiles, 320-row tiles: one per destination)",
 }
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic.md")

@@ -1786,21 +1786,30 @@ __global__ __launch_bounds__(256, WGS) void k_gemm_stream(const GemmArgs p) {
 // live 16-row tiles of a pass is a template parameter (one instantiation per
 // count, chosen per pass), so tiles past the group's last row issue neither
 // MFMAs nor activation DMA, and the loop body has no branches to split it.
-// Waves whose 64 channels all lie past N_out skip the arithmetic.  Work
+// Waves whose channels all lie past N_out skip the arithmetic.  Work
 // split, ring, swizzles and XCD-aware workgroup order are those
 // of k_gemm_stream; the strip's group scales sit in an LDS table after the
 // ring, in the same LDS object (with a second LDS object the compiler waits
 // for every outstanding DMA before reads of the table, draining the ring's
-// prefetch).
-template <int EPI, int RT, int NS = 3>
+// prefetch).  A wave owns TN 16-channel tiles (a strip of 64 TN channels);
+// it brings its own channels' weights into the ring, WWB bytes per chunk in
+// 1 KB DMA instructions, the last one on the lanes it needs when TN is odd.
+// TN only decides which channels a wave holds: every output is summed in the
+// same order, so the bits do not depend on it.
+template <int EPI, int RT, int NS = 3, int TN = 4>
 __global__ __launch_bounds__(256, 2) void k_gemm_stream4(const GemmArgs p) {
-  constexpr int TN = 4, WB = 32, CPR = 2;  // int4: 32 B per channel per 64-k chunk
+  constexpr int WB = 32, CPR = 2;  // int4: 32 B per channel per 64-k chunk
+  constexpr int SW = 64 * TN;      // channels of a strip
   constexpr int ROWS = RT * 16;
-  constexpr int W_BYTES = 256 * WB, A_BYTES = ROWS * 128, STAGE = W_BYTES + A_BYTES;
-  constexpr int W_LD = W_BYTES / 4096;
+  constexpr int WWB = 16 * TN * WB;  // a wave's weight bytes per chunk
+  constexpr int W_BYTES = 4 * WWB, A_BYTES = ROWS * 128, STAGE = W_BYTES + A_BYTES;
+  constexpr int W_LD = (WWB + 1023) / 1024;                 // DMA instructions per wave
+  constexpr int W_TAIL = (WWB - 1024 * (W_LD - 1)) / 16;    // lanes of the last one
   constexpr int SC_BYTES = kStreamScaleMax * 4;
+  static_assert(TN == 3 || TN == 4, "48- or 64-channel waves");
   static_assert(RT % 2 == 0 && RT >= 4 && RT <= 6, "whole DMA instructions per wave");
   static_assert(NS * STAGE + SC_BYTES <= 80 * 1024, "two workgroups per CU");
+  static_assert(STAGE % 1024 == 0 && W_BYTES % 1024 == 0, "1 KB-aligned DMA bases");
   static_assert(EPI != EPI_SWIGLU || TN == 4, "SwiGLU pairs channel c with c + 32");
   __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * STAGE + SC_BYTES];
   float* sc = reinterpret_cast<float*>(ring + NS * STAGE);
@@ -1814,7 +1823,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream4(const GemmArgs p) {
     const int x = bid & 7, local = bid >> 3, base = T >> 3, rem = T & 7;
     const int logical = x * base + min(x, rem) + local;
     g = logical / S;
-    nb = (logical - g * S) * 256;
+    nb = (logical - g * S) * SW;
   }
   int r_lo, r_hi;
   if (p.G == 0) {
@@ -1837,7 +1846,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream4(const GemmArgs p) {
     const int pr = r_lo + r < r_hi ? r_lo + r : r_lo;
     arow0[j] = p.a_rows ? p.a_rows[pr] : pr;
   }
-  // the strip's group scales, channel-major [256][ng]: one contiguous run of
+  // the strip's group scales, channel-major [SW][ng]: one contiguous run of
   // the scale array (channels past N_out read the last channel's).  The
   // loads are unconditional (indices clamped) and converted only after the
   // last one is issued, so all are in flight at once; a guarded load with
@@ -1846,7 +1855,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream4(const GemmArgs p) {
     constexpr int SCJ = kStreamScaleMax / 256;
     float scv[SCJ];
     const int64_t sb = g * p.s_gstride + static_cast<int64_t>(nb) * ng;
-    const int last = (min(p.N_out, nb + 256) - nb) * ng - 1;
+    const int last = (min(p.N_out, nb + SW) - nb) * ng - 1;
     if (p.s_f16) {
       const _Float16* s16 = reinterpret_cast<const _Float16*>(p.S) + sb;
       _Float16 hv[SCJ];
@@ -1861,13 +1870,19 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream4(const GemmArgs p) {
     }
 #pragma unroll
     for (int j = 0; j < SCJ; ++j)
-      if (tid + 256 * j < 256 * ng) sc[tid + 256 * j] = scv[j];
+      if (tid + 256 * j < SW * ng) sc[tid + 256 * j] = scv[j];
   }
-  const bool live = nb + 64 * wave < p.N_out;  // wave-uniform: some channel of this wave is stored
+  const bool live = nb + 16 * TN * wave < p.N_out;  // wave-uniform: some channel of this wave is stored
+  // byte b of the strip's row-major [SW][WB] chunk goes to byte b of the
+  // ring slot's weight region.  Its first byte for DMA instruction j of this
+  // wave: 256 channels, KB 4 j + w; 192 channels, wave w brings bytes
+  // [w WWB, (w + 1) WWB) (lanes past the tail of the last instruction are
+  // never issued; their address is clamped all the same).
+  auto wdst = [&](int j) { return TN == 4 ? (4 * j + wave) * 1024 : wave * WWB + 1024 * j; };
   const uint8_t* wsrc[W_LD];
 #pragma unroll
   for (int j = 0; j < W_LD; ++j) {
-    const int b = (4 * j + wave) * 1024 + 16 * lane;
+    const int b = TN == 4 ? wdst(j) + 16 * lane : wave * WWB + min(1024 * j + 16 * lane, WWB - 16);
     const int row = b / WB, pc = (b % WB) >> 4;
     const int lc = sw_chunk<CPR>(row, pc);
     const int n = min(nb + row, p.N_out - 1);  // channels past N_out: loaded, never stored
@@ -1891,8 +1906,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream4(const GemmArgs p) {
         uint8_t* base = ring + (kc % NS) * STAGE;
 #pragma unroll
         for (int j = 0; j < W_LD; ++j)
-          __builtin_amdgcn_global_load_lds((gbl_vptr)(wsrc[j] + static_cast<int64_t>(kc) * WB),
-                                           (lds_vptr)(base + (4 * j + wave) * 1024), 16, 0, 0);
+          if (j + 1 < W_LD || W_TAIL == 64 || lane < W_TAIL)
+            __builtin_amdgcn_global_load_lds((gbl_vptr)(wsrc[j] + static_cast<int64_t>(kc) * WB),
+                                             (lds_vptr)(base + wdst(j)), 16, 0, 0);
 #pragma unroll
         for (int j = 0; j < A_LD; ++j)
           __builtin_amdgcn_global_load_lds((gbl_vptr)(asrc[j] + kc * 64),
@@ -1927,7 +1943,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream4(const GemmArgs p) {
         WRaw<SMOE_INT4> wr[TN];
 #pragma unroll
         for (int t = 0; t < TN; ++t) {
-          const int row = wave * 64 + t * 16 + l16;
+          const int row = wave * 16 * TN + t * 16 + l16;
           wr[t].a = *reinterpret_cast<const u32x2*>(sw + row * WB + (sw_chunk<CPR>(row, q >> 1) << 4) +
                                                     ((q & 1) << 3));
           wr[t].s = sc[row * ng + kg];
@@ -1954,7 +1970,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream4(const GemmArgs p) {
           whi = nhi;
         }
       }
-      // lane: channels nb + 64 wave + 16 t + 4 q + (0..3) of row m0 + 16 rt + l16.
+      // lane: channels nb + 16 TN wave + 16 t + 4 q + (0..3) of row m0 + 16 rt + l16.
       // Its bias values and row weights are loaded before any math (one
       // memory round trip), at clamped indices for rows / channels never
       // stored.
@@ -1963,7 +1979,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream4(const GemmArgs p) {
       f32x4 bq[TN];
 #pragma unroll
       for (int t = 0; t < TN; ++t) {
-        const int c = min(nb + wave * 64 + 16 * t + 4 * q, p.N_out - 4);
+        const int c = min(nb + wave * 16 * TN + 16 * t + 4 * q, p.N_out - 4);
         const int b0 = EPI == EPI_SWIGLU ? (c >> 6) * 32 + (c & 31) : c;
         bq[t] = f32x4{0.f, 0.f, 0.f, 0.f};
         if (EPI != EPI_ROWSCALE && (EPI != EPI_SWIGLU || t < 2) && p.bias)
@@ -1985,7 +2001,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_stream4(const GemmArgs p) {
           if (row >= r_hi) continue;
 #pragma unroll
           for (int t = 0; t < TN; ++t) {
-            const int c = nb + wave * 64 + 16 * t + 4 * q;
+            const int c = nb + wave * 16 * TN + 16 * t + 4 * q;
             if (c >= p.N_out || (EPI == EPI_SWIGLU && t >= 2)) continue;
             const f32x4 v = acc[t][rt];
             float o[4];
@@ -2432,18 +2448,41 @@ int launch_stream_fmt(const GemmArgs& a, hipStream_t s) {
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
 }
 
-template <int RT, int NS = 3>
+template <int RT, int NS = 3, int TN = 4>
 int launch_stream4(const GemmArgs& a, hipStream_t s) {
-  const dim3 grid((a.N_out + 255) / 256, a.G == 0 ? 1 : a.G), block(256);
+  const dim3 grid((a.N_out + 64 * TN - 1) / (64 * TN), a.G == 0 ? 1 : a.G), block(256);
   switch (a.epi) {
-    case EPI_F32_BIAS: SMOE_LAUNCH((k_gemm_stream4<EPI_F32_BIAS, RT, NS>), grid, block, 0, s, a); break;
-    case EPI_ROWSCALE: SMOE_LAUNCH((k_gemm_stream4<EPI_ROWSCALE, RT, NS>), grid, block, 0, s, a); break;
-    case EPI_GELU: SMOE_LAUNCH((k_gemm_stream4<EPI_GELU, RT, NS>), grid, block, 0, s, a); break;
-    case EPI_SWIGLU: SMOE_LAUNCH((k_gemm_stream4<EPI_SWIGLU, RT, NS>), grid, block, 0, s, a); break;
-    case EPI_DOWN: SMOE_LAUNCH((k_gemm_stream4<EPI_DOWN, RT, NS>), grid, block, 0, s, a); break;
+    case EPI_F32_BIAS: SMOE_LAUNCH((k_gemm_stream4<EPI_F32_BIAS, RT, NS, TN>), grid, block, 0, s, a); break;
+    case EPI_ROWSCALE: SMOE_LAUNCH((k_gemm_stream4<EPI_ROWSCALE, RT, NS, TN>), grid, block, 0, s, a); break;
+    case EPI_GELU: SMOE_LAUNCH((k_gemm_stream4<EPI_GELU, RT, NS, TN>), grid, block, 0, s, a); break;
+    case EPI_SWIGLU:
+      if constexpr (TN == 4) {
+        SMOE_LAUNCH((k_gemm_stream4<EPI_SWIGLU, RT, NS, TN>), grid, block, 0, s, a);
+        break;
+      }
+      return SMOE_EINVAL;
+    case EPI_DOWN: SMOE_LAUNCH((k_gemm_stream4<EPI_DOWN, RT, NS, TN>), grid, block, 0, s, a); break;
     default: return SMOE_EINVAL;
   }
   return hipGetLastError() == hipSuccess ? SMOE_OK : SMOE_EHIP;
+}
+
+// The int4 strip width: 256 channels (four 64-channel waves), or 192 where
+// that fills the two workgroup slots per CU in fewer rounds of less work
+// each (C4's up GEMM, N_out 1408 over 64 groups: 6 strips of 256 fill 384 of
+// 512 slots, where the 128 CUs holding two workgroups set the time; 8 strips
+// of 192 fill all 512 with three quarters of the work each).  The cost of a
+// width is its rounds of workgroups times the work of one.
+int stream4_tn(const GemmArgs& a) {
+  if (a.epi == EPI_SWIGLU) return 4;
+  const int cus = device_cus();
+  const long long slots = 2LL * (cus > 0 ? cus : 256);
+  const long long groups = a.G == 0 ? 1 : a.G;
+  auto cost = [&](int tn) {
+    const long long wgs = (a.N_out + 64LL * tn - 1) / (64LL * tn) * groups;
+    return (wgs + slots - 1) / slots * tn;
+  };
+  return cost(3) < cost(4) ? 3 : 4;
 }
 
 // Two workgroups per CU (one's dequant and waits overlap the other's MFMAs):
@@ -2456,7 +2495,7 @@ int launch_stream(const GemmArgs& a, hipStream_t s) {
     case SMOE_INT4:
       if (256 * (a.K / a.group_size) > kStreamScaleMax || (a.group_size & (a.group_size - 1)))
         return SMOE_EUNSUPPORTED;
-      return launch_stream4<6>(a, s);
+      return stream4_tn(a) == 3 ? launch_stream4<6, 3, 3>(a, s) : launch_stream4<6>(a, s);
     default: return SMOE_EUNSUPPORTED;
   }
 }
