@@ -500,6 +500,41 @@ def test_stream_int4_experts_ragged_passes(act, group, sdt, h):
     assert one.sum() == 1 and (got[one] - ref[one]).abs().max() <= 1e-2 * scale + 1e-6
 
 
+def test_stream_int4_strip_width_keeps_bits():
+    """The int4 stream GEMM's strip width (192 or 256 channels) follows the
+    grid: H = 2048 output channels over 64 groups fill the two workgroup
+    slots per CU with 256-channel strips, over 32 groups the launcher takes
+    192.  The same 32 experts and routing, once alone and once with 32
+    more experts that no token chooses, must give the same bits (each output
+    is summed in the same order whatever the width), and the oracle's
+    values within the int4 tolerance."""
+    from spider_moe_amd.quant import quantize_int4
+    n8 = nat()
+    say("stream int4 strip width")
+    h, u, n, k, group = 2048, 256, 1536, 2, 128  # 48 / 96 rows per group: the stream kernel
+    g = torch.Generator().manual_seed(43)
+    first = torch.randint(0, 32, (n,), generator=g)
+    idx = torch.stack([first, (first + 1 + torch.randint(0, 31, (n,), generator=g)) % 32], 1)
+    w = torch.rand(n, k, generator=g)
+    msg = torch.randn(n, h, generator=g).to(torch.bfloat16)
+    qu = quantize_int4(torch.randn(64, u, h, generator=g) * 0.05, group, torch.float16)
+    qd = quantize_int4(torch.randn(64, h, u, generator=g) * 0.05, group, torch.float16)
+    bu = torch.randn(64, u, generator=g) * 0.1
+    bd = torch.randn(64, h, generator=g) * 0.1
+    outs = []
+    for e in (32, 64):
+        t = [x[:e].contiguous().to(dev) for x in (qu.packed, qd.packed, qu.scales, qd.scales, bu, bd)]
+        ex = _experts_struct(n8, n8.INT4, n8.ACT_GELU, e, h, u, t[0], t[1], s_up=t[2], s_down=t[3],
+                             b_up=t[4], b_down=t[5], group=group, scale_dtype=n8.F16)
+        outs.append(_run_delta(n8, ex, msg.to(dev), idx.to(torch.int32).to(dev), w.to(dev)))
+    assert torch.equal(outs[0], outs[1])
+    wu_f = torch.from_numpy(Q.int4_dequantize(qu.packed[:32].numpy(), qu.scales[:32].float().numpy(), group))
+    wd_f = torch.from_numpy(Q.int4_dequantize(qd.packed[:32].numpy(), qd.scales[:32].float().numpy(), group))
+    ref = _oracle_delta(msg.float(), idx, w, wu_f, bu[:32], wd_f, bd[:32])
+    scale = ref.abs().max()
+    assert (outs[0] - ref).abs().max() <= 1e-2 * scale + 1e-6, float((outs[0] - ref).abs().max() / scale)
+
+
 @pytest.mark.parametrize("group,sdt", [(32, torch.float32), (128, torch.float16)])
 def test_int4_experts_match_oracle(group, sdt):
     from spider_moe_amd.quant import quantize_int4
