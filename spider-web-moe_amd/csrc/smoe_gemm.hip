@@ -740,7 +740,8 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
   // table of the tile's 256 channels x K / group_size scales loaded into LDS
   // before the main loop, kept in the part of the ring that only the
   // output staging uses), rounded once to bf16 — the values every int4
-  // kernel here multiplies.
+  // kernel here multiplies.  The widening of stage k + 1 runs in the wave's
+  // MFMA phase of stage k, not in its memory phase.
   static_assert(WF == SMOE_BF16 || ((WF == SMOE_FP8_E4M3 || WF == SMOE_INT4) && PK),
                 "fp8 / int4 weights need their tile copy");
   constexpr bool F8 = WF == SMOE_FP8_E4M3;
@@ -891,23 +892,29 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
   bf16x8 wf[FN], af[FM];
   float sj[I4 ? FN : 1];  // int4: the lane's rows' scales of the current group
   int kg_cur = -1;
-  auto read_frags = [&](int stage) {
-    if constexpr (I4) {
-      const int kg = (stage * 32) >> gshift;
-      if (kg != kg_cur) {  // uniform: a new scale group every group_size / 32 stages
-        kg_cur = kg;
+  // int4: the lane's raw nibbles of `stage` (quad wn, tile j: 8 nibbles at
+  // 4 lane), and the scales of its group.  The widening runs one stage ahead,
+  // beside the MFMAs of the stage before (tile j once its MFMAs have read
+  // it), so the memory phase only reads the activation fragments.
+  uint32_t w4[I4 ? FN : 1];
+  auto load_w4 = [&](int stage) {
+    const int kg = (stage * 32) >> gshift;
+    if (kg != kg_cur) {  // uniform: a new scale group every group_size / 32 stages
+      kg_cur = kg;
 #pragma unroll
-        for (int j = 0; j < FN; ++j) sj[j] = stab[(wn * TN + j * 16 + fr) * ng + kg];
-      }
+      for (int j = 0; j < FN; ++j) sj[j] = stab[(wn * TN + j * 16 + fr) * ng + kg];
     }
+    const uint8_t* sb = ring + (stage % NS) * STAGE + A_BYTES;
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+      w4[j] = *reinterpret_cast<const uint32_t*>(sb + wn * 1024 + j * 256 + 4 * lane);
+  };
+  auto read_frags = [&](int stage) {
     const uint8_t* sa = ring + (stage % NS) * STAGE;
     const uint8_t* sb = sa + A_BYTES;
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
-      if constexpr (I4) {  // quad wn, tile j: the lane's 8 nibbles at 4 lane
-        const uint32_t w4 =
-            *reinterpret_cast<const uint32_t*>(sb + wn * 1024 + j * 256 + 4 * lane);
-        wf[j] = __builtin_bit_cast(bf16x8, int4x8_to_bf16x8(w4, sj[j]));
+      if constexpr (I4) {  // widened during the previous stage's MFMAs
       } else if constexpr (F8) {  // tile tt's half block: row fr, k 8 fc.. at 16 fr + 256 (fc >> 1) + 8 (fc & 1)
         const int tt = wn * TN / 16 + j;
         const u32x2 c = *reinterpret_cast<const u32x2*>(
@@ -944,6 +951,11 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
   else wait_vmcnt<0>();
   if constexpr (I4) wait_lgkm0();  // the scale table is written
   __builtin_amdgcn_s_barrier();
+  if constexpr (I4) {  // stage 0's weights, before the first memory phase
+    load_w4(0);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) wf[j] = __builtin_bit_cast(bf16x8, int4x8_to_bf16x8(w4[j], sj[j]));
+  }
   if (grp == 1) __builtin_amdgcn_s_barrier();  // group 1 starts half a step behind
   for (int k = 0; k < KT; ++k) {
     // MEM(k)
@@ -955,12 +967,22 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
     }
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();
-    // MFMA(k)
+    // MFMA(k); int4: stage k + 1's weights (landed before the barrier that
+    // ended this group's memory phase; the last stage re-reads itself)
+    if constexpr (I4) load_w4(min(k + 1, KT - 1));
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
+    for (int j = 0; j < FN; ++j) {
 #pragma unroll
       for (int i = 0; i < FM; ++i)
         acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wf[j], af[i], acc[j][i], 0, 0, 0);
+      if constexpr (I4) {
+        // the empty asm pins the widening before the barrier: left free, the
+        // compiler sinks it to its use, the next memory phase
+        u32x4 u = int4x8_to_bf16x8(w4[j], sj[j]);
+        asm volatile("" : "+v"(u));
+        wf[j] = __builtin_bit_cast(bf16x8, u);
+      }
+    }
     if (grp == 0 || k + 1 < KT) __builtin_amdgcn_s_barrier();
   }
   // (no DMA is outstanding here; the epilogue synchronises before it reuses the ring)
