@@ -202,6 +202,32 @@ def test_int4_prefill_keeps_weights_int4():
     assert (got.float() - plain.float()).abs().max() <= 2e-2
 
 
+@pytest.mark.parametrize("experts", ["fp8", "int4"])
+def test_quantized_prefill_full_shape_tiles_match_plain(experts):
+    """The C1 block (16384 tokens, H 1024, U 2816 SwiGLU; 2048 rows per
+    expert, so 320-row ping-pong tiles over 32 K stages of the up GEMM and 88
+    of the down) with fp8 / int4 experts: one loop on the weight tile copies
+    (fragments widened in registers) against the general kernels
+    (weight_tiles = False).  The routing is the same in both (it runs before
+    the experts), so only summation orders differ: every value finite and
+    within 2e-2."""
+    from spider_moe_amd.workloads import make_block
+    say("full-shape quantized prefill, tiles vs plain", experts)
+    wl = make_block("c1", experts=experts, group_size=128)
+    layer = wl.layer
+    with torch.no_grad():
+        tiles = layer(wl.h, wl.x0, 0).float()
+        assert layer._pack().desc.experts.w_up_tiles
+        layer.weight_tiles = False
+        plain = layer(wl.h, wl.x0, 0).float()
+        assert not layer._pack().desc.experts.w_up_tiles
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(tiles).all()) and bool(torch.isfinite(plain).all())
+    err = float((tiles - plain).abs().max())
+    say("max diff", err)
+    assert err <= 2e-2, err
+
+
 @pytest.mark.parametrize("experts,act", [("fp8", "swiglu"), ("int4", "gelu"), ("int4", "swiglu")])
 def test_block_prefill_quantized_experts(experts, act):
     """Quantized experts at prefill size (2048 tokens over 8 experts: ~512
