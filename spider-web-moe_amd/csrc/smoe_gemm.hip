@@ -967,8 +967,11 @@ __global__ __launch_bounds__(512, BM == 128 ? 2 : 1) void k_gemm_pp(const GemmAr
     }
     wait_lgkm0();
     __builtin_amdgcn_s_barrier();
-    // MFMA(k); int4: stage k + 1's weights (landed before the barrier that
-    // ended this group's memory phase; the last stage re-reads itself)
+    // MFMA(k); int4: stage k + 1's weights (the last stage re-reads itself).
+    // Only waves 0-3 (group 0) DMA int4 weights, and they waited for stage
+    // k + 1 before the barrier that ended group 0's memory phase of k, which
+    // precedes both groups' MFMA phase of k.  (fp8 weights are DMA'd by all
+    // eight waves, so group 0 could read group 1's part early: not here.)
     if constexpr (I4) load_w4(min(k + 1, KT - 1));
 #pragma unroll
     for (int j = 0; j < FN; ++j) {
